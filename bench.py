@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: Q4_0 decode GEMV with the FFN gate/up
+shape, N = 14336 rows x K = 4096, f32 activations, as woolly's
+simd::quantized_matvec computes it.  One step = one GEMV launch over one
+weight matrix already resident in HBM.  The timed loop rotates through 10
+distinct weight copies (10 x 33 MB = 330 MB, more than the 256 MB Infinity
+Cache), so every launch streams its weights from HBM.
+
+Prints ONE JSON line with:
+  value          algorithmic GB/s of the GEMV = bytes per launch / ms_per_step,
+                 bytes = N*K/32*18 (weights) + 4K (x) + 4N (y) = 33,103,872 B
+  roofline       the GEMV kernel's average launch duration from per-launch HIP
+                 events on the launch stream, against the 8 TB/s HBM peak
+  ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
+                 M=512, same run (the metric's second part)
+  cpu_baseline   the CPU oracle's scalar GEMV (woolly's quantized_matvec_q4_0_scalar
+                 order, 1 thread) on this host, a bounded sample of full-size calls
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_0 GEMV achieved HBM GB/s (% of peak); FFN-layer µs at M=1 and M=512"
+Q4_0 = 2
+N_ROWS, K = 14336, 4096
+REPLICAS = 10
+
+
+def gemv_bytes(n: int, k: int) -> int:
+    return n * (k // 32) * 18 + 4 * k + 4 * n
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bench_gemv(steps: int, warmup: int):
+    from woolly_amd import ops, synth
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+
+    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=3)
+    x = synth.activations(K, seed=3)
+    stream = Stream()
+    wbufs = [DeviceBuffer.from_array(w) for _ in range(REPLICAS)]
+    xb = DeviceBuffer.from_array(x)
+    yb = DeviceBuffer(4 * N_ROWS)
+
+    def launch(i: int) -> None:
+        ops.quantized_matvec(Q4_0, wbufs[i % REPLICAS], w.nbytes, xb, yb, N_ROWS, K, stream)
+
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+
+    # The K timed launches are captured once into a HIP graph and replayed
+    # with one launch, so the host's per-call overhead does not throttle the
+    # GPU; events on the launch stream bracket the replay.
+    with Graph.capture(stream) as graph:
+        for i in range(steps):
+            launch(i)
+    graph.launch(stream)  # untimed replay (first-launch setup)
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    ms_total = e0.elapsed_ms(e1)
+    graph.destroy()
+
+    # per-launch kernel duration: an event pair around every launch
+    n_pairs = min(steps, 200)
+    evs = [(Event(), Event()) for _ in range(n_pairs)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        launch(i)
+        b.record(stream)
+    stream.synchronize()
+    durs = np.array([a.elapsed_ms(b) for a, b in evs])
+    for a, b in evs:
+        a.destroy()
+        b.destroy()
+    return ms_total / steps, float(np.median(durs)), float(np.mean(durs))
+
+
+def bench_ffn(m: int, iters: int) -> float:
+    from woolly_amd import ops, synth
+    from woolly_amd.device import DeviceBuffer, Event, Stream
+
+    hidden, n_ff = 4096, 14336
+    L = synth.ffn_layer(Q4_0, hidden, n_ff, m, seed=5)
+    stream = Stream()
+    b = {k: DeviceBuffer.from_array(v) for k, v in L.items()}
+    out = DeviceBuffer(4 * m * hidden)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m)
+    ws = DeviceBuffer(wsz)
+
+    def run():
+        ops.ffn_swiglu(Q4_0, b["gate"], b["up"], b["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
+                       m, out, ws, wsz, stream)
+
+    for _ in range(3):
+        run()
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    for _ in range(iters):
+        run()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / iters * 1000.0
+
+
+def cpu_baseline(budget_s: float = 10.0) -> dict:
+    """The oracle's order-exact scalar Q4_0 GEMV on this host (1 thread)."""
+    from tests._oracle import Oracle
+    from woolly_amd import synth
+
+    orc = Oracle()
+    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=3)
+    x = synth.activations(K, seed=3)
+    orc.matvec_f32(Q4_0, w, x, N_ROWS, K)  # warm
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        orc.matvec_f32(Q4_0, w, x, N_ROWS, K)
+        calls += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / calls
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(gemv_bytes(N_ROWS, K) / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{calls} full 14336x4096 Q4_0 GEMV calls of the oracle's scalar "
+                   f"quantized_matvec_q4_0_scalar restatement, {dt * 1e3:.1f} ms each, "
+                   f"host '{cpu}', nproc={os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-layer timings")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    from woolly_amd import device
+
+    device.init(0)
+    log(f"[bench] device: {device.device_name()}")
+    ms_step, med_ms, mean_ms = bench_gemv(args.steps, args.warmup)
+    nbytes = gemv_bytes(N_ROWS, K)
+    value = nbytes / (ms_step * 1e-3) / 1e9
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    log(f"[bench] gemv: {ms_step * 1e3:.2f} us/step back-to-back, per-launch mean "
+        f"{mean_ms * 1e3:.2f} us (median {med_ms * 1e3:.2f})")
+
+    ffn = {}
+    if not args.no_ffn:
+        ffn["m1"] = round(bench_ffn(1, 50), 2)
+        log(f"[bench] ffn m=1: {ffn['m1']} us")
+        ffn["m512"] = round(bench_ffn(512, 3), 2)
+        log(f"[bench] ffn m=512: {ffn['m512']} us")
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu['value']} GB/s")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64: d=f16(|N(0,0.02)|), uniform nibbles, x~N(0,1))",
+        "config": {
+            "workload": "Q4_0 decode GEMV N=14336 x K=4096 (FFN gate/up), f32 x and y, "
+                        f"{REPLICAS} rotating weight copies in HBM",
+            "n_rows": N_ROWS, "k": K, "ggml_type": "Q4_0", "bytes_per_launch": nbytes,
+        },
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "gemv_pairs_kernel<Q4_0,4>",
+            "launch_us_mean": round(mean_ms * 1e3, 3),
+        },
+        "ffn_layer_us": ffn or None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

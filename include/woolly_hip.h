@@ -1,0 +1,204 @@
+/*
+ * woolly_hip.h -- C ABI of the MI355X (gfx950) backend for woolly's quantized
+ * matmul hot path: GGUF Q4_0 / Q4_1 / Q8_0 dequantization, quantized GEMV and
+ * GEMM, RMSNorm, SwiGLU, and the fused SwiGLU feed-forward layer.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (wh_status).  Nothing panics,
+ *    aborts or throws across the ABI; the reference's panics (assert_eq! on
+ *    k % 32, quantization.rs:1107) become WH_ERR_INVALID_SHAPE.  The message of
+ *    the last failure on the calling thread is available from wh_last_error().
+ *  - Plain pointers and sizes only.  Device pointers are addresses returned by
+ *    wh_malloc (or any HIP device allocation); "host" variants take host memory.
+ *  - Kernel entry points are asynchronous and ordered on the given stream
+ *    (NULL = the device's null stream).  The *_host variants are synchronous.
+ *  - Weight matrices use ggml's convention: N rows of K elements, each row K/32
+ *    consecutive blocks (quantization.rs:730-737; GGUF ne0 = K is fastest), in
+ *    the on-disk block format (BlockQ4_0 18 B, BlockQ4_1 20 B, BlockQ8_0 34 B,
+ *    quantization.rs:98-151).  Output buffers are always caller-allocated.
+ *  - Calls are thread-safe; the library keeps no hidden global streams.
+ */
+#ifndef WOOLLY_HIP_H
+#define WOOLLY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WH_API __attribute__((visibility("default")))
+
+/* Status codes.  Mirrors QuantizationError (quantization.rs:8-26),
+ * woolly_gguf::Error (crates/woolly-gguf/src/error.rs:11-64) and the panics of
+ * the scalar kernels. */
+typedef enum wh_status {
+  WH_OK = 0,
+  WH_ERR_UNSUPPORTED_TYPE = 1,  /* UnsupportedScheme / Error::InvalidTensorType */
+  WH_ERR_INVALID_SHAPE = 2,     /* k % 32 != 0 (assert_eq! at quantization.rs:729,1107) */
+  WH_ERR_BUFFER_TOO_SMALL = 3,  /* Error::BufferTooSmall{needed, available} */
+  WH_ERR_INVALID_ARGUMENT = 4,  /* QuantizationError::InvalidParameters, null/misaligned */
+  WH_ERR_HIP = 5,               /* a HIP runtime call failed */
+  WH_ERR_OOM = 6,               /* device allocation failed */
+  WH_ERR_NO_DEVICE = 7          /* no usable gfx950 device */
+} wh_status;
+
+/* GGMLType ids (crates/woolly-gguf/src/tensor_info.rs:15-30). */
+typedef enum wh_type {
+  WH_TYPE_F32 = 0,
+  WH_TYPE_F16 = 1,
+  WH_TYPE_Q4_0 = 2,
+  WH_TYPE_Q4_1 = 3,
+  WH_TYPE_Q8_0 = 8
+} wh_type;
+
+typedef struct wh_stream_opaque* wh_stream_t; /* a hipStream_t */
+typedef struct wh_event_opaque* wh_event_t;   /* a hipEvent_t */
+typedef struct wh_weight wh_weight;           /* device-resident quantized tensor */
+typedef struct wh_graph_opaque* wh_graph_t;   /* an instantiated hipGraphExec_t */
+
+/* ------------------------------------------------------------------ errors */
+WH_API const char* wh_status_string(int status);
+WH_API const char* wh_last_error(void);
+WH_API int wh_version(void);
+
+/* ------------------------------------------------- device, memory, streams */
+/* Selects the device for the calling thread and checks that it is gfx950. */
+WH_API int wh_init(int device);
+WH_API int wh_device_count(int* count);
+WH_API int wh_device_name(char* buf, size_t len);
+WH_API int wh_malloc(void** dptr, size_t nbytes);
+WH_API int wh_free(void* dptr);
+WH_API int wh_memcpy_h2d(void* dst, const void* src, size_t nbytes, wh_stream_t stream);
+WH_API int wh_memcpy_d2h(void* dst, const void* src, size_t nbytes, wh_stream_t stream);
+WH_API int wh_memcpy_d2d(void* dst, const void* src, size_t nbytes, wh_stream_t stream);
+/* Fills nbytes with the byte value using a kernel (safe under graph capture). */
+WH_API int wh_fill_bytes(void* dst, int value, size_t nbytes, wh_stream_t stream);
+WH_API int wh_stream_create(wh_stream_t* out);
+WH_API int wh_stream_destroy(wh_stream_t stream);
+WH_API int wh_stream_synchronize(wh_stream_t stream);
+WH_API int wh_device_synchronize(void);
+WH_API int wh_event_create(wh_event_t* out);
+WH_API int wh_event_destroy(wh_event_t event);
+WH_API int wh_event_record(wh_event_t event, wh_stream_t stream);
+WH_API int wh_event_synchronize(wh_event_t event);
+WH_API int wh_event_elapsed_ms(float* ms, wh_event_t start, wh_event_t end);
+
+/* HIP graphs: capture a sequence of stream-ordered calls once, replay it with
+ * one launch (e.g. a decode step's projections).  Capture needs a non-null
+ * stream; the entry points above record only kernel launches (no memset
+ * nodes), so every replay recomputes from the buffers' current contents. */
+WH_API int wh_graph_begin_capture(wh_stream_t stream);
+WH_API int wh_graph_end_capture(wh_stream_t stream, wh_graph_t* out);
+WH_API int wh_graph_launch(wh_graph_t graph, wh_stream_t stream);
+WH_API int wh_graph_destroy(wh_graph_t graph);
+
+/* ------------------------------------------------------------------ format */
+/* get_block_size / get_type_size, crates/woolly-gguf/src/dequantize.rs:208-242.
+ * Return 0 for types this backend does not handle. */
+WH_API size_t wh_block_size(int type);
+WH_API size_t wh_type_size(int type);
+/* TensorInfo::data_size, crates/woolly-gguf/src/tensor_info.rs:244-255. */
+WH_API int wh_tensor_nbytes(int type, uint64_t nelements, uint64_t* nbytes);
+
+/* ------------------------------------------------------- dequantization */
+/* woolly_gguf::dequantize(data, ggml_type, nelements)
+ *   (crates/woolly-gguf/src/dequantize.rs:189-205), and through it
+ *   dequantize_q4_0 / dequantize_q4_1 / dequantize_q8_0
+ *   (crates/woolly-tensor/src/quantization.rs:466, 490, 576) and
+ *   optimized::dequantize_blocks (quantization.rs:1171).
+ * Writes exactly nelements f32 values; bit-exact with the reference.
+ * F32 and F16 are accepted as in the reference.  WH_ERR_BUFFER_TOO_SMALL when
+ * nbytes < ceil(nelements/32) * type_size. */
+WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelements,
+                         float* out, wh_stream_t stream);
+
+/* ------------------------------------------------------ quantized GEMV */
+/* simd::quantized_matvec(weights, input, output, m, k)
+ *   (crates/woolly-tensor/src/quantization.rs:869-909):
+ *   output[r] = sum_k W[r, k] * input[k] for r < m.
+ * Covers Q4_0 and Q8_0 like the reference, and Q4_1, which the reference
+ * rejects with UnsupportedScheme (quantization.rs:905-907).
+ * weight_nbytes must be >= m * (k/32) * type_size. */
+WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbytes,
+                               const float* input, float* output, size_t m, size_t k,
+                               wh_stream_t stream);
+
+/* ------------------------------------------------------ quantized GEMM */
+/* Y[t, r] = sum_k X[t, k] * W[r, k] for t < n_tokens, r < n_rows.
+ * Replaces the projections woolly runs on fully dequantized f32 weights:
+ *   simd_matmul_optimized -> Gemm::compute (tensor_utils_simd.rs:855-914,
+ *   ops/matmul.rs:83-259) called from simd_ffn_forward
+ *   (tensor_utils_simd.rs:605-754) and compute_simd_swiglu_ffn
+ *   (model/lazy_transformer.rs:1073-1123), with ggml's [N][K] weight layout
+ *   instead of the [K][N] reshape at lazy_transformer.rs:1091-1101.
+ * X is row-major [n_tokens][k] f32, Y is row-major [n_tokens][n_rows] f32. */
+WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes,
+                               size_t n_rows, size_t k, const float* x, size_t n_tokens,
+                               float* y, wh_stream_t stream);
+
+/* --------------------------------------------------- elementwise / norms */
+/* rms_norm (crates/woolly-core/src/tensor_utils.rs:446-480):
+ *   out[t, i] = (x[t, i] / sqrt(sum_i x[t, i]^2 / hidden + eps)) * weight[i] */
+WH_API int wh_rms_norm(const float* x, const float* weight, float eps, size_t tokens,
+                       size_t hidden, float* out, wh_stream_t stream);
+/* swiglu (crates/woolly-core/src/tensor_utils.rs:512-532):
+ *   out[i] = gate[i] * (1 / (1 + exp(-gate[i]))) * up[i] */
+WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out,
+                     wh_stream_t stream);
+
+/* ------------------------------------------------------ SwiGLU FFN layer */
+/* One feed-forward layer with its RMSNorm prologue:
+ *   xh = rms_norm(x, gamma, eps); out = W_down (silu(W_gate xh) * (W_up xh))
+ * The call site it replaces is compute_simd_swiglu_ffn
+ *   (model/lazy_transformer.rs:1073-1123) with the preceding rms_norm of
+ *   process_layer (lazy_transformer.rs:98-258); FeedForward::forward
+ *   (model/feedforward.rs:93-127) and fused_rmsnorm_ffn
+ *   (model/fused_kernels.rs:403-455) compute the same layer.
+ * gate and up are [n_ff][hidden], down is [hidden][n_ff], all of `type`.
+ * The workspace must hold wh_ffn_workspace_bytes(hidden, n_ff, m) bytes of
+ * device memory (no allocation happens inside the call). */
+typedef struct wh_ffn_weights {
+  int type;
+  const void* gate;
+  const void* up;
+  const void* down;
+  size_t hidden;
+  size_t n_ff;
+} wh_ffn_weights;
+
+WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m);
+WH_API int wh_ffn_swiglu(const wh_ffn_weights* weights, const float* gamma, float eps,
+                         const float* x, size_t m, float* out, void* workspace,
+                         size_t workspace_bytes, wh_stream_t stream);
+
+/* ------------------------------------------------------- weight handles */
+/* Uploads one quantized tensor straight from host bytes (e.g. the GGUF mmap
+ * slice at data_start_offset + tensor.offset, crates/woolly-gguf/src/loader.rs:274),
+ * replacing GGUFLoader::tensor_data's to_vec copy (loader.rs:291) and the f32
+ * dequantization cache (model/lazy_loader.rs:599-659).  The handle owns its
+ * device memory until wh_weight_free; the host bytes are only read during the
+ * call.  The device layout is the GGUF block layout, so the handle's data can
+ * be passed to every kernel entry point above. */
+WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_bytes,
+                            size_t nbytes, wh_weight** out);
+WH_API int wh_weight_free(wh_weight* weight);
+WH_API const void* wh_weight_data(const wh_weight* weight);
+WH_API int wh_weight_info(const wh_weight* weight, int* type, size_t* n_rows, size_t* k,
+                          size_t* nbytes);
+
+/* ------------------------------------- synchronous host-pointer variants */
+/* Same semantics as the device entry points, on host memory, blocking.  They
+ * mirror the reference's slice-in / Vec-out signatures
+ * (dequantize_q4_0(&[BlockQ4_0]) -> Vec<f32>, quantized_matvec(&storage,
+ * &[f32], &mut [f32], m, k)). */
+WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t nelements,
+                              float* out);
+WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
+                                    const float* input, float* output, size_t m, size_t k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WOOLLY_HIP_H */

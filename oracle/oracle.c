@@ -1,0 +1,468 @@
+/*
+ * oracle.c -- CPU restatement of woolly's quantized matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never part of the
+ * product.  Build with -O2 -ffp-contract=off (oracle/Makefile) so that every
+ * `a*b + c` stays an unfused multiply then add, as in the Rust reference.
+ * See oracle.h for the list of functions and how each one is pinned.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* IEEE-754 binary16 -> binary32 widening, written from the bit layout.
+ * Restates half::f16::to_f32 as used at quantization.rs:470,495-496,581 and
+ * dequantize.rs:306,356-357,572 (half 2.x: exact widening, NaNs are quieted
+ * and keep their payload). */
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {
+      /* subnormal: man * 2^-24; normalise so bit 10 is the implicit one */
+      int e = -1;
+      do {
+        man <<= 1;
+        e++;
+      } while (!(man & 0x400u));
+      man &= 0x3FFu;
+      bits = sign | ((uint32_t)(112 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (man << 13);
+    if (man) bits |= 0x00400000u;
+  } else {
+    bits = sign | ((exp + 112u) << 23) | (man << 13);
+  }
+  return bits_f32(bits);
+}
+
+/* binary32 -> binary16 with round-to-nearest-even (half::f16::from_f32, used
+ * by the reference's KATs and by the synthetic-input generators). */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x = f32_bits(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t exp = (x >> 23) & 0xFFu;
+  uint32_t man = x & 0x7FFFFFu;
+  if (exp == 0xFFu) {
+    if (man) return (uint16_t)(sign | 0x7E00u | (man >> 13));
+    return (uint16_t)(sign | 0x7C00u);
+  }
+  int e = (int)exp - 112;
+  if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    man |= 0x800000u;
+    int shift = 14 - e;
+    uint32_t hm = man >> shift;
+    uint32_t rem = man & ((1u << shift) - 1u);
+    uint32_t halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (hm & 1u))) hm++;
+    return (uint16_t)(sign | hm);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+  uint32_t rem = man & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)h;
+}
+
+void orc_f16_to_f32_array(const uint16_t* h, size_t n, float* out) {
+  for (size_t i = 0; i < n; i++) out[i] = orc_f16_to_f32(h[i]);
+}
+void orc_f32_to_f16_array(const float* f, size_t n, uint16_t* out) {
+  for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(f[i]);
+}
+
+/* get_block_size / get_type_size, crates/woolly-gguf/src/dequantize.rs:208-242 */
+size_t orc_block_size(int type) {
+  switch (type) {
+    case ORC_F32:
+    case ORC_F16:
+      return 1;
+    case ORC_Q4_0:
+    case ORC_Q4_1:
+    case ORC_Q8_0:
+      return 32;
+    default:
+      return 0;
+  }
+}
+size_t orc_type_size(int type) {
+  switch (type) {
+    case ORC_F32:
+      return 4;
+    case ORC_F16:
+      return 2;
+    case ORC_Q4_0:
+      return 18;
+    case ORC_Q4_1:
+      return 20;
+    case ORC_Q8_0:
+      return 34;
+    default:
+      return 0;
+  }
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Dequantize one block of 32 elements into out[0..32).
+ *   Q4_0: quantization.rs:466-486 / dequantize.rs:286-327:
+ *         element j<16 = ((qs[j] & 0xF) - 8) * d, element j+16 = ((qs[j] >> 4) - 8) * d
+ *   Q4_1: quantization.rs:490-511 / dequantize.rs:337-378: q * d + m
+ *   Q8_0: quantization.rs:576-590 / dequantize.rs:553-586: (int8)qs[j] * d */
+static void dequant_block(int type, const uint8_t* b, float* out) {
+  if (type == ORC_Q4_0) {
+    float d = orc_f16_to_f32(rd16(b));
+    const uint8_t* qs = b + 2;
+    for (int j = 0; j < 16; j++) {
+      int x0 = (int)(qs[j] & 0x0F) - 8;
+      int x1 = (int)(qs[j] >> 4) - 8;
+      out[j] = (float)x0 * d;
+      out[j + 16] = (float)x1 * d;
+    }
+  } else if (type == ORC_Q4_1) {
+    float d = orc_f16_to_f32(rd16(b));
+    float m = orc_f16_to_f32(rd16(b + 2));
+    const uint8_t* qs = b + 4;
+    for (int j = 0; j < 16; j++) {
+      float x0 = (float)(qs[j] & 0x0F);
+      float x1 = (float)(qs[j] >> 4);
+      float p0 = x0 * d;
+      float p1 = x1 * d;
+      out[j] = p0 + m;
+      out[j + 16] = p1 + m;
+    }
+  } else { /* ORC_Q8_0 */
+    float d = orc_f16_to_f32(rd16(b));
+    const int8_t* qs = (const int8_t*)(b + 2);
+    for (int j = 0; j < 32; j++) out[j] = (float)qs[j] * d;
+  }
+}
+
+/* woolly_gguf::dequantize(data, ggml_type, nelements), dequantize.rs:189-205:
+ * nblocks = ceil(n / 32); BufferTooSmall when data is shorter than
+ * nblocks * type_size; the output is truncated to n elements. */
+int orc_dequantize(int type, const uint8_t* data, size_t nbytes, size_t nelements,
+                   float* out) {
+  size_t ts = orc_type_size(type);
+  if (ts == 0) return ORC_ERR_UNSUPPORTED_TYPE;
+  if (type == ORC_F32) {
+    if (nbytes != nelements * 4) return ORC_ERR_BUFFER_TOO_SMALL;
+    memcpy(out, data, nelements * 4);
+    return ORC_OK;
+  }
+  if (type == ORC_F16) {
+    if (nbytes != nelements * 2) return ORC_ERR_BUFFER_TOO_SMALL;
+    for (size_t i = 0; i < nelements; i++) out[i] = orc_f16_to_f32(rd16(data + 2 * i));
+    return ORC_OK;
+  }
+  size_t nb = (nelements + 31) / 32;
+  if (nbytes < nb * ts) return ORC_ERR_BUFFER_TOO_SMALL;
+  float tmp[32];
+  for (size_t b = 0; b < nb; b++) {
+    dequant_block(type, data + b * ts, tmp);
+    size_t base = b * 32;
+    size_t cnt = nelements - base < 32 ? nelements - base : 32;
+    memcpy(out + base, tmp, cnt * sizeof(float));
+  }
+  return ORC_OK;
+}
+
+static int check_matvec_args(int type, size_t k) {
+  if (type != ORC_Q4_0 && type != ORC_Q4_1 && type != ORC_Q8_0)
+    return ORC_ERR_UNSUPPORTED_TYPE;
+  if (k % 32 != 0) return ORC_ERR_INVALID_SHAPE;
+  return ORC_OK;
+}
+
+/* Order-exact f32 quantized matvec, y[row] = sum_k W[row,k] * x[k].
+ *   Q4_0: quantized_matvec_q4_0_scalar, quantization.rs:1100-1132
+ *         sum += (x0 * d) * input[off + j]; sum += (x1 * d) * input[off + j + 16]
+ *   Q8_0: quantized_matvec_q8_0_scalar, quantization.rs:1135-1163
+ *   Q4_1: no reference kernel (quantized_matvec returns UnsupportedScheme at
+ *         quantization.rs:905-907); defined as dequantize_q4_1
+ *         (quantization.rs:490-511) followed by the f32 dot in the Q4_0 order. */
+int orc_matvec_f32(int type, const uint8_t* w, const float* x, float* y, size_t m,
+                   size_t k) {
+  int st = check_matvec_args(type, k);
+  if (st) return st;
+  size_t nb = k / 32, ts = orc_type_size(type);
+  for (size_t row = 0; row < m; row++) {
+    float sum = 0.0f;
+    const uint8_t* rp = w + row * nb * ts;
+    for (size_t b = 0; b < nb; b++) {
+      const uint8_t* blk = rp + b * ts;
+      const float* in = x + b * 32;
+      if (type == ORC_Q4_0) {
+        float d = orc_f16_to_f32(rd16(blk));
+        const uint8_t* qs = blk + 2;
+        for (int j = 0; j < 16; j++) {
+          int x0 = (int)(qs[j] & 0x0F) - 8;
+          int x1 = (int)(qs[j] >> 4) - 8;
+          float w0 = (float)x0 * d;
+          float w1 = (float)x1 * d;
+          float p0 = w0 * in[j];
+          sum = sum + p0;
+          float p1 = w1 * in[j + 16];
+          sum = sum + p1;
+        }
+      } else if (type == ORC_Q8_0) {
+        float d = orc_f16_to_f32(rd16(blk));
+        const int8_t* qs = (const int8_t*)(blk + 2);
+        for (int j = 0; j < 32; j++) {
+          float wv = (float)qs[j] * d;
+          float p = wv * in[j];
+          sum = sum + p;
+        }
+      } else {
+        float deq[32];
+        dequant_block(ORC_Q4_1, blk, deq);
+        for (int j = 0; j < 16; j++) {
+          float p0 = deq[j] * in[j];
+          sum = sum + p0;
+          float p1 = deq[j + 16] * in[j + 16];
+          sum = sum + p1;
+        }
+      }
+    }
+    y[row] = sum;
+  }
+  return ORC_OK;
+}
+
+/* Same product accumulated in double: every dequantized weight is an exact
+ * f32 value and f32*f32 is exact in f64, so this is the precision oracle. */
+int orc_matvec_f64(int type, const uint8_t* w, const float* x, double* y, size_t m,
+                   size_t k) {
+  int st = check_matvec_args(type, k);
+  if (st) return st;
+  size_t nb = k / 32, ts = orc_type_size(type);
+  float deq[32];
+  for (size_t row = 0; row < m; row++) {
+    double sum = 0.0;
+    const uint8_t* rp = w + row * nb * ts;
+    for (size_t b = 0; b < nb; b++) {
+      dequant_block(type, rp + b * ts, deq);
+      const float* in = x + b * 32;
+      for (int j = 0; j < 32; j++) sum += (double)deq[j] * (double)in[j];
+    }
+    y[row] = sum;
+  }
+  return ORC_OK;
+}
+
+static void dequant_row(int type, const uint8_t* w, size_t row, size_t k, float* out) {
+  size_t nb = k / 32, ts = orc_type_size(type);
+  const uint8_t* rp = w + row * nb * ts;
+  for (size_t b = 0; b < nb; b++) dequant_block(type, rp + b * ts, out + b * 32);
+}
+
+/* Y[t, n] = sum_k X[t, k] * W[n, k] in double, for a subset of token rows.
+ * This is the quantized replacement of the projections in
+ * simd_ffn_forward (tensor_utils_simd.rs:605-754) using ggml's [N][K]
+ * weight convention (quantization.rs:730-737). */
+int orc_matmul_rows_f64(int type, const uint8_t* w, size_t n, size_t k, const float* x,
+                        size_t m, const int64_t* rows, size_t nrows, double* y) {
+  int st = check_matvec_args(type, k);
+  if (st) return st;
+  (void)m;
+  float* wrow = (float*)malloc(k * sizeof(float));
+  if (!wrow) return ORC_ERR_BUFFER_TOO_SMALL;
+  for (size_t j = 0; j < n; j++) {
+    dequant_row(type, w, j, k, wrow);
+    for (size_t r = 0; r < nrows; r++) {
+      const float* xr = x + (size_t)rows[r] * k;
+      double s = 0.0;
+      for (size_t i = 0; i < k; i++) s += (double)xr[i] * (double)wrow[i];
+      y[r * n + j] = s;
+    }
+  }
+  free(wrow);
+  return ORC_OK;
+}
+
+int orc_matmul_f64(int type, const uint8_t* w, size_t n, size_t k, const float* x,
+                   size_t m, double* y) {
+  int64_t* rows = (int64_t*)malloc((m ? m : 1) * sizeof(int64_t));
+  if (!rows) return ORC_ERR_BUFFER_TOO_SMALL;
+  for (size_t i = 0; i < m; i++) rows[i] = (int64_t)i;
+  int st = orc_matmul_rows_f64(type, w, n, k, x, m, rows, m, y);
+  free(rows);
+  return st;
+}
+
+/* Gemm::compute_naive, crates/woolly-tensor/src/ops/matmul.rs:608-646
+ * (no transposes): c[i*n+j] = alpha * sum_l a[i*k+l]*b[l*n+j] + beta * c[i*n+j]. */
+void orc_gemm_f32(const float* a, const float* b, float* c, size_t m, size_t n, size_t k,
+                  float alpha, float beta) {
+  for (size_t i = 0; i < m; i++) {
+    for (size_t j = 0; j < n; j++) {
+      float sum = 0.0f;
+      for (size_t l = 0; l < k; l++) {
+        float p = a[i * k + l] * b[l * n + j];
+        sum = sum + p;
+      }
+      float s1 = alpha * sum;
+      float s2 = beta * c[i * n + j];
+      c[i * n + j] = s1 + s2;
+    }
+  }
+}
+
+/* rms_norm, crates/woolly-core/src/tensor_utils.rs:446-480:
+ *   rms = sqrt(sum(x*x) / hidden + eps);  out = (x / rms) * w  */
+void orc_rms_norm_f32(const float* x, const float* w, float eps, size_t tokens,
+                      size_t hidden, float* out) {
+  for (size_t t = 0; t < tokens; t++) {
+    const float* xt = x + t * hidden;
+    float ss = 0.0f;
+    for (size_t i = 0; i < hidden; i++) {
+      float sq = xt[i] * xt[i];
+      ss = ss + sq;
+    }
+    float mean = ss / (float)hidden;
+    float rms = sqrtf(mean + eps);
+    for (size_t i = 0; i < hidden; i++) {
+      float nv = xt[i] / rms;
+      out[t * hidden + i] = nv * w[i];
+    }
+  }
+}
+
+void orc_rms_norm_f64(const float* x, const float* w, double eps, size_t tokens,
+                      size_t hidden, double* out) {
+  for (size_t t = 0; t < tokens; t++) {
+    const float* xt = x + t * hidden;
+    double ss = 0.0;
+    for (size_t i = 0; i < hidden; i++) ss += (double)xt[i] * (double)xt[i];
+    double rms = sqrt(ss / (double)hidden + eps);
+    for (size_t i = 0; i < hidden; i++) out[t * hidden + i] = ((double)xt[i] / rms) * w[i];
+  }
+}
+
+/* swiglu, crates/woolly-core/src/tensor_utils.rs:512-532:
+ *   silu_gate = g * (1 / (1 + exp(-g)));  out = silu_gate * u
+ * (the exact SiLU; not the approximations of simd_matmul.rs:1050-1108). */
+void orc_swiglu_f32(const float* gate, const float* up, size_t n, float* out) {
+  for (size_t i = 0; i < n; i++) {
+    float g = gate[i];
+    float e = expf(-g);
+    float den = 1.0f + e;
+    float sig = 1.0f / den;
+    float sg = g * sig;
+    out[i] = sg * up[i];
+  }
+}
+
+void orc_swiglu_f64(const double* gate, const double* up, size_t n, double* out) {
+  for (size_t i = 0; i < n; i++) {
+    double g = gate[i];
+    out[i] = g * (1.0 / (1.0 + exp(-g))) * up[i];
+  }
+}
+
+/* One SwiGLU FFN layer with its RMSNorm prologue, in double:
+ *   xh = rms_norm(x, gamma, eps)                 tensor_utils.rs:446-480
+ *   g = W_gate xh, u = W_up xh                   lazy_transformer.rs:1073-1123
+ *   h = silu(g) * u                              tensor_utils.rs:512-532
+ *   out = W_down h                               feedforward.rs:93-127
+ * Weights use ggml's [N][K] convention: gate/up are [n_ff][hidden] and down is
+ * [hidden][n_ff]. */
+int orc_ffn_rows_f64(int type, const uint8_t* w_gate, const uint8_t* w_up,
+                     const uint8_t* w_down, size_t hidden, size_t n_ff, const float* gamma,
+                     double eps, const float* x, const int64_t* tokens, size_t ntok,
+                     double* out) {
+  int st = check_matvec_args(type, hidden);
+  if (st) return st;
+  st = check_matvec_args(type, n_ff);
+  if (st) return st;
+  double* xh = (double*)malloc(hidden * sizeof(double));
+  double* g = (double*)malloc(n_ff * sizeof(double));
+  double* u = (double*)malloc(n_ff * sizeof(double));
+  double* h = (double*)malloc(n_ff * sizeof(double));
+  float* wrow = (float*)malloc((hidden > n_ff ? hidden : n_ff) * sizeof(float));
+  if (!xh || !g || !u || !h || !wrow) {
+    free(xh); free(g); free(u); free(h); free(wrow);
+    return ORC_ERR_BUFFER_TOO_SMALL;
+  }
+  for (size_t t = 0; t < ntok; t++) {
+    orc_rms_norm_f64(x + (size_t)tokens[t] * hidden, gamma, eps, 1, hidden, xh);
+    for (size_t j = 0; j < n_ff; j++) {
+      double sg = 0.0, su = 0.0;
+      dequant_row(type, w_gate, j, hidden, wrow);
+      for (size_t i = 0; i < hidden; i++) sg += (double)wrow[i] * xh[i];
+      dequant_row(type, w_up, j, hidden, wrow);
+      for (size_t i = 0; i < hidden; i++) su += (double)wrow[i] * xh[i];
+      g[j] = sg;
+      u[j] = su;
+    }
+    orc_swiglu_f64(g, u, n_ff, h);
+    for (size_t i = 0; i < hidden; i++) {
+      double s = 0.0;
+      dequant_row(type, w_down, i, n_ff, wrow);
+      for (size_t j = 0; j < n_ff; j++) s += (double)wrow[j] * h[j];
+      out[t * hidden + i] = s;
+    }
+  }
+  free(xh); free(g); free(u); free(h); free(wrow);
+  return ORC_OK;
+}
+
+int orc_ffn_f64(int type, const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
+                size_t hidden, size_t n_ff, const float* gamma, double eps, const float* x,
+                size_t m, double* out) {
+  int64_t* rows = (int64_t*)malloc((m ? m : 1) * sizeof(int64_t));
+  if (!rows) return ORC_ERR_BUFFER_TOO_SMALL;
+  for (size_t i = 0; i < m; i++) rows[i] = (int64_t)i;
+  int st = orc_ffn_rows_f64(type, w_gate, w_up, w_down, hidden, n_ff, gamma, eps, x, rows,
+                            m, out);
+  free(rows);
+  return st;
+}
+
+/* The same layer on woolly's CPU f32 path: rms_norm (f32 order), the
+ * order-exact scalar quantized matvec for each projection and token, and the
+ * exact SwiGLU.  This is the CPU baseline the GPU FFN is timed beside. */
+int orc_ffn_f32(int type, const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
+                size_t hidden, size_t n_ff, const float* gamma, float eps, const float* x,
+                size_t m, float* out) {
+  int st = check_matvec_args(type, hidden);
+  if (st) return st;
+  st = check_matvec_args(type, n_ff);
+  if (st) return st;
+  float* xh = (float*)malloc(hidden * sizeof(float));
+  float* g = (float*)malloc(n_ff * sizeof(float));
+  float* u = (float*)malloc(n_ff * sizeof(float));
+  float* h = (float*)malloc(n_ff * sizeof(float));
+  if (!xh || !g || !u || !h) {
+    free(xh); free(g); free(u); free(h);
+    return ORC_ERR_BUFFER_TOO_SMALL;
+  }
+  for (size_t t = 0; t < m; t++) {
+    orc_rms_norm_f32(x + t * hidden, gamma, eps, 1, hidden, xh);
+    orc_matvec_f32(type, w_gate, xh, g, n_ff, hidden);
+    orc_matvec_f32(type, w_up, xh, u, n_ff, hidden);
+    orc_swiglu_f32(g, u, n_ff, h);
+    orc_matvec_f32(type, w_down, h, out + t * hidden, hidden, n_ff);
+  }
+  free(xh); free(g); free(u); free(h);
+  return ORC_OK;
+}

@@ -1,0 +1,171 @@
+"""ctypes binding of the CPU oracle (oracle/_build/liboracle.so).
+
+Test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use this module, and only as the checker.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_LIB = ORACLE_DIR / "_build" / "liboracle.so"
+
+_p = C.c_void_p
+_sz = C.c_size_t
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+class Oracle:
+    def __init__(self):
+        if not ORACLE_LIB.exists():
+            subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+        lib = C.CDLL(str(ORACLE_LIB))
+        sig = {
+            "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "orc_f16_to_f32_array": (None, [_p, _sz, _p]),
+            "orc_f32_to_f16_array": (None, [_p, _sz, _p]),
+            "orc_block_size": (_sz, [C.c_int]),
+            "orc_type_size": (_sz, [C.c_int]),
+            "orc_dequantize": (C.c_int, [C.c_int, _p, _sz, _sz, _p]),
+            "orc_matvec_f32": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz]),
+            "orc_matvec_f64": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz]),
+            "orc_matmul_f64": (C.c_int, [C.c_int, _p, _sz, _sz, _p, _sz, _p]),
+            "orc_matmul_rows_f64": (C.c_int, [C.c_int, _p, _sz, _sz, _p, _sz, _p, _sz, _p]),
+            "orc_gemm_f32": (None, [_p, _p, _p, _sz, _sz, _sz, C.c_float, C.c_float]),
+            "orc_rms_norm_f32": (None, [_p, _p, C.c_float, _sz, _sz, _p]),
+            "orc_rms_norm_f64": (None, [_p, _p, C.c_double, _sz, _sz, _p]),
+            "orc_swiglu_f32": (None, [_p, _p, _sz, _p]),
+            "orc_swiglu_f64": (None, [_p, _p, _sz, _p]),
+            "orc_ffn_f64": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_double, _p, _sz, _p]),
+            "orc_ffn_rows_f64": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_double, _p, _p,
+                                           _sz, _p]),
+            "orc_ffn_f32": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_float, _p, _sz, _p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        self.lib = lib
+
+    # --- scalar helpers
+    def f16_to_f32(self, bits: np.ndarray) -> np.ndarray:
+        b = np.ascontiguousarray(bits, dtype=np.uint16)
+        out = np.empty(b.size, dtype=np.float32)
+        self.lib.orc_f16_to_f32_array(_ptr(b), b.size, _ptr(out))
+        return out
+
+    def f32_to_f16(self, vals: np.ndarray) -> np.ndarray:
+        v = np.ascontiguousarray(vals, dtype=np.float32)
+        out = np.empty(v.size, dtype=np.uint16)
+        self.lib.orc_f32_to_f16_array(_ptr(v), v.size, _ptr(out))
+        return out
+
+    def type_size(self, t: int) -> int:
+        return int(self.lib.orc_type_size(t))
+
+    def block_size(self, t: int) -> int:
+        return int(self.lib.orc_block_size(t))
+
+    # --- kernels
+    def dequantize(self, t: int, data: np.ndarray, n: int) -> tuple[int, np.ndarray]:
+        d = np.ascontiguousarray(data, dtype=np.uint8)
+        out = np.zeros(n, dtype=np.float32)
+        st = self.lib.orc_dequantize(t, _ptr(d), d.nbytes, n, _ptr(out))
+        return st, out
+
+    def matvec_f32(self, t, w, x, m, k):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(m, dtype=np.float32)
+        st = self.lib.orc_matvec_f32(t, _ptr(w), _ptr(x), _ptr(y), m, k)
+        return st, y
+
+    def matvec_f64(self, t, w, x, m, k):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(m, dtype=np.float64)
+        st = self.lib.orc_matvec_f64(t, _ptr(w), _ptr(x), _ptr(y), m, k)
+        return st, y
+
+    def matmul_rows_f64(self, t, w, n, k, x, m, rows):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        r = np.ascontiguousarray(rows, dtype=np.int64)
+        y = np.zeros((r.size, n), dtype=np.float64)
+        st = self.lib.orc_matmul_rows_f64(t, _ptr(w), n, k, _ptr(x), m, _ptr(r), r.size, _ptr(y))
+        assert st == 0
+        return y
+
+    def gemm_f32(self, a, b, c, m, n, k, alpha=1.0, beta=0.0):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        c = np.array(c, dtype=np.float32, copy=True)
+        self.lib.orc_gemm_f32(_ptr(a), _ptr(b), _ptr(c), m, n, k, alpha, beta)
+        return c
+
+    def rms_norm_f32(self, x, w, eps, tokens, hidden):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.zeros(tokens * hidden, dtype=np.float32)
+        self.lib.orc_rms_norm_f32(_ptr(x), _ptr(w), eps, tokens, hidden, _ptr(out))
+        return out
+
+    def rms_norm_f64(self, x, w, eps, tokens, hidden):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.zeros(tokens * hidden, dtype=np.float64)
+        self.lib.orc_rms_norm_f64(_ptr(x), _ptr(w), eps, tokens, hidden, _ptr(out))
+        return out
+
+    def swiglu_f32(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        out = np.zeros(g.size, dtype=np.float32)
+        self.lib.orc_swiglu_f32(_ptr(g), _ptr(u), g.size, _ptr(out))
+        return out
+
+    def swiglu_f64(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float64)
+        u = np.ascontiguousarray(u, dtype=np.float64)
+        out = np.zeros(g.size, dtype=np.float64)
+        self.lib.orc_swiglu_f64(_ptr(g), _ptr(u), g.size, _ptr(out))
+        return out
+
+    def ffn_rows_f64(self, t, gate, up, down, hidden, n_ff, gamma, eps, x, tokens):
+        tok = np.ascontiguousarray(tokens, dtype=np.int64)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros((tok.size, hidden), dtype=np.float64)
+        st = self.lib.orc_ffn_rows_f64(t, _ptr(gate), _ptr(up), _ptr(down), hidden, n_ff,
+                                       _ptr(np.ascontiguousarray(gamma, dtype=np.float32)), eps,
+                                       _ptr(x), _ptr(tok), tok.size, _ptr(out))
+        assert st == 0
+        return out
+
+    def ffn_f32(self, t, gate, up, down, hidden, n_ff, gamma, eps, x, m):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros((m, hidden), dtype=np.float32)
+        st = self.lib.orc_ffn_f32(t, _ptr(gate), _ptr(up), _ptr(down), hidden, n_ff,
+                                  _ptr(np.ascontiguousarray(gamma, dtype=np.float32)), eps,
+                                  _ptr(x), m, _ptr(out))
+        assert st == 0
+        return out
+
+
+def rel_l2(a, ref) -> float:
+    a = np.asarray(a, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(a - ref) / den) if den > 0 else float(np.linalg.norm(a - ref))
+
+
+def max_abs(a, ref) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(ref, np.float64)))) if np.size(a) else 0.0

@@ -1,0 +1,101 @@
+"""The C ABI library loads, exports every declared symbol, and reports the
+reference's error semantics for bad arguments without touching a GPU."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from woolly_amd import _lib, gguf, quantization
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "woolly_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"WH_API\s+[\w\s\*]+?\b(wh_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 30
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in woolly_hip.h but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_library_is_gfx950_only():
+    data = (ROOT / "woolly_amd" / "libwoolly_hip.so").read_bytes()
+    assert b"gfx950" in data
+
+
+def test_format_queries():
+    lib = _lib.load()
+    assert lib.wh_type_size(2) == 18 and lib.wh_type_size(3) == 20 and lib.wh_type_size(8) == 34
+    assert lib.wh_block_size(2) == 32 and lib.wh_block_size(0) == 1 and lib.wh_block_size(12) == 0
+    # tensor_info.rs:292-305: 64x64 Q4_0 -> 2304 bytes; 4x8 F32 -> 128 bytes
+    assert gguf.data_size(gguf.GGMLType.Q4_0, 4096) == 2304
+    assert gguf.data_size(gguf.GGMLType.F32, 32) == 128
+    assert gguf.get_type_size(gguf.GGMLType.Q8_0) == 34
+    assert lib.wh_status_string(2) == b"WH_ERR_INVALID_SHAPE"
+
+
+def test_matvec_argument_errors_need_no_gpu():
+    lib = _lib.load()
+    w = np.zeros(2 * 18 * 2, np.uint8)
+    x = np.zeros(64, np.float32)
+    y = np.zeros(2, np.float32)
+    # k % 32 != 0 -> the reference's assert_eq! panic becomes WH_ERR_INVALID_SHAPE
+    assert lib.wh_quantized_matvec(2, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
+                                   2, 48, None) == _lib.WH_ERR_INVALID_SHAPE
+    assert b"multiple of the block size" in lib.wh_last_error()
+    # unsupported scheme (Q4_K, id 12) -> UnsupportedScheme
+    assert lib.wh_quantized_matvec(12, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
+                                   2, 64, None) == _lib.WH_ERR_UNSUPPORTED_TYPE
+    # too few weight bytes -> BufferTooSmall{needed, available}
+    assert lib.wh_quantized_matvec(2, w.ctypes.data, 71, x.ctypes.data, y.ctypes.data,
+                                   2, 64, None) == _lib.WH_ERR_BUFFER_TOO_SMALL
+    assert b"needed 72 bytes, available 71" in lib.wh_last_error()
+    # m == 0 is a no-op
+    assert lib.wh_quantized_matvec(2, None, 0, None, None, 0, 64, None) == _lib.WH_OK
+    # null output with work to do
+    assert lib.wh_quantized_matvec(2, w.ctypes.data, w.nbytes, x.ctypes.data, None,
+                                   2, 64, None) == _lib.WH_ERR_INVALID_ARGUMENT
+
+
+def test_dequant_argument_errors_need_no_gpu():
+    with pytest.raises(gguf.BufferTooSmall) as e:
+        gguf.dequantize(bytes(35), gguf.GGMLType.Q4_0, 64)
+    assert e.value.needed == 36 and e.value.available == 35
+    with pytest.raises(gguf.InvalidTensorType):
+        gguf.dequantize(bytes(144), gguf.GGMLType.Q4_K, 256)
+    with pytest.raises(gguf.BufferTooSmall):
+        gguf.dequantize(bytes(10), gguf.GGMLType.F32, 4)   # F32 needs exactly 16 bytes
+    assert gguf.dequantize(b"", gguf.GGMLType.Q4_0, 0).size == 0
+
+
+def test_python_mirror_errors_need_no_gpu():
+    st = quantization.QuantizedStorage(quantization.QuantizationScheme.Q5_0, np.zeros(22, np.uint8))
+    with pytest.raises(quantization.QuantizationError.UnsupportedScheme):
+        quantization.simd.quantized_matvec(st, np.zeros(32, np.float32), np.zeros(1, np.float32),
+                                           1, 32)
+    st = quantization.QuantizedStorage.Q4_0(np.zeros(18, np.uint8))
+    with pytest.raises(quantization.QuantizationError.InvalidParameters):
+        quantization.simd.quantized_matvec(st, np.zeros(48, np.float32), np.zeros(1, np.float32),
+                                           1, 48)
+
+
+def test_ffn_and_weight_argument_errors_need_no_gpu():
+    lib = _lib.load()
+    w = _lib.wh_ffn_weights(2, 1, 1, 1, 4096, 14336)
+    assert lib.wh_ffn_swiglu(C.byref(w), 1, 1e-5, 1, 1, 1, 1, 0, None) == _lib.WH_ERR_BUFFER_TOO_SMALL
+    w = _lib.wh_ffn_weights(2, 1, 1, 1, 4010, 14336)
+    assert lib.wh_ffn_swiglu(C.byref(w), 1, 1e-5, 1, 1, 1, 1, 1 << 40, None) == _lib.WH_ERR_INVALID_SHAPE
+    assert lib.wh_ffn_workspace_bytes(4096, 14336, 1) >= 4 * (4096 + 3 * 14336)
+    h = C.c_void_p()
+    assert lib.wh_weight_upload(2, 4, 48, None, 0, C.byref(h)) == _lib.WH_ERR_INVALID_SHAPE
+    assert lib.wh_weight_upload(2, 4, 64, None, 10, C.byref(h)) == _lib.WH_ERR_BUFFER_TOO_SMALL
+    assert h.value is None

@@ -1,0 +1,355 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself: the
+reference's own known-answer tests (restated with their file:line), an
+independent implementation (numpy's IEEE binary16, numpy float64 linear
+algebra), closed forms, and brute force on tiny inputs.  A plausible mistake
+(swapped nibbles, a missing -8, a wrong scale byte, a transposed operand, a
+dropped epsilon) fails at least one of them; test_oracle_catches_planted_bugs
+demonstrates that with mutated numpy restatements.
+"""
+import numpy as np
+import pytest
+from scipy.special import expit
+
+from tests._oracle import max_abs, rel_l2
+from woolly_amd import synth
+
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
+
+
+def f16(x):
+    return int(np.float16(x).view(np.uint16))
+
+
+def block_q4_0(d, qs):
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
+    b[2:] = qs
+    return b
+
+
+def block_q4_1(d, m, qs):
+    b = np.zeros(20, np.uint8)
+    b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([f16(m)], np.uint16).view(np.uint8)
+    b[4:] = qs
+    return b
+
+
+def block_q8_0(d, qs):
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
+    b[2:] = np.asarray(qs, np.int8).view(np.uint8)
+    return b
+
+
+# ----------------------------------------------------------------- numpy twins
+def np_dequant(t, data, n):
+    """Independent vectorised decoder (numpy), written from the block layout."""
+    ts = {Q4_0: 18, Q4_1: 20, Q8_0: 34}[t]
+    nb = (n + 31) // 32
+    blk = np.asarray(data, np.uint8)[: nb * ts].reshape(nb, ts)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
+    if t == Q4_0:
+        qs = blk[:, 2:18]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32) - 8.0
+        out = q * d
+    elif t == Q4_1:
+        m = blk[:, 2:4].copy().view(np.float16).astype(np.float32)
+        qs = blk[:, 4:20]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32)
+        out = (q * d).astype(np.float32) + m
+    else:
+        q = blk[:, 2:34].view(np.int8).astype(np.float32)
+        out = q * d
+    return out.astype(np.float32).reshape(-1)[:n]
+
+
+# ------------------------------------------------------------------ f16 codec
+def test_f16_to_f32_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint16)
+    got = orc.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # NaNs: same sign and payload; the oracle quiets them like half::f16::to_f32.
+    g, r = got[nan].view(np.uint32), ref[nan].view(np.uint32)
+    assert np.array_equal(g & ~np.uint32(0x400000), r & ~np.uint32(0x400000))
+    assert np.all(g & np.uint32(0x400000))
+
+
+def test_f32_to_f16_rne(orc):
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(0.02),
+        rng.standard_normal(20000).astype(np.float32) * np.float32(3e4),
+        (rng.random(20000) * 1e-4).astype(np.float32),
+        np.array([0.0, -0.0, 65504, 65519.99, 65520, 1e9, -1e9, 2 ** -24, 2 ** -25,
+                  1.5 * 2 ** -25, 2 ** -26, 6.1e-5, np.inf, -np.inf], np.float32),
+        # exact ties between neighbouring f16 values (round half to even)
+        (np.arange(1, 2000, dtype=np.float32) * np.float32(2 ** -11) + np.float32(1.0)),
+    ])
+    got = orc.f32_to_f16(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# --------------------------------------------------- block sizes (reference)
+def test_block_sizes(orc):
+    # quantization.rs:1347-1356 (size_of 18 / 20 / 34), dequantize.rs:208-242
+    assert orc.type_size(Q4_0) == 18 and orc.type_size(Q4_1) == 20 and orc.type_size(Q8_0) == 34
+    assert orc.block_size(Q4_0) == 32 and orc.block_size(Q8_0) == 32
+    # tensor_info.rs:281-305: a 64x64 Q4_0 tensor is 128 blocks = 2304 bytes
+    assert (64 * 64 // 32) * orc.type_size(Q4_0) == 2304
+    # load_model.rs:294-327: 64 Q4_0 elements = 36 bytes
+    assert 2 * orc.type_size(Q4_0) == 36
+
+
+# ------------------------------------------------ dequantization KATs (reference)
+def test_kat_q4_0_dequantization(orc):
+    # quantization.rs:1294-1307: d = 2, qs = 0 -> every value -8 * 2 = -16
+    st, out = orc.dequantize(Q4_0, block_q4_0(2.0, [0] * 16), 32)
+    assert st == 0 and np.all(out == -16.0)
+
+
+def test_kat_q4_1_dequantization(orc):
+    # quantization.rs:1310-1326: d = 1, m = 5, qs = 0x01 -> [6] * 16 then [5] * 16
+    st, out = orc.dequantize(Q4_1, block_q4_1(1.0, 5.0, [0x01] * 16), 32)
+    assert st == 0
+    assert np.all(out[:16] == 6.0) and np.all(out[16:] == 5.0)
+
+
+def test_kat_q8_0_dequantization(orc):
+    # quantization.rs:1329-1344: qs[0] = 10, qs[1] = -5, d = 0.5 -> 5, -2.5
+    qs = np.zeros(32, np.int8)
+    qs[0], qs[1] = 10, -5
+    st, out = orc.dequantize(Q8_0, block_q8_0(0.5, qs), 32)
+    assert st == 0 and out[0] == 5.0 and out[1] == -2.5 and np.all(out[2:] == 0)
+
+
+def test_kat_optimized_dispatcher(orc):
+    # quantization.rs:1359-1386: [d=1, qs=0x11] -> -7; [d=2, qs=0x22] -> -12
+    data = np.concatenate([block_q4_0(1.0, [0x11] * 16), block_q4_0(2.0, [0x22] * 16)])
+    st, out = orc.dequantize(Q4_0, data, 64)
+    assert st == 0 and np.all(out[:32] == -7.0) and np.all(out[32:] == -12.0)
+
+
+def test_kat_simd_batch(orc):
+    # quantization.rs:1388-1409: 8 blocks, d = i + 1, qs = 0 -> -8 (i + 1)
+    data = np.concatenate([block_q4_0(i + 1.0, [0] * 16) for i in range(8)])
+    st, out = orc.dequantize(Q4_0, data, 256)
+    assert st == 0
+    assert np.array_equal(out, np.repeat(-8.0 * (np.arange(8) + 1), 32).astype(np.float32))
+
+
+def test_kat_parallel_integration_blocks(orc):
+    # woolly-core/tests/parallel_inference_integration.rs:159-210
+    d = [0.1 + i * 0.001 for i in range(64)]
+    q4 = np.concatenate([block_q4_0(d[i], [i % 16] * 16) for i in range(64)])
+    st, out = orc.dequantize(Q4_0, q4, 64 * 32)
+    assert st == 0
+    for i in range(64):
+        dv = np.float32(np.float16(d[i]))
+        # qs = i % 16 in every byte: low nibble i % 16, high nibble 0
+        assert np.all(out[32 * i:32 * i + 16] == np.float32((i % 16) - 8) * dv)
+        assert np.all(out[32 * i + 16:32 * i + 32] == np.float32(-8) * dv)
+    q8 = np.concatenate([block_q8_0(d[i], [i % 127] * 32) for i in range(64)])
+    st, out = orc.dequantize(Q8_0, q8, 64 * 32)
+    assert st == 0
+    for i in range(64):
+        assert np.all(out[32 * i:32 * i + 32] == np.float32(i % 127) * np.float32(np.float16(d[i])))
+
+
+def test_kat_bench_generators(orc):
+    # woolly-tensor/benches/simd_benchmarks.rs:18-46 deterministic patterns
+    nb = 40
+    q4 = np.concatenate([block_q4_0(0.5 + (i * 0.1) % 1.0, [(i + j) % 16 for j in range(16)])
+                         for i in range(nb)])
+    q8 = np.concatenate([block_q8_0(0.5 + (i * 0.1) % 1.0,
+                                    [((i + j) % 256) - 128 for j in range(32)]) for i in range(nb)])
+    for t, data in ((Q4_0, q4), (Q8_0, q8)):
+        st, out = orc.dequantize(t, data, nb * 32)
+        assert st == 0
+        assert np.array_equal(out.view(np.uint32), np_dequant(t, data, nb * 32).view(np.uint32))
+
+
+# ---------------------------------------------- dequantization vs numpy twin
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+@pytest.mark.parametrize("n", [32, 96, 1000, 4096])
+def test_dequant_matches_numpy(orc, t, n):
+    w = synth.quantized_weight(t, 1, ((n + 31) // 32) * 32, seed=7)
+    st, out = orc.dequantize(t, w, n)
+    assert st == 0
+    assert np.array_equal(out.view(np.uint32), np_dequant(t, w, n).view(np.uint32))
+
+
+def test_dequant_all_f16_scales(orc):
+    # every f16 bit pattern as a Q4_0 / Q8_0 scale, against the numpy decoder
+    nb = 65536
+    rng = np.random.default_rng(1)
+    q4 = np.zeros((nb, 18), np.uint8)
+    q4[:, 0:2] = np.arange(nb, dtype=np.uint16).view(np.uint8).reshape(nb, 2)
+    q4[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    st, out = orc.dequantize(Q4_0, q4.reshape(-1), nb * 32)
+    ref = np_dequant(Q4_0, q4.reshape(-1), nb * 32)
+    assert st == 0
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_dequant_errors(orc):
+    w = synth.quantized_weight(Q4_0, 1, 64, seed=1)
+    st, _ = orc.dequantize(Q4_0, w[:35], 64)   # needs 36 bytes
+    assert st == 3
+    st, _ = orc.dequantize(12, w, 64)          # Q4_K is not on this path
+    assert st == 1
+    st, out = orc.dequantize(Q4_0, w, 40)      # truncation to nelements
+    assert st == 0 and out.size == 40
+
+
+# ------------------------------------------------------------------- GEMV
+def test_gemv_closed_form_constant_nibbles(orc):
+    # Blocks whose 32 nibbles are all c_b: y[r] = sum_b d_b (c_b - 8) sum_{j in b} x_j
+    rng = np.random.default_rng(2)
+    m, k = 5, 256
+    nb = k // 32
+    c = rng.integers(0, 16, (m, nb))
+    d = np.abs(rng.standard_normal((m, nb))) * 0.05
+    w = np.concatenate([block_q4_0(d[r, b], [c[r, b] * 17] * 16) for r in range(m) for b in range(nb)])
+    x = rng.standard_normal(k).astype(np.float32)
+    dq = np.float16(d).astype(np.float64)
+    xs = x.astype(np.float64).reshape(nb, 32).sum(axis=1)
+    ref = (dq * (c - 8) * xs[None, :]).sum(axis=1)
+    st, y64 = orc.matvec_f64(Q4_0, w, x, m, k)
+    assert st == 0 and np.allclose(y64, ref, rtol=1e-12, atol=1e-12)
+    st, y32 = orc.matvec_f32(Q4_0, w, x, m, k)
+    assert st == 0 and rel_l2(y32, ref) < 1e-6
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+def test_gemv_brute_force_f64(orc, t):
+    m, k = 7, 192
+    w = synth.quantized_weight(t, m, k, seed=3)
+    x = synth.activations(k, seed=3)
+    dense = np_dequant(t, w, m * k).astype(np.float64).reshape(m, k)
+    ref = dense @ x.astype(np.float64)
+    st, y64 = orc.matvec_f64(t, w, x, m, k)
+    assert st == 0 and np.allclose(y64, ref, rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+def test_gemv_f32_evaluation_order(orc, t):
+    # numpy float32 emulation of quantized_matvec_*_scalar's sequence
+    # (quantization.rs:1100-1163): per block, for j < 16: sum += w[j]*x[j];
+    # sum += w[j+16]*x[j+16] (Q4_x), or j = 0..31 in order (Q8_0).
+    m, k = 3, 128
+    w = synth.quantized_weight(t, m, k, seed=4)
+    x = synth.activations(k, seed=4)
+    dense = np_dequant(t, w, m * k).reshape(m, k)
+    ref = np.zeros(m, np.float32)
+    for r in range(m):
+        s = np.float32(0)
+        for b in range(k // 32):
+            order = ([j for jj in range(16) for j in (jj, jj + 16)] if t != Q8_0 else range(32))
+            for j in order:
+                s = np.float32(s + np.float32(dense[r, 32 * b + j] * x[32 * b + j]))
+        ref[r] = s
+    st, y32 = orc.matvec_f32(t, w, x, m, k)
+    assert st == 0 and np.array_equal(y32.view(np.uint32), ref.view(np.uint32))
+
+
+def test_gemv_errors(orc):
+    w = synth.quantized_weight(Q4_0, 2, 64, seed=1)
+    x = np.zeros(64, np.float32)
+    assert orc.matvec_f32(Q4_0, w, x, 2, 48)[0] == 2   # k % 32 != 0
+    assert orc.matvec_f32(12, w, x, 2, 64)[0] == 1     # unsupported scheme
+
+
+# ------------------------------------------------------------------- GEMM KATs
+def test_gemm_kats(orc):
+    # matmul.rs:934-958: [[1,2,3],[4,5,6]] x [[7,8],[9,10],[11,12]] = [[58,64],[139,154]]
+    c = orc.gemm_f32([1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12], np.zeros(4), 2, 2, 3)
+    assert c.tolist() == [58, 64, 139, 154]
+    # matmul.rs:960-974 (MatVec): [[1,2,3],[4,5,6]] . [7,8,9] = [50, 122]
+    c = orc.gemm_f32([1, 2, 3, 4, 5, 6], [7, 8, 9], np.zeros(2), 2, 1, 3)
+    assert c.tolist() == [50, 122]
+    # tensor_utils.rs:608-620: [[1,2],[3,4]] x [[5,6],[7,8]] = [[19,22],[43,50]]
+    c = orc.gemm_f32([1, 2, 3, 4], [5, 6, 7, 8], np.zeros(4), 2, 2, 2)
+    assert c.tolist() == [19, 22, 43, 50]
+    # alpha / beta of compute_naive (matmul.rs:640-642)
+    c = orc.gemm_f32([1, 2, 3, 4], [5, 6, 7, 8], np.ones(4), 2, 2, 2, alpha=2.0, beta=3.0)
+    assert c.tolist() == [41, 47, 89, 103]
+
+
+def test_matmul_rows_f64(orc):
+    m, n, k = 4, 9, 128
+    w = synth.quantized_weight(Q8_0, n, k, seed=5)
+    x = synth.activations(m * k, seed=5).reshape(m, k)
+    dense = np_dequant(Q8_0, w, n * k).astype(np.float64).reshape(n, k)
+    ref = x.astype(np.float64) @ dense.T
+    y = orc.matmul_rows_f64(Q8_0, w, n, k, x, m, [3, 0])
+    assert np.allclose(y, ref[[3, 0]], rtol=1e-13, atol=1e-12)
+
+
+# --------------------------------------------------------- RMSNorm / SwiGLU
+def test_rms_norm(orc):
+    h = 64
+    # constant row c: out = c / sqrt(c^2 + eps) * w
+    x = np.full(h, 3.0, np.float32)
+    w = np.linspace(0.5, 1.5, h).astype(np.float32)
+    out = orc.rms_norm_f64(x, w, 1e-5, 1, h)
+    assert np.allclose(out, 3.0 / np.sqrt(9.0 + 1e-5) * w.astype(np.float64), rtol=1e-14)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, h)).astype(np.float32)
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-5) * w
+    assert np.allclose(orc.rms_norm_f64(x, w, 1e-5, 3, h).reshape(3, h), ref, rtol=1e-13)
+    assert rel_l2(orc.rms_norm_f32(x, w, 1e-5, 3, h), ref.reshape(-1)) < 1e-6
+    # eps matters: an all-zero row gives zeros, not NaN
+    assert np.all(orc.rms_norm_f32(np.zeros(h), w, 1e-5, 1, h) == 0)
+
+
+def test_swiglu(orc):
+    g = np.array([0.0, 50.0, -50.0, 1.0, -1.0, 3.5], np.float64)
+    u = np.array([2.0, 2.0, 2.0, 3.0, 3.0, -1.0], np.float64)
+    ref = g * expit(g) * u
+    assert np.allclose(orc.swiglu_f64(g, u), ref, rtol=1e-14, atol=1e-300)
+    assert orc.swiglu_f64(g, u)[0] == 0.0
+    assert np.allclose(orc.swiglu_f32(g, u), ref, rtol=1e-6, atol=1e-30)
+
+
+def test_ffn_composition(orc):
+    t, hd, ff, m = Q4_0, 64, 128, 2
+    L = synth.ffn_layer(t, hd, ff, m, seed=9)
+    deq = lambda a, r, c: np_dequant(t, a, r * c).astype(np.float64).reshape(r, c)
+    G, U, D = deq(L["gate"], ff, hd), deq(L["up"], ff, hd), deq(L["down"], hd, ff)
+    x = L["x"].astype(np.float64)
+    xh = x / np.sqrt((x ** 2).mean(axis=1, keepdims=True) + 1e-5) * L["gamma"]
+    g, u = xh @ G.T, xh @ U.T
+    ref = (g * expit(g) * u) @ D.T
+    out = orc.ffn_rows_f64(t, L["gate"], L["up"], L["down"], hd, ff, L["gamma"], 1e-5, L["x"],
+                           [0, 1])
+    assert np.allclose(out, ref, rtol=1e-11, atol=1e-11)
+    o32 = orc.ffn_f32(t, L["gate"], L["up"], L["down"], hd, ff, L["gamma"], 1e-5, L["x"], m)
+    assert rel_l2(o32, ref) < 1e-5
+
+
+def test_oracle_catches_planted_bugs(orc):
+    """Each plausible mistake, planted in a numpy restatement, fails a check above."""
+    # swapped nibble halves: fails the Q4_1 KAT ([6]*16 then [5]*16)
+    blk = block_q4_1(1.0, 5.0, [0x01] * 16)
+    qs = blk[4:]
+    swapped = np.concatenate([qs >> 4, qs & 15]).astype(np.float32) * 1.0 + 5.0
+    assert not (np.all(swapped[:16] == 6.0) and np.all(swapped[16:] == 5.0))
+    # missing -8 on Q4_0: fails the d=2, qs=0 KAT (-16)
+    assert not np.all(np.zeros(32) * 2.0 == -16.0)
+    # transposed GEMM operand: fails the [[58,64],[139,154]] KAT
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([7, 8, 9, 10, 11, 12], np.float32).reshape(2, 3)  # read as [N][K]
+    assert (a @ b.T).reshape(-1).tolist() != [58, 64, 139, 154]
+    # dropped epsilon in RMSNorm: fails the constant-row closed form
+    x = np.full(64, 3.0)
+    assert not np.allclose(x / np.sqrt(9.0), 3.0 / np.sqrt(9.0 + 1e-5), rtol=1e-14)
+    assert max_abs([0.0], [0.0]) == 0.0

@@ -1,0 +1,140 @@
+"""ctypes binding of libwoolly_hip.so (the C ABI in include/woolly_hip.h).
+
+The shared library is built in-tree by woolly_amd.build.  Loading it does not
+touch the GPU; every entry point that needs one fails with WH_ERR_NO_DEVICE
+(or a HIP error) when none is present.  There is no CPU fallback: if the
+library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libwoolly_hip.so"
+
+WH_OK = 0
+WH_ERR_UNSUPPORTED_TYPE = 1
+WH_ERR_INVALID_SHAPE = 2
+WH_ERR_BUFFER_TOO_SMALL = 3
+WH_ERR_INVALID_ARGUMENT = 4
+WH_ERR_HIP = 5
+WH_ERR_OOM = 6
+WH_ERR_NO_DEVICE = 7
+
+STATUS_NAMES = {
+    0: "WH_OK",
+    1: "WH_ERR_UNSUPPORTED_TYPE",
+    2: "WH_ERR_INVALID_SHAPE",
+    3: "WH_ERR_BUFFER_TOO_SMALL",
+    4: "WH_ERR_INVALID_ARGUMENT",
+    5: "WH_ERR_HIP",
+    6: "WH_ERR_OOM",
+    7: "WH_ERR_NO_DEVICE",
+}
+
+
+class WoollyHipError(RuntimeError):
+    """A non-zero wh_status returned by the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.message = message
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+class wh_ffn_weights(C.Structure):
+    _fields_ = [
+        ("type", C.c_int),
+        ("gate", C.c_void_p),
+        ("up", C.c_void_p),
+        ("down", C.c_void_p),
+        ("hidden", C.c_size_t),
+        ("n_ff", C.c_size_t),
+    ]
+
+
+_sz = C.c_size_t
+_vp = C.c_void_p
+_int = C.c_int
+_f32p = C.c_void_p  # float* passed as raw addresses
+
+# name -> (restype, argtypes).  This table is the list of exported symbols;
+# tests check that it matches the declarations in include/woolly_hip.h.
+SIGNATURES = {
+    "wh_status_string": (C.c_char_p, [_int]),
+    "wh_last_error": (C.c_char_p, []),
+    "wh_version": (_int, []),
+    "wh_init": (_int, [_int]),
+    "wh_device_count": (_int, [C.POINTER(_int)]),
+    "wh_device_name": (_int, [C.c_char_p, _sz]),
+    "wh_malloc": (_int, [C.POINTER(_vp), _sz]),
+    "wh_free": (_int, [_vp]),
+    "wh_memcpy_h2d": (_int, [_vp, _vp, _sz, _vp]),
+    "wh_memcpy_d2h": (_int, [_vp, _vp, _sz, _vp]),
+    "wh_memcpy_d2d": (_int, [_vp, _vp, _sz, _vp]),
+    "wh_fill_bytes": (_int, [_vp, _int, _sz, _vp]),
+    "wh_stream_create": (_int, [C.POINTER(_vp)]),
+    "wh_stream_destroy": (_int, [_vp]),
+    "wh_stream_synchronize": (_int, [_vp]),
+    "wh_device_synchronize": (_int, []),
+    "wh_event_create": (_int, [C.POINTER(_vp)]),
+    "wh_event_destroy": (_int, [_vp]),
+    "wh_event_record": (_int, [_vp, _vp]),
+    "wh_event_synchronize": (_int, [_vp]),
+    "wh_event_elapsed_ms": (_int, [C.POINTER(C.c_float), _vp, _vp]),
+    "wh_graph_begin_capture": (_int, [_vp]),
+    "wh_graph_end_capture": (_int, [_vp, C.POINTER(_vp)]),
+    "wh_graph_launch": (_int, [_vp, _vp]),
+    "wh_graph_destroy": (_int, [_vp]),
+    "wh_block_size": (_sz, [_int]),
+    "wh_type_size": (_sz, [_int]),
+    "wh_tensor_nbytes": (_int, [_int, C.c_uint64, C.POINTER(C.c_uint64)]),
+    "wh_dequantize": (_int, [_int, _vp, _sz, _sz, _f32p, _vp]),
+    "wh_quantized_matvec": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz, _vp]),
+    "wh_quantized_matmul": (_int, [_int, _vp, _sz, _sz, _sz, _f32p, _sz, _f32p, _vp]),
+    "wh_rms_norm": (_int, [_f32p, _f32p, C.c_float, _sz, _sz, _f32p, _vp]),
+    "wh_swiglu": (_int, [_f32p, _f32p, _sz, _f32p, _vp]),
+    "wh_ffn_workspace_bytes": (_sz, [_sz, _sz, _sz]),
+    "wh_ffn_swiglu": (_int, [C.POINTER(wh_ffn_weights), _f32p, C.c_float, _f32p, _sz, _f32p,
+                             _vp, _sz, _vp]),
+    "wh_weight_upload": (_int, [_int, _sz, _sz, _vp, _sz, C.POINTER(_vp)]),
+    "wh_weight_free": (_int, [_vp]),
+    "wh_weight_data": (_vp, [_vp]),
+    "wh_weight_info": (_int, [_vp, C.POINTER(_int), C.POINTER(_sz), C.POINTER(_sz),
+                              C.POINTER(_sz)]),
+    "wh_dequantize_host": (_int, [_int, _vp, _sz, _sz, _f32p]),
+    "wh_quantized_matvec_host": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz]),
+}
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Loads libwoolly_hip.so (raises if it has not been built)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m woolly_amd.build` "
+                "(there is no CPU fallback for the HIP path)")
+        lib = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().wh_last_error().decode(errors="replace")
+
+
+def check(status: int) -> None:
+    """Raises WoollyHipError for a non-zero status."""
+    if status != WH_OK:
+        raise WoollyHipError(status, last_error())

@@ -1,0 +1,557 @@
+// api.hip -- the C ABI of libwoolly_hip (include/woolly_hip.h): argument
+// validation with the reference's error semantics, device/stream plumbing,
+// weight handles and the synchronous host-pointer variants.  Kernels live in
+// dequant.hip, gemv.hip, gemm.hip and elementwise.hip.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "wh_common.hpp"
+
+struct wh_weight {
+  int type;
+  size_t n_rows;
+  size_t k;
+  size_t nbytes;
+  void* data;
+  int device;
+};
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+hipStream_t hs(wh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kMaxDevices = 64;
+int g_cu_count[kMaxDevices] = {0};
+std::mutex g_cu_mutex;
+
+int check_block_args(const char* fn, int type, size_t k) {
+  if (!wh::is_block_type(type))
+    return wh::set_error(WH_ERR_UNSUPPORTED_TYPE,
+                         "%s: unsupported quantization scheme (ggml type %d); supported: "
+                         "Q4_0 (2), Q4_1 (3), Q8_0 (8)",
+                         fn, type);
+  if (k % 32 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: k = %zu is not a multiple of the block size 32",
+                         fn, k);
+  return WH_OK;
+}
+
+int check_weight_bytes(const char* fn, int type, size_t rows, size_t k, size_t have) {
+  const size_t ts = wh::type_size(type);
+  const size_t nb = k / 32;
+  if (rows != 0 && nb != 0 && (rows > SIZE_MAX / nb || rows * nb > SIZE_MAX / ts))
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: %zu x %zu weight size overflows", fn, rows, k);
+  const size_t need = rows * nb * ts;
+  if (have < need)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "%s: buffer too small: needed %zu bytes, available %zu", fn, need, have);
+  return WH_OK;
+}
+
+int check_ptr(const char* fn, const char* what, const void* p, size_t align) {
+  if (p == nullptr)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: %s is a null pointer", fn, what);
+  if (!wh::aligned(p, align))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: %s is not %zu-byte aligned", fn, what, align);
+  return WH_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+namespace wh {
+
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int hip_error(hipError_t err, const char* what) {
+  const int st = (err == hipErrorOutOfMemory) ? WH_ERR_OOM : WH_ERR_HIP;
+  return set_error(st, "%s failed: %s (%d)", what, hipGetErrorString(err), static_cast<int>(err));
+}
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  {
+    std::lock_guard<std::mutex> lk(g_cu_mutex);
+    if (g_cu_count[dev] > 0) return g_cu_count[dev];
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  std::lock_guard<std::mutex> lk(g_cu_mutex);
+  g_cu_count[dev] = n;
+  return n;
+}
+
+}  // namespace wh
+
+extern "C" {
+
+WH_API const char* wh_status_string(int status) {
+  switch (status) {
+    case WH_OK: return "WH_OK";
+    case WH_ERR_UNSUPPORTED_TYPE: return "WH_ERR_UNSUPPORTED_TYPE";
+    case WH_ERR_INVALID_SHAPE: return "WH_ERR_INVALID_SHAPE";
+    case WH_ERR_BUFFER_TOO_SMALL: return "WH_ERR_BUFFER_TOO_SMALL";
+    case WH_ERR_INVALID_ARGUMENT: return "WH_ERR_INVALID_ARGUMENT";
+    case WH_ERR_HIP: return "WH_ERR_HIP";
+    case WH_ERR_OOM: return "WH_ERR_OOM";
+    case WH_ERR_NO_DEVICE: return "WH_ERR_NO_DEVICE";
+    default: return "WH_ERR_UNKNOWN";
+  }
+}
+
+WH_API const char* wh_last_error(void) { return g_last_error; }
+
+WH_API int wh_version(void) { return 1; }
+
+// ------------------------------------------------------------- device/memory
+WH_API int wh_device_count(int* count) {
+  if (!count) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_device_count: null count");
+  int n = 0;
+  const hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return wh::set_error(WH_ERR_NO_DEVICE, "hipGetDeviceCount failed: %s", hipGetErrorString(e));
+  }
+  *count = n;
+  return WH_OK;
+}
+
+WH_API int wh_init(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return wh::set_error(WH_ERR_NO_DEVICE, "wh_init: no HIP device is visible");
+  if (device < 0 || device >= n)
+    return wh::set_error(WH_ERR_NO_DEVICE, "wh_init: device %d out of range (%d visible)", device, n);
+  WH_HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  WH_HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return wh::set_error(WH_ERR_NO_DEVICE, "wh_init: device %d is %s; this library is built for gfx950",
+                         device, prop.gcnArchName);
+  (void)wh::cu_count();
+  return WH_OK;
+}
+
+WH_API int wh_device_name(char* buf, size_t len) {
+  if (!buf || len == 0) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_device_name: bad buffer");
+  int dev = 0;
+  WH_HIP_TRY(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  WH_HIP_TRY(hipGetDeviceProperties(&prop, dev));
+  std::snprintf(buf, len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+  return WH_OK;
+}
+
+WH_API int wh_malloc(void** dptr, size_t nbytes) {
+  if (!dptr) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_malloc: null output pointer");
+  *dptr = nullptr;
+  if (nbytes == 0) return WH_OK;
+  WH_HIP_TRY(hipMalloc(dptr, nbytes));
+  return WH_OK;
+}
+
+WH_API int wh_free(void* dptr) {
+  if (dptr) WH_HIP_TRY(hipFree(dptr));
+  return WH_OK;
+}
+
+WH_API int wh_memcpy_h2d(void* dst, const void* src, size_t nbytes, wh_stream_t stream) {
+  if (nbytes == 0) return WH_OK;
+  if (!dst || !src) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_memcpy_h2d: null pointer");
+  WH_HIP_TRY(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_memcpy_d2h(void* dst, const void* src, size_t nbytes, wh_stream_t stream) {
+  if (nbytes == 0) return WH_OK;
+  if (!dst || !src) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_memcpy_d2h: null pointer");
+  WH_HIP_TRY(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_memcpy_d2d(void* dst, const void* src, size_t nbytes, wh_stream_t stream) {
+  if (nbytes == 0) return WH_OK;
+  if (!dst || !src) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_memcpy_d2d: null pointer");
+  WH_HIP_TRY(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_fill_bytes(void* dst, int value, size_t nbytes, wh_stream_t stream) {
+  if (nbytes == 0) return WH_OK;
+  if (!dst) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_fill_bytes: null pointer");
+  return wh::launch_fill_bytes(dst, value, nbytes, hs(stream));
+}
+
+WH_API int wh_stream_create(wh_stream_t* out) {
+  if (!out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_stream_create: null output");
+  hipStream_t s;
+  WH_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = reinterpret_cast<wh_stream_t>(s);
+  return WH_OK;
+}
+
+WH_API int wh_stream_destroy(wh_stream_t stream) {
+  if (stream) WH_HIP_TRY(hipStreamDestroy(hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_stream_synchronize(wh_stream_t stream) {
+  WH_HIP_TRY(hipStreamSynchronize(hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_device_synchronize(void) {
+  WH_HIP_TRY(hipDeviceSynchronize());
+  return WH_OK;
+}
+
+WH_API int wh_event_create(wh_event_t* out) {
+  if (!out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_event_create: null output");
+  hipEvent_t e;
+  WH_HIP_TRY(hipEventCreate(&e));
+  *out = reinterpret_cast<wh_event_t>(e);
+  return WH_OK;
+}
+
+WH_API int wh_event_destroy(wh_event_t event) {
+  if (event) WH_HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+  return WH_OK;
+}
+
+WH_API int wh_event_record(wh_event_t event, wh_stream_t stream) {
+  if (!event) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_event_record: null event");
+  WH_HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(event), hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_event_synchronize(wh_event_t event) {
+  if (!event) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_event_synchronize: null event");
+  WH_HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
+  return WH_OK;
+}
+
+WH_API int wh_event_elapsed_ms(float* ms, wh_event_t start, wh_event_t end) {
+  if (!ms || !start || !end)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_event_elapsed_ms: null argument");
+  WH_HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                 reinterpret_cast<hipEvent_t>(end)));
+  return WH_OK;
+}
+
+// -------------------------------------------------------------------- graphs
+WH_API int wh_graph_begin_capture(wh_stream_t stream) {
+  if (!stream)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "graph capture needs a non-null stream");
+  WH_HIP_TRY(hipStreamBeginCapture(hs(stream), hipStreamCaptureModeThreadLocal));
+  return WH_OK;
+}
+
+WH_API int wh_graph_end_capture(wh_stream_t stream, wh_graph_t* out) {
+  if (!stream || !out)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_graph_end_capture: null argument");
+  *out = nullptr;
+  hipGraph_t g = nullptr;
+  WH_HIP_TRY(hipStreamEndCapture(hs(stream), &g));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return wh::hip_error(e, "hipGraphInstantiate");
+  *out = reinterpret_cast<wh_graph_t>(exec);
+  return WH_OK;
+}
+
+WH_API int wh_graph_launch(wh_graph_t graph, wh_stream_t stream) {
+  if (!graph) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_graph_launch: null graph");
+  WH_HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), hs(stream)));
+  return WH_OK;
+}
+
+WH_API int wh_graph_destroy(wh_graph_t graph) {
+  if (graph) WH_HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)));
+  return WH_OK;
+}
+
+// -------------------------------------------------------------------- format
+WH_API size_t wh_block_size(int type) {
+  switch (type) {
+    case WH_TYPE_F32:
+    case WH_TYPE_F16: return 1;
+    case WH_TYPE_Q4_0:
+    case WH_TYPE_Q4_1:
+    case WH_TYPE_Q8_0: return 32;
+    default: return 0;
+  }
+}
+
+WH_API size_t wh_type_size(int type) { return wh::type_size(type); }
+
+WH_API int wh_tensor_nbytes(int type, uint64_t nelements, uint64_t* nbytes) {
+  if (!nbytes) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_tensor_nbytes: null output");
+  const uint64_t bs = wh_block_size(type), ts = wh::type_size(type);
+  if (bs == 0) return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "wh_tensor_nbytes: unsupported type %d", type);
+  *nbytes = (nelements + bs - 1) / bs * ts;
+  return WH_OK;
+}
+
+// ---------------------------------------------------------- dequantization
+WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelements, float* out,
+                         wh_stream_t stream) {
+  const size_t ts = wh::type_size(type);
+  if (ts == 0)
+    return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "dequantize: invalid tensor type %d", type);
+  if (type == WH_TYPE_F32 || type == WH_TYPE_F16) {
+    if (nbytes != nelements * ts)
+      return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                           "dequantize: buffer too small: needed %zu bytes, available %zu",
+                           nelements * ts, nbytes);
+  } else {
+    const size_t need = (nelements + 31) / 32 * ts;
+    if (nbytes < need)
+      return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                           "dequantize: buffer too small: needed %zu bytes, available %zu", need,
+                           nbytes);
+  }
+  if (nelements == 0) return WH_OK;
+  int st = check_ptr("dequantize", "data", data, 1);
+  if (st) return st;
+  st = check_ptr("dequantize", "out", out, 4);
+  if (st) return st;
+  return wh::launch_dequantize(type, data, nelements, out, hs(stream));
+}
+
+// -------------------------------------------------------------------- GEMV
+WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbytes,
+                               const float* input, float* output, size_t m, size_t k,
+                               wh_stream_t stream) {
+  int st = check_block_args("quantized_matvec", type, k);
+  if (st) return st;
+  st = check_weight_bytes("quantized_matvec", type, m, k, weight_nbytes);
+  if (st) return st;
+  if (m == 0) return WH_OK;
+  st = check_ptr("quantized_matvec", "output", output, 4);
+  if (st) return st;
+  if (k == 0) return wh::launch_fill_bytes(output, 0, m * sizeof(float), hs(stream));
+  st = check_ptr("quantized_matvec", "weights", weights, 1);
+  if (st) return st;
+  st = check_ptr("quantized_matvec", "input", input, 4);
+  if (st) return st;
+  return wh::launch_gemv(type, weights, input, output, m, k, hs(stream));
+}
+
+// -------------------------------------------------------------------- GEMM
+WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes, size_t n_rows,
+                               size_t k, const float* x, size_t n_tokens, float* y,
+                               wh_stream_t stream) {
+  int st = check_block_args("quantized_matmul", type, k);
+  if (st) return st;
+  st = check_weight_bytes("quantized_matmul", type, n_rows, k, weight_nbytes);
+  if (st) return st;
+  if (n_rows == 0 || n_tokens == 0) return WH_OK;
+  st = check_ptr("quantized_matmul", "y", y, 4);
+  if (st) return st;
+  if (k == 0) return wh::launch_fill_bytes(y, 0, n_rows * n_tokens * sizeof(float), hs(stream));
+  st = check_ptr("quantized_matmul", "weights", weights, 1);
+  if (st) return st;
+  st = check_ptr("quantized_matmul", "x", x, 4);
+  if (st) return st;
+  return wh::launch_gemm(type, weights, n_rows, k, x, n_tokens, y, hs(stream));
+}
+
+// --------------------------------------------------------------- elementwise
+WH_API int wh_rms_norm(const float* x, const float* weight, float eps, size_t tokens, size_t hidden,
+                       float* out, wh_stream_t stream) {
+  if (tokens == 0 || hidden == 0) return WH_OK;
+  int st = check_ptr("rms_norm", "x", x, 4);
+  if (st) return st;
+  st = check_ptr("rms_norm", "weight", weight, 4);
+  if (st) return st;
+  st = check_ptr("rms_norm", "out", out, 4);
+  if (st) return st;
+  return wh::launch_rms_norm(x, weight, eps, tokens, hidden, out, hs(stream));
+}
+
+WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out, wh_stream_t stream) {
+  if (n == 0) return WH_OK;
+  int st = check_ptr("swiglu", "gate", gate, 4);
+  if (st) return st;
+  st = check_ptr("swiglu", "up", up, 4);
+  if (st) return st;
+  st = check_ptr("swiglu", "out", out, 4);
+  if (st) return st;
+  return wh::launch_swiglu(gate, up, n, out, hs(stream));
+}
+
+// ------------------------------------------------------------------- FFN
+WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m) {
+  return align_up(m * hidden * sizeof(float), 256) + 3 * align_up(m * n_ff * sizeof(float), 256);
+}
+
+WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps, const float* x,
+                         size_t m, float* out, void* workspace, size_t workspace_bytes,
+                         wh_stream_t stream) {
+  if (!w) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "ffn_swiglu: null weights");
+  int st = check_block_args("ffn_swiglu", w->type, w->hidden);
+  if (st) return st;
+  st = check_block_args("ffn_swiglu", w->type, w->n_ff);
+  if (st) return st;
+  if (m == 0 || w->hidden == 0) return WH_OK;
+  const size_t need = wh_ffn_workspace_bytes(w->hidden, w->n_ff, m);
+  if (workspace_bytes < need)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "ffn_swiglu: workspace too small: needed %zu bytes, available %zu", need,
+                         workspace_bytes);
+  if ((st = check_ptr("ffn_swiglu", "gate", w->gate, 1)) || (st = check_ptr("ffn_swiglu", "up", w->up, 1)) ||
+      (st = check_ptr("ffn_swiglu", "down", w->down, 1)) ||
+      (st = check_ptr("ffn_swiglu", "gamma", gamma, 4)) || (st = check_ptr("ffn_swiglu", "x", x, 4)) ||
+      (st = check_ptr("ffn_swiglu", "out", out, 4)) ||
+      (st = check_ptr("ffn_swiglu", "workspace", workspace, 256)))
+    return st;
+  const size_t H = w->hidden, F = w->n_ff;
+  char* ws = static_cast<char*>(workspace);
+  float* xh = reinterpret_cast<float*>(ws);
+  ws += align_up(m * H * sizeof(float), 256);
+  float* g = reinterpret_cast<float*>(ws);
+  ws += align_up(m * F * sizeof(float), 256);
+  float* u = reinterpret_cast<float*>(ws);
+  ws += align_up(m * F * sizeof(float), 256);
+  float* h = reinterpret_cast<float*>(ws);
+  hipStream_t s = hs(stream);
+  if ((st = wh::launch_rms_norm(x, gamma, eps, m, H, xh, s))) return st;
+  if (F == 0) return wh::launch_fill_bytes(out, 0, m * H * sizeof(float), s);
+  if ((st = wh::launch_gemm(w->type, w->gate, F, H, xh, m, g, s))) return st;
+  if ((st = wh::launch_gemm(w->type, w->up, F, H, xh, m, u, s))) return st;
+  if ((st = wh::launch_swiglu(g, u, m * F, h, s))) return st;
+  return wh::launch_gemm(w->type, w->down, H, F, h, m, out, s);
+}
+
+// ------------------------------------------------------------ weight handles
+WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_bytes,
+                            size_t nbytes, wh_weight** out) {
+  if (!out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_upload: null output");
+  *out = nullptr;
+  int st = check_block_args("weight_upload", type, k);
+  if (st) return st;
+  st = check_weight_bytes("weight_upload", type, n_rows, k, nbytes);
+  if (st) return st;
+  const size_t need = n_rows * (k / 32) * wh::type_size(type);
+  if (need > 0 && !host_bytes)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_upload: null host bytes");
+  wh_weight* wt = new (std::nothrow) wh_weight();
+  if (!wt) return wh::set_error(WH_ERR_OOM, "weight_upload: host allocation failed");
+  wt->type = type;
+  wt->n_rows = n_rows;
+  wt->k = k;
+  wt->nbytes = need;
+  wt->data = nullptr;
+  if (hipGetDevice(&wt->device) != hipSuccess) wt->device = -1;
+  if (need > 0) {
+    hipError_t e = hipMalloc(&wt->data, need);
+    if (e != hipSuccess) {
+      delete wt;
+      return wh::hip_error(e, "weight_upload: hipMalloc");
+    }
+    e = hipMemcpy(wt->data, host_bytes, need, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(wt->data);
+      delete wt;
+      return wh::hip_error(e, "weight_upload: hipMemcpy");
+    }
+  }
+  *out = wt;
+  return WH_OK;
+}
+
+WH_API int wh_weight_free(wh_weight* weight) {
+  if (!weight) return WH_OK;
+  if (weight->data) {
+    const hipError_t e = hipFree(weight->data);
+    delete weight;
+    if (e != hipSuccess) return wh::hip_error(e, "weight_free: hipFree");
+    return WH_OK;
+  }
+  delete weight;
+  return WH_OK;
+}
+
+WH_API const void* wh_weight_data(const wh_weight* weight) { return weight ? weight->data : nullptr; }
+
+WH_API int wh_weight_info(const wh_weight* weight, int* type, size_t* n_rows, size_t* k,
+                          size_t* nbytes) {
+  if (!weight) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_info: null handle");
+  if (type) *type = weight->type;
+  if (n_rows) *n_rows = weight->n_rows;
+  if (k) *k = weight->k;
+  if (nbytes) *nbytes = weight->nbytes;
+  return WH_OK;
+}
+
+// -------------------------------------------------- synchronous host variants
+namespace {
+struct DevBuf {
+  void* p = nullptr;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+};
+}  // namespace
+
+WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t nelements, float* out) {
+  const size_t ts = wh::type_size(type);
+  if (ts == 0)
+    return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "dequantize: invalid tensor type %d", type);
+  // Validate first with a null stream call that performs no work on failure.
+  if (nelements == 0) return wh_dequantize(type, data, nbytes, 0, out, nullptr);
+  if (!data || !out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "dequantize_host: null pointer");
+  const size_t in_bytes =
+      (type == WH_TYPE_F32 || type == WH_TYPE_F16) ? nelements * ts : (nelements + 31) / 32 * ts;
+  if (nbytes < in_bytes || ((type == WH_TYPE_F32 || type == WH_TYPE_F16) && nbytes != in_bytes))
+    return wh_dequantize(type, data, nbytes, nelements, out, nullptr);
+  DevBuf din, dout;
+  WH_HIP_TRY(hipMalloc(&din.p, in_bytes));
+  WH_HIP_TRY(hipMalloc(&dout.p, nelements * sizeof(float)));
+  WH_HIP_TRY(hipMemcpy(din.p, data, in_bytes, hipMemcpyHostToDevice));
+  int st = wh_dequantize(type, din.p, in_bytes, nelements, static_cast<float*>(dout.p), nullptr);
+  if (st) return st;
+  WH_HIP_TRY(hipMemcpy(out, dout.p, nelements * sizeof(float), hipMemcpyDeviceToHost));
+  return WH_OK;
+}
+
+WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
+                                    const float* input, float* output, size_t m, size_t k) {
+  int st = check_block_args("quantized_matvec", type, k);
+  if (st) return st;
+  st = check_weight_bytes("quantized_matvec", type, m, k, weight_nbytes);
+  if (st) return st;
+  if (m == 0) return WH_OK;
+  if (!output || (k > 0 && (!weights || !input)))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matvec_host: null pointer");
+  const size_t wbytes = m * (k / 32) * wh::type_size(type);
+  DevBuf dw, dx, dy;
+  if (wbytes) WH_HIP_TRY(hipMalloc(&dw.p, wbytes));
+  if (k) WH_HIP_TRY(hipMalloc(&dx.p, k * sizeof(float)));
+  WH_HIP_TRY(hipMalloc(&dy.p, m * sizeof(float)));
+  if (wbytes) WH_HIP_TRY(hipMemcpy(dw.p, weights, wbytes, hipMemcpyHostToDevice));
+  if (k) WH_HIP_TRY(hipMemcpy(dx.p, input, k * sizeof(float), hipMemcpyHostToDevice));
+  st = wh_quantized_matvec(type, dw.p, wbytes, static_cast<const float*>(dx.p),
+                           static_cast<float*>(dy.p), m, k, nullptr);
+  if (st) return st;
+  WH_HIP_TRY(hipMemcpy(output, dy.p, m * sizeof(float), hipMemcpyDeviceToHost));
+  return WH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// wh_common.hpp -- shared host/device helpers of libwoolly_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/woolly_hip.h"
+
+namespace wh {
+
+// ---------------------------------------------------------------- host side
+// Records the message of the last failure on this thread and returns status.
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a failed HIP call to WH_ERR_HIP / WH_ERR_OOM with its message.
+int hip_error(hipError_t err, const char* what);
+
+#define WH_HIP_TRY(expr)                                    \
+  do {                                                      \
+    hipError_t _e = (expr);                                 \
+    if (_e != hipSuccess) return ::wh::hip_error(_e, #expr); \
+  } while (0)
+
+// Checks the launch that was just issued on this thread.
+#define WH_LAUNCH_CHECK(name)                                 \
+  do {                                                        \
+    hipError_t _e = hipGetLastError();                        \
+    if (_e != hipSuccess) return ::wh::hip_error(_e, name);   \
+  } while (0)
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline size_t type_size(int type) {
+  switch (type) {
+    case WH_TYPE_F32: return 4;
+    case WH_TYPE_F16: return 2;
+    case WH_TYPE_Q4_0: return 18;
+    case WH_TYPE_Q4_1: return 20;
+    case WH_TYPE_Q8_0: return 34;
+    default: return 0;
+  }
+}
+inline bool is_block_type(int type) {
+  return type == WH_TYPE_Q4_0 || type == WH_TYPE_Q4_1 || type == WH_TYPE_Q8_0;
+}
+
+// Number of compute units of the current device (cached per device).
+int cu_count();
+
+// Launchers implemented in the .hip translation units.  Arguments have been
+// validated by the C ABI layer; these only choose kernels and launch them.
+int launch_dequantize(int type, const void* data, size_t nelements, float* out,
+                      hipStream_t stream);
+int launch_fill_bytes(void* dst, int value, size_t nbytes, hipStream_t stream);
+int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows,
+                size_t k, hipStream_t stream);
+int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x,
+                size_t n_tokens, float* y, hipStream_t stream);
+int launch_rms_norm(const float* x, const float* weight, float eps, size_t tokens,
+                    size_t hidden, float* out, hipStream_t stream);
+int launch_swiglu(const float* gate, const float* up, size_t n, float* out,
+                  hipStream_t stream);
+
+}  // namespace wh
+
+// -------------------------------------------------------------- device side
+namespace whd {
+
+// IEEE binary16 -> binary32 (v_cvt_f32_f16; exact, denormals preserved).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// Sum of v over the 64 lanes of the wavefront; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace whd
