@@ -96,6 +96,15 @@ int cu_count() {
   return n;
 }
 
+size_t max_lds_per_block() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+    return 65536;
+  return static_cast<size_t>(v);
+}
+
 }  // namespace wh
 
 extern "C" {
@@ -153,7 +162,8 @@ WH_API int wh_device_name(char* buf, size_t len) {
   WH_HIP_TRY(hipGetDevice(&dev));
   hipDeviceProp_t prop;
   WH_HIP_TRY(hipGetDeviceProperties(&prop, dev));
-  std::snprintf(buf, len, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+  std::snprintf(buf, len, "%s (%s, %d CUs, %zu KiB LDS/block, %d MHz)", prop.name, prop.gcnArchName,
+                prop.multiProcessorCount, wh::max_lds_per_block() / 1024, prop.clockRate / 1000);
   return WH_OK;
 }
 

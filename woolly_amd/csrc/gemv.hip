@@ -5,21 +5,15 @@
 // (quantization.rs:1100-1163).  W is N rows x K/32 blocks in the GGUF block
 // layout; Q4_1 is supported as dequantize_q4_1 composed with the f32 dot.
 //
-// Fast path ("pair" kernel).  Two consecutive blocks form a pair of 36 B
-// (Q4_0), 40 B (Q4_1) or 68 B (Q8_0): always a whole number of dwords and,
-// when a row has an even number of blocks, 4-byte aligned.  Lane l of a wave
-// owns pair l of the wave's K-slice in every row it visits, so its 64
-// activations stay in VGPRs for the whole kernel and each weight byte is
-// loaded exactly once with dword-granular vector loads (9/10/17 dwords per
-// lane, consecutive lanes reading consecutive 36/40/68-byte spans, so every
-// cache line fetched is consumed completely by the same instruction group).
+// Fast path (gemv_stream_kernel, below): two consecutive blocks form a pair
+// of 36 B (Q4_0), 40 B (Q4_1) or 68 B (Q8_0), a whole number of dwords and,
+// when a row has an even number of blocks, 4-byte aligned.  Lane l owns pair l
+// of its K-slice in every row, so its 64 activations stay in VGPRs; weights
+// arrive through coalesced 32/64/96-bit loads and a per-wave LDS transpose.
 // Nibbles are unpacked in registers (one AND, one SHIFT+AND per dword, then
 // v_cvt_f32_ubyte{0..3}); the f32 products accumulate per block and the block
 // scale is applied once per block.  Q4_0's "-8" is folded as
 // d * (sum q*x - 8 * sum x), with the per-block activation sums computed once.
-// Rows are reduced across the 64 lanes; when K needs more than one wave
-// (more than 64 pairs, e.g. K = 14336), the WG's waves split K and combine
-// their partial sums through LDS in a fixed order (deterministic).
 //
 // Generic path: one wave per row, lanes stride over blocks with byte loads;
 // used for odd block counts, unaligned pointers and K > 16384.
@@ -47,8 +41,9 @@ struct PairFmt<WH_TYPE_Q8_0> {
 
 // Accumulates the 4-bit quants of dword u, bytes [K0, K1), where byte k holds
 // qs[J0 + k]: low nibble -> element J0+k, high nibble -> element J0+k+16.
+// Four independent accumulators a[0..3] keep the FMA chains short.
 template <int K0, int K1, int J0>
-__device__ __forceinline__ float nib_dot(uint32_t u, const float* xv, float s) {
+__device__ __forceinline__ void nib_dot(uint32_t u, const float* xv, float* a) {
   uint32_t lo = u & 0x0F0F0F0Fu;
   uint32_t hi = (u >> 4) & 0x0F0F0F0Fu;
   // Hide the mask from the optimizer: otherwise it folds (lo >> 8k) & 0xFF
@@ -57,22 +52,23 @@ __device__ __forceinline__ float nib_dot(uint32_t u, const float* xv, float s) {
   asm("" : "+v"(hi));
 #pragma unroll
   for (int k = K0; k < K1; k++) {
-    s = __builtin_fmaf(static_cast<float>((lo >> (8 * k)) & 0xFFu), xv[J0 + k], s);
-    s = __builtin_fmaf(static_cast<float>((hi >> (8 * k)) & 0xFFu), xv[J0 + k + 16], s);
+    a[k & 1] = __builtin_fmaf(static_cast<float>((lo >> (8 * k)) & 0xFFu), xv[J0 + k], a[k & 1]);
+    a[2 + (k & 1)] =
+        __builtin_fmaf(static_cast<float>((hi >> (8 * k)) & 0xFFu), xv[J0 + k + 16], a[2 + (k & 1)]);
   }
-  return s;
 }
 
 // Accumulates the int8 quants of dword u, bytes [K0, K1), byte k = element J0+k.
 template <int K0, int K1, int J0>
-__device__ __forceinline__ float i8_dot(uint32_t u, const float* xv, float s) {
+__device__ __forceinline__ void i8_dot(uint32_t u, const float* xv, float* a) {
 #pragma unroll
   for (int k = K0; k < K1; k++) {
     const int q = static_cast<int>(static_cast<int8_t>((u >> (8 * k)) & 0xFFu));
-    s = __builtin_fmaf(static_cast<float>(q), xv[J0 + k], s);
+    a[k & 3] = __builtin_fmaf(static_cast<float>(q), xv[J0 + k], a[k & 3]);
   }
-  return s;
 }
+
+__device__ __forceinline__ float sum4(const float* a) { return (a[0] + a[1]) + (a[2] + a[3]); }
 
 // Dot product of one pair (two blocks, 64 elements) with the lane's
 // activations xv[0..64); xa / xb are the sums of xv over each block.
@@ -85,17 +81,17 @@ __device__ __forceinline__ float pair_dot<WH_TYPE_Q4_0>(const uint32_t* w, const
   // dwords: [dA|q0 q1] [q2..5] [q6..9] [q10..13] [q14 q15|dB] [B q0..3] .. [B q12..15]
   const float da = whd::f16_bits_to_f32(w[0] & 0xFFFFu);
   const float db = whd::f16_bits_to_f32(w[4] >> 16);
-  float sa = 0.f, sb = 0.f;
-  sa = nib_dot<2, 4, -2>(w[0], xv, sa);
-  sa = nib_dot<0, 4, 2>(w[1], xv, sa);
-  sa = nib_dot<0, 4, 6>(w[2], xv, sa);
-  sa = nib_dot<0, 4, 10>(w[3], xv, sa);
-  sa = nib_dot<0, 2, 14>(w[4], xv, sa);
-  sb = nib_dot<0, 4, 32>(w[5], xv, sb);
-  sb = nib_dot<0, 4, 36>(w[6], xv, sb);
-  sb = nib_dot<0, 4, 40>(w[7], xv, sb);
-  sb = nib_dot<0, 4, 44>(w[8], xv, sb);
-  return da * __builtin_fmaf(-8.f, xa, sa) + db * __builtin_fmaf(-8.f, xb, sb);
+  float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  nib_dot<2, 4, -2>(w[0], xv, a);
+  nib_dot<0, 4, 32>(w[5], xv, b);
+  nib_dot<0, 4, 2>(w[1], xv, a);
+  nib_dot<0, 4, 36>(w[6], xv, b);
+  nib_dot<0, 4, 6>(w[2], xv, a);
+  nib_dot<0, 4, 40>(w[7], xv, b);
+  nib_dot<0, 4, 10>(w[3], xv, a);
+  nib_dot<0, 4, 44>(w[8], xv, b);
+  nib_dot<0, 2, 14>(w[4], xv, a);
+  return da * __builtin_fmaf(-8.f, xa, sum4(a)) + db * __builtin_fmaf(-8.f, xb, sum4(b));
 }
 
 template <>
@@ -106,16 +102,16 @@ __device__ __forceinline__ float pair_dot<WH_TYPE_Q4_1>(const uint32_t* w, const
   const float ma = whd::f16_bits_to_f32(w[0] >> 16);
   const float db = whd::f16_bits_to_f32(w[5] & 0xFFFFu);
   const float mb = whd::f16_bits_to_f32(w[5] >> 16);
-  float sa = 0.f, sb = 0.f;
-  sa = nib_dot<0, 4, 0>(w[1], xv, sa);
-  sa = nib_dot<0, 4, 4>(w[2], xv, sa);
-  sa = nib_dot<0, 4, 8>(w[3], xv, sa);
-  sa = nib_dot<0, 4, 12>(w[4], xv, sa);
-  sb = nib_dot<0, 4, 32>(w[6], xv, sb);
-  sb = nib_dot<0, 4, 36>(w[7], xv, sb);
-  sb = nib_dot<0, 4, 40>(w[8], xv, sb);
-  sb = nib_dot<0, 4, 44>(w[9], xv, sb);
-  return __builtin_fmaf(da, sa, ma * xa) + __builtin_fmaf(db, sb, mb * xb);
+  float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  nib_dot<0, 4, 0>(w[1], xv, a);
+  nib_dot<0, 4, 32>(w[6], xv, b);
+  nib_dot<0, 4, 4>(w[2], xv, a);
+  nib_dot<0, 4, 36>(w[7], xv, b);
+  nib_dot<0, 4, 8>(w[3], xv, a);
+  nib_dot<0, 4, 40>(w[8], xv, b);
+  nib_dot<0, 4, 12>(w[4], xv, a);
+  nib_dot<0, 4, 44>(w[9], xv, b);
+  return __builtin_fmaf(da, sum4(a), ma * xa) + __builtin_fmaf(db, sum4(b), mb * xb);
 }
 
 template <>
@@ -124,25 +120,25 @@ __device__ __forceinline__ float pair_dot<WH_TYPE_Q8_0>(const uint32_t* w, const
   // dwords: [dA|q0 q1] [q2..5] .. [q26..29] [q30 q31|dB] [B q0..3] .. [B q28..31]
   const float da = whd::f16_bits_to_f32(w[0] & 0xFFFFu);
   const float db = whd::f16_bits_to_f32(w[8] >> 16);
-  float sa = 0.f, sb = 0.f;
-  sa = i8_dot<2, 4, -2>(w[0], xv, sa);
-  sa = i8_dot<0, 4, 2>(w[1], xv, sa);
-  sa = i8_dot<0, 4, 6>(w[2], xv, sa);
-  sa = i8_dot<0, 4, 10>(w[3], xv, sa);
-  sa = i8_dot<0, 4, 14>(w[4], xv, sa);
-  sa = i8_dot<0, 4, 18>(w[5], xv, sa);
-  sa = i8_dot<0, 4, 22>(w[6], xv, sa);
-  sa = i8_dot<0, 4, 26>(w[7], xv, sa);
-  sa = i8_dot<0, 2, 30>(w[8], xv, sa);
-  sb = i8_dot<0, 4, 32>(w[9], xv, sb);
-  sb = i8_dot<0, 4, 36>(w[10], xv, sb);
-  sb = i8_dot<0, 4, 40>(w[11], xv, sb);
-  sb = i8_dot<0, 4, 44>(w[12], xv, sb);
-  sb = i8_dot<0, 4, 48>(w[13], xv, sb);
-  sb = i8_dot<0, 4, 52>(w[14], xv, sb);
-  sb = i8_dot<0, 4, 56>(w[15], xv, sb);
-  sb = i8_dot<0, 4, 60>(w[16], xv, sb);
-  return da * sa + db * sb;
+  float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  i8_dot<2, 4, -2>(w[0], xv, a);
+  i8_dot<0, 4, 32>(w[9], xv, b);
+  i8_dot<0, 4, 2>(w[1], xv, a);
+  i8_dot<0, 4, 36>(w[10], xv, b);
+  i8_dot<0, 4, 6>(w[2], xv, a);
+  i8_dot<0, 4, 40>(w[11], xv, b);
+  i8_dot<0, 4, 10>(w[3], xv, a);
+  i8_dot<0, 4, 44>(w[12], xv, b);
+  i8_dot<0, 4, 14>(w[4], xv, a);
+  i8_dot<0, 4, 48>(w[13], xv, b);
+  i8_dot<0, 4, 18>(w[5], xv, a);
+  i8_dot<0, 4, 52>(w[14], xv, b);
+  i8_dot<0, 4, 22>(w[6], xv, a);
+  i8_dot<0, 4, 56>(w[15], xv, b);
+  i8_dot<0, 4, 26>(w[7], xv, a);
+  i8_dot<0, 4, 60>(w[16], xv, b);
+  i8_dot<0, 2, 30>(w[8], xv, a);
+  return da * sum4(a) + db * sum4(b);
 }
 
 // Exact per-element form of pair_dot for activations that are not all finite:
@@ -190,44 +186,126 @@ __device__ __forceinline__ float pair_dot_exact(const uint32_t* w, const float* 
   return acc;
 }
 
-constexpr int kWaves = 4;  // waves per workgroup of the pair kernel
+// ---------------------------------------------------------------------------
+// Streaming kernel.
+//
+// One persistent workgroup per CU, kWaves waves.  The row's pairs are split
+// into K-slices of at most 64 pairs (4096 elements); `ks` waves (1, 2 or 4)
+// cover one row and the workgroup's kWaves / ks row groups walk its contiguous
+// row range.  Lane l of a slice-s wave owns pair 64*s + l in every row, so its
+// 64 activations are read once (from an LDS copy of x staged by the whole
+// workgroup) and kept in VGPRs.  Each row slice is fetched with coalesced
+// V-dword loads (96-bit for Q4_0, 64-bit for Q4_1, 32-bit for Q8_0: a slice of
+// 64 pairs is exactly 3 / 5 / 17 such loads per lane), prefetched kPrefetch
+// rows ahead in registers, transposed through a wave-private LDS slab so that
+// each lane gets its own 36/40/68-byte pair, and reduced across lanes with
+// DPP.  With ks > 1 the slices' partial sums meet in LDS in a fixed order.
+constexpr int kWaves = 8;
+constexpr int kPrefetch = 2;
+constexpr int kMaxSlices = 4;  // K <= 4 * 4096
 
-// ks: waves splitting one row's K (1, 2 or 4); ps: pairs per K-slice (<= 64);
-// n_sets: number of R-row sets.  Workgroup w handles sets (it*rg + g) for
-// it = w, w + gridDim.x, ... where g = wave / ks and rg = kWaves / ks.
-template <int TYPE, int R>
-__global__ __launch_bounds__(256) void gemv_pairs_kernel(const uint8_t* __restrict__ W,
-                                                         const float* __restrict__ x,
-                                                         float* __restrict__ y, int n_rows,
-                                                         int pairs_per_row, int ks, int ps,
-                                                         int n_sets) {
+template <int TYPE>
+struct LoadFmt;  // V: dwords per vector load; NV: loads per full 64-pair slice
+template <>
+struct LoadFmt<WH_TYPE_Q4_0> {
+  static constexpr int V = 3, NV = 3;
+};
+template <>
+struct LoadFmt<WH_TYPE_Q4_1> {
+  static constexpr int V = 2, NV = 5;
+};
+template <>
+struct LoadFmt<WH_TYPE_Q8_0> {
+  static constexpr int V = 1, NV = 17;
+};
+
+// Sum over the wavefront; the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_mov<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_mov<0x140, 0xF>(v);  // row_mirror
+  v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15
+  v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31
+  return v;
+}
+
+template <int V>
+__device__ __forceinline__ void load_vec(const uint32_t* __restrict__ src, bool ok, uint32_t* dst) {
+#pragma unroll
+  for (int c = 0; c < V; c++) dst[c] = ok ? __builtin_nontemporal_load(src + c) : 0u;
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t* __restrict__ W,
+                                                                  const float* __restrict__ x,
+                                                                  float* __restrict__ y, int n_rows,
+                                                                  int pairs_per_row, int ks,
+                                                                  int rows_per_wg) {
   constexpr int DW = PairFmt<TYPE>::DW;
   constexpr int PB = PairFmt<TYPE>::BYTES;
-  __shared__ float red[kWaves][R];
+  constexpr int V = LoadFmt<TYPE>::V;
+  constexpr int NV = LoadFmt<TYPE>::NV;
+  constexpr int SLAB = DW * 64 + 4;
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int K = pairs_per_row * 64;
+  float* xs = reinterpret_cast<float*>(lds);                // x, 4 floats of padding per 64
+  uint32_t* slabs = lds + K + K / 16;                       // kWaves slabs of SLAB dwords
+  float* red = reinterpret_cast<float*>(slabs + kWaves * SLAB);
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int s = wave % ks;
   const int g = wave / ks;
-  const int rg = kWaves / ks;
-  const int p = s * ps + lane;
-  const bool active = lane < ps && p < pairs_per_row;
+  const int groups = kWaves / ks;
+  const int ps = min(64, pairs_per_row - 64 * s);           // pairs in this slice (> 0)
+  const int nd = DW * ps;                                   // dwords in one row slice
+  const bool active = lane < ps;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int r1 = min(n_rows, r0 + rows_per_wg);
+  const int nk = (r1 - r0 + groups - 1) / groups;           // row steps (uniform in the WG)
   const size_t row_bytes = static_cast<size_t>(pairs_per_row) * PB;
+  const uint8_t* slice_base = W + static_cast<size_t>(64 * s) * PB;
 
+  // Prefetch the first rows before anything else.
+  uint32_t buf[kPrefetch][DW];
+  auto fetch = [&](uint32_t* dst, int k) {
+    const int row = r0 + g + k * groups;
+    const bool rok = k < nk && row < r1;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(slice_base + static_cast<size_t>(row) * row_bytes);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = V * (64 * i + lane);
+      load_vec<V>(src + e, rok && e < nd, dst + V * i);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < kPrefetch; d++) fetch(buf[d], d);
+
+  // Stage x in LDS once for the workgroup, then each lane copies its 64 values.
+  for (int i = threadIdx.x; i < K / 4; i += kWaves * 64) {
+    const float4 t = reinterpret_cast<const float4*>(x)[i];
+    const int e = 4 * i;
+    *reinterpret_cast<float4*>(xs + e + (e >> 6) * 4) = t;
+  }
+  __syncthreads();
   float xv[64];
-  if (active) {
-    const float4* xp = reinterpret_cast<const float4*>(x + 64 * static_cast<size_t>(p));
+  {
+    const int p = 64 * s + (active ? lane : 0);
+    const float* xp = xs + 68 * p;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const float4 t = xp[i];
-      xv[4 * i + 0] = t.x;
-      xv[4 * i + 1] = t.y;
-      xv[4 * i + 2] = t.z;
-      xv[4 * i + 3] = t.w;
+      const float4 t = *reinterpret_cast<const float4*>(xp + 4 * i);
+      xv[4 * i + 0] = active ? t.x : 0.f;
+      xv[4 * i + 1] = active ? t.y : 0.f;
+      xv[4 * i + 2] = active ? t.z : 0.f;
+      xv[4 * i + 3] = active ? t.w : 0.f;
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 64; i++) xv[i] = 0.f;
   }
   float xa = 0.f, xb = 0.f;
 #pragma unroll
@@ -241,55 +319,52 @@ __global__ __launch_bounds__(256) void gemv_pairs_kernel(const uint8_t* __restri
   bool exact = false;
   if constexpr (TYPE != WH_TYPE_Q8_0) exact = __any(!(__builtin_isfinite(xa) && __builtin_isfinite(xb)));
 
-  for (int it = blockIdx.x; it * rg < n_sets; it += gridDim.x) {
-    const int set = it * rg + g;
-    const int row0 = set * R;
-    uint32_t wv[R][DW];
+  uint32_t* slab = slabs + wave * SLAB;
+  for (int kb = 0; kb < nk; kb += kPrefetch) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int row = row0 + r;
-      if (active && set < n_sets && row < n_rows) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(
-            W + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(p) * PB);
+    for (int d = 0; d < kPrefetch; d++) {
+      const int k = kb + d;
+      if (k >= nk) break;
+      const int row = r0 + g + k * groups;
+      // this row's slice -> LDS slab (dword e of the slice at slab[e])
 #pragma unroll
-        for (int j = 0; j < DW; j++) wv[r][j] = __builtin_nontemporal_load(src + j);
+      for (int i = 0; i < NV; i++)
+#pragma unroll
+        for (int c = 0; c < V; c++) slab[V * (64 * i + lane) + c] = buf[d][V * i + c];
+      fetch(buf[d], k + kPrefetch);
+      __builtin_amdgcn_wave_barrier();
+      uint32_t w[DW];
+#pragma unroll
+      for (int j = 0; j < DW; j++) w[j] = slab[DW * lane + j];
+      __builtin_amdgcn_wave_barrier();
+      float part = 0.f;
+      if (active) {
+        if constexpr (TYPE == WH_TYPE_Q8_0) {
+          part = pair_dot<TYPE>(w, xv, xa, xb);
+        } else {
+          part = exact ? pair_dot_exact<TYPE>(w, xv) : pair_dot<TYPE>(w, xv, xa, xb);
+        }
+      }
+      const float tot = wave_sum_to_lane63(part);
+      if (ks == 1) {
+        if (lane == 63 && row < r1) y[row] = tot;
       } else {
-#pragma unroll
-        for (int j = 0; j < DW; j++) wv[r][j] = 0u;
+        if (lane == 63) red[wave] = tot;
+        __syncthreads();
+        if (s == 0 && lane == 63 && row < r1) {
+          float t = red[g * ks];
+          for (int s2 = 1; s2 < ks; s2++) t += red[g * ks + s2];
+          y[row] = t;
+        }
+        __syncthreads();
       }
-    }
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      float part;
-      if constexpr (TYPE == WH_TYPE_Q8_0) {
-        part = pair_dot<TYPE>(wv[r], xv, xa, xb);
-      } else {
-        part = exact ? pair_dot_exact<TYPE>(wv[r], xv) : pair_dot<TYPE>(wv[r], xv, xa, xb);
-      }
-      acc[r] = whd::wave_sum(part);
-    }
-
-    if (ks == 1) {
-      if (lane == 0 && set < n_sets) {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-          if (row0 + r < n_rows) y[row0 + r] = acc[r];
-      }
-    } else {
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; r++) red[wave][r] = acc[r];
-      }
-      __syncthreads();
-      if (s == 0 && lane < R && set < n_sets && row0 + lane < n_rows) {
-        float t = 0.f;
-        for (int s2 = 0; s2 < ks; s2++) t += red[g * ks + s2][lane];
-        y[row0 + lane] = t;
-      }
-      __syncthreads();
     }
   }
+}
+
+size_t stream_lds_bytes(int type, int K) {
+  const int dw = type == WH_TYPE_Q4_0 ? 9 : (type == WH_TYPE_Q4_1 ? 10 : 17);
+  return 4u * static_cast<size_t>(K + K / 16 + kWaves * (dw * 64 + 4) + kWaves);
 }
 
 template <int TYPE>
@@ -318,23 +393,26 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
 template <int TYPE>
 int launch_typed(const uint8_t* w, const float* x, float* y, size_t n_rows, size_t k,
                  hipStream_t s) {
-  constexpr int R = 4;
   const size_t nb = k / 32;
   const int cus = wh::cu_count();
-  const bool fast = (nb % 2 == 0) && nb > 0 && nb / 2 <= 256 && wh::aligned(w, 4) &&
-                    wh::aligned(x, 16) && n_rows < (1u << 30);
+  const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k));
+  const bool fast = (nb % 2 == 0) && nb > 0 && nb / 2 <= 64 * kMaxSlices && wh::aligned(w, 4) &&
+                    wh::aligned(x, 16) && n_rows < (1u << 30) && lds <= wh::max_lds_per_block();
   if (fast) {
     const int P = static_cast<int>(nb / 2);
     int ks = (P + 63) / 64;
     if (ks == 3) ks = 4;
-    const int ps = (P + ks - 1) / ks;
-    const int rg = kWaves / ks;
-    const int n_sets = static_cast<int>((n_rows + R - 1) / R);
-    int grid = (n_sets + rg - 1) / rg;
-    const int cap = cus * 4;
-    if (grid > cap) grid = cap;
-    gemv_pairs_kernel<TYPE, R><<<grid, 256, 0, s>>>(w, x, y, static_cast<int>(n_rows), P, ks, ps,
-                                                     n_sets);
+    const int groups = kWaves / ks;
+    const size_t max_wg = (n_rows + groups - 1) / groups;
+    const int grid = static_cast<int>(max_wg < static_cast<size_t>(cus) ? max_wg : cus);
+    const int rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
+    if (lds > 65536) {
+      WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+    }
+    gemv_stream_kernel<TYPE><<<grid, kWaves * 64, lds, s>>>(w, x, y, static_cast<int>(n_rows), P,
+                                                            ks, rows_per_wg);
   } else {
     size_t grid = (n_rows + 3) / 4;
     const size_t cap = static_cast<size_t>(cus) * 16;

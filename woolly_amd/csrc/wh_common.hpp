@@ -46,6 +46,8 @@ inline bool is_block_type(int type) {
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
+// Largest LDS allocation one workgroup may use on the current device.
+size_t max_lds_per_block();
 
 // Launchers implemented in the .hip translation units.  Arguments have been
 // validated by the C ABI layer; these only choose kernels and launch them.
