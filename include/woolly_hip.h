@@ -133,10 +133,15 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
  *   (tensor_utils_simd.rs:605-754) and compute_simd_swiglu_ffn
  *   (model/lazy_transformer.rs:1073-1123), with ggml's [N][K] weight layout
  *   instead of the [K][N] reshape at lazy_transformer.rs:1091-1101.
- * X is row-major [n_tokens][k] f32, Y is row-major [n_tokens][n_rows] f32. */
+ * X is row-major [n_tokens][k] f32, Y is row-major [n_tokens][n_rows] f32.
+ * The MFMA path (more than 2 tokens) needs a device workspace of
+ * wh_quantized_matmul_workspace_bytes(type, n_tokens, k) bytes; the call
+ * itself never allocates.  WH_ERR_BUFFER_TOO_SMALL if it is missing. */
+WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_tokens, size_t k);
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes,
                                size_t n_rows, size_t k, const float* x, size_t n_tokens,
-                               float* y, wh_stream_t stream);
+                               float* y, void* workspace, size_t workspace_bytes,
+                               wh_stream_t stream);
 
 /* --------------------------------------------------- elementwise / norms */
 /* rms_norm (crates/woolly-core/src/tensor_utils.rs:446-480):

@@ -364,9 +364,14 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
 }
 
 // -------------------------------------------------------------------- GEMM
+WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_tokens, size_t k) {
+  if (!wh::is_block_type(type) || n_tokens <= wh::kGemvTokenLimit) return 0;
+  return wh::gemm_workspace_bytes(type, n_tokens, k);
+}
+
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes, size_t n_rows,
-                               size_t k, const float* x, size_t n_tokens, float* y,
-                               wh_stream_t stream) {
+                               size_t k, const float* x, size_t n_tokens, float* y, void* workspace,
+                               size_t workspace_bytes, wh_stream_t stream) {
   int st = check_block_args("quantized_matmul", type, k);
   if (st) return st;
   st = check_weight_bytes("quantized_matmul", type, n_rows, k, weight_nbytes);
@@ -379,7 +384,10 @@ WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbyt
   if (st) return st;
   st = check_ptr("quantized_matmul", "x", x, 4);
   if (st) return st;
-  return wh::launch_gemm(type, weights, n_rows, k, x, n_tokens, y, hs(stream));
+  if (workspace && !wh::aligned(workspace, 256))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matmul: workspace is not 256-byte aligned");
+  return wh::launch_gemm(type, weights, n_rows, k, x, n_tokens, y, workspace, workspace_bytes,
+                         hs(stream));
 }
 
 // --------------------------------------------------------------- elementwise
@@ -408,7 +416,11 @@ WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out, w
 
 // ------------------------------------------------------------------- FFN
 WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m) {
-  return align_up(m * hidden * sizeof(float), 256) + 3 * align_up(m * n_ff * sizeof(float), 256);
+  const size_t g1 = wh::gemm_workspace_bytes(WH_TYPE_Q4_1, m, hidden);
+  const size_t g2 = wh::gemm_workspace_bytes(WH_TYPE_Q4_1, m, n_ff);
+  const size_t gemm_ws = m <= wh::kGemvTokenLimit ? 0 : (g1 > g2 ? g1 : g2);
+  return align_up(m * hidden * sizeof(float), 256) + 3 * align_up(m * n_ff * sizeof(float), 256) +
+         gemm_ws;
 }
 
 WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps, const float* x,
@@ -440,13 +452,16 @@ WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps,
   float* u = reinterpret_cast<float*>(ws);
   ws += align_up(m * F * sizeof(float), 256);
   float* h = reinterpret_cast<float*>(ws);
+  ws += align_up(m * F * sizeof(float), 256);
+  void* gemm_ws = ws;
+  const size_t gemm_bytes = need - static_cast<size_t>(ws - static_cast<char*>(workspace));
   hipStream_t s = hs(stream);
   if ((st = wh::launch_rms_norm(x, gamma, eps, m, H, xh, s))) return st;
   if (F == 0) return wh::launch_fill_bytes(out, 0, m * H * sizeof(float), s);
-  if ((st = wh::launch_gemm(w->type, w->gate, F, H, xh, m, g, s))) return st;
-  if ((st = wh::launch_gemm(w->type, w->up, F, H, xh, m, u, s))) return st;
+  if ((st = wh::launch_gemm(w->type, w->gate, F, H, xh, m, g, gemm_ws, gemm_bytes, s))) return st;
+  if ((st = wh::launch_gemm(w->type, w->up, F, H, xh, m, u, gemm_ws, gemm_bytes, s))) return st;
   if ((st = wh::launch_swiglu(g, u, m * F, h, s))) return st;
-  return wh::launch_gemm(w->type, w->down, H, F, h, m, out, s);
+  return wh::launch_gemm(w->type, w->down, H, F, h, m, out, gemm_ws, gemm_bytes, s);
 }
 
 // ------------------------------------------------------------ weight handles

@@ -56,8 +56,12 @@ int launch_dequantize(int type, const void* data, size_t nelements, float* out,
 int launch_fill_bytes(void* dst, int value, size_t nbytes, hipStream_t stream);
 int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows,
                 size_t k, hipStream_t stream);
+// Token counts up to this use one streaming GEMV per token instead of MFMA.
+constexpr size_t kGemvTokenLimit = 2;
+size_t gemm_workspace_bytes(int type, size_t n_tokens, size_t k);
 int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x,
-                size_t n_tokens, float* y, hipStream_t stream);
+                size_t n_tokens, float* y, void* workspace, size_t workspace_bytes,
+                hipStream_t stream);
 int launch_rms_norm(const float* x, const float* weight, float eps, size_t tokens,
                     size_t hidden, float* out, hipStream_t stream);
 int launch_swiglu(const float* gate, const float* up, size_t n, float* out,

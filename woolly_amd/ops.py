@@ -50,10 +50,16 @@ def quantized_matvec(ggml_type: int, weights, weight_nbytes: int, x, y, m: int, 
                                                _p(y), m, k, _s(stream)))
 
 
+def matmul_workspace_bytes(ggml_type: int, n_tokens: int, k: int) -> int:
+    return int(_lib.load().wh_quantized_matmul_workspace_bytes(ggml_type, n_tokens, k))
+
+
 def quantized_matmul(ggml_type: int, weights, weight_nbytes: int, n_rows: int, k: int, x,
-                     n_tokens: int, y, stream: Stream | None = None) -> None:
+                     n_tokens: int, y, workspace=None, workspace_bytes: int = 0,
+                     stream: Stream | None = None) -> None:
     _lib.check(_lib.load().wh_quantized_matmul(ggml_type, _p(weights), weight_nbytes, n_rows, k,
-                                               _p(x), n_tokens, _p(y), _s(stream)))
+                                               _p(x), n_tokens, _p(y), _p(workspace) or None,
+                                               workspace_bytes, _s(stream)))
 
 
 def rms_norm(x, weight, eps: float, tokens: int, hidden: int, out,
