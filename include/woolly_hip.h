@@ -135,9 +135,11 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
  *   instead of the [K][N] reshape at lazy_transformer.rs:1091-1101.
  * X is row-major [n_tokens][k] f32, Y is row-major [n_tokens][n_rows] f32.
  * The MFMA path (more than 2 tokens) needs a device workspace of
- * wh_quantized_matmul_workspace_bytes(type, n_tokens, k) bytes; the call
- * itself never allocates.  WH_ERR_BUFFER_TOO_SMALL if it is missing. */
-WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_tokens, size_t k);
+ * wh_quantized_matmul_workspace_bytes(type, n_rows, k, n_tokens) bytes (256-byte
+ * aligned); the call itself never allocates.  WH_ERR_BUFFER_TOO_SMALL if it
+ * is missing or short. */
+WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_rows, size_t k,
+                                                  size_t n_tokens);
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes,
                                size_t n_rows, size_t k, const float* x, size_t n_tokens,
                                float* y, void* workspace, size_t workspace_bytes,

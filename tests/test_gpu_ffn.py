@@ -54,7 +54,7 @@ def test_swiglu(gpu, orc):
 @pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1])
 @pytest.mark.parametrize("m,n,k", [(1, 64, 256), (2, 100, 4096), (4, 300, 4096), (8, 1024, 4096),
                                    (3, 512, 14336), (130, 200, 512), (64, 129, 4096),
-                                   (257, 384, 1024)])
+                                   (257, 384, 1024), (512, 256, 14336), (100, 96, 96)])
 def test_matmul_parity(gpu, orc, t, m, n, k):
     print(f"[case] matmul type={t} m={m} n={n} k={k}", flush=True)
     w = synth.quantized_weight(t, n, k, seed=n + k)
@@ -62,7 +62,7 @@ def test_matmul_parity(gpu, orc, t, m, n, k):
     wb, wp = up(w)
     xb, xp = up(x)
     yb = DeviceBuffer(4 * m * n)
-    wsz = ops.matmul_workspace_bytes(t, m, k)
+    wsz = ops.matmul_workspace_bytes(t, n, k, m)
     ws = DeviceBuffer(max(wsz, 1))
     ops.quantized_matmul(t, wp, w.nbytes, n, k, xp, m, yb.ptr, ws, wsz)
     got = down(yb, np.float32, m * n).reshape(m, n)
@@ -139,7 +139,7 @@ def test_matmul_large_values_row_scaling(gpu, orc):
     wb, wp = up(w)
     xb, xp = up(x)
     yb = DeviceBuffer(4 * m * n)
-    wsz = ops.matmul_workspace_bytes(Q4_0, m, k)
+    wsz = ops.matmul_workspace_bytes(Q4_0, n, k, m)
     ws = DeviceBuffer(wsz)
     ops.quantized_matmul(Q4_0, wp, w.nbytes, n, k, xp, m, yb.ptr, ws, wsz)
     got = down(yb, np.float32, m * n).reshape(m, n)

@@ -92,7 +92,7 @@ SIGNATURES = {
     "wh_tensor_nbytes": (_int, [_int, C.c_uint64, C.POINTER(C.c_uint64)]),
     "wh_dequantize": (_int, [_int, _vp, _sz, _sz, _f32p, _vp]),
     "wh_quantized_matvec": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz, _vp]),
-    "wh_quantized_matmul_workspace_bytes": (_sz, [_int, _sz, _sz]),
+    "wh_quantized_matmul_workspace_bytes": (_sz, [_int, _sz, _sz, _sz]),
     "wh_quantized_matmul": (_int, [_int, _vp, _sz, _sz, _sz, _f32p, _sz, _f32p, _vp, _sz, _vp]),
     "wh_rms_norm": (_int, [_f32p, _f32p, C.c_float, _sz, _sz, _f32p, _vp]),
     "wh_swiglu": (_int, [_f32p, _f32p, _sz, _f32p, _vp]),

@@ -364,9 +364,10 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
 }
 
 // -------------------------------------------------------------------- GEMM
-WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_tokens, size_t k) {
-  if (!wh::is_block_type(type) || n_tokens <= wh::kGemvTokenLimit) return 0;
-  return wh::gemm_workspace_bytes(type, n_tokens, k);
+WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_rows, size_t k,
+                                                  size_t n_tokens) {
+  if (!wh::is_block_type(type) || n_tokens <= wh::kGemvTokenLimit || k == 0) return 0;
+  return wh::gemm_workspace_bytes_for(type, n_rows, n_tokens, k);
 }
 
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes, size_t n_rows,
@@ -416,8 +417,8 @@ WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out, w
 
 // ------------------------------------------------------------------- FFN
 WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m) {
-  const size_t g1 = wh::gemm_workspace_bytes(WH_TYPE_Q4_1, m, hidden);
-  const size_t g2 = wh::gemm_workspace_bytes(WH_TYPE_Q4_1, m, n_ff);
+  const size_t g1 = wh::gemm_workspace_bytes_for(WH_TYPE_Q4_1, n_ff, m, hidden);
+  const size_t g2 = wh::gemm_workspace_bytes_for(WH_TYPE_Q4_1, hidden, m, n_ff);
   const size_t gemm_ws = m <= wh::kGemvTokenLimit ? 0 : (g1 > g2 ? g1 : g2);
   return align_up(m * hidden * sizeof(float), 256) + 3 * align_up(m * n_ff * sizeof(float), 256) +
          gemm_ws;

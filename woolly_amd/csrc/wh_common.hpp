@@ -59,6 +59,7 @@ int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows
 // Token counts up to this use one streaming GEMV per token instead of MFMA.
 constexpr size_t kGemvTokenLimit = 2;
 size_t gemm_workspace_bytes(int type, size_t n_tokens, size_t k);
+size_t gemm_workspace_bytes_for(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x,
                 size_t n_tokens, float* y, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);

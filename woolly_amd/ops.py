@@ -50,8 +50,8 @@ def quantized_matvec(ggml_type: int, weights, weight_nbytes: int, x, y, m: int, 
                                                _p(y), m, k, _s(stream)))
 
 
-def matmul_workspace_bytes(ggml_type: int, n_tokens: int, k: int) -> int:
-    return int(_lib.load().wh_quantized_matmul_workspace_bytes(ggml_type, n_tokens, k))
+def matmul_workspace_bytes(ggml_type: int, n_rows: int, k: int, n_tokens: int) -> int:
+    return int(_lib.load().wh_quantized_matmul_workspace_bytes(ggml_type, n_rows, k, n_tokens))
 
 
 def quantized_matmul(ggml_type: int, weights, weight_nbytes: int, n_rows: int, k: int, x,
