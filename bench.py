@@ -126,6 +126,40 @@ def bench_ffn(m: int, iters: int) -> float:
     return e0.elapsed_ms(e1) / iters * 1000.0
 
 
+def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
+    """Device-to-device copies of a known size (HIP's copy kernel): the reference
+    the HBM byte counters of the GEMV are scaled by.  Returns GB/s."""
+    from woolly_amd.device import DeviceBuffer, Event, Stream
+    from woolly_amd import _lib
+
+    src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    src.fill(1)
+    stream = Stream()
+    lib = _lib.load()
+    e0, e1 = Event(), Event()
+    _lib.check(lib.wh_memcpy_d2d(dst.ptr, src.ptr, nbytes, stream.handle))
+    stream.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        _lib.check(lib.wh_memcpy_d2d(dst.ptr, src.ptr, nbytes, stream.handle))
+    e1.record(stream)
+    e1.synchronize()
+    return 2 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+
+
+def traffic_from_profile() -> int | None:
+    """HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
+    (scaled by the copy probe), as recorded in the committed profile summary."""
+    path = ROOT / "profiles" / "gemv_q4_0_14336x4096_pmc.txt"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s: float = 10.0) -> dict:
     """The oracle's order-exact scalar Q4_0 GEMV on this host (1 thread)."""
     from tests._oracle import Oracle
@@ -169,6 +203,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-layer timings")
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512"], default=None,
+                    help="run one leg only (for profiling); prints that leg's timing")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run only device-to-device copies of 256 MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -179,10 +217,23 @@ def main() -> int:
 
     device.init(0)
     log(f"[bench] device: {device.device_name()}")
+    if args.copy_probe:
+        print(json.dumps({"copy_probe_GBps": round(copy_probe(), 1), "bytes_per_copy": 256 << 20}))
+        return 0
+    if args.only == "gemv":
+        ms_step, _, _ = bench_gemv(args.steps, args.warmup)
+        print(json.dumps({"gemv_us": round(ms_step * 1e3, 3)}))
+        return 0
+    if args.only in ("ffn1", "ffn512"):
+        m = 1 if args.only == "ffn1" else 512
+        print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3), 2)}))
+        return 0
     ms_step, med_ms, mean_ms = bench_gemv(args.steps, args.warmup)
     nbytes = gemv_bytes(N_ROWS, K)
     value = nbytes / (ms_step * 1e-3) / 1e9
-    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    # the GEMV is the only kernel of a step: its average launch duration is the
+    # timed region (graph replay, events on the launch stream) divided by K
+    achieved = value
     log(f"[bench] gemv: {ms_step * 1e3:.2f} us/step back-to-back, per-launch mean "
         f"{mean_ms * 1e3:.2f} us (median {med_ms * 1e3:.2f})")
 
@@ -222,9 +273,10 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "gemv_pairs_kernel<Q4_0,4>",
-            "launch_us_mean": round(mean_ms * 1e3, 3),
+            "traffic": traffic_from_profile(),
+            "kernel": "gemv_stream_kernel<Q4_0>",
+            "launch_us_mean": round(ms_step * 1e3, 3),
+            "launch_us_eager_event_pairs": round(mean_ms * 1e3, 3),
         },
         "ffn_layer_us": ffn or None,
         "cpu_baseline": cpu,
