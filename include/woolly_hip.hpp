@@ -1,0 +1,214 @@
+// woolly_hip.hpp -- C++17 host-side mirror of woolly's quantization API, over
+// the C ABI of libwoolly_hip (woolly_hip.h).  Header-only.
+//
+// Names, argument meaning and errors follow the Rust reference so code (and
+// tests) written against it read the same:
+//   woolly::tensor::quantization   crates/woolly-tensor/src/quantization.rs
+//     BlockQ4_0 / BlockQ4_1 / BlockQ8_0              :98-151
+//     QuantizationError{UnsupportedScheme, InvalidParameters}   :8-26
+//     QuantizedStorage (Q4_0 / Q4_1 / Q8_0)           :154-170
+//     dequantize_q4_0 / dequantize_q4_1 / dequantize_q8_0       :466, 490, 576
+//     simd::quantized_matvec(weights, input, output, m, k)      :869-909
+//     optimized::dequantize_blocks(storage)           :1171-1210
+//   woolly::gguf                   crates/woolly-gguf/src
+//     GGMLType ids                                     tensor_info.rs:15-30
+//     dequantize(data, ggml_type, nelements)           dequantize.rs:189-205
+//     Error::{BufferTooSmall{needed, available}, InvalidTensorType}  error.rs:11-64
+// Every call runs the HIP kernels (synchronous host-memory entry points);
+// there is no CPU implementation in this header.
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <variant>
+#include <vector>
+
+#include "woolly_hip.h"
+
+namespace woolly {
+
+// f16 bit pattern helper (half::f16 is a 16-bit IEEE binary16 value).
+struct f16 {
+  uint16_t bits = 0;
+  static f16 from_bits(uint16_t b) { return f16{b}; }
+  // Round-to-nearest-even conversion (half::f16::from_f32).
+  static f16 from_f32(float v) {
+    uint32_t x;
+    std::memcpy(&x, &v, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    if (exp == 0xFFu) return f16{static_cast<uint16_t>(sign | 0x7C00u | (man ? 0x200u | (man >> 13) : 0u))};
+    const int e = static_cast<int>(exp) - 112;
+    if (e >= 31) return f16{static_cast<uint16_t>(sign | 0x7C00u)};
+    if (e <= 0) {
+      if (e < -10) return f16{static_cast<uint16_t>(sign)};
+      const uint32_t m = man | 0x800000u;
+      const int shift = 14 - e;
+      uint32_t h = m >> shift;
+      const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+      if (rem > half || (rem == half && (h & 1u))) h++;
+      return f16{static_cast<uint16_t>(sign | h)};
+    }
+    uint32_t h = sign | (static_cast<uint32_t>(e) << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return f16{static_cast<uint16_t>(h)};
+  }
+};
+
+namespace tensor {
+namespace quantization {
+
+#pragma pack(push, 1)
+struct BlockQ4_0 {
+  f16 d;
+  uint8_t qs[16];
+};
+struct BlockQ4_1 {
+  f16 d;
+  f16 m;
+  uint8_t qs[16];
+};
+struct BlockQ8_0 {
+  f16 d;
+  int8_t qs[32];
+};
+#pragma pack(pop)
+static_assert(sizeof(BlockQ4_0) == 18 && sizeof(BlockQ4_1) == 20 && sizeof(BlockQ8_0) == 34,
+              "GGUF block sizes");
+
+// QuantizationError (quantization.rs:8-26); thrown, as Result::Err would be returned.
+struct QuantizationError : std::runtime_error {
+  enum class Kind { UnsupportedScheme, InvalidParameters, Backend };
+  Kind kind;
+  QuantizationError(Kind k, const std::string& msg) : std::runtime_error(msg), kind(k) {}
+};
+
+inline void check_status(int st) {
+  if (st == WH_OK) return;
+  const std::string msg = wh_last_error();
+  if (st == WH_ERR_UNSUPPORTED_TYPE)
+    throw QuantizationError(QuantizationError::Kind::UnsupportedScheme, msg);
+  if (st == WH_ERR_INVALID_SHAPE || st == WH_ERR_BUFFER_TOO_SMALL || st == WH_ERR_INVALID_ARGUMENT)
+    throw QuantizationError(QuantizationError::Kind::InvalidParameters, msg);
+  throw QuantizationError(QuantizationError::Kind::Backend, msg);
+}
+
+// QuantizedStorage (quantization.rs:154-170), restricted to the block formats on this path.
+struct QuantizedStorage {
+  std::variant<std::vector<BlockQ4_0>, std::vector<BlockQ4_1>, std::vector<BlockQ8_0>> blocks;
+  static QuantizedStorage Q4_0(std::vector<BlockQ4_0> b) { return {std::move(b)}; }
+  static QuantizedStorage Q4_1(std::vector<BlockQ4_1> b) { return {std::move(b)}; }
+  static QuantizedStorage Q8_0(std::vector<BlockQ8_0> b) { return {std::move(b)}; }
+  int ggml_type() const {
+    return blocks.index() == 0 ? WH_TYPE_Q4_0 : (blocks.index() == 1 ? WH_TYPE_Q4_1 : WH_TYPE_Q8_0);
+  }
+  const void* data() const {
+    return std::visit([](const auto& v) { return static_cast<const void*>(v.data()); }, blocks);
+  }
+  size_t nbytes() const {
+    return std::visit([](const auto& v) { return v.size() * sizeof(v[0]); }, blocks);
+  }
+  size_t nblocks() const {
+    return std::visit([](const auto& v) { return v.size(); }, blocks);
+  }
+};
+
+namespace detail {
+inline std::vector<float> dequantize(int type, const void* data, size_t nbytes, size_t nblocks) {
+  std::vector<float> out(nblocks * 32);
+  if (!out.empty()) check_status(wh_dequantize_host(type, data, nbytes, out.size(), out.data()));
+  return out;
+}
+}  // namespace detail
+
+inline std::vector<float> dequantize_q4_0(const std::vector<BlockQ4_0>& blocks) {
+  return detail::dequantize(WH_TYPE_Q4_0, blocks.data(), blocks.size() * sizeof(BlockQ4_0), blocks.size());
+}
+inline std::vector<float> dequantize_q4_1(const std::vector<BlockQ4_1>& blocks) {
+  return detail::dequantize(WH_TYPE_Q4_1, blocks.data(), blocks.size() * sizeof(BlockQ4_1), blocks.size());
+}
+inline std::vector<float> dequantize_q8_0(const std::vector<BlockQ8_0>& blocks) {
+  return detail::dequantize(WH_TYPE_Q8_0, blocks.data(), blocks.size() * sizeof(BlockQ8_0), blocks.size());
+}
+
+namespace simd {
+// simd::quantized_matvec (quantization.rs:869-909), Q4_0 / Q8_0 like the
+// reference and Q4_1 in addition.  output[r] = sum_k W[r, k] * input[k].
+inline void quantized_matvec(const QuantizedStorage& weights, const std::vector<float>& input,
+                             std::vector<float>& output, size_t m, size_t k) {
+  if (input.size() < k || output.size() < m)
+    throw QuantizationError(QuantizationError::Kind::InvalidParameters, "input/output shorter than k/m");
+  check_status(wh_quantized_matvec_host(weights.ggml_type(), weights.data(), weights.nbytes(),
+                                        input.data(), output.data(), m, k));
+}
+inline std::vector<float> dequantize_q4_0_batch(const std::vector<BlockQ4_0>& b) { return dequantize_q4_0(b); }
+inline std::vector<float> dequantize_q4_1_batch(const std::vector<BlockQ4_1>& b) { return dequantize_q4_1(b); }
+inline std::vector<float> dequantize_q8_0_batch(const std::vector<BlockQ8_0>& b) { return dequantize_q8_0(b); }
+}  // namespace simd
+
+namespace optimized {
+// optimized::dequantize_blocks (quantization.rs:1171-1210).
+inline std::vector<float> dequantize_blocks(const QuantizedStorage& storage) {
+  return detail::dequantize(storage.ggml_type(), storage.data(), storage.nbytes(), storage.nblocks());
+}
+}  // namespace optimized
+
+}  // namespace quantization
+}  // namespace tensor
+
+namespace gguf {
+
+// Type ids of tensor_info.rs:14-60 (the subset a quantized Llama file carries).
+enum class GGMLType : uint32_t {
+  F32 = 0, F16 = 1, Q4_0 = 2, Q4_1 = 3, Q5_0 = 6, Q5_1 = 7, Q8_0 = 8, Q8_1 = 9,
+  Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15
+};
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct BufferTooSmall : Error {
+  size_t needed, available;
+  BufferTooSmall(size_t n, size_t a)
+      : Error("Buffer too small: needed " + std::to_string(n) + ", available " + std::to_string(a)),
+        needed(n), available(a) {}
+};
+struct InvalidTensorType : Error {
+  uint32_t type_id;
+  explicit InvalidTensorType(uint32_t t) : Error("Invalid tensor type: " + std::to_string(t)), type_id(t) {}
+};
+
+// woolly_gguf::dequantize(data, ggml_type, nelements) (dequantize.rs:189-205).
+inline std::vector<float> dequantize(const std::vector<uint8_t>& data, GGMLType type, size_t nelements) {
+  std::vector<float> out(nelements);
+  const int st = wh_dequantize_host(static_cast<int>(type), data.data(), data.size(), nelements,
+                                    nelements ? out.data() : nullptr);
+  if (st == WH_ERR_BUFFER_TOO_SMALL) {
+    const size_t ts = wh_type_size(static_cast<int>(type));
+    const size_t bs = wh_block_size(static_cast<int>(type));
+    const size_t needed = bs > 1 ? (nelements + bs - 1) / bs * ts : nelements * ts;
+    throw BufferTooSmall(needed, data.size());
+  }
+  if (st == WH_ERR_UNSUPPORTED_TYPE) throw InvalidTensorType(static_cast<uint32_t>(type));
+  if (st != WH_OK) throw Error(wh_last_error());
+  return out;
+}
+
+// Elements per block (tensor_info.rs:127-140): 32 for the legacy block
+// formats, 256 for the K-quants (super-blocks), 1 for plain types.  The formats
+// the library computes on are answered by the library itself.
+inline size_t get_block_size(GGMLType t) {
+  const size_t bs = wh_block_size(static_cast<int>(t));
+  if (bs) return bs;
+  const uint32_t id = static_cast<uint32_t>(t);
+  if (id >= 10 && id <= 15) return 256;
+  if (id >= 6 && id <= 9) return 32;
+  return 1;
+}
+// Bytes per block for the formats the library computes on; 0 otherwise.
+inline size_t get_type_size(GGMLType t) { return wh_type_size(static_cast<int>(t)); }
+
+}  // namespace gguf
+}  // namespace woolly

@@ -99,3 +99,16 @@ def test_ffn_and_weight_argument_errors_need_no_gpu():
     assert lib.wh_weight_upload(2, 4, 48, None, 0, C.byref(h)) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_weight_upload(2, 4, 64, None, 10, C.byref(h)) == _lib.WH_ERR_BUFFER_TOO_SMALL
     assert h.value is None
+
+
+def test_cpp_mirror_header_compiles_and_links():
+    """include/woolly_hip.hpp compiles stand-alone (C++17, -Werror) and the
+    mirror's test program links against the library (no GPU needed to build)."""
+    import subprocess
+
+    root = Path(__file__).resolve().parent.parent
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-x",
+                    "c++", "-I", str(root / "include"), "-"],
+                   input=b'#include "woolly_hip.hpp"\n', check=True)
+    subprocess.run(["make", "-s", "-C", str(root / "tests" / "cpp")], check=True)
+    assert (root / "tests" / "cpp" / "_build" / "test_mirror").exists()
