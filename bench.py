@@ -126,6 +126,34 @@ def bench_ffn(m: int, iters: int) -> float:
     return e0.elapsed_ms(e1) / iters * 1000.0
 
 
+def bench_gemm(m: int, iters: int) -> float:
+    """Q4_0 prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2), µs per call."""
+    from woolly_amd import ops, synth
+    from woolly_amd.device import DeviceBuffer, Event, Stream
+
+    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=4)
+    x = np.concatenate([synth.activations(K, seed=400 + t) for t in range(min(m, 64))])
+    x = np.resize(x, m * K).astype(np.float32)
+    stream = Stream()
+    wb, xb, yb = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer(4 * m * N_ROWS)
+    wsz = ops.matmul_workspace_bytes(Q4_0, N_ROWS, K, m)
+    ws = DeviceBuffer(max(wsz, 256))
+
+    def run():
+        ops.quantized_matmul(Q4_0, wb, w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
+
+    for _ in range(3):
+        run()
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    for _ in range(iters):
+        run()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / iters * 1000.0
+
+
 def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
     """Device-to-device copies of a known size (HIP's copy kernel): the reference
     the HBM byte counters of the GEMV are scaled by.  Returns GB/s."""
@@ -203,7 +231,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-layer timings")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512"], default=None,
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM M sweep")
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm512"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only device-to-device copies of 256 MiB (counter calibration)")
@@ -224,6 +253,9 @@ def main() -> int:
         ms_step, _, _ = bench_gemv(args.steps, args.warmup)
         print(json.dumps({"gemv_us": round(ms_step * 1e3, 3)}))
         return 0
+    if args.only == "gemm512":
+        print(json.dumps({"gemm_m512_us": round(bench_gemm(512, 5), 2)}))
+        return 0
     if args.only in ("ffn1", "ffn512"):
         m = 1 if args.only == "ffn1" else 512
         print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3), 2)}))
@@ -243,6 +275,17 @@ def main() -> int:
         log(f"[bench] ffn m=1: {ffn['m1']} us")
         ffn["m512"] = round(bench_ffn(512, 3), 2)
         log(f"[bench] ffn m=512: {ffn['m512']} us")
+
+    gemm = {}
+    if not args.no_gemm:
+        # M sweep of config 2 (GEMV -> MFMA crossover).  tflops = 2*M*N*K / time;
+        # the MFMA path issues two fp16 products per multiply-add (activation
+        # hi and lo halves), so its MFMA work is twice that.
+        for m in (1, 8, 64, 512, 2048):
+            us = bench_gemm(m, 20 if m <= 64 else 5)
+            tf = 2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12
+            gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}
+            log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s")
 
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
@@ -279,6 +322,7 @@ def main() -> int:
             "launch_us_eager_event_pairs": round(mean_ms * 1e3, 3),
         },
         "ffn_layer_us": ffn or None,
+        "prefill_gemm_q4_0_14336x4096": gemm or None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

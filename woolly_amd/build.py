@@ -34,6 +34,9 @@ HIPFLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the GEMM epilogue reads every MFMA tile with VALU
+    # ops, and results in AGPRs would cost a v_accvgpr_read per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}",
 ]
 

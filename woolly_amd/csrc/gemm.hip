@@ -210,7 +210,7 @@ constexpr int BKB = 2;  // blocks (of 32 k) per main-loop iteration
 // activations and raw weight bytes are fetched into registers while the
 // current iteration's MFMAs run.
 template <int TYPE>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(const uint8_t* __restrict__ W,
                                                         const _Float16* __restrict__ xhi,
                                                         const _Float16* __restrict__ xlo,
                                                         const float* __restrict__ rscale,
@@ -432,8 +432,11 @@ static size_t splitk_bytes(size_t n_rows, size_t n_tokens, int splits) {
 }
 
 size_t gemm_workspace_bytes_for(int type, size_t n_rows, size_t n_tokens, size_t k) {
-  return gemm_workspace_bytes(type, n_tokens, k) +
-         splitk_bytes(n_rows, n_tokens, gemm_splits(n_rows, n_tokens, k));
+  // enough for either kernel (the choice also depends on the weights' alignment)
+  const size_t a = gemm_workspace_bytes(type, n_tokens, k) +
+                   splitk_bytes(n_rows, n_tokens, gemm_splits(n_rows, n_tokens, k));
+  const size_t b = gemm_tiled_workspace_bytes(type, n_rows, n_tokens, k);
+  return a > b ? a : b;
 }
 
 int launch_gemm_mfma(int type, const void* w, size_t n_rows, size_t k, const float* x,
@@ -502,6 +505,7 @@ int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x
     return set_error(WH_ERR_BUFFER_TOO_SMALL,
                      "quantized_matmul: workspace too small: needed %zu bytes, available %zu", need,
                      workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (gemm_tiled_ok(type, w, k)) return launch_gemm_tiled(type, w, n_rows, k, x, n_tokens, y, workspace, s);
   return launch_gemm_mfma(type, w, n_rows, k, x, n_tokens, y, workspace, s);
 }
 

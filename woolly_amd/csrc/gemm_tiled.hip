@@ -1,0 +1,508 @@
+// gemm_tiled.hip -- quantized prefill GEMM Y = X W^T on gfx950, 16x16x32 MFMA.
+//
+// Replaces the projections woolly computes on fully dequantized f32 weights
+// (simd_matmul_optimized -> Gemm::compute, tensor_utils_simd.rs:855-914,
+// ops/matmul.rs:83-259, called from simd_ffn_forward tensor_utils_simd.rs:605-754):
+//   Y[t, r] = sum_k X[t, k] * W[r, k],  W in GGUF Q4_0 / Q4_1 / Q8_0 blocks.
+//
+// Numerics (same contract as the 32x32 kernel in gemm.hip).  Each activation
+// row is scaled by a power of two (largest magnitude in [2^13, 2^14)) and
+// split into fp16 hi and lo halves; weight quants are exact fp16 integers
+// (q - 8, q, or the int8 value).  One v_mfma_f32_16x16x32_f16 covers exactly
+// one 32-element block: the hi and lo products accumulate into a fresh f32
+// tile and the block scale is applied in f32,
+//   acc += d * (q . hi + q . lo)                 (Q4_0, Q8_0)
+//   acc += d * (q . hi + q . lo) + m * sum(x)    (Q4_1)
+//
+// Data flow.
+//   pack_a_kernel writes the activations pre-swizzled into MFMA fragment order:
+//     fragment (token tile T, block b, 16-token group i, limb) = 64 lanes x 8
+//     halves = 1 KiB, lane l holding token 16i + l%16 and the 8 k-slots of
+//     k-group l/16.  The k-slots follow the order in which a weight lane
+//     unpacks its nibbles, so a straight copy feeds the MFMA.
+//   gemm_tiled_kernel: 512 threads, a 128-token x 256-row tile, each wave
+//     64 tokens x 64 rows (4 x 4 MFMA tiles), two waves per SIMD.  Stages of two blocks are
+//     copied global -> LDS with global_load_lds (activation fragments as
+//     16-byte lanes, raw weight bytes as 4-byte lanes); three stages rotate so
+//     that two are in flight while one is computed.  Each lane unpacks its
+//     weight quants from LDS into fp16 with bit operations (magic-number
+//     conversion, exact), multiplies, and applies the block scale.
+//   Tiles are numbered so that the tiles resident on one XCD share a token
+//     tile: its 2 MiB of activation fragments stay in that XCD's L2.
+#include "wh_blocks.hpp"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int TBM = 128;              // tokens per tile
+constexpr int TBN = 256;              // weight rows per tile
+constexpr int WGM = 2, WGN = 4;       // wave grid (tokens x rows)
+constexpr int TWAVES = WGM * WGN;     // 8 waves, 2 per SIMD
+constexpr int WTM = TBM / WGM;        // wave tile: 64 tokens
+constexpr int WTN = TBN / WGN;        //            x 64 rows
+constexpr int IT = WTM / 16, NT = WTN / 16;  // 16 x 16 MFMA tiles per wave
+constexpr int SB = 2;                 // blocks per stage
+constexpr int NSTAGE = 3;
+constexpr int FRAG = 1024;            // bytes per activation fragment
+constexpr int A_STAGE = SB * 16 * FRAG;  // 2 blocks x (8 token groups x 2 limbs) fragments
+
+template <int TYPE>
+struct TFmt;
+template <>
+struct TFmt<WH_TYPE_Q4_0> {
+  static constexpr int TS = 18, QOFF = 2, DWB = 9;    // DWB: dwords per row per stage
+};
+template <>
+struct TFmt<WH_TYPE_Q4_1> {
+  static constexpr int TS = 20, QOFF = 4, DWB = 10;
+};
+template <>
+struct TFmt<WH_TYPE_Q8_0> {
+  static constexpr int TS = 34, QOFF = 2, DWB = 17;
+};
+
+// raw weight dwords per stage, rounded up to whole copy instructions
+template <int TYPE>
+constexpr int b_dma_per_wave() { return (TBN * TFmt<TYPE>::DWB + TWAVES * 64 - 1) / (TWAVES * 64); }
+template <int TYPE>
+constexpr int b_stage_bytes() { return b_dma_per_wave<TYPE>() * TWAVES * 64 * 4; }
+template <int TYPE>
+constexpr int s_stage_bytes() { return TYPE == WH_TYPE_Q4_1 ? SB * TBM * 4 : 0; }
+template <int TYPE>
+constexpr int stage_bytes() { return A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE>(); }
+
+// Element (within a block) held by k-slot s of k-group g.  For the 4-bit
+// formats the order is that of unpack_q4 below; Q8_0 keeps natural order.
+__device__ __forceinline__ int slot_elem(int type, int g, int s) {
+  if (type == WH_TYPE_Q8_0) return 8 * g + s;
+  const int p = (s & 3) == 1 ? 2 : ((s & 3) == 2 ? 1 : (s & 3));  // 0, 2, 1, 3
+  return (s < 4 ? 0 : 16) + 4 * g + p;
+}
+
+// ---------------------------------------------------------------- packing
+// One workgroup per token row t of the padded tile grid.  Rows t >= n_tokens
+// are written as zeros.  rscale[t] = 2^e with max|x_t| * 2^-e in [2^13, 2^14);
+// bsum (Q4_1 only) = per-block sums of hi + lo, laid out [T][b][128].
+__global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, int n_tokens, int k,
+                                                     int type, _Float16* __restrict__ frag,
+                                                     float* __restrict__ rscale, float* __restrict__ bsum) {
+  __shared__ float red[4];
+  const int t = blockIdx.x;
+  const bool live = t < n_tokens;
+  const float* xr = x + static_cast<size_t>(live ? t : 0) * k;
+  float mx = 0.f;
+  if (live)
+    for (int i = threadIdx.x; i < k; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.f && mx <= 3.4e38f) {
+    int ex;
+    frexpf(mx, &ex);          // mx = f * 2^ex, f in [0.5, 1)
+    e = ex - 14;              // mx * 2^-e in [2^13, 2^14)
+    if (e < -100) e = -100;
+  }
+  const float down = ldexpf(1.f, -e);
+  if (threadIdx.x == 0) rscale[t] = ldexpf(1.f, e);
+  const int nb = k / 32;
+  const int T = t / TBM, i16 = (t % TBM) / 16, tl = t % 16;
+  for (int p = threadIdx.x; p < nb * 4; p += 256) {  // (block, k-group) pairs
+    const int b = p >> 2, g = p & 3;
+    half8 hv, lv;
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const float v = live ? xr[32 * b + slot_elem(type, g, s)] * down : 0.f;  // exact scaling
+      const _Float16 h = static_cast<_Float16>(v);
+      const _Float16 l = static_cast<_Float16>(v - static_cast<float>(h));
+      hv[s] = h;
+      lv[s] = l;
+      part += static_cast<float>(h) + static_cast<float>(l);
+    }
+    const int lane = 16 * g + tl;
+    const size_t base = ((static_cast<size_t>(T) * nb + b) * 16 + 2 * i16) * 512 + 8 * lane;
+    *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
+    *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
+    if (bsum) {
+      // the four k-groups of a block are adjacent threads (p = 4b + g)
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * TBM + (t % TBM)] = part;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- weights
+// Unpacks the quants a weight lane of k-group g needs for one block into the
+// MFMA B operand (8 fp16 integers in slot_elem order).
+// 4-bit: one quant dword u = qs[4g .. 4g+3]; (u & 0x000F000F) | 0x6400 per
+// half is 1024 + q exactly, (u & 0x00F000F0) | 0x6400 is 1024 + 16 q; a
+// packed fp16 add / fma then yields q - 8 (Q4_0) or q (Q4_1) exactly.
+template <int TYPE>
+__device__ __forceinline__ half8 unpack_q4(uint32_t u) {
+  constexpr float OFF_LO = TYPE == WH_TYPE_Q4_0 ? -1032.f : -1024.f;
+  constexpr float OFF_HI = TYPE == WH_TYPE_Q4_0 ? -72.f : -64.f;
+  const uint32_t t8 = u >> 8;
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v lo_a = __builtin_bit_cast(half2v, (u & 0x000F000Fu) | 0x64006400u);
+  const half2v lo_b = __builtin_bit_cast(half2v, (t8 & 0x000F000Fu) | 0x64006400u);
+  const half2v hi_a = __builtin_bit_cast(half2v, (u & 0x00F000F0u) | 0x64006400u);
+  const half2v hi_b = __builtin_bit_cast(half2v, (t8 & 0x00F000F0u) | 0x64006400u);
+  const half2v off_lo = {static_cast<_Float16>(OFF_LO), static_cast<_Float16>(OFF_LO)};
+  const half2v off_hi = {static_cast<_Float16>(OFF_HI), static_cast<_Float16>(OFF_HI)};
+  const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+  const half2v r0 = lo_a + off_lo;                       // exact: integers below 2048
+  const half2v r1 = lo_b + off_lo;
+  const half2v r2 = __builtin_elementwise_fma(hi_a, sixteenth, off_hi);  // (1024 + 16q)/16 exact
+  const half2v r3 = __builtin_elementwise_fma(hi_b, sixteenth, off_hi);
+  half8 out;
+  out[0] = r0[0]; out[1] = r0[1]; out[2] = r1[0]; out[3] = r1[1];
+  out[4] = r2[0]; out[5] = r2[1]; out[6] = r3[0]; out[7] = r3[1];
+  return out;
+}
+
+// int8 quants q[8g .. 8g+7] (two dwords) -> fp16: bytes moved into the low
+// half of each 16-bit lane with v_perm, (b ^ 0x80) | 0x6400 = 1024 + q + 128,
+// minus 1152.
+__device__ __forceinline__ half8 unpack_q8(uint32_t u0, uint32_t u1) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  const half2v off = {static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
+  half8 out;
+  const uint32_t w[2] = {u0, u1};
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    // selector bytes: 0x0c gives 0x00
+    const uint32_t p0 = __builtin_amdgcn_perm(0u, w[i], 0x0c010c00u) ^ 0x64806480u;  // bytes 0, 1
+    const uint32_t p1 = __builtin_amdgcn_perm(0u, w[i], 0x0c030c02u) ^ 0x64806480u;  // bytes 2, 3
+    const half2v a = __builtin_bit_cast(half2v, p0) + off;
+    const half2v b = __builtin_bit_cast(half2v, p1) + off;
+    out[4 * i + 0] = a[0]; out[4 * i + 1] = a[1]; out[4 * i + 2] = b[0]; out[4 * i + 3] = b[1];
+  }
+  return out;
+}
+
+// Global -> LDS copies (global_load_lds): lane l's 16 (or 4) bytes at
+// base + voff land at LDS address lds + 16 l (4 l).  Issued through inline asm
+// so that the compiler does not treat them as pending LDS writes (it would
+// otherwise wait for every copy in flight before each LDS read); completion
+// is tracked explicitly with wait_vmcnt.  M0 is written here; the compiler
+// sets M0 itself before any instruction of its own that reads it.
+__device__ __forceinline__ void copy16_to_lds(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+               : "memory");
+}
+__device__ __forceinline__ void copy4_to_lds(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+               : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  // generic -> LDS address space (an address-space cast), then its 32-bit address
+  return static_cast<uint32_t>((uintptr_t)((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------- GEMM
+// Y (or split-K partial plane blockIdx.y) for one 128 x 256 tile over blocks
+// [kb0, kb1).  Grid: x = tiles (XCD-grouped order), y = K splits.
+template <int TYPE>
+__global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
+    const uint8_t* __restrict__ W, const _Float16* __restrict__ frag, const float* __restrict__ rscale,
+    const float* __restrict__ bsum, float* __restrict__ y, int n_tokens, int n_rows, int nb,
+    int blocks_per_split, int tiles_n, int n_tiles) {
+  constexpr int TS = TFmt<TYPE>::TS, QOFF = TFmt<TYPE>::QOFF, DWB = TFmt<TYPE>::DWB;
+  constexpr int BSTAGE = b_stage_bytes<TYPE>();
+  constexpr int STAGE = stage_bytes<TYPE>();
+  constexpr int A_DMA = A_STAGE / FRAG / TWAVES;                    // 4 per wave
+  constexpr int B_DMA = b_dma_per_wave<TYPE>();
+  constexpr int S_DMA = TYPE == WH_TYPE_Q4_1 ? 1 : 0;
+  constexpr int PER_STAGE = A_DMA + B_DMA + S_DMA;                  // vmcnt per stage
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave / WGN) * WTM;   // token offset of the wave tile
+  const int wn = (wave % WGN) * WTN;   // row offset of the wave tile
+
+  // tile index: tiles resident on one XCD (workgroup id mod 8) are consecutive
+  const int bid = blockIdx.x;
+  const int q = n_tiles / 8, rem = n_tiles % 8;
+  const int xcd = bid % 8, local = bid / 8;
+  const int L = xcd * q + min(xcd, rem) + local;
+  const int T = L / tiles_n, R = L % tiles_n;
+  const int t0 = T * TBM, r0 = R * TBN;
+
+  const int kb0 = blockIdx.y * blocks_per_split;
+  const int kb1 = min(nb, kb0 + blocks_per_split);
+  const int n_stages = (kb1 - kb0) / SB;
+  const size_t row_bytes = static_cast<size_t>(nb) * TS;
+
+  // Byte offset (from W) of each raw weight dword this lane copies per stage:
+  // dword gi of the stage's [row][DWB] chunk; rows past the end re-read the
+  // last row, and copies past the chunk (gi >= TBN * DWB, the rounding of the
+  // last instruction) land in the slot's tail, which is never read.  Offsets
+  // fit 32 bits (checked by the launcher).
+  uint32_t b_off[B_DMA];
+#pragma unroll
+  for (int c = 0; c < B_DMA; c++) {
+    const int gi = min(static_cast<int>(threadIdx.x) + TWAVES * 64 * c, TBN * DWB - 1);
+    const int row = min(r0 + gi / DWB, n_rows - 1);
+    b_off[c] = static_cast<uint32_t>(static_cast<size_t>(row) * row_bytes) + 4u * static_cast<uint32_t>(gi % DWB);
+  }
+  const uint32_t smem_base = lds_addr(smem);
+
+  auto issue = [&](int st) {
+    if (st >= n_stages) return;
+    const uint32_t slot = smem_base + (st % NSTAGE) * STAGE;
+    const int kb = kb0 + st * SB;
+    // activation fragments: this wave copies fragments [8 wave, 8 wave + 8) of
+    // the stage (block j = fi / 16; group and limb = fi % 16)
+#pragma unroll
+    for (int f = 0; f < A_DMA; f++) {
+      const int fi = wave * A_DMA + f;
+      const int j = fi >> 4;
+      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * 16 + (fi & 15)) * FRAG) + 16u * lane;
+      copy16_to_lds(frag, off, slot + fi * FRAG);
+    }
+    const uint32_t bslot = slot + A_STAGE;
+    const uint32_t kboff = static_cast<uint32_t>(kb) * TS;
+#pragma unroll
+    for (int c = 0; c < B_DMA; c++) copy4_to_lds(W, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
+    if constexpr (TYPE == WH_TYPE_Q4_1) {
+      // block sums [SB][128] of this token tile: 1 KiB = 64 chunks of 16 B,
+      // 8 per wave, copied by lanes 0..7 (one instruction per wave)
+      const int li = wave * 8 + lane;
+      const int j = li >> 5, c = li & 31;
+      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * TBM + 4 * c) * 4);
+      if (lane < 8) copy16_to_lds(bsum, off, slot + A_STAGE + BSTAGE + 128 * wave);
+    }
+  };
+
+  float4v acc[IT][NT];
+#pragma unroll
+  for (int i = 0; i < IT; i++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[i][n] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  const int g = lane >> 4;       // k-group
+  const int ln = lane & 15;      // token (A) / weight row (B) within a 16-tile
+
+  issue(0);
+  issue(1);
+  for (int st = 0; st < n_stages; st++) {
+    // stage st landed (this wave's copies): stage st + 1 may still be in flight
+    if (st + 1 < n_stages) wait_vmcnt<PER_STAGE>(); else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();   // every wave's copies of stage st are in LDS
+    issue(st + 2);                  // into the slot of stage st - 1, which all waves finished
+    const uint8_t* slot = smem + (st % NSTAGE) * STAGE;
+    const uint8_t* bslot = slot + A_STAGE;
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+      half8 ah[IT], al[IT];
+#pragma unroll
+      for (int i = 0; i < IT; i++) {
+        const int grp = (wm >> 4) + i;
+        ah[i] = *reinterpret_cast<const half8*>(slot + (j * 16 + 2 * grp) * FRAG + 16 * lane);
+        al[i] = *reinterpret_cast<const half8*>(slot + (j * 16 + 2 * grp + 1) * FRAG + 16 * lane);
+      }
+      float4v sx[IT];
+      if constexpr (TYPE == WH_TYPE_Q4_1) {
+        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * TBM;
+#pragma unroll
+        for (int i = 0; i < IT; i++) sx[i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
+      }
+      // Software pipeline over the row groups: the MFMAs of group n + 1 are
+      // issued before the block-scale FMAs of group n, so the matrix pipe and
+      // the VALU work on independent data; each group's weight bytes are read
+      // from LDS one group ahead.
+      auto load_w = [&](int n, uint32_t& u0, uint32_t& u1, uint32_t& dm) {
+        const int row = wn + 16 * n + ln;
+        const uint8_t* rb = bslot + row * (DWB * 4) + j * TS;     // this block's bytes
+        const uint16_t* r16 = reinterpret_cast<const uint16_t*>(rb);
+        if constexpr (TYPE == WH_TYPE_Q8_0) {
+          const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rb + QOFF + 8 * g);
+          u0 = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
+          u1 = static_cast<uint32_t>(q16[2]) | (static_cast<uint32_t>(q16[3]) << 16);
+        } else {
+          const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rb + QOFF + 4 * g);
+          u0 = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
+          u1 = 0u;
+        }
+        dm = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
+                                  : static_cast<uint32_t>(r16[0]);
+      };
+      auto mfmas = [&](uint32_t u0, uint32_t u1, float4v* c) {
+        half8 bw;
+        if constexpr (TYPE == WH_TYPE_Q8_0) bw = unpack_q8(u0, u1);
+        else bw = unpack_q4<TYPE>(u0);
+#pragma unroll
+        for (int i = 0; i < IT; i++) c[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < IT; i++) c[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw, c[i], 0, 0, 0);
+      };
+      auto scale = [&](int n, uint32_t dm, const float4v* c) {
+        // d in an f32 register: the FMAs below are then plain v_fmac_f32
+        // (VOP2) instead of mixed-precision v_fma_mix_f32 (VOP3P, slower)
+        float d = whd::f16_bits_to_f32(dm & 0xFFFFu);
+        asm("" : "+v"(d));
+        const float mm = TYPE == WH_TYPE_Q4_1 ? whd::f16_bits_to_f32(dm >> 16) : 0.f;
+#pragma unroll
+        for (int i = 0; i < IT; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float v = __builtin_fmaf(d, c[i][r], acc[i][n][r]);
+            if constexpr (TYPE == WH_TYPE_Q4_1) v = __builtin_fmaf(mm, sx[i][r], v);
+            acc[i][n][r] = v;
+          }
+      };
+      float4v cc[2][IT];
+      uint32_t wq0[2], wq1[2], wdm[2];
+      load_w(0, wq0[0], wq1[0], wdm[0]);
+      load_w(1, wq0[1], wq1[1], wdm[1]);
+      mfmas(wq0[0], wq1[0], cc[0]);
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        const int cur = n & 1, nxt = cur ^ 1;
+        const uint32_t dm_n = wdm[cur];
+        if (n + 1 < NT) {
+          mfmas(wq0[nxt], wq1[nxt], cc[nxt]);
+          if (n + 2 < NT) load_w(n + 2, wq0[cur], wq1[cur], wdm[cur]);
+        }
+        scale(n, dm_n, cc[cur]);
+      }
+    }
+  }
+
+  // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
+  float* out = y + static_cast<size_t>(blockIdx.y) * n_tokens * n_rows;
+#pragma unroll
+  for (int i = 0; i < IT; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int t = t0 + wm + 16 * i + 4 * g + r;
+      if (t >= n_tokens) continue;
+      const float sc = rscale[t];
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        const int row = r0 + wn + 16 * n + ln;
+        if (row < n_rows) out[static_cast<size_t>(t) * n_rows + row] = acc[i][n][r] * sc;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                  size_t n, float* __restrict__ y) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float v = part[i];
+    for (int s = 1; s < splits; s++) v += part[static_cast<size_t>(s) * n + i];
+    y[i] = v;
+  }
+}
+
+template <int TYPE>
+int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
+                 const float* rs, const float* bs, float* part, int splits, hipStream_t s) {
+  const int nb = static_cast<int>(k / 32);
+  const int tiles_n = static_cast<int>((n_rows + TBN - 1) / TBN);
+  const int tiles_m = static_cast<int>((n_tokens + TBM - 1) / TBM);
+  int bps = (nb + splits - 1) / splits;
+  bps = (bps + SB - 1) / SB * SB;
+  const size_t lds = static_cast<size_t>(NSTAGE) * stage_bytes<TYPE>();
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
+  gemm_tiled_kernel<TYPE><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, part, static_cast<int>(n_tokens),
+                                                       static_cast<int>(n_rows), nb, bps, tiles_n,
+                                                       tiles_m * tiles_n);
+  WH_LAUNCH_CHECK("tiled gemm kernel launch");
+  return WH_OK;
+}
+
+size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+}  // namespace
+
+namespace wh {
+
+// The tiled kernel needs whole block pairs per row (k % 64 == 0), 4-byte
+// aligned rows and weights, and an LDS budget the device provides.
+bool gemm_tiled_ok(int type, const void* w, size_t k) {
+  const size_t ts = type_size(type);
+  if (ts == 0 || k == 0 || k % 64 != 0 || !aligned(w, 4) || ((k / 32) * ts) % 4 != 0) return false;
+  const size_t lds = NSTAGE * static_cast<size_t>(
+      type == WH_TYPE_Q4_0 ? stage_bytes<WH_TYPE_Q4_0>()
+                           : (type == WH_TYPE_Q4_1 ? stage_bytes<WH_TYPE_Q4_1>() : stage_bytes<WH_TYPE_Q8_0>()));
+  return lds <= max_lds_per_block();
+}
+
+int gemm_tiled_splits(size_t n_rows, size_t n_tokens, size_t k) {
+  const size_t tiles = ((n_rows + TBN - 1) / TBN) * ((n_tokens + TBM - 1) / TBM);
+  const size_t nb = k / 32;
+  const size_t cus = static_cast<size_t>(cu_count());
+  int s = 1;
+  while (s < 8 && tiles * s * 2 <= cus && nb / (2 * s) >= 32) s *= 2;
+  return s;
+}
+
+size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
+  const size_t tm = (n_tokens + TBM - 1) / TBM * TBM;   // padded tokens
+  size_t b = al256(tm * k * 4) + al256(tm * 4);
+  if (type == WH_TYPE_Q4_1) b += al256(tm * (k / 32) * 4);
+  const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
+  if (splits > 1) b += al256(static_cast<size_t>(splits) * n_rows * n_tokens * 4);
+  return b;
+}
+
+int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
+                      float* y, void* workspace, hipStream_t s) {
+  const size_t tm = (n_tokens + TBM - 1) / TBM * TBM;
+  char* ws = static_cast<char*>(workspace);
+  _Float16* frag = reinterpret_cast<_Float16*>(ws);
+  ws += al256(tm * k * 4);
+  float* rs = reinterpret_cast<float*>(ws);
+  ws += al256(tm * 4);
+  float* bs = nullptr;
+  if (type == WH_TYPE_Q4_1) {
+    bs = reinterpret_cast<float*>(ws);
+    ws += al256(tm * (k / 32) * 4);
+  }
+  const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
+  float* part = splits > 1 ? reinterpret_cast<float*>(ws) : y;
+  pack_a_kernel<<<static_cast<unsigned>(tm), 256, 0, s>>>(x, static_cast<int>(n_tokens), static_cast<int>(k),
+                                                          type, frag, rs, bs);
+  WH_LAUNCH_CHECK("pack kernel launch");
+  const uint8_t* wp = static_cast<const uint8_t*>(w);
+  int st;
+  switch (type) {
+    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
+    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
+    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
+    default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
+  }
+  if (st != WH_OK) return st;
+  if (splits > 1) {
+    const size_t n = n_rows * n_tokens;
+    size_t gsz = (n + 255) / 256;
+    const size_t cap = static_cast<size_t>(cu_count()) * 8;
+    if (gsz > cap) gsz = cap;
+    tiled_splitk_reduce_kernel<<<static_cast<unsigned>(gsz), 256, 0, s>>>(part, splits, n, y);
+    WH_LAUNCH_CHECK("split-K reduce launch");
+  }
+  return WH_OK;
+}
+
+}  // namespace wh
