@@ -457,8 +457,19 @@ WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps,
   void* gemm_ws = ws;
   const size_t gemm_bytes = need - static_cast<size_t>(ws - static_cast<char*>(workspace));
   hipStream_t s = hs(stream);
-  if ((st = wh::launch_rms_norm(x, gamma, eps, m, H, xh, s))) return st;
   if (F == 0) return wh::launch_fill_bytes(out, 0, m * H * sizeof(float), s);
+  if (m <= wh::kGemvTokenLimit) {
+    // decode: RMSNorm, gate, up and SwiGLU in one streaming kernel per token,
+    // then the down GEMV; the unfused sequence below when the layout does not fit
+    bool fused = true;
+    for (size_t t = 0; t < m && fused; t++) {
+      st = wh::launch_ffn_gate_up(w->type, w->gate, w->up, x + t * H, gamma, eps, h + t * F, F, H, s);
+      if (st == WH_ERR_INVALID_SHAPE) fused = false;
+      else if (st) return st;
+    }
+    if (fused) return wh::launch_gemm(w->type, w->down, H, F, h, m, out, gemm_ws, gemm_bytes, s);
+  }
+  if ((st = wh::launch_rms_norm(x, gamma, eps, m, H, xh, s))) return st;
   if ((st = wh::launch_gemm(w->type, w->gate, F, H, xh, m, g, gemm_ws, gemm_bytes, s))) return st;
   if ((st = wh::launch_gemm(w->type, w->up, F, H, xh, m, u, gemm_ws, gemm_bytes, s))) return st;
   if ((st = wh::launch_swiglu(g, u, m * F, h, s))) return st;

@@ -241,9 +241,17 @@ __device__ __forceinline__ void load_vec(const uint32_t* __restrict__ src, bool 
   for (int c = 0; c < V; c++) dst[c] = ok ? __builtin_nontemporal_load(src + c) : 0u;
 }
 
-template <int TYPE>
+// FFN = true: the FFN's first half for one token (the decode step): x is
+// RMS-normalised with gamma while staged (rms = sqrt(sum x^2 / K + eps),
+// x_hat = (x / rms) * gamma, tensor_utils.rs:446-480), the gate row (W) and
+// the up row (W2) of every output index are streamed side by side, and
+// y = silu(gate . x_hat) * (up . x_hat) (tensor_utils.rs:512-532).
+template <int TYPE, bool FFN>
 __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t* __restrict__ W,
+                                                                  const uint8_t* __restrict__ W2,
                                                                   const float* __restrict__ x,
+                                                                  const float* __restrict__ gamma,
+                                                                  float eps,
                                                                   float* __restrict__ y, int n_rows,
                                                                   int pairs_per_row, int ks,
                                                                   int rows_per_wg) {
@@ -252,11 +260,12 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   constexpr int V = LoadFmt<TYPE>::V;
   constexpr int NV = LoadFmt<TYPE>::NV;
   constexpr int SLAB = DW * 64 + 4;
+  constexpr int NM = FFN ? 2 : 1;                           // weight matrices streamed
   extern __shared__ __align__(16) uint32_t lds[];
   const int K = pairs_per_row * 64;
   float* xs = reinterpret_cast<float*>(lds);                // x, 4 floats of padding per 64
-  uint32_t* slabs = lds + K + K / 16;                       // kWaves slabs of SLAB dwords
-  float* red = reinterpret_cast<float*>(slabs + kWaves * SLAB);
+  uint32_t* slabs = lds + K + K / 16;                       // kWaves * NM slabs of SLAB dwords
+  float* red = reinterpret_cast<float*>(slabs + kWaves * NM * SLAB);  // NM * kWaves partials
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -270,18 +279,24 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   const int r1 = min(n_rows, r0 + rows_per_wg);
   const int nk = (r1 - r0 + groups - 1) / groups;           // row steps (uniform in the WG)
   const size_t row_bytes = static_cast<size_t>(pairs_per_row) * PB;
-  const uint8_t* slice_base = W + static_cast<size_t>(64 * s) * PB;
+  const uint8_t* slice_base[NM];
+  slice_base[0] = W + static_cast<size_t>(64 * s) * PB;
+  if constexpr (FFN) slice_base[NM - 1] = W2 + static_cast<size_t>(64 * s) * PB;
 
   // Prefetch the first rows before anything else.
-  uint32_t buf[kPrefetch][DW];
-  auto fetch = [&](uint32_t* dst, int k) {
+  uint32_t buf[kPrefetch][NM][DW];
+  auto fetch = [&](uint32_t (*dst)[DW], int k) {
     const int row = r0 + g + k * groups;
     const bool rok = k < nk && row < r1;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(slice_base + static_cast<size_t>(row) * row_bytes);
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-      const int e = V * (64 * i + lane);
-      load_vec<V>(src + e, rok && e < nd, dst + V * i);
+    for (int mtx = 0; mtx < NM; mtx++) {
+      const uint32_t* src =
+          reinterpret_cast<const uint32_t*>(slice_base[mtx] + static_cast<size_t>(row) * row_bytes);
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        const int e = V * (64 * i + lane);
+        load_vec<V>(src + e, rok && e < nd, dst[mtx] + V * i);
+      }
     }
   };
 #pragma unroll
@@ -294,6 +309,26 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
     *reinterpret_cast<float4*>(xs + e + (e >> 6) * 4) = t;
   }
   __syncthreads();
+  if constexpr (FFN) {
+    // RMSNorm of the staged x: fixed-shape reduction, then x_hat in place.
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+      const float v = xs[i + (i >> 6) * 4];
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = whd::wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) total += red[w];
+    const float rms = sqrtf(total / static_cast<float>(K) + eps);
+    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+      float* p = xs + i + (i >> 6) * 4;
+      *p = (*p / rms) * gamma[i];
+    }
+    __syncthreads();
+  }
   float xv[64];
   {
     const int p = 64 * s + (active ? lane : 0);
@@ -319,42 +354,57 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   bool exact = false;
   if constexpr (TYPE != WH_TYPE_Q8_0) exact = __any(!(__builtin_isfinite(xa) && __builtin_isfinite(xb)));
 
-  uint32_t* slab = slabs + wave * SLAB;
+  uint32_t* slab = slabs + wave * NM * SLAB;
+  // y = silu(g) * u, the SiLU in the reference's form g * (1 / (1 + exp(-g)))
+  auto combine = [](float gv, float uv) { return FFN ? (gv * (1.0f / (1.0f + expf(-gv)))) * uv : gv; };
   for (int kb = 0; kb < nk; kb += kPrefetch) {
 #pragma unroll
     for (int d = 0; d < kPrefetch; d++) {
       const int k = kb + d;
       if (k >= nk) break;
       const int row = r0 + g + k * groups;
-      // this row's slice -> LDS slab (dword e of the slice at slab[e])
+      // this row's slice(s) -> LDS slab(s) (dword e of a slice at slab[e])
 #pragma unroll
-      for (int i = 0; i < NV; i++)
+      for (int mtx = 0; mtx < NM; mtx++)
 #pragma unroll
-        for (int c = 0; c < V; c++) slab[V * (64 * i + lane) + c] = buf[d][V * i + c];
+        for (int i = 0; i < NV; i++)
+#pragma unroll
+          for (int c = 0; c < V; c++) slab[mtx * SLAB + V * (64 * i + lane) + c] = buf[d][mtx][V * i + c];
       fetch(buf[d], k + kPrefetch);
       __builtin_amdgcn_wave_barrier();
-      uint32_t w[DW];
+      float tot[NM];
 #pragma unroll
-      for (int j = 0; j < DW; j++) w[j] = slab[DW * lane + j];
-      __builtin_amdgcn_wave_barrier();
-      float part = 0.f;
-      if (active) {
-        if constexpr (TYPE == WH_TYPE_Q8_0) {
-          part = pair_dot<TYPE>(w, xv, xa, xb);
-        } else {
-          part = exact ? pair_dot_exact<TYPE>(w, xv) : pair_dot<TYPE>(w, xv, xa, xb);
+      for (int mtx = 0; mtx < NM; mtx++) {
+        uint32_t w[DW];
+#pragma unroll
+        for (int j = 0; j < DW; j++) w[j] = slab[mtx * SLAB + DW * lane + j];
+        float part = 0.f;
+        if (active) {
+          if constexpr (TYPE == WH_TYPE_Q8_0) {
+            part = pair_dot<TYPE>(w, xv, xa, xb);
+          } else {
+            part = exact ? pair_dot_exact<TYPE>(w, xv) : pair_dot<TYPE>(w, xv, xa, xb);
+          }
         }
+        tot[mtx] = wave_sum_to_lane63(part);
       }
-      const float tot = wave_sum_to_lane63(part);
+      __builtin_amdgcn_wave_barrier();
       if (ks == 1) {
-        if (lane == 63 && row < r1) y[row] = tot;
+        if (lane == 63 && row < r1) y[row] = combine(tot[0], tot[NM - 1]);
       } else {
-        if (lane == 63) red[wave] = tot;
+        if (lane == 63) {
+#pragma unroll
+          for (int mtx = 0; mtx < NM; mtx++) red[mtx * kWaves + wave] = tot[mtx];
+        }
         __syncthreads();
         if (s == 0 && lane == 63 && row < r1) {
-          float t = red[g * ks];
-          for (int s2 = 1; s2 < ks; s2++) t += red[g * ks + s2];
-          y[row] = t;
+          float t[NM];
+#pragma unroll
+          for (int mtx = 0; mtx < NM; mtx++) {
+            t[mtx] = red[mtx * kWaves + g * ks];
+            for (int s2 = 1; s2 < ks; s2++) t[mtx] += red[mtx * kWaves + g * ks + s2];
+          }
+          y[row] = combine(t[0], t[NM - 1]);
         }
         __syncthreads();
       }
@@ -362,9 +412,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   }
 }
 
-size_t stream_lds_bytes(int type, int K) {
+size_t stream_lds_bytes(int type, int K, int nm) {
   const int dw = type == WH_TYPE_Q4_0 ? 9 : (type == WH_TYPE_Q4_1 ? 10 : 17);
-  return 4u * static_cast<size_t>(K + K / 16 + kWaves * (dw * 64 + 4) + kWaves);
+  return 4u * static_cast<size_t>(K + K / 16 + nm * kWaves * (dw * 64 + 4) + nm * kWaves);
 }
 
 template <int TYPE>
@@ -390,36 +440,51 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
   }
 }
 
+// Chooses the streaming kernel when its layout conditions hold (an even
+// number of blocks per row, at most 4 K-slices, 4-byte aligned weights,
+// 16-byte aligned x, LDS within the device limit).
+template <int TYPE, bool FFN>
+bool stream_ok(const uint8_t* w, const uint8_t* w2, const float* x, size_t n_rows, size_t k) {
+  const size_t nb = k / 32;
+  const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k), FFN ? 2 : 1);
+  return (nb % 2 == 0) && nb > 0 && nb / 2 <= 64 * kMaxSlices && wh::aligned(w, 4) &&
+         (!FFN || wh::aligned(w2, 4)) && wh::aligned(x, 16) && n_rows < (1u << 30) &&
+         lds <= wh::max_lds_per_block();
+}
+
+template <int TYPE, bool FFN>
+int launch_stream(const uint8_t* w, const uint8_t* w2, const float* x, const float* gamma, float eps,
+                  float* y, size_t n_rows, size_t k, hipStream_t s) {
+  const int cus = wh::cu_count();
+  const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k), FFN ? 2 : 1);
+  const int P = static_cast<int>(k / 64);
+  int ks = (P + 63) / 64;
+  if (ks == 3) ks = 4;
+  const int groups = kWaves / ks;
+  const size_t max_wg = (n_rows + groups - 1) / groups;
+  const int grid = static_cast<int>(max_wg < static_cast<size_t>(cus) ? max_wg : cus);
+  const int rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
+  if (lds > 65536) {
+    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE, FFN>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  }
+  gemv_stream_kernel<TYPE, FFN><<<grid, kWaves * 64, lds, s>>>(w, w2, x, gamma, eps, y,
+                                                               static_cast<int>(n_rows), P, ks, rows_per_wg);
+  WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
+  return WH_OK;
+}
+
 template <int TYPE>
 int launch_typed(const uint8_t* w, const float* x, float* y, size_t n_rows, size_t k,
                  hipStream_t s) {
+  if (stream_ok<TYPE, false>(w, nullptr, x, n_rows, k))
+    return launch_stream<TYPE, false>(w, nullptr, x, nullptr, 0.f, y, n_rows, k, s);
   const size_t nb = k / 32;
-  const int cus = wh::cu_count();
-  const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k));
-  const bool fast = (nb % 2 == 0) && nb > 0 && nb / 2 <= 64 * kMaxSlices && wh::aligned(w, 4) &&
-                    wh::aligned(x, 16) && n_rows < (1u << 30) && lds <= wh::max_lds_per_block();
-  if (fast) {
-    const int P = static_cast<int>(nb / 2);
-    int ks = (P + 63) / 64;
-    if (ks == 3) ks = 4;
-    const int groups = kWaves / ks;
-    const size_t max_wg = (n_rows + groups - 1) / groups;
-    const int grid = static_cast<int>(max_wg < static_cast<size_t>(cus) ? max_wg : cus);
-    const int rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
-    if (lds > 65536) {
-      WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds)));
-    }
-    gemv_stream_kernel<TYPE><<<grid, kWaves * 64, lds, s>>>(w, x, y, static_cast<int>(n_rows), P,
-                                                            ks, rows_per_wg);
-  } else {
-    size_t grid = (n_rows + 3) / 4;
-    const size_t cap = static_cast<size_t>(cus) * 16;
-    if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
-    gemv_generic_kernel<TYPE><<<static_cast<unsigned>(grid), 256, 0, s>>>(w, x, y, n_rows, nb);
-  }
+  size_t grid = (n_rows + 3) / 4;
+  const size_t cap = static_cast<size_t>(wh::cu_count()) * 16;
+  if (grid > cap) grid = cap;
+  if (grid < 1) grid = 1;
+  gemv_generic_kernel<TYPE><<<static_cast<unsigned>(grid), 256, 0, s>>>(w, x, y, n_rows, nb);
   WH_LAUNCH_CHECK("gemv kernel launch");
   return WH_OK;
 }
@@ -427,6 +492,29 @@ int launch_typed(const uint8_t* w, const float* x, float* y, size_t n_rows, size
 }  // namespace
 
 namespace wh {
+
+// The FFN's first half for one token, fused (see gemv_stream_kernel<., true>):
+// h = silu(W_gate x_hat) * (W_up x_hat), x_hat = rms_norm(x, gamma, eps).
+// Returns WH_ERR_INVALID_SHAPE without launching when the fused kernel's
+// layout conditions do not hold; the caller then runs the unfused sequence.
+int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x, const float* gamma,
+                       float eps, float* h, size_t n_ff, size_t hidden, hipStream_t s) {
+  const uint8_t* g = static_cast<const uint8_t*>(gate);
+  const uint8_t* u = static_cast<const uint8_t*>(up);
+  switch (type) {
+    case WH_TYPE_Q4_0:
+      if (!stream_ok<WH_TYPE_Q4_0, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q4_0, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+    case WH_TYPE_Q4_1:
+      if (!stream_ok<WH_TYPE_Q4_1, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q4_1, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+    case WH_TYPE_Q8_0:
+      if (!stream_ok<WH_TYPE_Q8_0, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q8_0, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+    default:
+      return WH_ERR_INVALID_SHAPE;
+  }
+}
 
 int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k,
                 hipStream_t s) {

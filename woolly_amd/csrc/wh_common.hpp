@@ -56,6 +56,11 @@ int launch_dequantize(int type, const void* data, size_t nelements, float* out,
 int launch_fill_bytes(void* dst, int value, size_t nbytes, hipStream_t stream);
 int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows,
                 size_t k, hipStream_t stream);
+// FFN gate/up for one token with RMSNorm and SwiGLU fused into the streaming
+// GEMV; WH_ERR_INVALID_SHAPE (nothing launched) when its layout does not fit.
+int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x,
+                       const float* gamma, float eps, float* h, size_t n_ff, size_t hidden,
+                       hipStream_t stream);
 // Token counts up to this use one streaming GEMV per token instead of MFMA.
 constexpr size_t kGemvTokenLimit = 2;
 size_t gemm_workspace_bytes(int type, size_t n_tokens, size_t k);
