@@ -412,6 +412,200 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   }
 }
 
+// ---------------------------------------------------------------------------
+// Ring kernel: same work split and arithmetic as gemv_stream_kernel, but each
+// wave's row slices are copied global -> LDS with global_load_lds_dwordx4
+// (lane l's 16 bytes land at slot + 16 l) into a wave-private ring of RD
+// slots, RD - 1 rows ahead of the row being computed.  No VGPRs hold the
+// prefetched rows and no LDS stores are issued for them.  The copies are
+// issued through inline asm (the compiler would otherwise wait for every copy
+// in flight before each LDS read); every wave issues exactly NI copies per
+// matrix per row, so completion is tracked with a constant vmcnt.
+__device__ __forceinline__ void ring_copy16(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void ring_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>((uintptr_t)((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+template <int TYPE>
+constexpr int ring_ni() { return (PairFmt<TYPE>::DW * 64 * 4 + 1023) / 1024; }  // copies per full slice
+
+template <int TYPE, bool FFN, int RD>
+__global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* __restrict__ W,
+                                                                const uint8_t* __restrict__ W2,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ gamma,
+                                                                float eps, float* __restrict__ y,
+                                                                int n_rows, int pairs_per_row, int ks,
+                                                                int rows_per_wg) {
+  constexpr int DW = PairFmt<TYPE>::DW;
+  constexpr int PB = PairFmt<TYPE>::BYTES;
+  constexpr int NM = FFN ? 2 : 1;
+  constexpr int NI = ring_ni<TYPE>();
+  constexpr int SLOT = DW * 64 * 4;                         // bytes per slot (a full slice)
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int K = pairs_per_row * 64;
+  float* xs = reinterpret_cast<float*>(lds);
+  uint8_t* ring = reinterpret_cast<uint8_t*>(lds + K + K / 16);      // kWaves * NM * RD slots
+  float* red = reinterpret_cast<float*>(ring + kWaves * NM * RD * SLOT);
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int s = wave % ks;
+  const int g = wave / ks;
+  const int groups = kWaves / ks;
+  const int ps = min(64, pairs_per_row - 64 * s);
+  const int nbytes = PB * ps;                               // bytes of one row slice (multiple of 16)
+  const bool active = lane < ps;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int r1 = min(n_rows, r0 + rows_per_wg);
+  const int nk = (r1 - r0 + groups - 1) / groups;
+  const uint32_t row_bytes = static_cast<uint32_t>(pairs_per_row) * PB;
+  const uint32_t slice_off = static_cast<uint32_t>(64 * s) * PB;
+  uint8_t* my_ring = ring + wave * NM * RD * SLOT;
+  const uint32_t ring_lds = lds_u32(my_ring);
+
+  // Copies of row step k into slot k % RD.  Rows past the range re-read the
+  // range's last row; in a slice's last copy instruction the lanes past the
+  // slice are masked off (lane 0 stays on and repeats the last chunk into the
+  // unused tail of the slot, so every wave issues the same number of copies).
+  const int nchunks = nbytes / 16;
+  auto issue = [&](int k) {
+    const int row = min(r0 + g + k * groups, r1 - 1);
+    const uint32_t base_off = static_cast<uint32_t>(row) * row_bytes + slice_off;
+#pragma unroll
+    for (int mtx = 0; mtx < NM; mtx++) {
+      const uint32_t slot = ring_lds + static_cast<uint32_t>((mtx * RD + (k % RD)) * SLOT);
+      const void* base = mtx ? static_cast<const void*>(W2) : static_cast<const void*>(W);
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        const int c = 64 * i + lane;
+        if (c < nchunks || lane == 0)
+          ring_copy16(base, base_off + 16u * static_cast<uint32_t>(min(c, nchunks - 1)), slot + 1024u * i);
+      }
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < RD - 1; d++)
+    if (d < nk) issue(d);
+
+  // Stage x in LDS once for the workgroup, then each lane copies its 64 values.
+  for (int i = threadIdx.x; i < K / 4; i += kWaves * 64) {
+    const float4 t = reinterpret_cast<const float4*>(x)[i];
+    const int e = 4 * i;
+    *reinterpret_cast<float4*>(xs + e + (e >> 6) * 4) = t;
+  }
+  __syncthreads();
+  if constexpr (FFN) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+      const float v = xs[i + (i >> 6) * 4];
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = whd::wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) total += red[w];
+    const float rms = sqrtf(total / static_cast<float>(K) + eps);
+    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+      float* p = xs + i + (i >> 6) * 4;
+      *p = (*p / rms) * gamma[i];
+    }
+    __syncthreads();
+  }
+  float xv[64];
+  {
+    const int p = 64 * s + (active ? lane : 0);
+    const float* xp = xs + 68 * p;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float4 t = *reinterpret_cast<const float4*>(xp + 4 * i);
+      xv[4 * i + 0] = active ? t.x : 0.f;
+      xv[4 * i + 1] = active ? t.y : 0.f;
+      xv[4 * i + 2] = active ? t.z : 0.f;
+      xv[4 * i + 3] = active ? t.w : 0.f;
+    }
+  }
+  float xa = 0.f, xb = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    xa += xv[i];
+    xb += xv[32 + i];
+  }
+  bool exact = false;
+  if constexpr (TYPE != WH_TYPE_Q8_0) exact = __any(!(__builtin_isfinite(xa) && __builtin_isfinite(xb)));
+
+  auto combine = [](float gv, float uv) { return FFN ? (gv * (1.0f / (1.0f + expf(-gv)))) * uv : gv; };
+  for (int k = 0; k < nk; k++) {
+    const int row = r0 + g + k * groups;
+    if (k + RD - 1 < nk) {
+      issue(k + RD - 1);                   // into the slot of step k - 1, already consumed
+      ring_wait<(RD - 1) * NM * NI>();     // the copies of steps k + 1 .. k + RD - 1 may be in flight
+    } else {
+      ring_wait<0>();
+    }
+    float tot[NM];
+#pragma unroll
+    for (int mtx = 0; mtx < NM; mtx++) {
+      const uint32_t* slot = reinterpret_cast<const uint32_t*>(my_ring + (mtx * RD + (k % RD)) * SLOT);
+      uint32_t w[DW];
+#pragma unroll
+      for (int j = 0; j < DW; j++) w[j] = slot[DW * (active ? lane : 0) + j];
+      float part = 0.f;
+      if (active) {
+        if constexpr (TYPE == WH_TYPE_Q8_0) {
+          part = pair_dot<TYPE>(w, xv, xa, xb);
+        } else {
+          part = exact ? pair_dot_exact<TYPE>(w, xv) : pair_dot<TYPE>(w, xv, xa, xb);
+        }
+      }
+      tot[mtx] = wave_sum_to_lane63(part);
+    }
+    if (ks == 1) {
+      if (lane == 63 && row < r1) y[row] = combine(tot[0], tot[NM - 1]);
+    } else {
+      if (lane == 63) {
+#pragma unroll
+        for (int mtx = 0; mtx < NM; mtx++) red[mtx * kWaves + wave] = tot[mtx];
+      }
+      // LDS-only barrier: a __syncthreads() here would also wait for the
+      // weight copies in flight
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (s == 0 && lane == 63 && row < r1) {
+        float t[NM];
+#pragma unroll
+        for (int mtx = 0; mtx < NM; mtx++) {
+          t[mtx] = red[mtx * kWaves + g * ks];
+          for (int s2 = 1; s2 < ks; s2++) t[mtx] += red[mtx * kWaves + g * ks + s2];
+        }
+        y[row] = combine(t[0], t[NM - 1]);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+  }
+  ring_wait<0>();  // no copy may land in LDS after the workgroup has exited
+}
+
+size_t ring_lds_bytes(int type, int K, int nm, int rd) {
+  const int dw = type == WH_TYPE_Q4_0 ? 9 : (type == WH_TYPE_Q4_1 ? 10 : 17);
+  return 4u * static_cast<size_t>(K + K / 16) + static_cast<size_t>(kWaves) * nm * rd * dw * 64 * 4 +
+         4u * nm * kWaves;
+}
+
 size_t stream_lds_bytes(int type, int K, int nm) {
   const int dw = type == WH_TYPE_Q4_0 ? 9 : (type == WH_TYPE_Q4_1 ? 10 : 17);
   return 4u * static_cast<size_t>(K + K / 16 + nm * kWaves * (dw * 64 + 4) + nm * kWaves);
@@ -452,6 +646,22 @@ bool stream_ok(const uint8_t* w, const uint8_t* w2, const float* x, size_t n_row
          lds <= wh::max_lds_per_block();
 }
 
+#ifndef WH_GEMV_RING
+#define WH_GEMV_RING 1
+#endif
+
+template <int TYPE, bool FFN, int RD>
+int launch_ring(const uint8_t* w, const uint8_t* w2, const float* x, const float* gamma, float eps,
+                float* y, size_t n_rows, size_t k, int grid, int ks, int rows_per_wg, size_t lds,
+                hipStream_t s) {
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_ring_kernel<TYPE, FFN, RD>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  gemv_ring_kernel<TYPE, FFN, RD><<<grid, kWaves * 64, lds, s>>>(w, w2, x, gamma, eps, y, static_cast<int>(n_rows),
+                                                                 static_cast<int>(k / 64), ks, rows_per_wg);
+  WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
+  return WH_OK;
+}
+
 template <int TYPE, bool FFN>
 int launch_stream(const uint8_t* w, const uint8_t* w2, const float* x, const float* gamma, float eps,
                   float* y, size_t n_rows, size_t k, hipStream_t s) {
@@ -464,6 +674,29 @@ int launch_stream(const uint8_t* w, const uint8_t* w2, const float* x, const flo
   const size_t max_wg = (n_rows + groups - 1) / groups;
   const int grid = static_cast<int>(max_wg < static_cast<size_t>(cus) ? max_wg : cus);
   const int rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
+  // Ring kernel: every K-slice a whole number of 16-byte chunks, 32-bit byte
+  // offsets, and a ring of at least two slots per wave within the LDS limit.
+  const int tail = P % 64;
+  const bool chunks_ok = (PairFmt<TYPE>::BYTES * 64) % 16 == 0 && (PairFmt<TYPE>::BYTES * tail) % 16 == 0;
+  // Measured on MI355X (14336 x 4096 and 4096 x 14336): the ring wins for
+  // Q8_0 (more bytes per row) and for the FFN's two matrices; the 4-bit
+  // single-matrix GEMV is bound by its unpacking arithmetic and keeps the
+  // register-staged kernel.
+  const bool ring_pays = TYPE == WH_TYPE_Q8_0 || FFN;
+  if (WH_GEMV_RING && ring_pays && chunks_ok &&
+      n_rows * (k / 64) * PairFmt<TYPE>::BYTES < (static_cast<size_t>(1) << 32)) {
+    const int nm = FFN ? 2 : 1;
+    const size_t maxl = wh::max_lds_per_block();
+    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 4) <= maxl)
+      return launch_ring<TYPE, FFN, 4>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
+                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 4), s);
+    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 3) <= maxl)
+      return launch_ring<TYPE, FFN, 3>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
+                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 3), s);
+    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 2) <= maxl)
+      return launch_ring<TYPE, FFN, 2>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
+                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 2), s);
+  }
   if (lds > 65536) {
     WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE, FFN>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
