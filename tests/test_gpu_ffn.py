@@ -54,7 +54,8 @@ def test_swiglu(gpu, orc):
 @pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1])
 @pytest.mark.parametrize("m,n,k", [(1, 64, 256), (2, 100, 4096), (4, 300, 4096), (8, 1024, 4096),
                                    (3, 512, 14336), (130, 200, 512), (64, 129, 4096),
-                                   (257, 384, 1024), (512, 256, 14336), (100, 96, 96)])
+                                   (257, 384, 1024), (512, 256, 14336), (100, 96, 96),
+                                   (17, 768, 4096), (32, 300, 2048), (33, 256, 1024), (16, 4096, 14336)])
 def test_matmul_parity(gpu, orc, t, m, n, k):
     print(f"[case] matmul type={t} m={m} n={n} k={k}", flush=True)
     w = synth.quantized_weight(t, n, k, seed=n + k)

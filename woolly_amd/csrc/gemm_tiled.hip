@@ -20,15 +20,16 @@
 //     halves = 1 KiB, lane l holding token 16i + l%16 and the 8 k-slots of
 //     k-group l/16.  The k-slots follow the order in which a weight lane
 //     unpacks its nibbles, so a straight copy feeds the MFMA.
-//   gemm_tiled_kernel: 512 threads, a 128-token x 256-row tile, each wave
-//     64 tokens x 64 rows (4 x 4 MFMA tiles), two waves per SIMD.  Stages of two blocks are
-//     copied global -> LDS with global_load_lds (activation fragments as
-//     16-byte lanes, raw weight bytes as 4-byte lanes); three stages rotate so
-//     that two are in flight while one is computed.  Each lane unpacks its
+//   gemm_tiled_kernel: 512 threads, a BM-token x 256-row tile (BM = 16, 32,
+//     64 or 128 from the token count, so small batches do not multiply
+//     padding), two waves per SIMD.  Stages of two blocks are copied
+//     global -> LDS with global_load_lds (activation fragments as 16-byte
+//     lanes, raw weight bytes as 4-byte lanes); NSTAGE stages rotate so that
+//     NSTAGE - 1 are in flight while one is computed.  Each lane unpacks its
 //     weight quants from LDS into fp16 with bit operations (magic-number
 //     conversion, exact), multiplies, and applies the block scale.
 //   Tiles are numbered so that the tiles resident on one XCD share a token
-//     tile: its 2 MiB of activation fragments stay in that XCD's L2.
+//     tile, whose activation fragments then stay in that XCD's L2.
 #include "wh_blocks.hpp"
 
 namespace {
@@ -37,17 +38,23 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int TBM = 128;              // tokens per tile
 constexpr int TBN = 256;              // weight rows per tile
-constexpr int WGM = 2, WGN = 4;       // wave grid (tokens x rows)
-constexpr int TWAVES = WGM * WGN;     // 8 waves, 2 per SIMD
-constexpr int WTM = TBM / WGM;        // wave tile: 64 tokens
-constexpr int WTN = TBN / WGN;        //            x 64 rows
-constexpr int IT = WTM / 16, NT = WTN / 16;  // 16 x 16 MFMA tiles per wave
+constexpr int TWAVES = 8;             // 2 per SIMD
 constexpr int SB = 2;                 // blocks per stage
-constexpr int NSTAGE = 3;
-constexpr int FRAG = 1024;            // bytes per activation fragment
-constexpr int A_STAGE = SB * 16 * FRAG;  // 2 blocks x (8 token groups x 2 limbs) fragments
+constexpr int FRAG = 1024;            // bytes per activation fragment (16 tokens x 32 k, one limb)
+
+// Wave grid per token-tile height BM: WGM x WGN waves, each a (BM / WGM) x
+// (TBN / WGN) tile of 16 x 16 MFMA tiles.
+template <int BM>
+struct TCfg {
+  static constexpr int WGM = BM == 128 ? 2 : 1;
+  static constexpr int WGN = TWAVES / WGM;
+  static constexpr int WTM = BM / WGM, WTN = TBN / WGN;
+  static constexpr int IT = WTM / 16, NT = WTN / 16;
+  static constexpr int FPB = BM / 8;                       // fragments per block (groups x limbs)
+  static constexpr int A_STAGE = SB * FPB * FRAG;
+  static constexpr int NSTAGE = BM <= 32 ? 4 : 3;
+};
 
 template <int TYPE>
 struct TFmt;
@@ -69,10 +76,12 @@ template <int TYPE>
 constexpr int b_dma_per_wave() { return (TBN * TFmt<TYPE>::DWB + TWAVES * 64 - 1) / (TWAVES * 64); }
 template <int TYPE>
 constexpr int b_stage_bytes() { return b_dma_per_wave<TYPE>() * TWAVES * 64 * 4; }
-template <int TYPE>
-constexpr int s_stage_bytes() { return TYPE == WH_TYPE_Q4_1 ? SB * TBM * 4 : 0; }
-template <int TYPE>
-constexpr int stage_bytes() { return A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE>(); }
+template <int TYPE, int BM>
+constexpr int s_stage_bytes() { return TYPE == WH_TYPE_Q4_1 ? SB * BM * 4 : 0; }
+template <int TYPE, int BM>
+constexpr int stage_bytes() { return TCfg<BM>::A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE, BM>(); }
+template <int TYPE, int BM>
+constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(TCfg<BM>::NSTAGE) * stage_bytes<TYPE, BM>(); }
 
 // Element (within a block) held by k-slot s of k-group g.  For the 4-bit
 // formats the order is that of unpack_q4 below; Q8_0 keeps natural order.
@@ -83,11 +92,12 @@ __device__ __forceinline__ int slot_elem(int type, int g, int s) {
 }
 
 // ---------------------------------------------------------------- packing
-// One workgroup per token row t of the padded tile grid.  Rows t >= n_tokens
-// are written as zeros.  rscale[t] = 2^e with max|x_t| * 2^-e in [2^13, 2^14);
-// bsum (Q4_1 only) = per-block sums of hi + lo, laid out [T][b][128].
+// One workgroup per token row t of the padded tile grid (token tiles of bm
+// rows).  Rows t >= n_tokens are written as zeros.  rscale[t] = 2^e with
+// max|x_t| * 2^-e in [2^13, 2^14); bsum (Q4_1 only) = per-block sums of
+// hi + lo, laid out [T][b][bm].
 __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, int n_tokens, int k,
-                                                     int type, _Float16* __restrict__ frag,
+                                                     int type, int bm, _Float16* __restrict__ frag,
                                                      float* __restrict__ rscale, float* __restrict__ bsum) {
   __shared__ float red[4];
   const int t = blockIdx.x;
@@ -111,7 +121,7 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
   const float down = ldexpf(1.f, -e);
   if (threadIdx.x == 0) rscale[t] = ldexpf(1.f, e);
   const int nb = k / 32;
-  const int T = t / TBM, i16 = (t % TBM) / 16, tl = t % 16;
+  const int T = t / bm, i16 = (t % bm) / 16, tl = t % 16, fpb = bm / 8;
   for (int p = threadIdx.x; p < nb * 4; p += 256) {  // (block, k-group) pairs
     const int b = p >> 2, g = p & 3;
     half8 hv, lv;
@@ -126,14 +136,14 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
       part += static_cast<float>(h) + static_cast<float>(l);
     }
     const int lane = 16 * g + tl;
-    const size_t base = ((static_cast<size_t>(T) * nb + b) * 16 + 2 * i16) * 512 + 8 * lane;
+    const size_t base = ((static_cast<size_t>(T) * nb + b) * fpb + 2 * i16) * 512 + 8 * lane;
     *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
     *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
     if (bsum) {
       // the four k-groups of a block are adjacent threads (p = 4b + g)
       part += __shfl_xor(part, 1, 64);
       part += __shfl_xor(part, 2, 64);
-      if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * TBM + (t % TBM)] = part;
+      if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
     }
   }
 }
@@ -215,26 +225,40 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---------------------------------------------------------------- GEMM
-// Y (or split-K partial plane blockIdx.y) for one 128 x 256 tile over blocks
+template <int N>
+__device__ __forceinline__ void wait_stages(int n) {  // at most n stages of N copies in flight
+  if (n >= 2) wait_vmcnt<2 * N>();
+  else if (n == 1) wait_vmcnt<N>();
+  else wait_vmcnt<0>();
+}
+
+// Y (or split-K partial plane blockIdx.y) for one BM x 256 tile over blocks
 // [kb0, kb1).  Grid: x = tiles (XCD-grouped order), y = K splits.
-template <int TYPE>
+template <int TYPE, int BM>
 __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint8_t* __restrict__ W, const _Float16* __restrict__ frag, const float* __restrict__ rscale,
     const float* __restrict__ bsum, float* __restrict__ y, int n_tokens, int n_rows, int nb,
     int blocks_per_split, int tiles_n, int n_tiles) {
+  using C = TCfg<BM>;
+  constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = C::NSTAGE;
+  constexpr int A_STAGE = C::A_STAGE;
   constexpr int TS = TFmt<TYPE>::TS, QOFF = TFmt<TYPE>::QOFF, DWB = TFmt<TYPE>::DWB;
   constexpr int BSTAGE = b_stage_bytes<TYPE>();
-  constexpr int STAGE = stage_bytes<TYPE>();
-  constexpr int A_DMA = A_STAGE / FRAG / TWAVES;                    // 4 per wave
+  constexpr int STAGE = stage_bytes<TYPE, BM>();
+  constexpr int A_FR = SB * FPB;                                    // fragments per stage
+  constexpr int A_DMA = (A_FR + TWAVES - 1) / TWAVES;               // copies per wave (wrapping)
   constexpr int B_DMA = b_dma_per_wave<TYPE>();
+  constexpr int S_CH = SB * BM / 4;                                 // Q4_1 block-sum chunks per stage
+  constexpr int S_PW = S_CH / TWAVES;                               // ... per wave (>= 1)
   constexpr int S_DMA = TYPE == WH_TYPE_Q4_1 ? 1 : 0;
   constexpr int PER_STAGE = A_DMA + B_DMA + S_DMA;                  // vmcnt per stage
+  static_assert((NSTAGE - 2) * PER_STAGE < 64, "vmcnt range");
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = (wave / WGN) * WTM;   // token offset of the wave tile
-  const int wn = (wave % WGN) * WTN;   // row offset of the wave tile
+  const int wm = (wave / C::WGN) * C::WTM;   // token offset of the wave tile
+  const int wn = (wave % C::WGN) * C::WTN;   // row offset of the wave tile
 
   // tile index: tiles resident on one XCD (workgroup id mod 8) are consecutive
   const int bid = blockIdx.x;
@@ -242,11 +266,11 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   const int xcd = bid % 8, local = bid / 8;
   const int L = xcd * q + min(xcd, rem) + local;
   const int T = L / tiles_n, R = L % tiles_n;
-  const int t0 = T * TBM, r0 = R * TBN;
+  const int t0 = T * BM, r0 = R * TBN;
 
   const int kb0 = blockIdx.y * blocks_per_split;
   const int kb1 = min(nb, kb0 + blocks_per_split);
-  const int n_stages = (kb1 - kb0) / SB;
+  const int n_stages = kb1 > kb0 ? (kb1 - kb0) / SB : 0;
   const size_t row_bytes = static_cast<size_t>(nb) * TS;
 
   // Byte offset (from W) of each raw weight dword this lane copies per stage:
@@ -267,13 +291,14 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     if (st >= n_stages) return;
     const uint32_t slot = smem_base + (st % NSTAGE) * STAGE;
     const int kb = kb0 + st * SB;
-    // activation fragments: this wave copies fragments [8 wave, 8 wave + 8) of
-    // the stage (block j = fi / 16; group and limb = fi % 16)
+    // activation fragments (block j = fi / FPB); when a stage has fewer
+    // fragments than A_DMA * TWAVES, some are copied twice (same data, same place)
 #pragma unroll
     for (int f = 0; f < A_DMA; f++) {
-      const int fi = wave * A_DMA + f;
-      const int j = fi >> 4;
-      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * 16 + (fi & 15)) * FRAG) + 16u * lane;
+      const int fi = (wave * A_DMA + f) % A_FR;
+      const int j = fi / FPB;
+      const uint32_t off =
+          static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * FPB + fi % FPB) * FRAG) + 16u * lane;
       copy16_to_lds(frag, off, slot + fi * FRAG);
     }
     const uint32_t bslot = slot + A_STAGE;
@@ -281,12 +306,12 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
 #pragma unroll
     for (int c = 0; c < B_DMA; c++) copy4_to_lds(W, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
     if constexpr (TYPE == WH_TYPE_Q4_1) {
-      // block sums [SB][128] of this token tile: 1 KiB = 64 chunks of 16 B,
-      // 8 per wave, copied by lanes 0..7 (one instruction per wave)
-      const int li = wave * 8 + lane;
-      const int j = li >> 5, c = li & 31;
-      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * TBM + 4 * c) * 4);
-      if (lane < 8) copy16_to_lds(bsum, off, slot + A_STAGE + BSTAGE + 128 * wave);
+      // block sums [SB][BM] of this token tile: S_CH chunks of 16 B, S_PW per
+      // wave, copied by lanes 0 .. S_PW - 1 (one instruction per wave)
+      const int ci = wave * S_PW + lane;
+      const int j = ci / (BM / 4), cc = ci % (BM / 4);
+      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * BM + 4 * cc) * 4);
+      if (lane < S_PW) copy16_to_lds(bsum, off, slot + A_STAGE + BSTAGE + 16 * S_PW * wave);
     }
   };
 
@@ -299,13 +324,13 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   const int g = lane >> 4;       // k-group
   const int ln = lane & 15;      // token (A) / weight row (B) within a 16-tile
 
-  issue(0);
-  issue(1);
+#pragma unroll
+  for (int st = 0; st < NSTAGE - 1; st++) issue(st);
   for (int st = 0; st < n_stages; st++) {
-    // stage st landed (this wave's copies): stage st + 1 may still be in flight
-    if (st + 1 < n_stages) wait_vmcnt<PER_STAGE>(); else wait_vmcnt<0>();
+    // stage st landed (this wave's copies); later issued stages may be in flight
+    wait_stages<PER_STAGE>(min(NSTAGE - 2, n_stages - 1 - st));
     __builtin_amdgcn_s_barrier();   // every wave's copies of stage st are in LDS
-    issue(st + 2);                  // into the slot of stage st - 1, which all waves finished
+    issue(st + NSTAGE - 1);         // into the slot of stage st - 1, which all waves finished
     const uint8_t* slot = smem + (st % NSTAGE) * STAGE;
     const uint8_t* bslot = slot + A_STAGE;
 #pragma unroll
@@ -314,12 +339,12 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
 #pragma unroll
       for (int i = 0; i < IT; i++) {
         const int grp = (wm >> 4) + i;
-        ah[i] = *reinterpret_cast<const half8*>(slot + (j * 16 + 2 * grp) * FRAG + 16 * lane);
-        al[i] = *reinterpret_cast<const half8*>(slot + (j * 16 + 2 * grp + 1) * FRAG + 16 * lane);
+        ah[i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp) * FRAG + 16 * lane);
+        al[i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp + 1) * FRAG + 16 * lane);
       }
       float4v sx[IT];
       if constexpr (TYPE == WH_TYPE_Q4_1) {
-        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * TBM;
+        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * BM;
 #pragma unroll
         for (int i = 0; i < IT; i++) sx[i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
       }
@@ -354,7 +379,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       };
       auto scale = [&](int n, uint32_t dm, const float4v* c) {
         // d in an f32 register: the FMAs below are then plain v_fmac_f32
-        // (VOP2) instead of mixed-precision v_fma_mix_f32 (VOP3P, slower)
         float d = whd::f16_bits_to_f32(dm & 0xFFFFu);
         asm("" : "+v"(d));
         const float mm = TYPE == WH_TYPE_Q4_1 ? whd::f16_bits_to_f32(dm >> 16) : 0.f;
@@ -370,7 +394,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       float4v cc[2][IT];
       uint32_t wq0[2], wq1[2], wdm[2];
       load_w(0, wq0[0], wq1[0], wdm[0]);
-      load_w(1, wq0[1], wq1[1], wdm[1]);
+      if (NT > 1) load_w(1, wq0[1], wq1[1], wdm[1]);
       mfmas(wq0[0], wq1[0], cc[0]);
 #pragma unroll
       for (int n = 0; n < NT; n++) {
@@ -384,6 +408,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       }
     }
   }
+  wait_vmcnt<0>();  // (no copies remain: every issued stage was consumed)
 
   // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
   float* out = y + static_cast<size_t>(blockIdx.y) * n_tokens * n_rows;
@@ -413,23 +438,47 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* _
   }
 }
 
+// Token-tile height for a token count: the smallest of 16, 32, 64, 128 that
+// holds it (one tile) or 128 beyond.
+int tile_bm(size_t n_tokens) { return n_tokens <= 16 ? 16 : (n_tokens <= 32 ? 32 : (n_tokens <= 64 ? 64 : 128)); }
+
+template <int TYPE, int BM>
+int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
+              const float* rs, const float* bs, float* part, int splits, hipStream_t s) {
+  const int nb = static_cast<int>(k / 32);
+  const int tiles_n = static_cast<int>((n_rows + TBN - 1) / TBN);
+  const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
+  int bps = (nb + splits - 1) / splits;
+  bps = (bps + SB - 1) / SB * SB;
+  const size_t lds = tiled_lds_bytes<TYPE, BM>();
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
+  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, part, static_cast<int>(n_tokens),
+                                                           static_cast<int>(n_rows), nb, bps, tiles_n,
+                                                           tiles_m * tiles_n);
+  WH_LAUNCH_CHECK("tiled gemm kernel launch");
+  return WH_OK;
+}
+
 template <int TYPE>
 int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
                  const float* rs, const float* bs, float* part, int splits, hipStream_t s) {
-  const int nb = static_cast<int>(k / 32);
-  const int tiles_n = static_cast<int>((n_rows + TBN - 1) / TBN);
-  const int tiles_m = static_cast<int>((n_tokens + TBM - 1) / TBM);
-  int bps = (nb + splits - 1) / splits;
-  bps = (bps + SB - 1) / SB * SB;
-  const size_t lds = static_cast<size_t>(NSTAGE) * stage_bytes<TYPE>();
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-  dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
-  gemm_tiled_kernel<TYPE><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, part, static_cast<int>(n_tokens),
-                                                       static_cast<int>(n_rows), nb, bps, tiles_n,
-                                                       tiles_m * tiles_n);
-  WH_LAUNCH_CHECK("tiled gemm kernel launch");
-  return WH_OK;
+  switch (tile_bm(n_tokens)) {
+    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
+    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
+    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
+    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
+  }
+}
+
+template <int TYPE>
+size_t max_lds_typed() {
+  size_t a = tiled_lds_bytes<TYPE, 16>(), b = tiled_lds_bytes<TYPE, 32>();
+  size_t c = tiled_lds_bytes<TYPE, 64>(), d = tiled_lds_bytes<TYPE, 128>();
+  size_t m = a > b ? a : b;
+  m = m > c ? m : c;
+  return m > d ? m : d;
 }
 
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
@@ -439,27 +488,37 @@ size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 namespace wh {
 
 // The tiled kernel needs whole block pairs per row (k % 64 == 0), 4-byte
-// aligned rows and weights, and an LDS budget the device provides.
-bool gemm_tiled_ok(int type, const void* w, size_t k) {
+// aligned rows and weights, byte offsets into the weights, the activation
+// fragments and the block sums that fit 32 bits, and an LDS budget the device
+// provides.
+bool gemm_tiled_ok(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens) {
   const size_t ts = type_size(type);
   if (ts == 0 || k == 0 || k % 64 != 0 || !aligned(w, 4) || ((k / 32) * ts) % 4 != 0) return false;
-  const size_t lds = NSTAGE * static_cast<size_t>(
-      type == WH_TYPE_Q4_0 ? stage_bytes<WH_TYPE_Q4_0>()
-                           : (type == WH_TYPE_Q4_1 ? stage_bytes<WH_TYPE_Q4_1>() : stage_bytes<WH_TYPE_Q8_0>()));
+  const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
+  const size_t tm = (n_tokens + bm - 1) / bm * bm;
+  const size_t lim = static_cast<size_t>(1) << 32;
+  if (n_rows * (k / 32) * ts >= lim || tm * k * 4 >= lim) return false;
+  const size_t lds = type == WH_TYPE_Q4_0 ? max_lds_typed<WH_TYPE_Q4_0>()
+                                          : (type == WH_TYPE_Q4_1 ? max_lds_typed<WH_TYPE_Q4_1>()
+                                                                  : max_lds_typed<WH_TYPE_Q8_0>());
   return lds <= max_lds_per_block();
 }
 
+// Split-K factor: the largest power of two up to 8 that keeps the workgroups
+// within one per CU and every split at least 16 blocks deep.
 int gemm_tiled_splits(size_t n_rows, size_t n_tokens, size_t k) {
-  const size_t tiles = ((n_rows + TBN - 1) / TBN) * ((n_tokens + TBM - 1) / TBM);
+  const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
+  const size_t tiles = ((n_rows + TBN - 1) / TBN) * ((n_tokens + bm - 1) / bm);
   const size_t nb = k / 32;
   const size_t cus = static_cast<size_t>(cu_count());
   int s = 1;
-  while (s < 8 && tiles * s * 2 <= cus && nb / (2 * s) >= 32) s *= 2;
+  while (s < 8 && tiles * s * 2 <= cus && nb / (2 * s) >= 16) s *= 2;
   return s;
 }
 
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
-  const size_t tm = (n_tokens + TBM - 1) / TBM * TBM;   // padded tokens
+  const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
+  const size_t tm = (n_tokens + bm - 1) / bm * bm;   // padded tokens
   size_t b = al256(tm * k * 4) + al256(tm * 4);
   if (type == WH_TYPE_Q4_1) b += al256(tm * (k / 32) * 4);
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
@@ -469,7 +528,8 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
 
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
                       float* y, void* workspace, hipStream_t s) {
-  const size_t tm = (n_tokens + TBM - 1) / TBM * TBM;
+  const int bm = tile_bm(n_tokens);
+  const size_t tm = (n_tokens + bm - 1) / bm * bm;
   char* ws = static_cast<char*>(workspace);
   _Float16* frag = reinterpret_cast<_Float16*>(ws);
   ws += al256(tm * k * 4);
@@ -483,7 +543,7 @@ int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const fl
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
   float* part = splits > 1 ? reinterpret_cast<float*>(ws) : y;
   pack_a_kernel<<<static_cast<unsigned>(tm), 256, 0, s>>>(x, static_cast<int>(n_tokens), static_cast<int>(k),
-                                                          type, frag, rs, bs);
+                                                          type, bm, frag, rs, bs);
   WH_LAUNCH_CHECK("pack kernel launch");
   const uint8_t* wp = static_cast<const uint8_t*>(w);
   int st;

@@ -474,9 +474,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
   const uint32_t ring_lds = lds_u32(my_ring);
 
   // Copies of row step k into slot k % RD.  Rows past the range re-read the
-  // range's last row; in a slice's last copy instruction the lanes past the
-  // slice are masked off (lane 0 stays on and repeats the last chunk into the
-  // unused tail of the slot, so every wave issues the same number of copies).
+  // range's last row; lanes past the slice are masked off, and copy
+  // instructions wholly past it are replaced by lane 0 re-copying the last
+  // chunk onto itself, so every wave issues the same number of copies.
   const int nchunks = nbytes / 16;
   auto issue = [&](int k) {
     const int row = min(r0 + g + k * groups, r1 - 1);
@@ -487,9 +487,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
       const void* base = mtx ? static_cast<const void*>(W2) : static_cast<const void*>(W);
 #pragma unroll
       for (int i = 0; i < NI; i++) {
-        const int c = 64 * i + lane;
-        if (c < nchunks || lane == 0)
-          ring_copy16(base, base_off + 16u * static_cast<uint32_t>(min(c, nchunks - 1)), slot + 1024u * i);
+        if (64 * i < nchunks) {
+          const int c = 64 * i + lane;
+          if (c < nchunks) ring_copy16(base, base_off + 16u * static_cast<uint32_t>(c), slot + 1024u * i);
+        } else if (lane == 0) {
+          // padding copy (constant copy count): the slice's last chunk onto itself
+          const uint32_t last = 16u * static_cast<uint32_t>(nchunks - 1);
+          ring_copy16(base, base_off + last, slot + last);
+        }
       }
     }
   };
