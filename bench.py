@@ -232,8 +232,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-layer timings")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM M sweep")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm512"], default=None,
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
+    ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only device-to-device copies of 256 MiB (counter calibration)")
     args = ap.parse_args()
@@ -253,8 +254,8 @@ def main() -> int:
         ms_step, _, _ = bench_gemv(args.steps, args.warmup)
         print(json.dumps({"gemv_us": round(ms_step * 1e3, 3)}))
         return 0
-    if args.only == "gemm512":
-        print(json.dumps({"gemm_m512_us": round(bench_gemm(512, 5), 2)}))
+    if args.only == "gemm":
+        print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5), 2)}))
         return 0
     if args.only in ("ffn1", "ffn512"):
         m = 1 if args.only == "ffn1" else 512

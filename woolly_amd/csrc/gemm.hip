@@ -505,7 +505,7 @@ int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x
     return set_error(WH_ERR_BUFFER_TOO_SMALL,
                      "quantized_matmul: workspace too small: needed %zu bytes, available %zu", need,
                      workspace ? workspace_bytes : static_cast<size_t>(0));
-  if (gemm_tiled_ok(type, w, n_rows, k, n_tokens)) return launch_gemm_tiled(type, w, n_rows, k, x, n_tokens, y, workspace, s);
+  if (gemm_tiled_ok(type, w, x, n_rows, k, n_tokens)) return launch_gemm_tiled(type, w, n_rows, k, x, n_tokens, y, workspace, s);
   return launch_gemm_mfma(type, w, n_rows, k, x, n_tokens, y, workspace, s);
 }
 

@@ -53,49 +53,70 @@ struct TCfg {
   static constexpr int IT = WTM / 16, NT = WTN / 16;
   static constexpr int FPB = BM / 8;                       // fragments per block (groups x limbs)
   static constexpr int A_STAGE = SB * FPB * FRAG;
-  static constexpr int NSTAGE = BM <= 32 ? 4 : 3;
 };
 
 template <int TYPE>
 struct TFmt;
 template <>
 struct TFmt<WH_TYPE_Q4_0> {
-  static constexpr int TS = 18, QOFF = 2, DWB = 9;    // DWB: dwords per row per stage
+  static constexpr int TS = 18, QOFF = 2;
 };
 template <>
 struct TFmt<WH_TYPE_Q4_1> {
-  static constexpr int TS = 20, QOFF = 4, DWB = 10;
+  static constexpr int TS = 20, QOFF = 4;
 };
 template <>
 struct TFmt<WH_TYPE_Q8_0> {
-  static constexpr int TS = 34, QOFF = 2, DWB = 17;
+  static constexpr int TS = 34, QOFF = 2;
 };
+// dwords per weight row per stage (SB whole blocks)
+template <int TYPE>
+constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
+static_assert(SB * 18 % 4 == 0 && SB * 34 % 4 == 0, "stage rows must be whole dwords");
 
 // raw weight dwords per stage, rounded up to whole copy instructions
 template <int TYPE>
-constexpr int b_dma_per_wave() { return (TBN * TFmt<TYPE>::DWB + TWAVES * 64 - 1) / (TWAVES * 64); }
+constexpr int b_dma_per_wave() { return (TBN * dwb<TYPE>() + TWAVES * 64 - 1) / (TWAVES * 64); }
 template <int TYPE>
 constexpr int b_stage_bytes() { return b_dma_per_wave<TYPE>() * TWAVES * 64 * 4; }
 template <int TYPE, int BM>
 constexpr int s_stage_bytes() { return TYPE == WH_TYPE_Q4_1 ? SB * BM * 4 : 0; }
 template <int TYPE, int BM>
 constexpr int stage_bytes() { return TCfg<BM>::A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE, BM>(); }
+// Copy instructions per wave per stage (the vmcnt of one stage): activation
+// fragments, raw weight dwords, Q4_1 block sums.
 template <int TYPE, int BM>
-constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(TCfg<BM>::NSTAGE) * stage_bytes<TYPE, BM>(); }
-
-// Element (within a block) held by k-slot s of k-group g.  For the 4-bit
-// formats the order is that of unpack_q4 below; Q8_0 keeps natural order.
-__device__ __forceinline__ int slot_elem(int type, int g, int s) {
-  if (type == WH_TYPE_Q8_0) return 8 * g + s;
-  const int p = (s & 3) == 1 ? 2 : ((s & 3) == 2 ? 1 : (s & 3));  // 0, 2, 1, 3
-  return (s < 4 ? 0 : 16) + 4 * g + p;
+constexpr int per_stage() {
+  return (SB * TCfg<BM>::FPB + TWAVES - 1) / TWAVES + b_dma_per_wave<TYPE>() + (TYPE == WH_TYPE_Q4_1 ? 1 : 0);
 }
+// Ring depth: as many stages as 160 KiB of LDS holds, 3 to 8 (a deeper ring
+// keeps more weight bytes in flight where a stage is small), with the copies
+// of the stages in flight behind the one awaited countable by vmcnt (< 64).
+template <int TYPE, int BM>
+constexpr int nstage() {
+  constexpr int n = 160 * 1024 / stage_bytes<TYPE, BM>();
+  constexpr int v = 2 + 63 / per_stage<TYPE, BM>();
+  constexpr int m = n < v ? n : v;
+  return m < 3 ? 3 : (m > 8 ? 8 : m);
+}
+template <int TYPE, int BM>
+constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>()) * stage_bytes<TYPE, BM>(); }
+
+// K-slot order of an MFMA operand: k-slot s (0..7) of k-group g (0..3) holds
+// block element 8g + s for Q8_0, and for the 4-bit formats element
+// (s < 4 ? 0 : 16) + 4g + {0, 2, 1, 3}[s % 4], the order unpack_q4 below
+// produces the quants in.
 
 // ---------------------------------------------------------------- packing
 // One workgroup per token row t of the padded tile grid (token tiles of bm
 // rows).  Rows t >= n_tokens are written as zeros.  rscale[t] = 2^e with
 // max|x_t| * 2^-e in [2^13, 2^14); bsum (Q4_1 only) = per-block sums of
 // hi + lo, laid out [T][b][bm].
+// Thread p of a chunk owns the (block, k-group) pairs p, p + 256, ...: the 8
+// elements of a pair are two float4 loads (slot_elem order), all issued
+// before the first use; a row of up to 256 * PPT pairs (k <= 64 * PPT) is
+// read once and packed from registers, longer rows are read a second time.
+constexpr int PPT = 8;
 __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, int n_tokens, int k,
                                                      int type, int bm, _Float16* __restrict__ frag,
                                                      float* __restrict__ rscale, float* __restrict__ bsum) {
@@ -103,9 +124,31 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
   const int t = blockIdx.x;
   const bool live = t < n_tokens;
   const float* xr = x + static_cast<size_t>(live ? t : 0) * k;
+  const int nb = k / 32, npairs = nb * 4;
+  const int nchunks = (npairs + 256 * PPT - 1) / (256 * PPT);
+  const bool q8 = type == WH_TYPE_Q8_0;
+  float4 va[PPT], vb[PPT];
+  auto load = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < PPT; i++) {
+      const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+      va[i] = vb[i] = float4{0.f, 0.f, 0.f, 0.f};
+      if (live && p < npairs) {
+        const int b = p >> 2, g = p & 3;
+        const float* src = xr + 32 * b + (q8 ? 8 * g : 4 * g);
+        va[i] = *reinterpret_cast<const float4*>(src);
+        vb[i] = *reinterpret_cast<const float4*>(src + (q8 ? 4 : 16));
+      }
+    }
+  };
   float mx = 0.f;
-  if (live)
-    for (int i = threadIdx.x; i < k; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+  for (int c = 0; c < nchunks; c++) {
+    load(c);
+#pragma unroll
+    for (int i = 0; i < PPT; i++)
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(va[i].x), fabsf(va[i].y)), fmaxf(fabsf(va[i].z), fabsf(va[i].w))),
+                           fmaxf(fmaxf(fabsf(vb[i].x), fabsf(vb[i].y)), fmaxf(fabsf(vb[i].z), fabsf(vb[i].w)))));
+  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -120,30 +163,44 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
   }
   const float down = ldexpf(1.f, -e);
   if (threadIdx.x == 0) rscale[t] = ldexpf(1.f, e);
-  const int nb = k / 32;
   const int T = t / bm, i16 = (t % bm) / 16, tl = t % 16, fpb = bm / 8;
-  for (int p = threadIdx.x; p < nb * 4; p += 256) {  // (block, k-group) pairs
-    const int b = p >> 2, g = p & 3;
-    half8 hv, lv;
-    float part = 0.f;
+  for (int c = 0; c < nchunks; c++) {
+    if (nchunks > 1) load(c);   // one chunk: its values are still in registers
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const float v = live ? xr[32 * b + slot_elem(type, g, s)] * down : 0.f;  // exact scaling
-      const _Float16 h = static_cast<_Float16>(v);
-      const _Float16 l = static_cast<_Float16>(v - static_cast<float>(h));
-      hv[s] = h;
-      lv[s] = l;
-      part += static_cast<float>(h) + static_cast<float>(l);
-    }
-    const int lane = 16 * g + tl;
-    const size_t base = ((static_cast<size_t>(T) * nb + b) * fpb + 2 * i16) * 512 + 8 * lane;
-    *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
-    *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
-    if (bsum) {
-      // the four k-groups of a block are adjacent threads (p = 4b + g)
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
-      if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
+    for (int i = 0; i < PPT; i++) {
+      const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+      if (p >= npairs) break;   // uniform across the four lanes of a block
+      const int b = p >> 2, g = p & 3;
+      // slot order: 4-bit formats {0, 2, 1, 3} within each half, Q8_0 natural
+      float v[8];
+      if (q8) {
+        v[0] = va[i].x; v[1] = va[i].y; v[2] = va[i].z; v[3] = va[i].w;
+        v[4] = vb[i].x; v[5] = vb[i].y; v[6] = vb[i].z; v[7] = vb[i].w;
+      } else {
+        v[0] = va[i].x; v[1] = va[i].z; v[2] = va[i].y; v[3] = va[i].w;
+        v[4] = vb[i].x; v[5] = vb[i].z; v[6] = vb[i].y; v[7] = vb[i].w;
+      }
+      half8 hv, lv;
+      float part = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const float sv = v[s] * down;  // exact scaling
+        const _Float16 h = static_cast<_Float16>(sv);
+        const _Float16 l = static_cast<_Float16>(sv - static_cast<float>(h));
+        hv[s] = h;
+        lv[s] = l;
+        part += static_cast<float>(h) + static_cast<float>(l);
+      }
+      const int lane = 16 * g + tl;
+      const size_t base = ((static_cast<size_t>(T) * nb + b) * fpb + 2 * i16) * 512 + 8 * lane;
+      *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
+      *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
+      if (bsum) {
+        // the four k-groups of a block are adjacent lanes (p = 4b + g)
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
+      }
     }
   }
 }
@@ -225,11 +282,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---------------------------------------------------------------- GEMM
-template <int N>
-__device__ __forceinline__ void wait_stages(int n) {  // at most n stages of N copies in flight
-  if (n >= 2) wait_vmcnt<2 * N>();
-  else if (n == 1) wait_vmcnt<N>();
-  else wait_vmcnt<0>();
+// Waits until at most min(n, J) stages of N copies each are in flight.
+template <int N, int J>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (J == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= J) wait_vmcnt<J * N>();
+    else wait_stages<N, J - 1>(n);
+  }
 }
 
 // Y (or split-K partial plane blockIdx.y) for one BM x 256 tile over blocks
@@ -240,9 +301,9 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const float* __restrict__ bsum, float* __restrict__ y, int n_tokens, int n_rows, int nb,
     int blocks_per_split, int tiles_n, int n_tiles) {
   using C = TCfg<BM>;
-  constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = C::NSTAGE;
+  constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = nstage<TYPE, BM>();
   constexpr int A_STAGE = C::A_STAGE;
-  constexpr int TS = TFmt<TYPE>::TS, QOFF = TFmt<TYPE>::QOFF, DWB = TFmt<TYPE>::DWB;
+  constexpr int TS = TFmt<TYPE>::TS, QOFF = TFmt<TYPE>::QOFF, DWB = dwb<TYPE>();
   constexpr int BSTAGE = b_stage_bytes<TYPE>();
   constexpr int STAGE = stage_bytes<TYPE, BM>();
   constexpr int A_FR = SB * FPB;                                    // fragments per stage
@@ -252,6 +313,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   constexpr int S_PW = S_CH / TWAVES;                               // ... per wave (>= 1)
   constexpr int S_DMA = TYPE == WH_TYPE_Q4_1 ? 1 : 0;
   constexpr int PER_STAGE = A_DMA + B_DMA + S_DMA;                  // vmcnt per stage
+  static_assert(PER_STAGE == per_stage<TYPE, BM>(), "copy count");
   static_assert((NSTAGE - 2) * PER_STAGE < 64, "vmcnt range");
   extern __shared__ __align__(16) uint8_t smem[];
 
@@ -328,7 +390,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   for (int st = 0; st < NSTAGE - 1; st++) issue(st);
   for (int st = 0; st < n_stages; st++) {
     // stage st landed (this wave's copies); later issued stages may be in flight
-    wait_stages<PER_STAGE>(min(NSTAGE - 2, n_stages - 1 - st));
+    wait_stages<PER_STAGE, NSTAGE - 2>(n_stages - 1 - st);
     __builtin_amdgcn_s_barrier();   // every wave's copies of stage st are in LDS
     issue(st + NSTAGE - 1);         // into the slot of stage st - 1, which all waves finished
     const uint8_t* slot = smem + (st % NSTAGE) * STAGE;
@@ -473,12 +535,13 @@ int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, con
 }
 
 template <int TYPE>
-size_t max_lds_typed() {
-  size_t a = tiled_lds_bytes<TYPE, 16>(), b = tiled_lds_bytes<TYPE, 32>();
-  size_t c = tiled_lds_bytes<TYPE, 64>(), d = tiled_lds_bytes<TYPE, 128>();
-  size_t m = a > b ? a : b;
-  m = m > c ? m : c;
-  return m > d ? m : d;
+size_t lds_typed(int bm) {
+  switch (bm) {
+    case 16: return tiled_lds_bytes<TYPE, 16>();
+    case 32: return tiled_lds_bytes<TYPE, 32>();
+    case 64: return tiled_lds_bytes<TYPE, 64>();
+    default: return tiled_lds_bytes<TYPE, 128>();
+  }
 }
 
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
@@ -487,20 +550,21 @@ size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 
 namespace wh {
 
-// The tiled kernel needs whole block pairs per row (k % 64 == 0), 4-byte
-// aligned rows and weights, byte offsets into the weights, the activation
+// The tiled kernel needs whole stages per row (k a multiple of 32 SB), 4-byte
+// aligned rows and weights, 16-byte aligned activations, byte offsets into the weights, the activation
 // fragments and the block sums that fit 32 bits, and an LDS budget the device
 // provides.
-bool gemm_tiled_ok(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens) {
+bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens) {
   const size_t ts = type_size(type);
-  if (ts == 0 || k == 0 || k % 64 != 0 || !aligned(w, 4) || ((k / 32) * ts) % 4 != 0) return false;
+  if (ts == 0 || k == 0 || k % (32 * SB) != 0 || !aligned(w, 4) || !aligned(x, 16) || ((k / 32) * ts) % 4 != 0) return false;
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;
   const size_t lim = static_cast<size_t>(1) << 32;
   if (n_rows * (k / 32) * ts >= lim || tm * k * 4 >= lim) return false;
-  const size_t lds = type == WH_TYPE_Q4_0 ? max_lds_typed<WH_TYPE_Q4_0>()
-                                          : (type == WH_TYPE_Q4_1 ? max_lds_typed<WH_TYPE_Q4_1>()
-                                                                  : max_lds_typed<WH_TYPE_Q8_0>());
+  const int b = static_cast<int>(bm);
+  const size_t lds = type == WH_TYPE_Q4_0 ? lds_typed<WH_TYPE_Q4_0>(b)
+                                          : (type == WH_TYPE_Q4_1 ? lds_typed<WH_TYPE_Q4_1>(b)
+                                                                  : lds_typed<WH_TYPE_Q8_0>(b));
   return lds <= max_lds_per_block();
 }
 

@@ -69,7 +69,7 @@ int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x
                 size_t n_tokens, float* y, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);
 // Tiled 16x16x32 MFMA kernel (gemm_tiled.hip): eligibility, workspace, launch.
-bool gemm_tiled_ok(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens);
+bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens);
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x,
                       size_t n_tokens, float* y, void* workspace, hipStream_t stream);
