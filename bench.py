@@ -17,8 +17,12 @@ Prints ONE JSON line with:
                  events on the launch stream, against the 8 TB/s HBM peak
   ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
                  M=512, same run (the metric's second part)
-  cpu_baseline   the CPU oracle's scalar GEMV (woolly's quantized_matvec_q4_0_scalar
-                 order, 1 thread) on this host, a bounded sample of full-size calls
+  gemv_other_configs  the other decode GEMV configurations: Q4_0 4096x4096,
+                 Q8_0 and Q4_1 14336x4096 (µs, algorithmic GB/s, fraction of peak)
+  cpu_baseline   the reference's intended SIMD GEMV (8-lane AVX2 FMA, restated in
+                 the test oracle) on up to 16 host threads, a bounded sample of
+                 full-size calls; cpu_baseline_scalar: the order-exact scalar
+                 quantized_matvec_q4_0_scalar on 1 thread
 """
 from __future__ import annotations
 
@@ -41,27 +45,34 @@ N_ROWS, K = 14336, 4096
 REPLICAS = 10
 
 
-def gemv_bytes(n: int, k: int) -> int:
-    return n * (k // 32) * 18 + 4 * k + 4 * n
+TYPE_SIZE = {2: 18, 3: 20, 8: 34}
+
+
+def gemv_bytes(n: int, k: int, t: int = Q4_0) -> int:
+    return n * (k // 32) * TYPE_SIZE[t] + 4 * k + 4 * n
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def bench_gemv(steps: int, warmup: int):
+def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int = K, seed: int = 3,
+               replicas: int = REPLICAS):
+    """GEMV y = W x of type t, n x k: (ms per launch over a graph replay of
+    `steps` launches, median and mean of event-bracketed eager launches).
+    `replicas` weight copies are rotated so the weights come from HBM."""
     from woolly_amd import ops, synth
     from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
 
-    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=3)
-    x = synth.activations(K, seed=3)
+    w = synth.quantized_weight(t, n, k, seed=seed)
+    x = synth.activations(k, seed=seed)
     stream = Stream()
-    wbufs = [DeviceBuffer.from_array(w) for _ in range(REPLICAS)]
+    wbufs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
     xb = DeviceBuffer.from_array(x)
-    yb = DeviceBuffer(4 * N_ROWS)
+    yb = DeviceBuffer(4 * n)
 
     def launch(i: int) -> None:
-        ops.quantized_matvec(Q4_0, wbufs[i % REPLICAS], w.nbytes, xb, yb, N_ROWS, K, stream)
+        ops.quantized_matvec(t, wbufs[i % replicas], w.nbytes, xb, yb, n, k, stream)
 
     for i in range(warmup):
         launch(i)
@@ -188,40 +199,67 @@ def traffic_from_profile() -> int | None:
     return None
 
 
-def cpu_baseline(budget_s: float = 10.0) -> dict:
-    """The oracle's order-exact scalar Q4_0 GEMV on this host (1 thread)."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_calls(fn, budget_s: float) -> tuple[int, float]:
+    fn()  # warm
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        fn()
+        calls += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return calls, (time.perf_counter() - t0) / calls
+
+
+def cpu_baselines(budget_s: float = 8.0) -> tuple[dict | None, dict]:
+    """The target GEMV on this host's CPU, timed with the test oracle:
+    (1) the reference's intended SIMD path (8-lane AVX2 FMA restatement,
+    nibble order fixed) on up to 16 threads -- the reported cpu_baseline;
+    (2) the order-exact scalar quantized_matvec_q4_0_scalar on 1 thread, the
+    reference's default x86 behaviour.  ~budget_s of CPU work each."""
     from tests._oracle import Oracle
     from woolly_amd import synth
 
     orc = Oracle()
     w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=3)
     x = synth.activations(K, seed=3)
-    orc.matvec_f32(Q4_0, w, x, N_ROWS, K)  # warm
-    t0 = time.perf_counter()
-    calls = 0
-    while True:
-        orc.matvec_f32(Q4_0, w, x, N_ROWS, K)
-        calls += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = (time.perf_counter() - t0) / calls
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": round(gemv_bytes(N_ROWS, K) / dt / 1e9, 3),
+    nbytes = gemv_bytes(N_ROWS, K)
+    cpu, nproc = _cpu_model(), os.cpu_count()
+    simd = None
+    if orc.simd_available():
+        threads = max(1, min(16, nproc or 1))
+        calls, dt = _time_calls(lambda: orc.matvec_simd_mt(Q4_0, w, x, N_ROWS, K, threads), budget_s)
+        simd = {
+            "value": round(nbytes / dt / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"{calls} full 14336x4096 Q4_0 GEMV calls of the oracle's restatement of "
+                       f"the reference's AVX2 qmatvec_q4_0_avx2 (8-lane FMA, nibble order fixed), "
+                       f"rows split over {threads} threads, {dt * 1e3:.2f} ms each, "
+                       f"host '{cpu}', nproc={nproc}"),
+        }
+    calls, dt = _time_calls(lambda: orc.matvec_f32(Q4_0, w, x, N_ROWS, K), budget_s)
+    scalar = {
+        "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{calls} full 14336x4096 Q4_0 GEMV calls of the oracle's scalar "
+        "sample": (f"{calls} full 14336x4096 Q4_0 GEMV calls of the oracle's order-exact "
                    f"quantized_matvec_q4_0_scalar restatement, {dt * 1e3:.1f} ms each, "
-                   f"host '{cpu}', nproc={os.cpu_count()}"),
+                   f"host '{cpu}', nproc={nproc}"),
     }
+    return simd, scalar
 
 
 def main() -> int:
@@ -232,6 +270,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-layer timings")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM M sweep")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other decode GEMV configurations (4096x4096 Q4_0, Q8_0, Q4_1)")
     ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
@@ -288,9 +328,24 @@ def main() -> int:
             gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}
             log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s")
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    # the other decode GEMV configurations (config 0, 1a, 1b); replicas keep
+    # each timed set of weights above the 256 MB Infinity Cache
+    gemv_cfg = {}
+    if not args.no_configs:
+        for name, t, n, k, seed, reps in (("c0_q4_0_4096x4096", Q4_0, 4096, 4096, 0, 32),
+                                          ("c1a_q8_0_14336x4096", 8, 14336, 4096, 1, 5),
+                                          ("c1b_q4_1_14336x4096", 3, 14336, 4096, 2, 8)):
+            ms, _, _ = bench_gemv(100, 10, t, n, k, seed, reps)
+            gbs = gemv_bytes(n, k, t) / (ms * 1e-3) / 1e9
+            gemv_cfg[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+                              "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t)}
+            log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+
+    cpu, cpu_scalar = (None, None) if args.no_cpu else cpu_baselines()
     if cpu:
-        log(f"[bench] cpu baseline: {cpu['value']} GB/s")
+        log(f"[bench] cpu baseline (simd, {cpu['cores']} threads): {cpu['value']} GB/s")
+    if cpu_scalar:
+        log(f"[bench] cpu baseline (scalar, 1 thread): {cpu_scalar['value']} GB/s")
 
     line = {
         "metric": METRIC,
@@ -324,7 +379,9 @@ def main() -> int:
         },
         "ffn_layer_us": ffn or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,
+        "gemv_other_configs": gemv_cfg or None,
         "cpu_baseline": cpu,
+        "cpu_baseline_scalar": cpu_scalar,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -95,6 +95,14 @@ int orc_ffn_f32(int type, const uint8_t* w_gate, const uint8_t* w_up, const uint
                 size_t hidden, size_t n_ff, const float* gamma, float eps, const float* x,
                 size_t m, float* out);
 
+/* Multi-threaded 8-lane restatement of the reference's intended AVX2 GEMV
+ * (qmatvec_q4_0_avx2 / qmatvec_q8_0_avx2, quantization.rs:720-840, nibble
+ * order fixed), oracle_simd.c; the benchmark's CPU baseline.  Returns
+ * ORC_ERR_UNSUPPORTED_TYPE when the CPU lacks AVX2/FMA. */
+int orc_simd_available(void);
+int orc_matvec_simd_mt(int type, const uint8_t* w, const float* x, float* y, size_t m, size_t k,
+                       int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,8 @@ class Oracle:
             "orc_ffn_rows_f64": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_double, _p, _p,
                                            _sz, _p]),
             "orc_ffn_f32": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_float, _p, _sz, _p]),
+            "orc_simd_available": (C.c_int, []),
+            "orc_matvec_simd_mt": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, C.c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -87,6 +89,16 @@ class Oracle:
         x = np.ascontiguousarray(x, dtype=np.float32)
         y = np.zeros(m, dtype=np.float32)
         st = self.lib.orc_matvec_f32(t, _ptr(w), _ptr(x), _ptr(y), m, k)
+        return st, y
+
+    def simd_available(self) -> bool:
+        return bool(self.lib.orc_simd_available())
+
+    def matvec_simd_mt(self, t, w, x, m, k, threads):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(m, dtype=np.float32)
+        st = self.lib.orc_matvec_simd_mt(t, _ptr(w), _ptr(x), _ptr(y), m, k, threads)
         return st, y
 
     def matvec_f64(self, t, w, x, m, k):

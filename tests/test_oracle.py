@@ -261,6 +261,24 @@ def test_gemv_f32_evaluation_order(orc, t):
     assert st == 0 and np.array_equal(y32.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+def test_gemv_simd_mt_baseline(orc, t):
+    # The benchmark's CPU baseline (the reference's 8-lane AVX2 GEMV restated,
+    # nibble order fixed): within f32 rounding of the f64 brute force, and the
+    # same bits for any thread count (rows are independent).
+    if not orc.simd_available():
+        pytest.skip("CPU without AVX2/FMA")
+    m, k = 37, 512
+    w = synth.quantized_weight(t, m, k, seed=9)
+    x = synth.activations(k, seed=9)
+    ref = np_dequant(t, w, m * k).astype(np.float64).reshape(m, k) @ x.astype(np.float64)
+    st, y1 = orc.matvec_simd_mt(t, w, x, m, k, 1)
+    assert st == 0 and rel_l2(y1, ref) < 1e-6
+    st, y5 = orc.matvec_simd_mt(t, w, x, m, k, 5)
+    assert st == 0 and np.array_equal(y1.view(np.uint32), y5.view(np.uint32))
+    assert orc.matvec_simd_mt(t, w, x, m, 48, 2)[0] == 2
+
+
 def test_gemv_errors(orc):
     w = synth.quantized_weight(Q4_0, 2, 64, seed=1)
     x = np.zeros(64, np.float32)
