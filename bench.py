@@ -18,7 +18,9 @@ Prints ONE JSON line with:
   ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
                  M=512, same run (the metric's second part)
   gemv_other_configs  the other decode GEMV configurations: Q4_0 4096x4096,
-                 Q8_0 and Q4_1 14336x4096 (µs, algorithmic GB/s, fraction of peak)
+                 Q8_0 and Q4_1 14336x4096, and the other decode-step shapes (k/v
+                 projections, FFN down, the Q8_0 128256x4096 output head):
+                 µs, algorithmic GB/s, fraction of peak
   cpu_baseline   the reference's intended SIMD GEMV (8-lane AVX2 FMA, restated in
                  the test oracle) on up to 16 host threads, a bounded sample of
                  full-size calls; cpu_baseline_scalar: the order-exact scalar
@@ -334,7 +336,12 @@ def main() -> int:
     if not args.no_configs:
         for name, t, n, k, seed, reps in (("c0_q4_0_4096x4096", Q4_0, 4096, 4096, 0, 32),
                                           ("c1a_q8_0_14336x4096", 8, 14336, 4096, 1, 5),
-                                          ("c1b_q4_1_14336x4096", 3, 14336, 4096, 2, 8)):
+                                          ("c1b_q4_1_14336x4096", 3, 14336, 4096, 2, 8),
+                                          # decode-step shapes: k/v projections, FFN down,
+                                          # the Q8_0 output head
+                                          ("attn_kv_q4_0_1024x4096", Q4_0, 1024, 4096, 6, 120),
+                                          ("ffn_down_q4_0_4096x14336", Q4_0, 4096, 14336, 6, 10),
+                                          ("head_q8_0_128256x4096", 8, 128256, 4096, 6, 1)):
             ms, _, _ = bench_gemv(100, 10, t, n, k, seed, reps)
             gbs = gemv_bytes(n, k, t) / (ms * 1e-3) / 1e9
             gemv_cfg[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),

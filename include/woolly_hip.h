@@ -41,7 +41,13 @@ typedef enum wh_status {
   WH_ERR_INVALID_ARGUMENT = 4,  /* QuantizationError::InvalidParameters, null/misaligned */
   WH_ERR_HIP = 5,               /* a HIP runtime call failed */
   WH_ERR_OOM = 6,               /* device allocation failed */
-  WH_ERR_NO_DEVICE = 7          /* no usable gfx950 device */
+  WH_ERR_NO_DEVICE = 7,         /* no usable gfx950 device */
+  WH_ERR_IO = 8,                /* Error::Io (open/map failure, unexpected end of file) */
+  WH_ERR_INVALID_MAGIC = 9,     /* Error::InvalidMagic */
+  WH_ERR_UNSUPPORTED_VERSION = 10, /* Error::UnsupportedVersion */
+  WH_ERR_INVALID_METADATA = 11, /* Error::InvalidMetadata / InvalidString / InvalidTensorInfo */
+  WH_ERR_NOT_FOUND = 12,        /* Error::TensorNotFound, or a metadata key that is absent */
+  WH_ERR_TYPE_MISMATCH = 13     /* metadata value of another type (the reference's get_* -> None) */
 } wh_status;
 
 /* GGMLType ids (crates/woolly-gguf/src/tensor_info.rs:15-30). */
@@ -187,7 +193,8 @@ WH_API int wh_ffn_swiglu(const wh_ffn_weights* weights, const float* gamma, floa
  * dequantization cache (model/lazy_loader.rs:599-659).  The handle owns its
  * device memory until wh_weight_free; the host bytes are only read during the
  * call.  The device layout is the GGUF block layout, so the handle's data can
- * be passed to every kernel entry point above. */
+ * be passed to every kernel entry point above.  F32 and F16 tensors (norm
+ * weights, embeddings) are accepted as n_rows x k plain elements. */
 WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_bytes,
                             size_t nbytes, wh_weight** out);
 WH_API int wh_weight_free(wh_weight* weight);
@@ -204,6 +211,106 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
                               float* out);
 WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
                                     const float* input, float* output, size_t m, size_t k);
+
+/* --------------------------------------------------------------- GGUF files */
+/* A parsed GGUF file: header, metadata key/values and the tensor table of
+ * woolly-gguf's GGUFLoader (crates/woolly-gguf/src/loader.rs:111-200), over a
+ * read-only memory map.  Parsing follows GGUFHeader::read_from (format.rs:74-103),
+ * GGUFMetadata::read_from (metadata.rs:153-178), MetadataValue::read_from
+ * (metadata.rs:86-124) and TensorInfo::read_from (tensor_info.rs:203-238); the
+ * data section starts at the header's end rounded up to general.alignment
+ * (a u32, default 32; loader.rs:148-164, 662-667).  Every read is bounds-checked:
+ * a truncated file fails with WH_ERR_IO ("unexpected end of file"), as the
+ * reference's Cursor reads do.  Strings must be valid UTF-8 (InvalidString).
+ * Keys and tensor names that occur twice resolve to the last occurrence (the
+ * reference inserts into a HashMap); the *_at calls enumerate in file order.
+ * A handle is immutable after open and may be shared between threads. */
+typedef struct wh_gguf wh_gguf;
+#define WH_GGUF_MAX_DIMS 8
+
+/* GGUFLoader::from_path (loader.rs:112-133): opens and maps `path`. */
+WH_API int wh_gguf_open(const char* path, wh_gguf** out);
+/* GGUFLoader::from_mmap (loader.rs:136-200) over caller memory; the bytes are
+ * borrowed and must outlive the handle. */
+WH_API int wh_gguf_open_buffer(const void* data, size_t nbytes, wh_gguf** out);
+WH_API int wh_gguf_close(wh_gguf* g);
+
+typedef struct wh_gguf_header {
+  uint32_t version;             /* 1..3 (GGUFVersion::is_supported, format.rs:54-56) */
+  uint64_t tensor_count;        /* as stored in the header */
+  uint64_t metadata_kv_count;   /* as stored in the header */
+  uint32_t alignment;           /* loader.alignment() */
+  uint64_t data_offset;         /* absolute offset of the data section */
+  uint64_t file_size;           /* loader.file_size() */
+  uint64_t total_tensor_size;   /* loader.total_tensor_size(), distinct names */
+} wh_gguf_header;
+WH_API int wh_gguf_get_header(const wh_gguf* g, wh_gguf_header* out);
+
+/* TensorInfo (tensor_info.rs:187-255). name is NUL-terminated and lives as
+ * long as the handle; dims[n_dims..] are 0. */
+typedef struct wh_gguf_tensor {
+  const char* name;
+  uint32_t n_dims;
+  uint64_t dims[WH_GGUF_MAX_DIMS];
+  int ggml_type;
+  uint64_t offset;      /* relative to the data section */
+  uint64_t n_elements;  /* TensorInfo::n_elements */
+  uint64_t data_size;   /* TensorInfo::data_size */
+} wh_gguf_tensor;
+/* i-th tensor in file order (i < number of tensors). */
+WH_API int wh_gguf_tensor_at(const wh_gguf* g, uint64_t i, wh_gguf_tensor* out);
+/* loader.tensor_info(name): index of the tensor; WH_ERR_NOT_FOUND if absent. */
+WH_API int wh_gguf_find_tensor(const wh_gguf* g, const char* name, uint64_t* index);
+/* loader.tensor_data(name) (loader.rs:230-295) without the copy: a pointer into
+ * the mapping and its size; WH_ERR_BUFFER_TOO_SMALL{needed, available} when the
+ * tensor runs past the end of the file (loader.rs:276-282). */
+WH_API int wh_gguf_tensor_data(const wh_gguf* g, uint64_t i, const void** data, size_t* nbytes);
+/* Uploads tensor i to a device weight handle straight from the mapping
+ * (wh_weight_upload with K = dims[0], rows = dims[1] * dims[2] * ...):
+ * replaces load_tensor_data_direct's to_vec (loader.rs:291) and the f32
+ * dequantization cache.  Q4_0, Q4_1, Q8_0, F32 and F16 tensors. */
+WH_API int wh_gguf_upload(const wh_gguf* g, uint64_t i, wh_weight** out);
+
+/* Metadata value types (metadata.rs:13-42). */
+typedef enum wh_gguf_value_type {
+  WH_GGUF_U8 = 0, WH_GGUF_I8 = 1, WH_GGUF_U16 = 2, WH_GGUF_I16 = 3,
+  WH_GGUF_U32 = 4, WH_GGUF_I32 = 5, WH_GGUF_F32 = 6, WH_GGUF_BOOL = 7,
+  WH_GGUF_STRING = 8, WH_GGUF_ARRAY = 9, WH_GGUF_U64 = 10, WH_GGUF_I64 = 11,
+  WH_GGUF_F64 = 12
+} wh_gguf_value_type;
+/* i-th key/value in file order: key (NUL-terminated, lives with the handle)
+ * and value type. */
+WH_API int wh_gguf_kv_at(const wh_gguf* g, uint64_t i, const char** key, int* value_type);
+WH_API int wh_gguf_find_kv(const wh_gguf* g, const char* key, uint64_t* index);
+/* Typed getters (GGUFMetadata::get_u32 / get_u64 / get_i32 / get_f32 /
+ * get_bool / get_string, metadata.rs:186-233): WH_ERR_NOT_FOUND for an absent
+ * key, WH_ERR_TYPE_MISMATCH for a value of another type. */
+WH_API int wh_gguf_get_u32(const wh_gguf* g, const char* key, uint32_t* out);
+WH_API int wh_gguf_get_u64(const wh_gguf* g, const char* key, uint64_t* out);
+WH_API int wh_gguf_get_i32(const wh_gguf* g, const char* key, int32_t* out);
+WH_API int wh_gguf_get_f32(const wh_gguf* g, const char* key, float* out);
+WH_API int wh_gguf_get_bool(const wh_gguf* g, const char* key, int* out);
+/* String value: pointer into the mapping (not NUL-terminated) and length. */
+WH_API int wh_gguf_get_string(const wh_gguf* g, const char* key, const char** data, size_t* len);
+/* Any scalar value (types 0-7, 10-12) of key/value i, as its little-endian
+ * bytes in out[0 .. size) (bool: one byte 0/1). */
+WH_API int wh_gguf_kv_scalar(const wh_gguf* g, uint64_t i, int* value_type, void* out8);
+/* Array value of key/value i: element type and count; for fixed-size element
+ * types `data` points at the packed little-endian elements in the mapping
+ * (unaligned), for strings and nested arrays it is NULL. */
+WH_API int wh_gguf_kv_array(const wh_gguf* g, uint64_t i, int* elem_type, uint64_t* count,
+                            const void** data);
+/* j-th element of a string array (pointer into the mapping, length). */
+WH_API int wh_gguf_kv_array_string(const wh_gguf* g, uint64_t i, uint64_t j, const char** data,
+                                   size_t* len);
+/* String value of key/value i. */
+WH_API int wh_gguf_kv_string(const wh_gguf* g, uint64_t i, const char** data, size_t* len);
+
+/* GGMLType traits for every id the reference knows (tensor_info.rs:75-183):
+ * block size, bytes per block (per element for plain types), quantized or not.
+ * WH_ERR_UNSUPPORTED_TYPE (Error::InvalidTensorType) for other ids. */
+WH_API int wh_ggml_type_traits(int ggml_type, size_t* block_size, size_t* type_size,
+                               int* is_quantized);
 
 #ifdef __cplusplus
 }

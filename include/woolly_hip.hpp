@@ -14,12 +14,16 @@
 //     GGMLType ids                                     tensor_info.rs:15-30
 //     dequantize(data, ggml_type, nelements)           dequantize.rs:189-205
 //     Error::{BufferTooSmall{needed, available}, InvalidTensorType}  error.rs:11-64
+//     GGUFLoader (from_path, tensor_info, tensor_names, tensor_data, metadata
+//       getters, alignment, file_size, total_tensor_size)   loader.rs:111-490
 // Every call runs the HIP kernels (synchronous host-memory entry points);
 // there is no CPU implementation in this header.
 #pragma once
 
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
+#include <utility>
 #include <stdexcept>
 #include <string>
 #include <variant>
@@ -209,6 +213,145 @@ inline size_t get_block_size(GGMLType t) {
 }
 // Bytes per block for the formats the library computes on; 0 otherwise.
 inline size_t get_type_size(GGMLType t) { return wh_type_size(static_cast<int>(t)); }
+
+struct Io : Error {
+  using Error::Error;
+};
+struct InvalidMagic : Error {
+  using Error::Error;
+};
+struct UnsupportedVersion : Error {
+  uint32_t version;
+  UnsupportedVersion(uint32_t v, const std::string& m) : Error(m), version(v) {}
+};
+struct InvalidMetadata : Error {
+  using Error::Error;
+};
+struct TensorNotFound : Error {
+  using Error::Error;
+};
+
+// TensorInfo (tensor_info.rs:187-258).
+struct TensorInfo {
+  std::string name;
+  std::vector<uint64_t> dims;
+  uint32_t ggml_type = 0;
+  uint64_t offset = 0, n_elements = 0, data_size = 0;
+  const std::vector<uint64_t>& shape() const { return dims; }
+};
+
+// GGUFLoader (loader.rs:111-490) over the library's native parser: the file
+// stays memory-mapped, tensor_data() is a zero-copy view, upload() moves a
+// tensor to the GPU straight from the mapping.
+class GGUFLoader {
+ public:
+  static GGUFLoader from_path(const std::string& path) {
+    wh_gguf* g = nullptr;
+    check(wh_gguf_open(path.c_str(), &g), path);
+    return GGUFLoader(g);
+  }
+  GGUFLoader(GGUFLoader&& o) noexcept : g_(o.g_), h_(o.h_) { o.g_ = nullptr; }
+  GGUFLoader(const GGUFLoader&) = delete;
+  GGUFLoader& operator=(const GGUFLoader&) = delete;
+  ~GGUFLoader() {
+    if (g_) wh_gguf_close(g_);
+  }
+
+  uint32_t version() const { return h_.version; }
+  uint64_t tensor_count() const { return h_.tensor_count; }
+  uint64_t metadata_kv_count() const { return h_.metadata_kv_count; }
+  uint32_t alignment() const { return h_.alignment; }
+  uint64_t data_start_offset() const { return h_.data_offset; }
+  size_t file_size() const { return static_cast<size_t>(h_.file_size); }
+  uint64_t total_tensor_size() const { return h_.total_tensor_size; }
+
+  // tensor_info(name): empty when absent (the reference's None).
+  bool tensor_info(const std::string& name, TensorInfo* out) const {
+    uint64_t i;
+    if (wh_gguf_find_tensor(g_, name.c_str(), &i) != WH_OK) return false;
+    *out = info_at(i);
+    return true;
+  }
+  std::vector<std::string> tensor_names() const {
+    std::vector<std::string> v;
+    for (uint64_t i = 0; i < h_.tensor_count; i++) v.push_back(info_at(i).name);
+    return v;
+  }
+  // tensor_data(name) without the copy: pointer into the mapping + size.
+  std::pair<const uint8_t*, size_t> tensor_data(const std::string& name) const {
+    const void* p = nullptr;
+    size_t n = 0;
+    check(wh_gguf_tensor_data(g_, index(name), &p, &n), name);
+    return {static_cast<const uint8_t*>(p), n};
+  }
+  // Device-resident weight straight from the mapping (release with wh_weight_free).
+  wh_weight* upload(const std::string& name) const {
+    wh_weight* w = nullptr;
+    check(wh_gguf_upload(g_, index(name), &w), name);
+    return w;
+  }
+  // GGUFMetadata getters (metadata.rs:186-233): false when absent or of another type.
+  bool get_u32(const std::string& key, uint32_t* v) const { return wh_gguf_get_u32(g_, key.c_str(), v) == WH_OK; }
+  bool get_u64(const std::string& key, uint64_t* v) const { return wh_gguf_get_u64(g_, key.c_str(), v) == WH_OK; }
+  bool get_i32(const std::string& key, int32_t* v) const { return wh_gguf_get_i32(g_, key.c_str(), v) == WH_OK; }
+  bool get_f32(const std::string& key, float* v) const { return wh_gguf_get_f32(g_, key.c_str(), v) == WH_OK; }
+  bool get_bool(const std::string& key, bool* v) const {
+    int b;
+    if (wh_gguf_get_bool(g_, key.c_str(), &b) != WH_OK) return false;
+    *v = b != 0;
+    return true;
+  }
+  bool get_string(const std::string& key, std::string* v) const {
+    const char* p;
+    size_t n;
+    if (wh_gguf_get_string(g_, key.c_str(), &p, &n) != WH_OK) return false;
+    v->assign(p, n);
+    return true;
+  }
+  std::string architecture() const {
+    std::string s;
+    get_string("general.architecture", &s);
+    return s;
+  }
+
+ private:
+  explicit GGUFLoader(wh_gguf* g) : g_(g) { wh_gguf_get_header(g_, &h_); }
+  static void check(int st, const std::string& what) {
+    if (st == WH_OK) return;
+    const std::string m = wh_last_error();
+    switch (st) {
+      case WH_ERR_IO: throw Io(m);
+      case WH_ERR_INVALID_MAGIC: throw InvalidMagic(m);
+      case WH_ERR_UNSUPPORTED_VERSION: {
+        const size_t p = m.rfind(' ');
+        throw UnsupportedVersion(static_cast<uint32_t>(std::strtoul(m.c_str() + p + 1, nullptr, 10)), m);
+      }
+      case WH_ERR_INVALID_METADATA: throw InvalidMetadata(m);
+      case WH_ERR_NOT_FOUND: throw TensorNotFound("Tensor not found: " + what);
+      case WH_ERR_UNSUPPORTED_TYPE: throw Error(m);
+      default: throw Error(m);
+    }
+  }
+  uint64_t index(const std::string& name) const {
+    uint64_t i = 0;
+    check(wh_gguf_find_tensor(g_, name.c_str(), &i), name);
+    return i;
+  }
+  TensorInfo info_at(uint64_t i) const {
+    wh_gguf_tensor t;
+    check(wh_gguf_tensor_at(g_, i, &t), "");
+    TensorInfo r;
+    r.name = t.name;
+    r.dims.assign(t.dims, t.dims + t.n_dims);
+    r.ggml_type = static_cast<uint32_t>(t.ggml_type);
+    r.offset = t.offset;
+    r.n_elements = t.n_elements;
+    r.data_size = t.data_size;
+    return r;
+  }
+  wh_gguf* g_ = nullptr;
+  wh_gguf_header h_{};
+};
 
 }  // namespace gguf
 }  // namespace woolly

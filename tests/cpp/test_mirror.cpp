@@ -2,12 +2,17 @@
 // reference's own Rust unit tests so the two read side by side:
 //   crates/woolly-tensor/src/quantization.rs:1293-1407
 //   crates/woolly-gguf/src/dequantize.rs:613-633
+//   crates/woolly-gguf/tests/load_model.rs:214-300 (GGUF loader, on a file
+//     written here with the same layout as its MockGGUFBuilder)
 // plus closed-form checks of simd::quantized_matvec and of the error mapping.
 // Every computation runs on the GPU through libwoolly_hip.  Exit status 0 iff
 // all tests pass; one line per test.
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
 #include <functional>
+#include <string>
 #include <vector>
 
 #include "woolly_hip.hpp"
@@ -44,6 +49,27 @@ BlockQ4_0 q4_0(float d, uint8_t fill) {
   b.d = f16::from_f32(d);
   std::memset(b.qs, fill, sizeof b.qs);
   return b;
+}
+
+// GGUF bytes in the layout of load_model.rs:15-145 (version 3, padding to 32).
+struct GgufWriter {
+  std::vector<uint8_t> b;
+  void u32(uint32_t v) { b.insert(b.end(), reinterpret_cast<uint8_t*>(&v), reinterpret_cast<uint8_t*>(&v) + 4); }
+  void u64(uint64_t v) { b.insert(b.end(), reinterpret_cast<uint8_t*>(&v), reinterpret_cast<uint8_t*>(&v) + 8); }
+  void str(const std::string& s) {
+    u64(s.size());
+    b.insert(b.end(), s.begin(), s.end());
+  }
+};
+
+std::string write_temp(const std::vector<uint8_t>& bytes) {
+  char path[] = "/tmp/woolly_mirror_XXXXXX";
+  const int fd = mkstemp(path);
+  if (fd < 0) throw std::runtime_error("mkstemp failed");
+  const ssize_t n = write(fd, bytes.data(), bytes.size());
+  close(fd);
+  if (n != static_cast<ssize_t>(bytes.size())) throw std::runtime_error("short write");
+  return path;
 }
 
 }  // namespace
@@ -216,6 +242,105 @@ int main() {
     const auto r = gguf::dequantize(one, gguf::GGMLType::Q4_0, 20);
     EXPECT(r.size() == 20);
     for (float v : r) EXPECT(v == -8.0f);
+  });
+
+  // load_model.rs:214-300 (tensors, mapped access, quantized tensors) and the
+  // upload of a mapped Q4_0 tensor, whose GEMV must equal the host-pointer one.
+  run("gguf_loader_tensors_and_upload", [] {
+    const int rows = 4, k = 64;
+    std::vector<BlockQ4_0> w;
+    for (int r = 0; r < rows; r++)
+      for (int b = 0; b < k / 32; b++) w.push_back(q4_0(0.25f * (r + 1), static_cast<uint8_t>(0x1F + 16 * b + r)));
+    GgufWriter g;
+    g.b = {'G', 'G', 'U', 'F'};
+    g.u32(3);
+    g.u64(2);  // tensors
+    g.u64(2);  // metadata
+    g.str("general.architecture");
+    g.u32(8);
+    g.str("llama");
+    g.str("llama.block_count");
+    g.u32(4);
+    g.u32(32);
+    g.str("blk.0.ffn_gate.weight");
+    g.u32(2);
+    g.u64(k);
+    g.u64(rows);
+    g.u32(2);
+    g.u64(0);
+    g.str("output_norm.weight");
+    g.u32(1);
+    g.u64(16);
+    g.u32(0);
+    g.u64(w.size() * sizeof(BlockQ4_0));
+    while (g.b.size() % 32) g.b.push_back(0);
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(w.data());
+    g.b.insert(g.b.end(), wb, wb + w.size() * sizeof(BlockQ4_0));
+    for (int i = 0; i < 16; i++) {
+      const float v = 0.5f * i;
+      const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
+      g.b.insert(g.b.end(), p, p + 4);
+    }
+    const std::string path = write_temp(g.b);
+    auto ld = gguf::GGUFLoader::from_path(path);
+    unlink(path.c_str());
+    EXPECT(ld.version() == 3 && ld.tensor_count() == 2 && ld.metadata_kv_count() == 2);
+    EXPECT(ld.architecture() == "llama");
+    uint32_t nl = 0;
+    EXPECT(ld.get_u32("llama.block_count", &nl) && nl == 32);
+    uint64_t nl64 = 0;
+    EXPECT(!ld.get_u64("llama.block_count", &nl64));  // other type -> none
+    gguf::TensorInfo ti;
+    EXPECT(ld.tensor_info("blk.0.ffn_gate.weight", &ti));
+    EXPECT(ti.shape().size() == 2 && ti.dims[0] == 64 && ti.dims[1] == 4 && ti.ggml_type == 2);
+    EXPECT(ti.n_elements == 256 && ti.data_size == 8 * 18);
+    EXPECT(!ld.tensor_info("missing", &ti));
+    bool not_found = false;
+    try {
+      ld.tensor_data("missing");
+    } catch (const gguf::TensorNotFound&) {
+      not_found = true;
+    }
+    EXPECT(not_found);
+    const auto norm = ld.tensor_data("output_norm.weight");
+    EXPECT(norm.second == 64);
+    float f7;
+    std::memcpy(&f7, norm.first + 28, 4);
+    EXPECT(f7 == 3.5f);
+    EXPECT(ld.total_tensor_size() == 8 * 18 + 64 && ld.file_size() == g.b.size());
+    // device upload from the mapping; GEMV vs the host-pointer path
+    wh_weight* dw = ld.upload("blk.0.ffn_gate.weight");
+    std::vector<float> x(k);
+    for (int i = 0; i < k; i++) x[i] = std::sin(0.3f * i);
+    float *dx, *dy;
+    EXPECT(wh_malloc(reinterpret_cast<void**>(&dx), 4 * k) == WH_OK);
+    EXPECT(wh_malloc(reinterpret_cast<void**>(&dy), 4 * rows) == WH_OK);
+    EXPECT(wh_memcpy_h2d(dx, x.data(), 4 * k, nullptr) == WH_OK);
+    EXPECT(wh_quantized_matvec(2, wh_weight_data(dw), 8 * 18, dx, dy, rows, k, nullptr) == WH_OK);
+    std::vector<float> y(rows), yh(rows);
+    EXPECT(wh_memcpy_d2h(y.data(), dy, 4 * rows, nullptr) == WH_OK);
+    EXPECT(wh_stream_synchronize(nullptr) == WH_OK);
+    simd::quantized_matvec(QuantizedStorage::Q4_0(w), x, yh, rows, k);
+    for (int r = 0; r < rows; r++) EXPECT(y[r] == yh[r]);
+    wh_free(dx);
+    wh_free(dy);
+    wh_weight_free(dw);
+    // load_model.rs:300-330 error cases
+    bool io = false, magic = false;
+    try {
+      gguf::GGUFLoader::from_path("/non/existent/file.gguf");
+    } catch (const gguf::Io&) {
+      io = true;
+    }
+    const std::string bad = write_temp(std::vector<uint8_t>{'B', 'A', 'D', '!', 0, 0, 0, 0, 0, 0, 0, 0,
+                                                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0});
+    try {
+      gguf::GGUFLoader::from_path(bad);
+    } catch (const gguf::InvalidMagic&) {
+      magic = true;
+    }
+    unlink(bad.c_str());
+    EXPECT(io && magic);
   });
 
   std::printf("%s: %d failed\n", g_failed ? "FAILED" : "PASSED", g_failed);

@@ -50,7 +50,9 @@ def test_gemv_unaligned_weights(gpu, orc, t, w_off):
 
 
 @pytest.mark.parametrize("t,m,k", [(Q4_0, 14336, 4096), (Q4_0, 4096, 4096), (Q8_0, 14336, 4096),
-                                   (Q4_1, 14336, 4096), (Q4_0, 4096, 14336)])
+                                   (Q4_1, 14336, 4096), (Q4_0, 4096, 14336),
+                                   (Q4_0, 1024, 4096),      # k/v projections (8 KV heads x 128)
+                                   (Q8_0, 128256, 4096)])   # Q8_0 output head (vocab 128256)
 def test_gemv_benchmark_shapes(gpu, orc, t, m, k):
     print(f"[case] gemv full type={t} {m}x{k}", flush=True)
     w = synth.quantized_weight(t, m, k, seed=3)

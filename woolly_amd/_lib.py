@@ -21,6 +21,12 @@ WH_ERR_INVALID_ARGUMENT = 4
 WH_ERR_HIP = 5
 WH_ERR_OOM = 6
 WH_ERR_NO_DEVICE = 7
+WH_ERR_IO = 8
+WH_ERR_INVALID_MAGIC = 9
+WH_ERR_UNSUPPORTED_VERSION = 10
+WH_ERR_INVALID_METADATA = 11
+WH_ERR_NOT_FOUND = 12
+WH_ERR_TYPE_MISMATCH = 13
 
 STATUS_NAMES = {
     0: "WH_OK",
@@ -31,6 +37,12 @@ STATUS_NAMES = {
     5: "WH_ERR_HIP",
     6: "WH_ERR_OOM",
     7: "WH_ERR_NO_DEVICE",
+    8: "WH_ERR_IO",
+    9: "WH_ERR_INVALID_MAGIC",
+    10: "WH_ERR_UNSUPPORTED_VERSION",
+    11: "WH_ERR_INVALID_METADATA",
+    12: "WH_ERR_NOT_FOUND",
+    13: "WH_ERR_TYPE_MISMATCH",
 }
 
 
@@ -51,6 +63,33 @@ class wh_ffn_weights(C.Structure):
         ("down", C.c_void_p),
         ("hidden", C.c_size_t),
         ("n_ff", C.c_size_t),
+    ]
+
+
+GGUF_MAX_DIMS = 8
+
+
+class wh_gguf_header(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("tensor_count", C.c_uint64),
+        ("metadata_kv_count", C.c_uint64),
+        ("alignment", C.c_uint32),
+        ("data_offset", C.c_uint64),
+        ("file_size", C.c_uint64),
+        ("total_tensor_size", C.c_uint64),
+    ]
+
+
+class wh_gguf_tensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("n_dims", C.c_uint32),
+        ("dims", C.c_uint64 * GGUF_MAX_DIMS),
+        ("ggml_type", C.c_int),
+        ("offset", C.c_uint64),
+        ("n_elements", C.c_uint64),
+        ("data_size", C.c_uint64),
     ]
 
 
@@ -106,6 +145,29 @@ SIGNATURES = {
                               C.POINTER(_sz)]),
     "wh_dequantize_host": (_int, [_int, _vp, _sz, _sz, _f32p]),
     "wh_quantized_matvec_host": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz]),
+    "wh_gguf_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
+    "wh_gguf_open_buffer": (_int, [_vp, _sz, C.POINTER(_vp)]),
+    "wh_gguf_close": (_int, [_vp]),
+    "wh_gguf_get_header": (_int, [_vp, C.POINTER(wh_gguf_header)]),
+    "wh_gguf_tensor_at": (_int, [_vp, C.c_uint64, C.POINTER(wh_gguf_tensor)]),
+    "wh_gguf_find_tensor": (_int, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "wh_gguf_tensor_data": (_int, [_vp, C.c_uint64, C.POINTER(_vp), C.POINTER(_sz)]),
+    "wh_gguf_upload": (_int, [_vp, C.c_uint64, C.POINTER(_vp)]),
+    "wh_gguf_kv_at": (_int, [_vp, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(_int)]),
+    "wh_gguf_find_kv": (_int, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "wh_gguf_get_u32": (_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "wh_gguf_get_u64": (_int, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "wh_gguf_get_i32": (_int, [_vp, C.c_char_p, C.POINTER(C.c_int32)]),
+    "wh_gguf_get_f32": (_int, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
+    "wh_gguf_get_bool": (_int, [_vp, C.c_char_p, C.POINTER(_int)]),
+    "wh_gguf_get_string": (_int, [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(_sz)]),
+    "wh_gguf_kv_scalar": (_int, [_vp, C.c_uint64, C.POINTER(_int), _vp]),
+    "wh_gguf_kv_array": (_int, [_vp, C.c_uint64, C.POINTER(_int), C.POINTER(C.c_uint64),
+                                C.POINTER(_vp)]),
+    "wh_gguf_kv_array_string": (_int, [_vp, C.c_uint64, C.c_uint64, C.POINTER(_vp),
+                                       C.POINTER(_sz)]),
+    "wh_gguf_kv_string": (_int, [_vp, C.c_uint64, C.POINTER(_vp), C.POINTER(_sz)]),
+    "wh_ggml_type_traits": (_int, [_int, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_int)]),
 }
 
 _lock = threading.Lock()

@@ -119,6 +119,12 @@ WH_API const char* wh_status_string(int status) {
     case WH_ERR_HIP: return "WH_ERR_HIP";
     case WH_ERR_OOM: return "WH_ERR_OOM";
     case WH_ERR_NO_DEVICE: return "WH_ERR_NO_DEVICE";
+    case WH_ERR_IO: return "WH_ERR_IO";
+    case WH_ERR_INVALID_MAGIC: return "WH_ERR_INVALID_MAGIC";
+    case WH_ERR_UNSUPPORTED_VERSION: return "WH_ERR_UNSUPPORTED_VERSION";
+    case WH_ERR_INVALID_METADATA: return "WH_ERR_INVALID_METADATA";
+    case WH_ERR_NOT_FOUND: return "WH_ERR_NOT_FOUND";
+    case WH_ERR_TYPE_MISMATCH: return "WH_ERR_TYPE_MISMATCH";
     default: return "WH_ERR_UNKNOWN";
   }
 }
@@ -481,11 +487,23 @@ WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_
                             size_t nbytes, wh_weight** out) {
   if (!out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_upload: null output");
   *out = nullptr;
-  int st = check_block_args("weight_upload", type, k);
-  if (st) return st;
-  st = check_weight_bytes("weight_upload", type, n_rows, k, nbytes);
-  if (st) return st;
-  const size_t need = n_rows * (k / 32) * wh::type_size(type);
+  size_t need;
+  if (type == WH_TYPE_F32 || type == WH_TYPE_F16) {
+    // plain tensors (norm weights, f16 embeddings): n_rows x k elements
+    const size_t es = wh::type_size(type);
+    if (k != 0 && (n_rows > SIZE_MAX / k || n_rows * k > SIZE_MAX / es))
+      return wh::set_error(WH_ERR_INVALID_SHAPE, "weight_upload: %zu x %zu tensor size overflows", n_rows, k);
+    need = n_rows * k * es;
+    if (nbytes < need)
+      return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                           "weight_upload: buffer too small: needed %zu bytes, available %zu", need, nbytes);
+  } else {
+    int st = check_block_args("weight_upload", type, k);
+    if (st) return st;
+    st = check_weight_bytes("weight_upload", type, n_rows, k, nbytes);
+    if (st) return st;
+    need = n_rows * (k / 32) * wh::type_size(type);
+  }
   if (need > 0 && !host_bytes)
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_upload: null host bytes");
   wh_weight* wt = new (std::nothrow) wh_weight();

@@ -98,6 +98,16 @@ class Weight:
         self.handle = h.value
         self.ggml_type, self.n_rows, self.k = ggml_type, n_rows, k
 
+    @classmethod
+    def from_handle(cls, handle: int) -> "Weight":
+        """Wraps a wh_weight* made by another entry point (wh_gguf_upload)."""
+        w = cls.__new__(cls)
+        w.handle = handle
+        t, n, k = C.c_int(), C.c_size_t(), C.c_size_t()
+        _lib.check(_lib.load().wh_weight_info(handle, C.byref(t), C.byref(n), C.byref(k), None))
+        w.ggml_type, w.n_rows, w.k = t.value, n.value, k.value
+        return w
+
     @property
     def ptr(self) -> int:
         return int(_lib.load().wh_weight_data(self.handle) or 0)
