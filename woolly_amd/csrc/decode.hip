@@ -1,0 +1,261 @@
+// decode.hip -- the single-token decode step: C ABI of the fused attention
+// projections, the attention, the residual projections, one layer and the
+// whole step (host code; the kernels live in gemv.hip and attention.hip).
+//
+// One layer for one token (LazyTransformer::process_layer,
+// crates/woolly-core/src/model/lazy_transformer.rs:98-258) is six launches:
+//   1. qkv = [Wq; Wk; Wv] rms_norm(x, attn_norm)      gemv, 3 stacked matrices + RMSNorm
+//   2-3. attention partials + combine (RoPE, KV store) attention.hip
+//   4. x = x + Wo attn                                gemv + residual
+//   5. h = silu(Wg x_hat) (Wu x_hat), x_hat = rms_norm(x, ffn_norm)
+//                                                     fused gate/up gemv
+//   6. x = x + Wd h                                   gemv + residual
+// and the step ends with logits = Wout rms_norm(x, output_norm) (gemv +
+// RMSNorm).  Nothing here allocates or synchronises, so a caller can capture
+// the step into a HIP graph.
+#include <cmath>
+
+#include "wh_common.hpp"
+
+namespace {
+
+hipStream_t hs(wh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+int check_type(const char* fn, int type) {
+  if (!wh::is_block_type(type))
+    return wh::set_error(WH_ERR_UNSUPPORTED_TYPE,
+                         "%s: unsupported quantization scheme (ggml type %d); supported: Q4_0 (2), Q4_1 (3), Q8_0 (8)",
+                         fn, type);
+  return WH_OK;
+}
+
+// Fused GEMV with the RMSNorm done separately when the fused kernel does not
+// take the shape: x_hat into `scratch` (k floats), then the same call without
+// gamma.
+int gemv_fused_or_split(int type, const void* const* mats, const size_t* rows, int n_mats, const float* x,
+                        const float* gamma, float eps, const float* residual, float* y, size_t k, float* scratch,
+                        hipStream_t s) {
+  int st = wh::launch_gemv_fused(type, mats, rows, n_mats, x, gamma, eps, residual, y, k, s);
+  if (st != WH_ERR_INVALID_SHAPE || !gamma) return st;
+  if (!scratch) return wh::set_error(WH_ERR_BUFFER_TOO_SMALL, "fused gemv: workspace needed for this shape");
+  st = wh::launch_rms_norm(x, gamma, eps, 1, k, scratch, s);
+  if (st) return st;
+  return wh::launch_gemv_fused(type, mats, rows, n_mats, scratch, nullptr, 0.f, residual, y, k, s);
+}
+
+// Workspace of the decode step (all offsets 256-byte aligned).
+struct StepWs {
+  float* qkv;     // (n_heads + 2 n_kv_heads) * head_dim
+  float* attn;    // n_heads * head_dim
+  float* h;       // n_ff
+  float* u;       // n_ff (unfused FFN only)
+  float* xn;      // hidden (RMSNorm scratch for shapes the fused kernels do not take)
+  float* part;    // attention partials
+  size_t bytes;
+};
+
+StepWs step_layout(const wh_llama_model* m, void* base) {
+  StepWs w{};
+  char* p = static_cast<char*>(base);
+  size_t off = 0;
+  const size_t qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+  auto take = [&](size_t bytes) {
+    float* r = p ? reinterpret_cast<float*>(p + off) : nullptr;
+    off += al256(bytes);
+    return r;
+  };
+  w.qkv = take(4 * (qd + 2 * kvd));
+  w.attn = take(4 * qd);
+  w.h = take(4 * m->n_ff);
+  w.u = take(4 * m->n_ff);
+  w.xn = take(4 * (m->hidden > m->n_ff ? m->hidden : m->n_ff));
+  w.part = take(wh::attention_workspace_bytes(m->n_heads, m->head_dim, m->max_ctx, m->n_kv_heads));
+  w.bytes = off;
+  return w;
+}
+
+int check_model(const char* fn, const wh_llama_model* m) {
+  if (!m || !m->layers || !m->rope_inv_freq)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: null model, layers or rope_inv_freq", fn);
+  int st = check_type(fn, m->type);
+  if (st) return st;
+  if (m->hidden == 0 || m->hidden % 32 != 0 || m->n_ff % 32 != 0 || (m->n_heads * m->head_dim) % 32 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: hidden, n_ff and n_heads * head_dim must be multiples of 32",
+                         fn);
+  if (!wh::attention_shape_ok(m->n_heads, m->n_kv_heads, m->head_dim))
+    return wh::set_error(WH_ERR_INVALID_SHAPE,
+                         "%s: attention shape not supported (head_dim 64 or 128, n_heads a multiple of "
+                         "n_kv_heads, at most 8 query heads per KV head)",
+                         fn);
+  if (m->max_ctx == 0) return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: max_ctx is 0", fn);
+  for (size_t l = 0; l < m->n_layers; l++) {
+    const wh_llama_layer& L = m->layers[l];
+    if (!L.k_cache || !L.v_cache || !wh::aligned(L.k_cache, 16) || !wh::aligned(L.v_cache, 16))
+      return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: layer %zu KV caches must be non-null and 16-byte aligned",
+                           fn, l);
+  }
+  return WH_OK;
+}
+
+int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, float* x, const StepWs& w,
+               hipStream_t s) {
+  const size_t D = m->head_dim, qd = m->n_heads * D, kvd = m->n_kv_heads * D;
+  // 1. qkv
+  const void* mats[3] = {L.wq, L.wk, L.wv};
+  const size_t rows[3] = {qd, kvd, kvd};
+  int st = gemv_fused_or_split(m->type, mats, rows, 3, x, L.attn_norm, m->eps, nullptr, w.qkv, m->hidden, w.xn, s);
+  if (st) return st;
+  // 2-3. attention
+  st = wh::launch_attention_decode(w.qkv, L.k_cache, L.v_cache, pos, m->n_heads, m->n_kv_heads, D,
+                                   m->rope_inv_freq, w.attn, w.part, s);
+  if (st) return st;
+  // 4. x += Wo attn
+  const void* wo[1] = {L.wo};
+  const size_t hr[1] = {m->hidden};
+  st = wh::launch_gemv_fused(m->type, wo, hr, 1, w.attn, nullptr, 0.f, x, x, qd, s);
+  if (st) return st;
+  // 5. h = silu(gate) * up of rms_norm(x)
+  st = wh::launch_ffn_gate_up(m->type, L.w_gate, L.w_up, x, L.ffn_norm, m->eps, w.h, m->n_ff, m->hidden, s);
+  if (st == WH_ERR_INVALID_SHAPE) {
+    // unfused: rms_norm -> gate, up -> swiglu
+    st = wh::launch_rms_norm(x, L.ffn_norm, m->eps, 1, m->hidden, w.xn, s);
+    if (!st) st = wh::launch_gemv(m->type, L.w_gate, w.xn, w.h, m->n_ff, m->hidden, s);
+    if (!st) st = wh::launch_gemv(m->type, L.w_up, w.xn, w.u, m->n_ff, m->hidden, s);
+    if (!st) st = wh::launch_swiglu(w.h, w.u, m->n_ff, w.h, s);
+  }
+  if (st) return st;
+  // 6. x += Wd h
+  const void* wd[1] = {L.w_down};
+  return wh::launch_gemv_fused(m->type, wd, hr, 1, w.h, nullptr, 0.f, x, x, m->n_ff, s);
+}
+
+}  // namespace
+
+WH_API int wh_rope_inv_freq(float base, size_t head_dim, float* out_host) {
+  if (!out_host) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "rope_inv_freq: null output");
+  if (head_dim == 0 || head_dim % 2 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "rope_inv_freq: head_dim %zu must be even", head_dim);
+  // ops/mod.rs:490-494, in f32: freqs[i] = 1.0 / base.powf(2.0 * i / head_dim)
+  for (size_t i = 0; i < head_dim / 2; i++) {
+    const float e = (2.0f * static_cast<float>(i)) / static_cast<float>(head_dim);
+    out_host[i] = 1.0f / powf(base, e);
+  }
+  return WH_OK;
+}
+
+WH_API size_t wh_attention_qkv_workspace_bytes(size_t hidden) { return 4 * hidden; }
+
+WH_API int wh_attention_qkv(int type, const void* wq, const void* wk, const void* wv, size_t q_rows,
+                            size_t kv_rows, size_t hidden, const float* gamma, float eps, const float* x,
+                            float* qkv, void* workspace, size_t workspace_bytes, wh_stream_t stream) {
+  int st = check_type("attention_qkv", type);
+  if (st) return st;
+  if (hidden % 32 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "attention_qkv: hidden = %zu is not a multiple of 32", hidden);
+  if (!wq || !wk || !wv || !gamma || !x || !qkv)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "attention_qkv: null pointer");
+  if (q_rows + 2 * kv_rows == 0) return WH_OK;
+  float* scratch = workspace_bytes >= 4 * hidden ? static_cast<float*>(workspace) : nullptr;
+  const void* mats[3] = {wq, wk, wv};
+  const size_t rows[3] = {q_rows, kv_rows, kv_rows};
+  return gemv_fused_or_split(type, mats, rows, 3, x, gamma, eps, nullptr, qkv, hidden, scratch, hs(stream));
+}
+
+WH_API size_t wh_attention_workspace_bytes(size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_ctx) {
+  return wh::attention_workspace_bytes(n_heads, head_dim, max_ctx, n_kv_heads);
+}
+
+WH_API int wh_attention_decode(const float* qkv, void* k_cache, void* v_cache, size_t pos, size_t n_heads,
+                               size_t n_kv_heads, size_t head_dim, const float* inv_freq, float* out,
+                               void* workspace, size_t workspace_bytes, wh_stream_t stream) {
+  if (!qkv || !k_cache || !v_cache || !inv_freq || !out || !workspace)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "attention_decode: null pointer");
+  if (!wh::attention_shape_ok(n_heads, n_kv_heads, head_dim))
+    return wh::set_error(WH_ERR_INVALID_SHAPE,
+                         "attention_decode: head_dim %zu, %zu heads, %zu KV heads not supported", head_dim,
+                         n_heads, n_kv_heads);
+  if (!wh::aligned(k_cache, 16) || !wh::aligned(v_cache, 16))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "attention_decode: caches must be 16-byte aligned");
+  const size_t need = wh::attention_workspace_bytes(n_heads, head_dim, pos + 1, n_kv_heads);
+  if (workspace_bytes < need)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "attention_decode: workspace too small: needed %zu bytes, available %zu", need,
+                         workspace_bytes);
+  return wh::launch_attention_decode(qkv, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim, inv_freq, out,
+                                     workspace, hs(stream));
+}
+
+WH_API int wh_quantized_matvec_residual(int type, const void* weights, size_t weight_nbytes, const float* input,
+                                        const float* residual, float* output, size_t m, size_t k,
+                                        wh_stream_t stream) {
+  int st = check_type("quantized_matvec_residual", type);
+  if (st) return st;
+  if (k % 32 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "quantized_matvec_residual: k = %zu is not a multiple of 32", k);
+  const size_t need = m * (k / 32) * wh::type_size(type);
+  if (weight_nbytes < need)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "quantized_matvec_residual: buffer too small: needed %zu bytes, available %zu", need,
+                         weight_nbytes);
+  if (m == 0) return WH_OK;
+  if (!weights || !input || !residual || !output)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matvec_residual: null pointer");
+  if (m >= (static_cast<size_t>(1) << 31))
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "quantized_matvec_residual: %zu rows exceed 2^31", m);
+  const void* mats[1] = {weights};
+  const size_t rows[1] = {m};
+  return wh::launch_gemv_fused(type, mats, rows, 1, input, nullptr, 0.f, residual, output, k, hs(stream));
+}
+
+WH_API size_t wh_llama_decode_workspace_bytes(const wh_llama_model* model) {
+  if (!model) return 0;
+  return step_layout(model, nullptr).bytes;
+}
+
+WH_API int wh_llama_layer_decode(const wh_llama_model* model, size_t layer, size_t pos, float* x, void* workspace,
+                                 size_t workspace_bytes, wh_stream_t stream) {
+  int st = check_model("llama_layer_decode", model);
+  if (st) return st;
+  if (layer >= model->n_layers)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_layer_decode: layer %zu of %zu", layer, model->n_layers);
+  if (pos >= model->max_ctx)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "llama_layer_decode: position %zu beyond max_ctx %zu", pos,
+                         model->max_ctx);
+  const StepWs w = step_layout(model, workspace);
+  if (!workspace || workspace_bytes < w.bytes)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "llama_layer_decode: workspace too small: needed %zu bytes, available %zu", w.bytes,
+                         workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!x) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_layer_decode: null x");
+  return layer_step(model, model->layers[layer], pos, x, w, hs(stream));
+}
+
+WH_API int wh_llama_decode_step(const wh_llama_model* model, size_t pos, float* x, float* logits, void* workspace,
+                                size_t workspace_bytes, wh_stream_t stream) {
+  int st = check_model("llama_decode_step", model);
+  if (st) return st;
+  if (pos >= model->max_ctx)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "llama_decode_step: position %zu beyond max_ctx %zu", pos,
+                         model->max_ctx);
+  const StepWs w = step_layout(model, workspace);
+  if (!workspace || workspace_bytes < w.bytes)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "llama_decode_step: workspace too small: needed %zu bytes, available %zu", w.bytes,
+                         workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!x) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_decode_step: null x");
+  for (size_t l = 0; l < model->n_layers; l++) {
+    st = layer_step(model, model->layers[l], pos, x, w, hs(stream));
+    if (st) return st;
+  }
+  if (!logits) return WH_OK;
+  st = check_type("llama_decode_step (output head)", model->output_type);
+  if (st) return st;
+  if (!model->output || !model->output_norm)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_decode_step: null output head or output_norm");
+  const void* head[1] = {model->output};
+  const size_t rows[1] = {model->vocab};
+  return gemv_fused_or_split(model->output_type, head, rows, 1, x, model->output_norm, model->eps, nullptr, logits,
+                             model->hidden, w.xn, hs(stream));
+}

@@ -17,6 +17,8 @@
 //
 // Generic path: one wave per row, lanes stride over blocks with byte loads;
 // used for odd block counts, unaligned pointers and K > 16384.
+#include <algorithm>
+
 #include "wh_blocks.hpp"
 
 namespace {
@@ -241,20 +243,64 @@ __device__ __forceinline__ void load_vec(const uint32_t* __restrict__ src, bool 
   for (int c = 0; c < V; c++) dst[c] = ok ? __builtin_nontemporal_load(src + c) : 0u;
 }
 
+// Arguments of the streaming kernels.  Plain mode (FFN = false): the output
+// rows are stacked from up to three matrices with the same K, rows [0, n0)
+// from W, [n0, n0 + n1) from W2, the rest from W3 (a single matrix has
+// n0 = n_rows); this is how the Q, K and V projections of one token run as one
+// launch.  FFN mode: W (gate) and W2 (up) are streamed side by side.  With
+// gamma set, x is RMS-normalised while staged (rms = sqrt(sum x^2 / K + eps),
+// x_hat = (x / rms) * gamma, tensor_utils.rs:446-480); with residual set,
+// y[row] = residual[row] + result (the residual adds of process_layer,
+// lazy_transformer.rs:98-258).
+struct GemvArgs {
+  const uint8_t* W;
+  const uint8_t* W2;
+  const uint8_t* W3;
+  int n0, n1;
+  const float* x;
+  const float* gamma;
+  float eps;
+  const float* residual;
+  float* y;
+  int n_rows, pairs_per_row, ks, rows_per_wg;
+};
+
+// Compile-time variants of the streaming kernels (MODE bit set): RMSNorm of
+// x while staged, residual add at the store, rows stacked from up to three
+// matrices.  The plain GEMV (MODE 0) carries none of their code.
+constexpr int kNorm = 1, kResid = 2, kStack = 4;
+
+// Matrix and local row of output row `row` in plain (stacked) mode.
+__device__ __forceinline__ const uint8_t* stacked_row(const GemvArgs& a, int row, int* local) {
+  int r = row;
+  const uint8_t* b = a.W;
+  if (r >= a.n0) {
+    r -= a.n0;
+    b = a.W2;
+    if (r >= a.n1) {
+      r -= a.n1;
+      b = a.W3;
+    }
+  }
+  *local = r;
+  return b;
+}
+
+// RMSNorm of the x staged in LDS (padded layout, 4 floats per 64), in place;
+// red holds kWaves partial sums.  Fixed-shape reduction: deterministic.
+__device__ __forceinline__ void norm_staged_x(float* xs, float* red, int K, const float* gamma, float eps,
+                                              int wave, int lane);
+
 // FFN = true: the FFN's first half for one token (the decode step): x is
 // RMS-normalised with gamma while staged (rms = sqrt(sum x^2 / K + eps),
 // x_hat = (x / rms) * gamma, tensor_utils.rs:446-480), the gate row (W) and
 // the up row (W2) of every output index are streamed side by side, and
 // y = silu(gate . x_hat) * (up . x_hat) (tensor_utils.rs:512-532).
-template <int TYPE, bool FFN>
-__global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t* __restrict__ W,
-                                                                  const uint8_t* __restrict__ W2,
-                                                                  const float* __restrict__ x,
-                                                                  const float* __restrict__ gamma,
-                                                                  float eps,
-                                                                  float* __restrict__ y, int n_rows,
-                                                                  int pairs_per_row, int ks,
-                                                                  int rows_per_wg) {
+template <int TYPE, bool FFN, int MODE>
+__global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const GemvArgs a) {
+  const int n_rows = a.n_rows, pairs_per_row = a.pairs_per_row, ks = a.ks, rows_per_wg = a.rows_per_wg;
+  const float* __restrict__ x = a.x;
+  float* __restrict__ y = a.y;
   constexpr int DW = PairFmt<TYPE>::DW;
   constexpr int PB = PairFmt<TYPE>::BYTES;
   constexpr int V = LoadFmt<TYPE>::V;
@@ -279,19 +325,20 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
   const int r1 = min(n_rows, r0 + rows_per_wg);
   const int nk = (r1 - r0 + groups - 1) / groups;           // row steps (uniform in the WG)
   const size_t row_bytes = static_cast<size_t>(pairs_per_row) * PB;
-  const uint8_t* slice_base[NM];
-  slice_base[0] = W + static_cast<size_t>(64 * s) * PB;
-  if constexpr (FFN) slice_base[NM - 1] = W2 + static_cast<size_t>(64 * s) * PB;
+  const size_t slice_off = static_cast<size_t>(64 * s) * PB;
 
   // Prefetch the first rows before anything else.
   uint32_t buf[kPrefetch][NM][DW];
   auto fetch = [&](uint32_t (*dst)[DW], int k) {
     const int row = r0 + g + k * groups;
     const bool rok = k < nk && row < r1;
+    int local = row;
+    const uint8_t* base0 = a.W;
+    if constexpr ((MODE & kStack) != 0) base0 = stacked_row(a, rok ? row : r0, &local);
 #pragma unroll
     for (int mtx = 0; mtx < NM; mtx++) {
-      const uint32_t* src =
-          reinterpret_cast<const uint32_t*>(slice_base[mtx] + static_cast<size_t>(row) * row_bytes);
+      const uint8_t* base = mtx ? a.W2 : base0;
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(base + slice_off + static_cast<size_t>(local) * row_bytes);
 #pragma unroll
       for (int i = 0; i < NV; i++) {
         const int e = V * (64 * i + lane);
@@ -309,26 +356,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
     *reinterpret_cast<float4*>(xs + e + (e >> 6) * 4) = t;
   }
   __syncthreads();
-  if constexpr (FFN) {
-    // RMSNorm of the staged x: fixed-shape reduction, then x_hat in place.
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
-      const float v = xs[i + (i >> 6) * 4];
-      ss = __builtin_fmaf(v, v, ss);
-    }
-    ss = whd::wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) total += red[w];
-    const float rms = sqrtf(total / static_cast<float>(K) + eps);
-    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
-      float* p = xs + i + (i >> 6) * 4;
-      *p = (*p / rms) * gamma[i];
-    }
-    __syncthreads();
-  }
+  if constexpr ((MODE & kNorm) != 0) norm_staged_x(xs, red, K, a.gamma, a.eps, wave, lane);
   float xv[64];
   {
     const int p = 64 * s + (active ? lane : 0);
@@ -390,7 +418,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
       }
       __builtin_amdgcn_wave_barrier();
       if (ks == 1) {
-        if (lane == 63 && row < r1) y[row] = combine(tot[0], tot[NM - 1]);
+        if (lane == 63 && row < r1) y[row] = ((MODE & kResid) != 0 ? a.residual[row] : 0.f) + combine(tot[0], tot[NM - 1]);
       } else {
         if (lane == 63) {
 #pragma unroll
@@ -404,7 +432,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
             t[mtx] = red[mtx * kWaves + g * ks];
             for (int s2 = 1; s2 < ks; s2++) t[mtx] += red[mtx * kWaves + g * ks + s2];
           }
-          y[row] = combine(t[0], t[NM - 1]);
+          y[row] = ((MODE & kResid) != 0 ? a.residual[row] : 0.f) + combine(t[0], t[NM - 1]);
         }
         __syncthreads();
       }
@@ -421,9 +449,17 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const uint8_t*
 // issued through inline asm (the compiler would otherwise wait for every copy
 // in flight before each LDS read); every wave issues exactly NI copies per
 // matrix per row, so completion is tracked with a constant vmcnt.
+// `base` and `lds` are wave-uniform; readfirstlane puts them in SGPRs.  The
+// builtin returns a signed int: each half is taken back to uint32_t before
+// the halves are joined (a sign-extended low half would corrupt the pointer).
 __device__ __forceinline__ void ring_copy16(const void* base, uint32_t voff, uint32_t lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint64_t ub = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(reinterpret_cast<const void*>(ub)),
+               "s"(m0)
                : "memory");
 }
 template <int N>
@@ -438,14 +474,11 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 template <int TYPE>
 constexpr int ring_ni() { return (PairFmt<TYPE>::DW * 64 * 4 + 1023) / 1024; }  // copies per full slice
 
-template <int TYPE, bool FFN, int RD>
-__global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* __restrict__ W,
-                                                                const uint8_t* __restrict__ W2,
-                                                                const float* __restrict__ x,
-                                                                const float* __restrict__ gamma,
-                                                                float eps, float* __restrict__ y,
-                                                                int n_rows, int pairs_per_row, int ks,
-                                                                int rows_per_wg) {
+template <int TYPE, bool FFN, int RD, int MODE>
+__global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const GemvArgs a) {
+  const int n_rows = a.n_rows, pairs_per_row = a.pairs_per_row, ks = a.ks, rows_per_wg = a.rows_per_wg;
+  const float* __restrict__ x = a.x;
+  float* __restrict__ y = a.y;
   constexpr int DW = PairFmt<TYPE>::DW;
   constexpr int PB = PairFmt<TYPE>::BYTES;
   constexpr int NM = FFN ? 2 : 1;
@@ -480,11 +513,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
   const int nchunks = nbytes / 16;
   auto issue = [&](int k) {
     const int row = min(r0 + g + k * groups, r1 - 1);
-    const uint32_t base_off = static_cast<uint32_t>(row) * row_bytes + slice_off;
+    int local = row;
+    const uint8_t* base0 = a.W;
+    if constexpr ((MODE & kStack) != 0) base0 = stacked_row(a, row, &local);
+    const uint32_t base_off = static_cast<uint32_t>(local) * row_bytes + slice_off;
 #pragma unroll
     for (int mtx = 0; mtx < NM; mtx++) {
       const uint32_t slot = ring_lds + static_cast<uint32_t>((mtx * RD + (k % RD)) * SLOT);
-      const void* base = mtx ? static_cast<const void*>(W2) : static_cast<const void*>(W);
+      const void* base = mtx ? static_cast<const void*>(a.W2) : static_cast<const void*>(base0);
 #pragma unroll
       for (int i = 0; i < NI; i++) {
         if (64 * i < nchunks) {
@@ -509,25 +545,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
     *reinterpret_cast<float4*>(xs + e + (e >> 6) * 4) = t;
   }
   __syncthreads();
-  if constexpr (FFN) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
-      const float v = xs[i + (i >> 6) * 4];
-      ss = __builtin_fmaf(v, v, ss);
-    }
-    ss = whd::wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) total += red[w];
-    const float rms = sqrtf(total / static_cast<float>(K) + eps);
-    for (int i = threadIdx.x; i < K; i += kWaves * 64) {
-      float* p = xs + i + (i >> 6) * 4;
-      *p = (*p / rms) * gamma[i];
-    }
-    __syncthreads();
-  }
+  if constexpr ((MODE & kNorm) != 0) norm_staged_x(xs, red, K, a.gamma, a.eps, wave, lane);
   float xv[64];
   {
     const int p = 64 * s + (active ? lane : 0);
@@ -577,7 +595,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
       tot[mtx] = wave_sum_to_lane63(part);
     }
     if (ks == 1) {
-      if (lane == 63 && row < r1) y[row] = combine(tot[0], tot[NM - 1]);
+      if (lane == 63 && row < r1) y[row] = ((MODE & kResid) != 0 ? a.residual[row] : 0.f) + combine(tot[0], tot[NM - 1]);
     } else {
       if (lane == 63) {
 #pragma unroll
@@ -595,7 +613,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
           t[mtx] = red[mtx * kWaves + g * ks];
           for (int s2 = 1; s2 < ks; s2++) t[mtx] += red[mtx * kWaves + g * ks + s2];
         }
-        y[row] = combine(t[0], t[NM - 1]);
+        y[row] = ((MODE & kResid) != 0 ? a.residual[row] : 0.f) + combine(t[0], t[NM - 1]);
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
@@ -603,6 +621,27 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const uint8_t* _
     }
   }
   ring_wait<0>();  // no copy may land in LDS after the workgroup has exited
+}
+
+__device__ __forceinline__ void norm_staged_x(float* xs, float* red, int K, const float* gamma, float eps,
+                                              int wave, int lane) {
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+    const float v = xs[i + (i >> 6) * 4];
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = whd::wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) total += red[w];
+  const float rms = sqrtf(total / static_cast<float>(K) + eps);
+  for (int i = threadIdx.x; i < K; i += kWaves * 64) {
+    float* p = xs + i + (i >> 6) * 4;
+    *p = (*p / rms) * gamma[i];
+  }
+  __syncthreads();
 }
 
 size_t ring_lds_bytes(int type, int K, int nm, int rd) {
@@ -616,61 +655,77 @@ size_t stream_lds_bytes(int type, int K, int nm) {
   return 4u * static_cast<size_t>(K + K / 16 + nm * kWaves * (dw * 64 + 4) + nm * kWaves);
 }
 
+// One wave per output row, lanes stride over blocks with byte loads.  Rows
+// are stacked from up to three matrices and the residual is added as in the
+// streaming kernels (a.n_rows rows, K = 32 nb; no RMSNorm: the caller
+// normalises x first).
 template <int TYPE>
-__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __restrict__ W,
-                                                           const float* __restrict__ x,
-                                                           float* __restrict__ y, size_t n_rows,
-                                                           size_t nb) {
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs a, size_t nb) {
   constexpr int TS = whd::BlockFmt<TYPE>::BYTES;
   const int lane = threadIdx.x & 63;
+  const size_t n_rows = static_cast<size_t>(a.n_rows);
   const size_t stride = static_cast<size_t>(gridDim.x) * (blockDim.x >> 6);
   for (size_t row = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
        row < n_rows; row += stride) {
+    int local;
+    const uint8_t* W = stacked_row(a, static_cast<int>(row), &local);
     float acc = 0.f;
     for (size_t b = lane; b < nb; b += 64) {
       float v[32];
-      whd::decode_block_bytes<TYPE>(W + (row * nb + b) * TS, v);
-      const float* xb = x + b * 32;
+      whd::decode_block_bytes<TYPE>(W + (static_cast<size_t>(local) * nb + b) * TS, v);
+      const float* xb = a.x + b * 32;
 #pragma unroll
       for (int j = 0; j < 32; j++) acc = __builtin_fmaf(v[j], xb[j], acc);
     }
     acc = whd::wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    if (lane == 0) a.y[row] = (a.residual ? a.residual[row] : 0.f) + acc;
   }
+}
+
+template <int TYPE>
+int launch_generic(const GemvArgs& a, size_t k, hipStream_t s) {
+  size_t grid = (static_cast<size_t>(a.n_rows) + 3) / 4;
+  const size_t cap = static_cast<size_t>(wh::cu_count()) * 16;
+  if (grid > cap) grid = cap;
+  if (grid < 1) grid = 1;
+  gemv_generic_kernel<TYPE><<<static_cast<unsigned>(grid), 256, 0, s>>>(a, k / 32);
+  WH_LAUNCH_CHECK("gemv kernel launch");
+  return WH_OK;
 }
 
 // Chooses the streaming kernel when its layout conditions hold (an even
 // number of blocks per row, at most 4 K-slices, 4-byte aligned weights,
 // 16-byte aligned x, LDS within the device limit).
 template <int TYPE, bool FFN>
-bool stream_ok(const uint8_t* w, const uint8_t* w2, const float* x, size_t n_rows, size_t k) {
+bool stream_ok(const GemvArgs& a, size_t k) {
   const size_t nb = k / 32;
   const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k), FFN ? 2 : 1);
-  return (nb % 2 == 0) && nb > 0 && nb / 2 <= 64 * kMaxSlices && wh::aligned(w, 4) &&
-         (!FFN || wh::aligned(w2, 4)) && wh::aligned(x, 16) && n_rows < (1u << 30) &&
-         lds <= wh::max_lds_per_block();
+  const bool w2_used = FFN || a.n1 > 0;
+  const bool w3_used = !FFN && a.n_rows > a.n0 + a.n1;
+  return (nb % 2 == 0) && nb > 0 && nb / 2 <= 64 * kMaxSlices && wh::aligned(a.W, 4) &&
+         (!w2_used || wh::aligned(a.W2, 4)) && (!w3_used || wh::aligned(a.W3, 4)) && wh::aligned(a.x, 16) &&
+         a.n_rows >= 0 && lds <= wh::max_lds_per_block();
 }
 
 #ifndef WH_GEMV_RING
 #define WH_GEMV_RING 1
 #endif
 
-template <int TYPE, bool FFN, int RD>
-int launch_ring(const uint8_t* w, const uint8_t* w2, const float* x, const float* gamma, float eps,
-                float* y, size_t n_rows, size_t k, int grid, int ks, int rows_per_wg, size_t lds,
-                hipStream_t s) {
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_ring_kernel<TYPE, FFN, RD>),
+template <int TYPE, bool FFN, int RD, int MODE>
+int launch_ring(const GemvArgs& a, int grid, size_t lds, hipStream_t s) {
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_ring_kernel<TYPE, FFN, RD, MODE>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-  gemv_ring_kernel<TYPE, FFN, RD><<<grid, kWaves * 64, lds, s>>>(w, w2, x, gamma, eps, y, static_cast<int>(n_rows),
-                                                                 static_cast<int>(k / 64), ks, rows_per_wg);
+  gemv_ring_kernel<TYPE, FFN, RD, MODE><<<grid, kWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
   return WH_OK;
 }
 
-template <int TYPE, bool FFN>
-int launch_stream(const uint8_t* w, const uint8_t* w2, const float* x, const float* gamma, float eps,
-                  float* y, size_t n_rows, size_t k, hipStream_t s) {
+// Fills the work split of `a` (K-slices per row, workgroups, rows per
+// workgroup) and launches the ring or the register-staged kernel variant MODE.
+template <int TYPE, bool FFN, int MODE>
+int launch_stream(GemvArgs a, size_t k, hipStream_t s) {
   const int cus = wh::cu_count();
+  const size_t n_rows = static_cast<size_t>(a.n_rows);
   const size_t lds = stream_lds_bytes(TYPE, static_cast<int>(k), FFN ? 2 : 1);
   const int P = static_cast<int>(k / 64);
   int ks = (P + 63) / 64;
@@ -678,53 +733,75 @@ int launch_stream(const uint8_t* w, const uint8_t* w2, const float* x, const flo
   const int groups = kWaves / ks;
   const size_t max_wg = (n_rows + groups - 1) / groups;
   const int grid = static_cast<int>(max_wg < static_cast<size_t>(cus) ? max_wg : cus);
-  const int rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
+  a.pairs_per_row = P;
+  a.ks = ks;
+  a.rows_per_wg = static_cast<int>((n_rows + grid - 1) / grid);
   // Ring kernel: every K-slice a whole number of 16-byte chunks, 32-bit byte
-  // offsets, and a ring of at least two slots per wave within the LDS limit.
+  // offsets within each matrix, and a ring of at least two slots per wave
+  // within the LDS limit.
   const int tail = P % 64;
   const bool chunks_ok = (PairFmt<TYPE>::BYTES * 64) % 16 == 0 && (PairFmt<TYPE>::BYTES * tail) % 16 == 0;
+  const size_t max_mrows = FFN ? n_rows
+                               : std::max({static_cast<size_t>(a.n0), static_cast<size_t>(a.n1),
+                                           n_rows - std::min(n_rows, static_cast<size_t>(a.n0 + a.n1))});
   // Measured on MI355X (14336 x 4096 and 4096 x 14336): the ring wins for
   // Q8_0 (more bytes per row) and for the FFN's two matrices; the 4-bit
   // single-matrix GEMV is bound by its unpacking arithmetic and keeps the
   // register-staged kernel.
   const bool ring_pays = TYPE == WH_TYPE_Q8_0 || FFN;
   if (WH_GEMV_RING && ring_pays && chunks_ok &&
-      n_rows * (k / 64) * PairFmt<TYPE>::BYTES < (static_cast<size_t>(1) << 32)) {
+      max_mrows * (k / 64) * PairFmt<TYPE>::BYTES < (static_cast<size_t>(1) << 32)) {
     const int nm = FFN ? 2 : 1;
     const size_t maxl = wh::max_lds_per_block();
-    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 4) <= maxl)
-      return launch_ring<TYPE, FFN, 4>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
-                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 4), s);
-    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 3) <= maxl)
-      return launch_ring<TYPE, FFN, 3>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
-                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 3), s);
-    if (ring_lds_bytes(TYPE, static_cast<int>(k), nm, 2) <= maxl)
-      return launch_ring<TYPE, FFN, 2>(w, w2, x, gamma, eps, y, n_rows, k, grid, ks, rows_per_wg,
-                                       ring_lds_bytes(TYPE, static_cast<int>(k), nm, 2), s);
+    const int K = static_cast<int>(k);
+    if (ring_lds_bytes(TYPE, K, nm, 4) <= maxl)
+      return launch_ring<TYPE, FFN, 4, MODE>(a, grid, ring_lds_bytes(TYPE, K, nm, 4), s);
+    if (ring_lds_bytes(TYPE, K, nm, 3) <= maxl)
+      return launch_ring<TYPE, FFN, 3, MODE>(a, grid, ring_lds_bytes(TYPE, K, nm, 3), s);
+    if (ring_lds_bytes(TYPE, K, nm, 2) <= maxl)
+      return launch_ring<TYPE, FFN, 2, MODE>(a, grid, ring_lds_bytes(TYPE, K, nm, 2), s);
   }
   if (lds > 65536) {
-    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE, FFN>),
+    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE, FFN, MODE>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   }
-  gemv_stream_kernel<TYPE, FFN><<<grid, kWaves * 64, lds, s>>>(w, w2, x, gamma, eps, y,
-                                                               static_cast<int>(n_rows), P, ks, rows_per_wg);
+  gemv_stream_kernel<TYPE, FFN, MODE><<<grid, kWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
   return WH_OK;
+}
+
+// The variants the decode step uses get their own code: Q/K/V (norm +
+// stacked), the output head (norm), the residual projections; any other
+// combination runs the variant with every feature on.
+template <int TYPE>
+int launch_fused_mode(const GemvArgs& a, size_t k, int mode, hipStream_t s) {
+  switch (mode) {
+    case 0: return launch_stream<TYPE, false, 0>(a, k, s);
+    case kNorm: return launch_stream<TYPE, false, kNorm>(a, k, s);
+    case kResid: return launch_stream<TYPE, false, kResid>(a, k, s);
+    case kNorm | kStack: return launch_stream<TYPE, false, kNorm | kStack>(a, k, s);
+    default: return launch_stream<TYPE, false, kNorm | kResid | kStack>(a, k, s);
+  }
+}
+
+GemvArgs plain_args(const uint8_t* w, const float* x, float* y, size_t n_rows) {
+  GemvArgs a{};
+  a.W = a.W2 = a.W3 = w;
+  a.n0 = static_cast<int>(n_rows);
+  a.n1 = 0;
+  a.x = x;
+  a.y = y;
+  a.n_rows = static_cast<int>(n_rows);
+  return a;
 }
 
 template <int TYPE>
 int launch_typed(const uint8_t* w, const float* x, float* y, size_t n_rows, size_t k,
                  hipStream_t s) {
-  if (stream_ok<TYPE, false>(w, nullptr, x, n_rows, k))
-    return launch_stream<TYPE, false>(w, nullptr, x, nullptr, 0.f, y, n_rows, k, s);
-  const size_t nb = k / 32;
-  size_t grid = (n_rows + 3) / 4;
-  const size_t cap = static_cast<size_t>(wh::cu_count()) * 16;
-  if (grid > cap) grid = cap;
-  if (grid < 1) grid = 1;
-  gemv_generic_kernel<TYPE><<<static_cast<unsigned>(grid), 256, 0, s>>>(w, x, y, n_rows, nb);
-  WH_LAUNCH_CHECK("gemv kernel launch");
-  return WH_OK;
+  if (n_rows >= (1u << 31)) return wh::set_error(WH_ERR_INVALID_SHAPE, "gemv: %zu rows exceed 2^31", n_rows);
+  const GemvArgs a = plain_args(w, x, y, n_rows);
+  if (n_rows < (1u << 30) && stream_ok<TYPE, false>(a, k)) return launch_stream<TYPE, false, 0>(a, k, s);
+  return launch_generic<TYPE>(a, k, s);
 }
 
 }  // namespace
@@ -737,20 +814,63 @@ namespace wh {
 // layout conditions do not hold; the caller then runs the unfused sequence.
 int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x, const float* gamma,
                        float eps, float* h, size_t n_ff, size_t hidden, hipStream_t s) {
-  const uint8_t* g = static_cast<const uint8_t*>(gate);
-  const uint8_t* u = static_cast<const uint8_t*>(up);
+  if (n_ff == 0) return WH_OK;
+  if (n_ff >= (1u << 30) || !gamma) return WH_ERR_INVALID_SHAPE;
+  GemvArgs a = plain_args(static_cast<const uint8_t*>(gate), x, h, n_ff);
+  a.W2 = static_cast<const uint8_t*>(up);
+  a.gamma = gamma;
+  a.eps = eps;
   switch (type) {
     case WH_TYPE_Q4_0:
-      if (!stream_ok<WH_TYPE_Q4_0, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
-      return launch_stream<WH_TYPE_Q4_0, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+      if (!stream_ok<WH_TYPE_Q4_0, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q4_0, true, kNorm>(a, hidden, s);
     case WH_TYPE_Q4_1:
-      if (!stream_ok<WH_TYPE_Q4_1, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
-      return launch_stream<WH_TYPE_Q4_1, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+      if (!stream_ok<WH_TYPE_Q4_1, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q4_1, true, kNorm>(a, hidden, s);
     case WH_TYPE_Q8_0:
-      if (!stream_ok<WH_TYPE_Q8_0, true>(g, u, x, n_ff, hidden)) return WH_ERR_INVALID_SHAPE;
-      return launch_stream<WH_TYPE_Q8_0, true>(g, u, x, gamma, eps, h, n_ff, hidden, s);
+      if (!stream_ok<WH_TYPE_Q8_0, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      return launch_stream<WH_TYPE_Q8_0, true, kNorm>(a, hidden, s);
     default:
       return WH_ERR_INVALID_SHAPE;
+  }
+}
+
+// Fused single-token GEMV: up to three matrices with the same K stacked by
+// rows (rows[i] rows of mats[i]), optional RMSNorm of x (gamma, eps) and
+// optional residual add (y may alias residual: each row is read and written
+// by one lane).  With gamma set and a layout the streaming kernels do not
+// take, WH_ERR_INVALID_SHAPE without launching (the caller normalises x and
+// calls again without gamma).
+int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int n_mats, const float* x,
+                      const float* gamma, float eps, const float* residual, float* y, size_t k,
+                      hipStream_t s) {
+  size_t n = 0;
+  for (int i = 0; i < n_mats; i++) n += rows[i];
+  if (n == 0) return WH_OK;
+  if (n >= (1u << 30) || n_mats < 1 || n_mats > 3) return WH_ERR_INVALID_SHAPE;
+  GemvArgs a = plain_args(static_cast<const uint8_t*>(mats[0]), x, y, n);
+  a.n0 = static_cast<int>(rows[0]);
+  a.n1 = n_mats > 1 ? static_cast<int>(rows[1]) : 0;
+  a.W2 = n_mats > 1 ? static_cast<const uint8_t*>(mats[1]) : a.W;
+  a.W3 = n_mats > 2 ? static_cast<const uint8_t*>(mats[2]) : a.W2;
+  a.gamma = gamma;
+  a.eps = eps;
+  a.residual = residual;
+  // Without the normalisation the generic kernel takes every shape; with it,
+  // the caller normalises x first when the streaming kernels do not apply.
+  const int mode = (gamma ? kNorm : 0) | (residual ? kResid : 0) | (n_mats > 1 ? kStack : 0);
+  switch (type) {
+    case WH_TYPE_Q4_0:
+      if (stream_ok<WH_TYPE_Q4_0, false>(a, k)) return launch_fused_mode<WH_TYPE_Q4_0>(a, k, mode, s);
+      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q4_0>(a, k, s);
+    case WH_TYPE_Q4_1:
+      if (stream_ok<WH_TYPE_Q4_1, false>(a, k)) return launch_fused_mode<WH_TYPE_Q4_1>(a, k, mode, s);
+      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q4_1>(a, k, s);
+    case WH_TYPE_Q8_0:
+      if (stream_ok<WH_TYPE_Q8_0, false>(a, k)) return launch_fused_mode<WH_TYPE_Q8_0>(a, k, mode, s);
+      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q8_0>(a, k, s);
+    default:
+      return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "gemv: unsupported type %d", type);
   }
 }
 
@@ -762,7 +882,7 @@ int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows
     case WH_TYPE_Q4_0: return launch_typed<WH_TYPE_Q4_0>(wp, x, y, n_rows, k, s);
     case WH_TYPE_Q4_1: return launch_typed<WH_TYPE_Q4_1>(wp, x, y, n_rows, k, s);
     case WH_TYPE_Q8_0: return launch_typed<WH_TYPE_Q8_0>(wp, x, y, n_rows, k, s);
-    default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemv: unsupported type %d", type);
+    default: return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "gemv: unsupported type %d", type);
   }
 }
 

@@ -61,6 +61,12 @@ int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows
 int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x,
                        const float* gamma, float eps, float* h, size_t n_ff, size_t hidden,
                        hipStream_t stream);
+// Single-token GEMV over up to three row-stacked matrices with the same K,
+// optional RMSNorm prologue (gamma != null) and residual add (residual !=
+// null); WH_ERR_INVALID_SHAPE (nothing launched) when its layout does not fit.
+int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int n_mats, const float* x,
+                      const float* gamma, float eps, const float* residual, float* y, size_t k,
+                      hipStream_t stream);
 // Token counts up to this use one streaming GEMV per token instead of MFMA.
 constexpr size_t kGemvTokenLimit = 2;
 size_t gemm_workspace_bytes(int type, size_t n_tokens, size_t k);
@@ -73,6 +79,12 @@ bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x,
                       size_t n_tokens, float* y, void* workspace, hipStream_t stream);
+// Decode attention (attention.hip).
+size_t attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t max_ctx, size_t n_kv_heads);
+bool attention_shape_ok(size_t n_heads, size_t n_kv_heads, size_t head_dim);
+int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size_t pos, size_t n_heads,
+                            size_t n_kv_heads, size_t head_dim, const float* inv_freq, float* out, void* ws,
+                            hipStream_t stream);
 int launch_rms_norm(const float* x, const float* weight, float eps, size_t tokens,
                     size_t hidden, float* out, hipStream_t stream);
 int launch_swiglu(const float* gate, const float* up, size_t n, float* out,

@@ -130,3 +130,84 @@ class Weight:
                 self.handle = None
         except Exception:
             pass
+
+
+# ------------------------------------------------------------ decode step
+def rope_inv_freq(base: float, head_dim: int):
+    """RoPE inverse frequencies 1 / base^(2i/d) in f32 (host array)."""
+    import numpy as np
+
+    out = np.zeros(head_dim // 2, np.float32)
+    _lib.check(_lib.load().wh_rope_inv_freq(base, head_dim, out.ctypes.data))
+    return out
+
+
+def attention_qkv_workspace_bytes(hidden: int) -> int:
+    return int(_lib.load().wh_attention_qkv_workspace_bytes(hidden))
+
+
+def attention_qkv(ggml_type: int, wq, wk, wv, q_rows: int, kv_rows: int, hidden: int, gamma,
+                  eps: float, x, qkv, workspace=None, workspace_bytes: int = 0,
+                  stream: Stream | None = None) -> None:
+    _lib.check(_lib.load().wh_attention_qkv(ggml_type, _p(wq), _p(wk), _p(wv), q_rows, kv_rows, hidden,
+                                            _p(gamma), eps, _p(x), _p(qkv), _p(workspace) or None,
+                                            workspace_bytes, _s(stream)))
+
+
+def attention_workspace_bytes(n_heads: int, n_kv_heads: int, head_dim: int, max_ctx: int) -> int:
+    return int(_lib.load().wh_attention_workspace_bytes(n_heads, n_kv_heads, head_dim, max_ctx))
+
+
+def attention_decode(qkv, k_cache, v_cache, pos: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                     inv_freq, out, workspace, workspace_bytes: int,
+                     stream: Stream | None = None) -> None:
+    _lib.check(_lib.load().wh_attention_decode(_p(qkv), _p(k_cache), _p(v_cache), pos, n_heads,
+                                               n_kv_heads, head_dim, _p(inv_freq), _p(out),
+                                               _p(workspace), workspace_bytes, _s(stream)))
+
+
+def quantized_matvec_residual(ggml_type: int, weights, weight_nbytes: int, x, residual, y, m: int,
+                              k: int, stream: Stream | None = None) -> None:
+    _lib.check(_lib.load().wh_quantized_matvec_residual(ggml_type, _p(weights), weight_nbytes, _p(x),
+                                                        _p(residual), _p(y), m, k, _s(stream)))
+
+
+class LlamaModel:
+    """A Llama-shaped model on the device for the decode step: `layers` is a
+    list of dicts of device buffers (attn_norm, wq, wk, wv, wo, ffn_norm,
+    w_gate, w_up, w_down, k_cache, v_cache); wraps wh_llama_model."""
+
+    def __init__(self, ggml_type: int, dims: dict, layers: list, inv_freq_dev, output_norm=None,
+                 output=None, output_type: int = GGML_Q8_0) -> None:
+        self._keep = (layers, inv_freq_dev, output_norm, output)
+        arr = (_lib.wh_llama_layer * len(layers))()
+        for i, L in enumerate(layers):
+            for name, _ in _lib.wh_llama_layer._fields_:
+                setattr(arr[i], name, _p(L[name]) or None)
+        self._layers = arr
+        m = _lib.wh_llama_model()
+        m.type = ggml_type
+        for key in ("hidden", "n_heads", "n_kv_heads", "head_dim", "n_ff", "max_ctx", "vocab"):
+            setattr(m, key, dims[key])
+        m.n_layers = len(layers)
+        m.eps = dims.get("eps", 1e-5)
+        m.rope_inv_freq = _p(inv_freq_dev)
+        m.layers = C.cast(arr, C.POINTER(_lib.wh_llama_layer))
+        m.output_norm = _p(output_norm) or None
+        m.output_type = output_type
+        m.output = _p(output) or None
+        self.model = m
+
+    def workspace_bytes(self) -> int:
+        return int(_lib.load().wh_llama_decode_workspace_bytes(C.byref(self.model)))
+
+    def layer_decode(self, layer: int, pos: int, x, workspace, workspace_bytes: int,
+                     stream: Stream | None = None) -> None:
+        _lib.check(_lib.load().wh_llama_layer_decode(C.byref(self.model), layer, pos, _p(x),
+                                                     _p(workspace), workspace_bytes, _s(stream)))
+
+    def decode_step(self, pos: int, x, logits, workspace, workspace_bytes: int,
+                    stream: Stream | None = None) -> None:
+        _lib.check(_lib.load().wh_llama_decode_step(C.byref(self.model), pos, _p(x),
+                                                    _p(logits) or None, _p(workspace), workspace_bytes,
+                                                    _s(stream)))
