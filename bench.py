@@ -21,6 +21,9 @@ Prints ONE JSON line with:
                  Q8_0 and Q4_1 14336x4096, and the other decode-step shapes (k/v
                  projections, FFN down, the Q8_0 128256x4096 output head):
                  µs, algorithmic GB/s, fraction of peak
+  decode_step_llama3_8b_q4_0  config 4: one decode step (32 Q4_0 layers,
+                 Q8_0 head, f16 KV cache at context 4096) replayed as one HIP graph:
+                 tokens/s and algorithmic GB/s (weights + KV cache read once)
   cpu_baseline   the reference's intended SIMD GEMV (8-lane AVX2 FMA, restated in
                  the test oracle) on up to 16 host threads, a bounded sample of
                  full-size calls; cpu_baseline_scalar: the order-exact scalar
@@ -167,6 +170,83 @@ def bench_gemm(m: int, iters: int) -> float:
     return e0.elapsed_ms(e1) / iters * 1000.0
 
 
+# config 4: Llama-3-8B-shaped decode step
+L8B = dict(hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, n_ff=14336, vocab=128256,
+           n_layers=32, ctx=4096, rope_base=500000.0, eps=1e-5)
+
+
+def decode_bytes(c: dict = L8B) -> int:
+    """Algorithmic HBM bytes of one decode step at context c['ctx']: every
+    weight once, the whole KV cache of every layer once, norms, x and logits."""
+    h, q, kv, f = c["hidden"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"], c["n_ff"]
+    per_layer = (2 * q * h + 2 * kv * h + 3 * f * h) // 32 * 18 + 2 * 4 * h
+    kv_read = c["n_layers"] * 2 * c["ctx"] * kv * 2
+    head = c["vocab"] * h // 32 * 34 + 4 * h
+    return c["n_layers"] * per_layer + kv_read + head + 4 * h + 4 * c["vocab"]
+
+
+def bench_decode(steps: int, c: dict = L8B) -> dict:
+    """One decode step of a random-init 32-layer Llama-3-8B-shaped Q4_0 model
+    with a Q8_0 output head, f16 KV cache filled ~N(0,1), at position
+    ctx - 1 (attention over ctx positions).  The step (all layers + head) is
+    captured once into a HIP graph and replayed; returns timings."""
+    from woolly_amd import ops, synth
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+
+    h, nh, nkv, d, f = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["n_ff"]
+    rng = np.random.default_rng(6)
+    # one layer's weights, uploaded to every layer's own buffers
+    mats = {"wq": (nh * d, h), "wk": (nkv * d, h), "wv": (nkv * d, h), "wo": (h, nh * d),
+            "w_gate": (f, h), "w_up": (f, h), "w_down": (h, f)}
+    host = {k: synth.quantized_weight(Q4_0, n, kk, seed=60 + i) for i, (k, (n, kk)) in enumerate(mats.items())}
+    kc = rng.standard_normal((c["ctx"], nkv, d)).astype(np.float16)
+    vc = rng.standard_normal((c["ctx"], nkv, d)).astype(np.float16)
+    layers = []
+    for li in range(c["n_layers"]):
+        L = {k: DeviceBuffer.from_array(v) for k, v in host.items()}
+        L["attn_norm"] = DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+        L["ffn_norm"] = DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+        L["k_cache"] = DeviceBuffer.from_array(kc)
+        L["v_cache"] = DeviceBuffer.from_array(vc)
+        layers.append(L)
+    # Q8_0 head: 1/8 of the rows generated, tiled into the full matrix
+    part = synth.quantized_weight(8, c["vocab"] // 8, h, seed=70)
+    head = DeviceBuffer(part.nbytes * 8)
+    for i in range(8):
+        head.upload(part, offset=i * part.nbytes)
+    onorm = DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+    inv = DeviceBuffer.from_array(ops.rope_inv_freq(c["rope_base"], d))
+    model = ops.LlamaModel(Q4_0, dict(hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=d, n_ff=f,
+                                      max_ctx=c["ctx"], vocab=c["vocab"], eps=c["eps"]),
+                           layers, inv, onorm, head, 8)
+    wsz = model.workspace_bytes()
+    ws = DeviceBuffer(wsz)
+    x0 = synth.activations(h, seed=6)
+    xb, lb = DeviceBuffer.from_array(x0), DeviceBuffer(4 * c["vocab"])
+    stream = Stream()
+    pos = c["ctx"] - 1
+    for _ in range(3):
+        model.decode_step(pos, xb, lb, ws, wsz, stream)
+    stream.synchronize()
+    with Graph.capture(stream) as graph:
+        model.decode_step(pos, xb, lb, ws, wsz, stream)
+    graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    for _ in range(steps):
+        graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    graph.destroy()
+    logits = lb.download(np.float32, c["vocab"])
+    nb = decode_bytes(c)
+    return {"tokens_per_s": round(1000.0 / ms, 1), "ms_per_token": round(ms, 4), "bytes_per_token": nb,
+            "GBps": round(nb / (ms * 1e-3) / 1e9, 1), "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "ctx": c["ctx"], "layers": c["n_layers"], "logits_finite": bool(np.all(np.isfinite(logits)))}
+
+
 def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
     """Device-to-device copies of a known size (HIP's copy kernel): the reference
     the HBM byte counters of the GEMV are scaled by.  Returns GB/s."""
@@ -274,7 +354,8 @@ def main() -> int:
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM M sweep")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other decode GEMV configurations (4096x4096 Q4_0, Q8_0, Q4_1)")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm"], default=None,
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode step")
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
     ap.add_argument("--copy-probe", action="store_true",
@@ -298,6 +379,9 @@ def main() -> int:
         return 0
     if args.only == "gemm":
         print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5), 2)}))
+        return 0
+    if args.only == "decode":
+        print(json.dumps({"decode_step": bench_decode(10)}))
         return 0
     if args.only in ("ffn1", "ffn512"):
         m = 1 if args.only == "ffn1" else 512
@@ -348,6 +432,12 @@ def main() -> int:
                               "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t)}
             log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
 
+    decode = None
+    if not args.no_decode:
+        decode = bench_decode(20)
+        log(f"[bench] decode step (config 4, ctx {decode['ctx']}): {decode['ms_per_token']} ms/token, "
+            f"{decode['tokens_per_s']} tokens/s, {decode['GBps']} GB/s")
+
     cpu, cpu_scalar = (None, None) if args.no_cpu else cpu_baselines()
     if cpu:
         log(f"[bench] cpu baseline (simd, {cpu['cores']} threads): {cpu['value']} GB/s")
@@ -387,6 +477,7 @@ def main() -> int:
         "ffn_layer_us": ffn or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,
         "gemv_other_configs": gemv_cfg or None,
+        "decode_step_llama3_8b_q4_0": decode,
         "cpu_baseline": cpu,
         "cpu_baseline_scalar": cpu_scalar,
     }

@@ -164,20 +164,56 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 }
 
 // out[h][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c.
+// One workgroup per query head: the chunk maxima and weights are reduced by
+// all threads (weights kept in LDS), then 256 / D thread groups each sum a
+// fixed subset of the chunks for every d and meet in LDS in a fixed order.
 template <int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                         int n_chunks) {
-  const int h = blockIdx.x, d = threadIdx.x;
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
+                                                                    float* __restrict__ out, int n_chunks) {
+  constexpr int NG = kAttnThreads / D;  // chunk groups
+  extern __shared__ float cw[];         // [n_chunks] weights, then [NG][D] partial sums, [8] reduction
+  float* accs = cw + n_chunks;
+  float* red = accs + NG * D;
+  const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const float* ph = part + static_cast<size_t>(h) * n_chunks * (D + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < n_chunks; c++) M = fmaxf(M, ph[c * (D + 2)]);
-  float L = 0.f, acc = 0.f;
-  for (int c = 0; c < n_chunks; c++) {
-    const float w = expf(ph[c * (D + 2)] - M);
-    L = __builtin_fmaf(ph[c * (D + 2) + 1], w, L);
-    acc = __builtin_fmaf(ph[c * (D + 2) + 2 + d], w, acc);
+  float m = -INFINITY;
+  for (int c = t; c < n_chunks; c += kAttnThreads) m = fmaxf(m, ph[static_cast<size_t>(c) * (D + 2)]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < kAttnThreads / 64; w++) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float l = 0.f;
+  for (int c = t; c < n_chunks; c += kAttnThreads) {
+    const float w = expf(ph[static_cast<size_t>(c) * (D + 2)] - M);
+    cw[c] = w;
+    l = __builtin_fmaf(ph[static_cast<size_t>(c) * (D + 2) + 1], w, l);
   }
-  out[h * D + d] = acc / L;
+  l = whd::wave_sum(l);
+  if (lane == 0) red[wave] = l;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnThreads / 64; w++) L += red[w];
+  const int d = t % D, grp = t / D;
+  float a0 = 0.f, a1 = 0.f;
+  int c = grp;
+  for (; c + NG < n_chunks; c += 2 * NG) {
+    a0 = __builtin_fmaf(cw[c], ph[static_cast<size_t>(c) * (D + 2) + 2 + d], a0);
+    a1 = __builtin_fmaf(cw[c + NG], ph[static_cast<size_t>(c + NG) * (D + 2) + 2 + d], a1);
+  }
+  if (c < n_chunks) a0 = __builtin_fmaf(cw[c], ph[static_cast<size_t>(c) * (D + 2) + 2 + d], a0);
+  accs[grp * D + d] = a0 + a1;
+  __syncthreads();
+  if (grp == 0) {
+    float acc = accs[d];
+#pragma unroll
+    for (int g = 1; g < NG; g++) acc += accs[g * D + d];
+    out[h * D + d] = acc / L;
+  }
 }
 
 // Positions per workgroup: enough chunks for about two workgroups per CU,
@@ -191,6 +227,10 @@ int attn_chunk(size_t ctx, size_t n_kv_heads) {
   if (c < 64) c = 64;
   if (c > 256) c = 256;
   return static_cast<int>(c);
+}
+
+size_t combine_lds(int D, int n_chunks) {
+  return 4u * (static_cast<size_t>(n_chunks) + static_cast<size_t>(kAttnThreads / D) * D + 8);
 }
 
 template <int D>
@@ -222,6 +262,14 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
   const int G = static_cast<int>(n_heads / n_kv_heads);
   float* part = static_cast<float*>(ws);
   const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+  const size_t clds = combine_lds(static_cast<int>(head_dim), n_chunks);
+  if (clds > wh::max_lds_per_block())
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "attention: context of %zu positions exceeds the combine's LDS", pos + 1);
+  if (clds > 65536) {
+    WH_HIP_TRY(hipFuncSetAttribute(head_dim == 128 ? reinterpret_cast<const void*>(&attn_combine_kernel<128>)
+                                                   : reinterpret_cast<const void*>(&attn_combine_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(clds)));
+  }
   dim3 grid(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(n_chunks));
   if (head_dim == 128) {
     const size_t lds = partial_lds<128>(G, chunk);
@@ -231,7 +279,8 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<128><<<static_cast<unsigned>(n_heads), 128, 0, s>>>(part, out, n_chunks);
+    attn_combine_kernel<128><<<static_cast<unsigned>(n_heads), kAttnThreads, clds, s>>>(
+        part, out, n_chunks);
   } else {
     const size_t lds = partial_lds<64>(G, chunk);
     WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<64>),
@@ -240,7 +289,8 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<64><<<static_cast<unsigned>(n_heads), 64, 0, s>>>(part, out, n_chunks);
+    attn_combine_kernel<64><<<static_cast<unsigned>(n_heads), kAttnThreads, clds, s>>>(
+        part, out, n_chunks);
   }
   WH_LAUNCH_CHECK("attention combine launch");
   return WH_OK;
