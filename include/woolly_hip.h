@@ -131,6 +131,17 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
                                const float* input, float* output, size_t m, size_t k,
                                wh_stream_t stream);
 
+/* Which single-token GEMV kernels the library launches (no counterpart in the
+ * reference: a switch for comparing the two implementations on one device).
+ * WH_GEMV_AUTO (default): the matrix-core kernel (int8 MFMA on exact limbs of
+ * the activations) for the shapes it takes, the streaming VALU kernels
+ * otherwise; WH_GEMV_STREAM: streaming kernels only.  Applies to
+ * wh_quantized_matvec, the fused decode GEMVs and the M <= 2 FFN gate/up.
+ * The previous setting is stored in *previous when it is not NULL.
+ * WH_ERR_INVALID_ARGUMENT for an unknown mode (nothing changes). */
+enum { WH_GEMV_AUTO = 0, WH_GEMV_STREAM = 1 };
+WH_API int wh_gemv_select(int mode, int* previous);
+
 /* ------------------------------------------------------ quantized GEMM */
 /* Y[t, r] = sum_k X[t, k] * W[r, k] for t < n_tokens, r < n_rows.
  * Replaces the projections woolly runs on fully dequantized f32 weights:

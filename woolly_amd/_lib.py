@@ -124,6 +124,7 @@ SIGNATURES = {
     "wh_status_string": (C.c_char_p, [_int]),
     "wh_last_error": (C.c_char_p, []),
     "wh_version": (_int, []),
+    "wh_gemv_select": (_int, [_int, C.POINTER(_int)]),
     "wh_init": (_int, [_int]),
     "wh_device_count": (_int, [C.POINTER(_int)]),
     "wh_device_name": (_int, [C.c_char_p, _sz]),

@@ -133,6 +133,14 @@ WH_API const char* wh_last_error(void) { return g_last_error; }
 
 WH_API int wh_version(void) { return 1; }
 
+WH_API int wh_gemv_select(int mode, int* previous) {
+  if (mode != WH_GEMV_AUTO && mode != WH_GEMV_STREAM)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "gemv_select: unknown mode %d", mode);
+  const int prev = wh::gemv_mode_exchange(mode);
+  if (previous) *previous = prev;
+  return WH_OK;
+}
+
 // ------------------------------------------------------------- device/memory
 WH_API int wh_device_count(int* count) {
   if (!count) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_device_count: null count");

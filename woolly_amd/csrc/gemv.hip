@@ -18,6 +18,7 @@
 // Generic path: one wave per row, lanes stride over blocks with byte loads;
 // used for odd block counts, unaligned pointers and K > 16384.
 #include <algorithm>
+#include <atomic>
 
 #include "wh_blocks.hpp"
 
@@ -795,10 +796,26 @@ GemvArgs plain_args(const uint8_t* w, const float* x, float* y, size_t n_rows) {
   return a;
 }
 
+std::atomic<int> g_gemv_mode{WH_GEMV_AUTO};
+
+// The matrix-core kernel pays for its activation preparation and its 16-row
+// steps on short rows and few rows; below these sizes the streaming kernels
+// are used.
+bool use_mfma(int type, size_t n_rows, size_t k) {
+  return g_gemv_mode.load(std::memory_order_relaxed) == WH_GEMV_AUTO && k >= 1024 && n_rows >= 64 &&
+         wh::gemv_mfma_ok(type, n_rows, k);
+}
+
 template <int TYPE>
 int launch_typed(const uint8_t* w, const float* x, float* y, size_t n_rows, size_t k,
                  hipStream_t s) {
   if (n_rows >= (1u << 31)) return wh::set_error(WH_ERR_INVALID_SHAPE, "gemv: %zu rows exceed 2^31", n_rows);
+  if (use_mfma(TYPE, n_rows, k)) {
+    const void* mats[1] = {w};
+    const size_t rows[1] = {n_rows};
+    const int st = wh::launch_gemv_mfma(TYPE, mats, rows, 1, false, x, nullptr, 0.f, nullptr, y, n_rows, k, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   const GemvArgs a = plain_args(w, x, y, n_rows);
   if (n_rows < (1u << 30) && stream_ok<TYPE, false>(a, k)) return launch_stream<TYPE, false, 0>(a, k, s);
   return launch_generic<TYPE>(a, k, s);
@@ -812,10 +829,18 @@ namespace wh {
 // h = silu(W_gate x_hat) * (W_up x_hat), x_hat = rms_norm(x, gamma, eps).
 // Returns WH_ERR_INVALID_SHAPE without launching when the fused kernel's
 // layout conditions do not hold; the caller then runs the unfused sequence.
+int gemv_mode_exchange(int mode) { return g_gemv_mode.exchange(mode); }
+
 int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x, const float* gamma,
                        float eps, float* h, size_t n_ff, size_t hidden, hipStream_t s) {
   if (n_ff == 0) return WH_OK;
   if (n_ff >= (1u << 30) || !gamma) return WH_ERR_INVALID_SHAPE;
+  if (use_mfma(type, n_ff, hidden)) {
+    const void* mats[2] = {gate, up};
+    const size_t rows[2] = {n_ff, n_ff};
+    const int st = launch_gemv_mfma(type, mats, rows, 2, true, x, gamma, eps, nullptr, h, n_ff, hidden, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   GemvArgs a = plain_args(static_cast<const uint8_t*>(gate), x, h, n_ff);
   a.W2 = static_cast<const uint8_t*>(up);
   a.gamma = gamma;
@@ -856,6 +881,10 @@ int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int
   a.gamma = gamma;
   a.eps = eps;
   a.residual = residual;
+  if (use_mfma(type, n, k)) {
+    const int st = launch_gemv_mfma(type, mats, rows, n_mats, false, x, gamma, eps, residual, y, n, k, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   // Without the normalisation the generic kernel takes every shape; with it,
   // the caller normalises x first when the streaming kernels do not apply.
   const int mode = (gamma ? kNorm : 0) | (residual ? kResid : 0) | (n_mats > 1 ? kStack : 0);

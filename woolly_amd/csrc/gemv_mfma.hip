@@ -1,0 +1,564 @@
+// gemv_mfma.hip -- quantized matrix-vector product y = W x on the int8 matrix
+// cores of gfx950 (v_mfma_i32_16x16x32_i8).
+//
+// Reference: simd::quantized_matvec (crates/woolly-tensor/src/quantization.rs:869-909)
+// with its scalar kernels quantized_matvec_q4_0_scalar / _q8_0_scalar
+// (quantization.rs:1100-1163); Q4_1 as dequantize_q4_1 (:490-511) composed with
+// the f32 dot.  The fused variants add the RMSNorm prologue (tensor_utils.rs:446-480),
+// the residual adds of process_layer (lazy_transformer.rs:98-258) and the SwiGLU
+// epilogue h = silu(gate . x) * (up . x) (tensor_utils.rs:512-532).
+//
+// Arithmetic.  Every weight of a block is an exact small integer q (Q4_0 and
+// Q4_1: the nibble 0..15, Q8_0: the int8 quant) times the block scale d.  The
+// activations of one 256-element chunk are written as
+//     x = 2^-e * (2^24 l0 + 2^16 l1 + 2^8 l2 + l3),   |l0| <= 65, l1..l3 int8,
+// with e chosen per chunk so that max|x| * 2^e lies in [2^29, 2^30): every
+// element within 2^-6 of the chunk's largest is represented exactly (its 24
+// significant bits fit), the others to 2^-31 of the chunk maximum.  One MFMA
+// per block multiplies the four limbs (rows 0..3 of the A operand) with the
+// block's quants (the B operand, one weight row per column): the int32
+// accumulation is exact.  Four consecutive blocks share one accumulator, their
+// limbs placed in rows 4j..4j+3, so lane group j of the result holds block j's
+// four limb sums and one FMA per lane applies the four block scales:
+// d * (2^24 C0 + 2^16 C1 + 2^8 C2 + C3), the Q4_0 offset -8 entering as
+// -8 * (sum of each limb) through the accumulator input, the Q4_1 minimum as
+// m * sum(x).
+//
+// Data flow.  A workgroup of 16 waves owns a contiguous range of output rows;
+// a step streams 16 of its rows (one per wave) over one K-segment of at most
+// 4 KB with coalesced 16-byte buffer loads, so the workgroup reads a
+// contiguous region of the weights per step.  The loads land in registers one
+// step ahead, are written into a 2-slot LDS ring (one LDS-only barrier per
+// step), and every wave then computes one 4-pair chunk of the segment for all
+// 16 rows.  Out-of-range rows are given an empty buffer range: their loads
+// return zeros without touching memory.  Row sums are reduced across the 16
+// waves in a fixed order (deterministic) one step later by a rotating wave.
+//
+// Activations that are not finite cannot be written as limbs: a wave whose
+// chunk holds inf or NaN computes that chunk per element instead,
+// ((q - 8) * d) * x accumulated like the reference, so inf/NaN propagate as in
+// quantized_matvec_q4_0_scalar (quantization.rs:1121-1124).
+#include "wh_blocks.hpp"
+
+typedef int mg_v4i __attribute__((ext_vector_type(4)));
+
+// raw buffer load of 16 bytes (llvm.amdgcn.raw.buffer.load.v4i32)
+__device__ mg_v4i mg_buffer_load_x4(mg_v4i rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+namespace {
+
+// Buffer resource of a raw byte range: loads at offsets >= nbytes return 0
+// without a memory access.
+__device__ __forceinline__ mg_v4i mg_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  mg_v4i r;
+  r[0] = static_cast<int>(static_cast<uint32_t>(a));
+  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xFFFFu);  // stride 0
+  r[2] = static_cast<int>(nbytes);
+  r[3] = 0x00020000;  // 32-bit data format, raw access
+  return r;
+}
+
+constexpr int kMgWaves = 16;                   // waves per workgroup
+constexpr int kMgSegMax = 16 * 64 * 4;        // bytes of one row segment (at most 4 loads)
+constexpr int kMgPad = 16;                     // LDS row padding (bank spread)
+constexpr int kMgLimbBytes = 4 * 32;            // four limbs of one block
+constexpr int kMgStage = 8 * kMgLimbBytes + 8 * 16;  // limb staging bytes per chunk (+ limb sums)
+constexpr int kMgNt = 2;                       // streaming (non-temporal) loads
+constexpr int kMgNorm = 1, kMgFfn = 2;         // kernel variants
+
+template <int TYPE>
+struct MgFmt;
+template <>
+struct MgFmt<WH_TYPE_Q4_0> {
+  static constexpr int PB = 36;  // bytes of two blocks
+};
+template <>
+struct MgFmt<WH_TYPE_Q4_1> {
+  static constexpr int PB = 40;
+};
+template <>
+struct MgFmt<WH_TYPE_Q8_0> {
+  static constexpr int PB = 68;
+};
+
+// Output rows [0, n_out).  Plain mode: row r is row r of the matrices W0, W1,
+// W2 stacked (n0 rows of W0, n1 of W1, the rest of W2).  FFN mode: W0 = gate,
+// W1 = up, y[r] = silu(gate_r . x_hat) * (up_r . x_hat).  gamma set: x is
+// RMS-normalised first; residual set: y[r] = residual[r] + (W x)[r].
+struct MgArgs {
+  const uint8_t* W0;
+  const uint8_t* W1;
+  const uint8_t* W2;
+  int n0, n1;
+  const float* x;
+  const float* gamma;
+  float eps;
+  const float* residual;
+  float* y;
+  int n_out, ppr, seg_pairs, rows_per_wg;
+};
+
+// k-slot (0..7) of lane group g that element el (0..31) of a block feeds:
+// Q4: slots 0..3 = low nibbles of quant bytes 4g..4g+3 (elements 4g..4g+3),
+// slots 4..7 = their high nibbles (elements 16+4g..); Q8_0: element 8g + slot.
+template <int TYPE>
+__device__ __forceinline__ int mg_slot_offset(int el) {
+  if constexpr (TYPE == WH_TYPE_Q8_0) return el;
+  return 8 * ((el & 15) >> 2) + (el & 3) + (el >= 16 ? 4 : 0);
+}
+
+// B operand of lane group g for the two blocks of the pair at pw (LDS).
+template <int TYPE>
+__device__ __forceinline__ void mg_quants(const uint32_t* pw, int g, long& qa, long& qb) {
+  auto split = [](uint32_t u) -> long {
+    return static_cast<long>(u & 0x0F0F0F0Fu) | (static_cast<long>((u >> 4) & 0x0F0F0F0Fu) << 32);
+  };
+  if constexpr (TYPE == WH_TYPE_Q4_0) {
+    // [dA|q0 q1] [q2..5] .. [q14 q15|dB] [B q0..3] ..: quant bytes 4g..4g+3 of block A
+    // start at byte 2 + 4g
+    qa = split(__builtin_amdgcn_alignbit(pw[g + 1], pw[g], 16));
+    qb = split(pw[5 + g]);
+  } else if constexpr (TYPE == WH_TYPE_Q4_1) {
+    // [dA|mA] [A q0..3] .. [A q12..15] [dB|mB] [B q0..3] ..
+    qa = split(pw[1 + g]);
+    qb = split(pw[6 + g]);
+  } else {
+    // [dA|q0 q1] [q2..5] .. [q30 q31|dB] [B q0..3] ..: quant bytes 8g..8g+7 of block A
+    // start at byte 2 + 8g
+    const uint32_t w0 = pw[2 * g], w1 = pw[2 * g + 1], w2 = pw[2 * g + 2];
+    const uint32_t lo = __builtin_amdgcn_alignbit(w1, w0, 16);
+    const uint32_t hi = __builtin_amdgcn_alignbit(w2, w1, 16);
+    qa = static_cast<long>(lo) | (static_cast<long>(hi) << 32);
+    qb = static_cast<long>(pw[9 + 2 * g]) | (static_cast<long>(pw[10 + 2 * g]) << 32);
+  }
+}
+
+// Per-element dot product of one pair (64 weights at byte pointer p, in LDS)
+// with x[0..64) (global memory), normalised as x * inv * gamma when gamma is
+// set: w = (q - 8) * d, q * d + m or q * d as in dequantize_q4_0 / _q4_1 /
+// _q8_0, then w * x accumulated.  Used for chunks with non-finite activations.
+template <int TYPE>
+__device__ float mg_pair_exact(const uint8_t* p, const float* x, const float* gamma, float rms) {
+  constexpr int BB = whd::BlockFmt<TYPE>::BYTES;
+  float s = 0.f;
+  for (int blk = 0; blk < 2; blk++) {
+    const uint8_t* b = p + blk * BB;
+    const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
+    float m = 0.f;
+    if constexpr (TYPE == WH_TYPE_Q4_1)
+      m = whd::f16_bits_to_f32(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
+#pragma unroll 2
+    for (int el = 0; el < 32; el++) {
+      float w;
+      if constexpr (TYPE == WH_TYPE_Q4_0) {
+        const uint32_t q = b[2 + (el & 15)];
+        w = static_cast<float>(static_cast<int>(el < 16 ? (q & 15u) : (q >> 4)) - 8) * d;
+      } else if constexpr (TYPE == WH_TYPE_Q4_1) {
+        const uint32_t q = b[4 + (el & 15)];
+        w = __fadd_rn(__fmul_rn(static_cast<float>(el < 16 ? (q & 15u) : (q >> 4)), d), m);
+      } else {
+        w = static_cast<float>(static_cast<int8_t>(b[2 + el])) * d;
+      }
+      float xv = x[32 * blk + el];
+      if (gamma) xv = (xv / rms) * gamma[32 * blk + el];
+      s = __builtin_fmaf(w, xv, s);
+    }
+  }
+  return s;
+}
+
+// NL: 16-byte loads per lane per step (row segments of up to 1024 NL bytes).
+template <int TYPE, int NSEG, int NL, int MODE>
+__global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a) {
+  constexpr int PB = MgFmt<TYPE>::PB;
+  constexpr bool FFN = (MODE & kMgFfn) != 0;
+  constexpr bool NORM = (MODE & kMgNorm) != 0;
+  constexpr bool Q41 = TYPE == WH_TYPE_Q4_1;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int S = a.seg_pairs;
+  const uint32_t seg_bytes = static_cast<uint32_t>(S) * PB;
+  const uint32_t rstr = seg_bytes + kMgPad;
+  const uint32_t slot_bytes = 16 * rstr;
+  const size_t row_bytes = static_cast<size_t>(a.ppr) * PB;
+  const int K = a.ppr * 64;
+  uint8_t* ring = lds;
+  uint8_t* stage = lds + 2 * slot_bytes + wave * NSEG * kMgStage;  // per segment: limbs, block sums
+  float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * NSEG * kMgStage);  // [2][16][16]
+  float* misc = part + 2 * kMgWaves * 16;                                                    // [16] + [16]
+  float* res_lds = misc + 32;                                                                 // residual rows
+
+  const int r0 = blockIdx.x * a.rows_per_wg;
+  const int r1 = min(a.n_out, r0 + a.rows_per_wg);
+  const int G = (r1 - r0 + 15) >> 4;
+  const int GT = FFN ? 2 * G : G;          // row groups streamed
+  const bool owns = wave < (S >> 2);       // computes chunk `wave` of every segment
+
+  // Row (16 q + wave) of streamed group q: its bytes, or an empty range.
+  auto row_src = [&](int q, const uint8_t** base) -> bool {
+    const int gi = FFN ? (q >> 1) : q;
+    const int row = r0 + 16 * gi + wave;
+    if (q >= GT || row >= r1) return false;
+    int local = row;
+    const uint8_t* w = a.W0;
+    if constexpr (FFN) {
+      w = (q & 1) ? a.W1 : a.W0;
+    } else {
+      if (local >= a.n0) {
+        local -= a.n0;
+        w = a.W1;
+        if (local >= a.n1) {
+          local -= a.n1;
+          w = a.W2;
+        }
+      }
+    }
+    *base = w + static_cast<size_t>(local) * row_bytes;
+    return true;
+  };
+  mg_v4i buf[NL];
+  auto load = [&](int q, int seg) {
+    const uint8_t* base = a.W0;
+    const bool ok = row_src(q, &base);
+    const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes, ok ? seg_bytes : 0u);
+#pragma unroll
+    for (int i = 0; i < NL; i++) buf[i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
+  };
+
+  // The residual rows of the workgroup go to LDS first: inside the step loop a
+  // global load would make its consumer wait for every weight load in flight.
+  if (!FFN && a.residual) {
+    for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) res_lds[i] = a.residual[r0 + i];
+  }
+  // ---- activations of this wave's chunks (4 consecutive per lane), then the first weights
+  float xv[NSEG][4];
+  float gv[NSEG][4];
+#pragma unroll
+  for (int seg = 0; seg < NSEG; seg++) {
+    const int base = (seg * S + 4 * wave) * 64 + 4 * lane;
+    float4 xt = make_float4(0.f, 0.f, 0.f, 0.f), gt = xt;
+    if (owns) {
+      xt = *reinterpret_cast<const float4*>(a.x + base);
+      if constexpr (NORM) gt = *reinterpret_cast<const float4*>(a.gamma + base);
+    }
+    xv[seg][0] = xt.x, xv[seg][1] = xt.y, xv[seg][2] = xt.z, xv[seg][3] = xt.w;
+    gv[seg][0] = gt.x, gv[seg][1] = gt.y, gv[seg][2] = gt.z, gv[seg][3] = gt.w;
+  }
+  load(0, 0);
+
+  float rms = 1.f;
+  if constexpr (NORM) {
+    // rms = sqrt(sum x^2 / K + eps), x_hat = (x / rms) * gamma (tensor_utils.rs:446-480)
+    float ss = 0.f;
+#pragma unroll
+    for (int seg = 0; seg < NSEG; seg++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) ss = __builtin_fmaf(xv[seg][i], xv[seg][i], ss);
+    ss = whd::wave_sum(ss);
+    if (lane == 0) misc[wave] = ss;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMgWaves; w++) tot += misc[w];
+    rms = sqrtf(tot / static_cast<float>(K) + a.eps);
+#pragma unroll
+    for (int seg = 0; seg < NSEG; seg++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xv[seg][i] = (xv[seg][i] / rms) * gv[seg][i];
+  }
+
+  // ---- limbs of each chunk -> this wave's staging area (the MFMA A operands are
+  // read from it: the lanes of rows 4j..4j+3 of block j's operand, zeros elsewhere)
+  int ex[NSEG];
+  bool exact[NSEG];
+#pragma unroll
+  for (int seg = 0; seg < NSEG; seg++) {
+    float mx = 0.f;
+    bool fin = true;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      mx = fmaxf(mx, fabsf(xv[seg][i]));
+      fin = fin && __builtin_isfinite(xv[seg][i]);  // fmaxf drops NaN
+    }
+    exact[seg] = __any(!fin);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    int e = 0;
+    if (mx > 0.f && !exact[seg]) {
+      int ee;
+      frexpf(mx, &ee);
+      e = 30 - ee;
+    }
+    ex[seg] = e;
+    int8_t* xop = reinterpret_cast<int8_t*>(stage + seg * kMgStage);
+    int* bs_lds = reinterpret_cast<int*>(stage + seg * kMgStage + 8 * kMgLimbBytes);
+    int bs[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int el_c = 4 * lane + i;  // element of the chunk
+      // |x * 2^e| < 2^30: the conversion is exact for the chunk's larger elements
+      const int xi = exact[seg] ? 0 : static_cast<int>(rintf(ldexpf(xv[seg][i], e)));
+      const int l3 = static_cast<int>(static_cast<int8_t>(xi & 0xFF));
+      int t = (xi - l3) >> 8;
+      const int l2 = static_cast<int>(static_cast<int8_t>(t & 0xFF));
+      t = (t - l2) >> 8;
+      const int l1 = static_cast<int>(static_cast<int8_t>(t & 0xFF));
+      const int l0 = (t - l1) >> 8;
+      int8_t* p = xop + (el_c >> 5) * kMgLimbBytes + mg_slot_offset<TYPE>(el_c & 31);
+      p[0] = static_cast<int8_t>(l0);
+      p[32] = static_cast<int8_t>(l1);
+      p[64] = static_cast<int8_t>(l2);
+      p[96] = static_cast<int8_t>(l3);
+      bs[0] += l0;
+      bs[1] += l1;
+      bs[2] += l2;
+      bs[3] += l3;
+    }
+    // a block is 8 consecutive lanes
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      bs[r] += __shfl_xor(bs[r], 4, 64);
+      bs[r] += __shfl_xor(bs[r], 2, 64);
+      bs[r] += __shfl_xor(bs[r], 1, 64);
+    }
+    if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+  // A operands of segment seg: lanes outside rows 4j..4j+3 of block j keep the
+  // zeros set here
+  long xo[8];
+  mg_v4i cin[2];  // Q4_0: -8 * limb sums of block 4t + g (accumulator input)
+  float bsum[2];  // Q4_1: sum of the block's activations, in units of 2^-e
+#pragma unroll
+  for (int lb = 0; lb < 8; lb++) xo[lb] = 0;
+  auto get_x = [&](int seg) {
+    const int8_t* xop = reinterpret_cast<const int8_t*>(stage + seg * kMgStage);
+    const int* bs_lds = reinterpret_cast<const int*>(stage + seg * kMgStage + 8 * kMgLimbBytes);
+#pragma unroll
+    for (int lb = 0; lb < 8; lb++)
+      if ((n >> 2) == (lb & 3)) xo[lb] = *reinterpret_cast<const long*>(xop + lb * kMgLimbBytes + 32 * (n & 3) + 8 * g);
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int4 v = *reinterpret_cast<const int4*>(bs_lds + 4 * (4 * t + g));
+      if constexpr (TYPE == WH_TYPE_Q4_0) cin[t] = (mg_v4i){-8 * v.x, -8 * v.y, -8 * v.z, -8 * v.w};
+      else cin[t] = (mg_v4i){0, 0, 0, 0};
+      bsum[t] = __builtin_fmaf(static_cast<float>(v.x), 16777216.f,
+                               __builtin_fmaf(static_cast<float>(v.y), 65536.f,
+                                              __builtin_fmaf(static_cast<float>(v.z), 256.f, static_cast<float>(v.w))));
+    }
+  };
+  if constexpr (NSEG == 1) get_x(0);
+
+  // Sum of group q over the 16 waves (fixed order), then the output row.
+  auto finish = [&](int q) {
+    if (lane >= 16) return;
+    const float* pp = part + (q & 1) * kMgWaves * 16 + n;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMgWaves; w++) v += pp[16 * w];
+    const int gi = FFN ? (q >> 1) : q;
+    const int row = r0 + 16 * gi + n;
+    if constexpr (FFN) {
+      if ((q & 1) == 0) {
+        misc[16 + n] = v;  // gate, combined with up one group later
+        return;
+      }
+      const float gt = misc[16 + n];
+      if (row < r1) a.y[row] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+    } else {
+      if (row < r1) a.y[row] = (a.residual ? res_lds[row - r0] : 0.f) + v;
+    }
+  };
+
+  float acc = 0.f;
+  for (int q = 0; q < GT; q++) {
+#pragma unroll
+    for (int seg = 0; seg < NSEG; seg++) {
+      const int s = q * NSEG + seg;
+      uint8_t* slot = ring + (s & 1) * slot_bytes;
+      {
+        uint8_t* dst = slot + wave * rstr;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+          const uint32_t o = 16u * (64 * i + lane);
+          if (o < seg_bytes) *reinterpret_cast<mg_v4i*>(dst + o) = buf[i];
+        }
+      }
+      if (seg + 1 < NSEG) load(q, seg + 1);
+      else load(q + 1, 0);
+      // LDS-only barrier (a __syncthreads() would also wait for the loads in flight)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
+      if (owns) {
+        if constexpr (NSEG > 1) get_x(seg);
+        const uint8_t* rowp = slot + n * rstr + wave * 4 * PB;
+        if (!exact[seg]) {
+          // scale (and minimum) of block 4t + g
+          uint32_t dm[2];
+#pragma unroll
+          for (int t = 0; t < 2; t++) {
+            const int blk = 4 * t + g;
+            const uint8_t* bp = rowp + (blk >> 1) * PB + (blk & 1) * (PB / 2);
+            if constexpr (Q41) dm[t] = *reinterpret_cast<const uint32_t*>(bp);
+            else dm[t] = *reinterpret_cast<const uint16_t*>(bp);
+          }
+          mg_v4i C[2];
+#pragma unroll
+          for (int t = 0; t < 2; t++) C[t] = cin[t];
+#pragma unroll
+          for (int p = 0; p < 4; p++) {
+            long qa, qb;
+            mg_quants<TYPE>(reinterpret_cast<const uint32_t*>(rowp + p * PB), g, qa, qb);
+            C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p], qa, C[p >> 1], 0, 0, 0);
+            C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p + 1], qb, C[p >> 1], 0, 0, 0);
+          }
+          float sacc = 0.f;
+#pragma unroll
+          for (int t = 0; t < 2; t++) {
+            const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
+                                           __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
+                                                          __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
+                                                                         static_cast<float>(C[t][3]))));
+            const float d = whd::f16_bits_to_f32(dm[t] & 0xFFFFu);
+            sacc = __builtin_fmaf(d, f, sacc);
+            if constexpr (Q41) sacc = __builtin_fmaf(whd::f16_bits_to_f32(dm[t] >> 16), bsum[t], sacc);
+          }
+          acc += ldexpf(sacc, -ex[seg]);
+        } else {
+          // lane group g: pair g of the chunk, row n
+          const int e0 = (seg * S + 4 * wave + g) * 64;
+          acc += mg_pair_exact<TYPE>(rowp + g * PB, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+        }
+      }
+      if (seg == NSEG - 1) {
+        float v = acc + __shfl_xor(acc, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (g == 0) part[(q & 1) * kMgWaves * 16 + wave * 16 + n] = v;
+        acc = 0.f;
+      }
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
+}
+
+size_t mg_lds_bytes(int type, int seg_pairs, int nseg, int rows_per_wg) {
+  const int pb = type == WH_TYPE_Q4_0 ? 36 : (type == WH_TYPE_Q4_1 ? 40 : 68);
+  return 2u * 16u * static_cast<size_t>(seg_pairs * pb + kMgPad) + static_cast<size_t>(kMgWaves) * nseg * kMgStage +
+         4u * (2 * kMgWaves * 16 + 32 + static_cast<size_t>(rows_per_wg));
+}
+
+// Segments: the fewest (1 .. 4) that split the row into whole 4-pair chunks,
+// at most 16 chunks and 4 KB per segment; 0 when none does.
+int mg_segments(int type, size_t ppr) {
+  const size_t pb = type == WH_TYPE_Q4_0 ? 36 : (type == WH_TYPE_Q4_1 ? 40 : 68);
+  if (ppr == 0 || ppr % 4 != 0) return 0;
+  for (int ns = 1; ns <= 4; ns++) {
+    if (ppr % ns != 0) continue;
+    const size_t s = ppr / ns;
+    if (s % 4 == 0 && s / 4 <= kMgWaves && s * pb <= kMgSegMax) return ns;
+  }
+  return 0;
+}
+
+template <int TYPE, int NSEG, int NL, int MODE>
+int mg_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
+  auto* fn = &gemv_mfma_kernel<TYPE, NSEG, NL, MODE>;
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(lds)));
+  fn<<<grid, kMgWaves * 64, lds, s>>>(a);
+  WH_LAUNCH_CHECK("gemv (mfma) kernel launch");
+  return WH_OK;
+}
+
+template <int TYPE, int NL, int MODE>
+int mg_dispatch_nl(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t s) {
+  switch (nseg) {
+    case 1: return mg_launch<TYPE, 1, NL, MODE>(a, grid, lds, s);
+    case 2: return mg_launch<TYPE, 2, NL, MODE>(a, grid, lds, s);
+    case 3: return mg_launch<TYPE, 3, NL, MODE>(a, grid, lds, s);
+    default: return mg_launch<TYPE, 4, NL, MODE>(a, grid, lds, s);
+  }
+}
+
+template <int TYPE, int MODE>
+int mg_dispatch(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t s) {
+  const int seg_bytes = a.seg_pairs * MgFmt<TYPE>::PB;
+  return seg_bytes <= 3072 ? mg_dispatch_nl<TYPE, 3, MODE>(a, nseg, grid, lds, s)
+                           : mg_dispatch_nl<TYPE, 4, MODE>(a, nseg, grid, lds, s);
+}
+
+template <int TYPE>
+int mg_typed(const MgArgs& a, int nseg, int mode, int grid, size_t lds, hipStream_t s) {
+  switch (mode) {
+    case 0: return mg_dispatch<TYPE, 0>(a, nseg, grid, lds, s);
+    case kMgNorm: return mg_dispatch<TYPE, kMgNorm>(a, nseg, grid, lds, s);
+    default: return mg_dispatch<TYPE, kMgNorm | kMgFfn>(a, nseg, grid, lds, s);
+  }
+}
+
+}  // namespace
+
+namespace wh {
+
+bool gemv_mfma_ok(int type, size_t n_out, size_t k) {
+  if (!(type == WH_TYPE_Q4_0 || type == WH_TYPE_Q4_1 || type == WH_TYPE_Q8_0)) return false;
+  if (n_out == 0 || n_out >= (1u << 30) || k % 64 != 0) return false;
+  return mg_segments(type, k / 64) > 0;
+}
+
+// mats / rows: up to three row-stacked matrices with the same K (ffn: gate, up
+// with n_out rows each).  Returns WH_ERR_INVALID_SHAPE without launching when
+// the layout does not fit this kernel.
+int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
+                     const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
+                     hipStream_t s) {
+  if (n_out == 0) return WH_OK;
+  if (!gemv_mfma_ok(type, n_out, k) || n_mats < 1 || n_mats > 3 || (ffn && (n_mats != 2 || !gamma)))
+    return WH_ERR_INVALID_SHAPE;
+  for (int i = 0; i < n_mats; i++)
+    if (!aligned(mats[i], 4)) return WH_ERR_INVALID_SHAPE;
+  if (!aligned(x, 16) || (gamma && !aligned(gamma, 16))) return WH_ERR_INVALID_SHAPE;
+  const size_t ppr = k / 64;
+  const int nseg = mg_segments(type, ppr);
+  MgArgs a{};
+  a.W0 = static_cast<const uint8_t*>(mats[0]);
+  a.W1 = n_mats > 1 ? static_cast<const uint8_t*>(mats[1]) : a.W0;
+  a.W2 = n_mats > 2 ? static_cast<const uint8_t*>(mats[2]) : a.W1;
+  a.n0 = ffn ? static_cast<int>(n_out) : static_cast<int>(rows[0]);
+  a.n1 = (!ffn && n_mats > 1) ? static_cast<int>(rows[1]) : 0;
+  a.x = x;
+  a.gamma = gamma;
+  a.eps = eps;
+  a.residual = ffn ? nullptr : residual;
+  a.y = y;
+  a.n_out = static_cast<int>(n_out);
+  a.ppr = static_cast<int>(ppr);
+  a.seg_pairs = static_cast<int>(ppr / nseg);
+  // one workgroup per CU (or per 16 rows when there are fewer), rows split evenly
+  const size_t groups = (n_out + 15) / 16;
+  const size_t cus = static_cast<size_t>(cu_count());
+  size_t grid = groups < cus ? groups : cus;
+  a.rows_per_wg = static_cast<int>((n_out + grid - 1) / grid);
+  grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
+  const size_t lds = mg_lds_bytes(type, a.seg_pairs, nseg, a.residual ? a.rows_per_wg : 0);
+  if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
+  const int mode = ffn ? (kMgNorm | kMgFfn) : (gamma ? kMgNorm : 0);
+  switch (type) {
+    case WH_TYPE_Q4_0: return mg_typed<WH_TYPE_Q4_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
+    case WH_TYPE_Q4_1: return mg_typed<WH_TYPE_Q4_1>(a, nseg, mode, static_cast<int>(grid), lds, s);
+    default: return mg_typed<WH_TYPE_Q8_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
+  }
+}
+
+}  // namespace wh

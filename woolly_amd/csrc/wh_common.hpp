@@ -67,6 +67,16 @@ int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* 
 int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int n_mats, const float* x,
                       const float* gamma, float eps, const float* residual, float* y, size_t k,
                       hipStream_t stream);
+// Single-token GEMV on the int8 matrix cores (gemv_mfma.hip): whether the shape
+// fits, and the launch (WH_ERR_INVALID_SHAPE without launching otherwise).
+// mats / rows: up to three row-stacked matrices with the same K; ffn: mats =
+// {gate, up}, y = silu(gate x_hat) * (up x_hat) over n_out rows.
+bool gemv_mfma_ok(int type, size_t n_out, size_t k);
+int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
+                     const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
+                     hipStream_t stream);
+// WH_GEMV_AUTO / WH_GEMV_STREAM (wh_gemv_select); returns the previous mode.
+int gemv_mode_exchange(int mode);
 // Token counts up to this use one streaming GEMV per token instead of MFMA.
 constexpr size_t kGemvTokenLimit = 2;
 size_t gemm_workspace_bytes(int type, size_t n_tokens, size_t k);

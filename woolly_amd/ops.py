@@ -50,6 +50,18 @@ def quantized_matvec(ggml_type: int, weights, weight_nbytes: int, x, y, m: int, 
                                                _p(y), m, k, _s(stream)))
 
 
+GEMV_AUTO, GEMV_STREAM = 0, 1
+
+
+def gemv_select(mode: int) -> int:
+    """Chooses the single-token GEMV kernels (GEMV_AUTO: the int8 matrix-core
+    kernel where the shape fits, GEMV_STREAM: the streaming kernels only);
+    returns the previous mode."""
+    prev = C.c_int(0)
+    _lib.check(_lib.load().wh_gemv_select(int(mode), C.byref(prev)))
+    return int(prev.value)
+
+
 def matmul_workspace_bytes(ggml_type: int, n_rows: int, k: int, n_tokens: int) -> int:
     return int(_lib.load().wh_quantized_matmul_workspace_bytes(ggml_type, n_rows, k, n_tokens))
 
