@@ -56,7 +56,11 @@ typedef enum wh_type {
   WH_TYPE_F16 = 1,
   WH_TYPE_Q4_0 = 2,
   WH_TYPE_Q4_1 = 3,
-  WH_TYPE_Q8_0 = 8
+  WH_TYPE_Q8_0 = 8,
+  /* 256-element K-quant blocks in woolly-gguf's layout (dequantize.rs:404-536,
+   * which differs from ggml's): dequantization and GEMV only. */
+  WH_TYPE_Q4_K = 12,
+  WH_TYPE_Q6_K = 14
 } wh_type;
 
 typedef struct wh_stream_opaque* wh_stream_t; /* a hipStream_t */
@@ -116,7 +120,10 @@ WH_API int wh_tensor_nbytes(int type, uint64_t nelements, uint64_t* nbytes);
  *   optimized::dequantize_blocks (quantization.rs:1171).
  * Writes exactly nelements f32 values; bit-exact with the reference.
  * F32 and F16 are accepted as in the reference.  WH_ERR_BUFFER_TOO_SMALL when
- * nbytes < ceil(nelements/32) * type_size. */
+ * nbytes < ceil(nelements/32) * type_size.
+ * Q4_K and Q6_K (dequantize_q4_k_scalar / dequantize_q6_k, dequantize.rs:404-536)
+ * decode 256-element blocks; a buffer shorter than ceil(nelements/256) *
+ * type_size is Error::InvalidTensorInfo there, WH_ERR_INVALID_METADATA here. */
 WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelements,
                          float* out, wh_stream_t stream);
 
@@ -124,9 +131,11 @@ WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelem
 /* simd::quantized_matvec(weights, input, output, m, k)
  *   (crates/woolly-tensor/src/quantization.rs:869-909):
  *   output[r] = sum_k W[r, k] * input[k] for r < m.
- * Covers Q4_0 and Q8_0 like the reference, and Q4_1, which the reference
- * rejects with UnsupportedScheme (quantization.rs:905-907).
- * weight_nbytes must be >= m * (k/32) * type_size. */
+ * Covers Q4_0 and Q8_0 like the reference, and Q4_1, Q4_K and Q6_K, which the
+ * reference rejects with UnsupportedScheme (quantization.rs:905-907); those
+ * are defined as the reference's dequantization followed by the f32 dot.
+ * k must be a multiple of the block size (32, or 256 for Q4_K / Q6_K) and
+ * weight_nbytes >= m * (k/block size) * type_size. */
 WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbytes,
                                const float* input, float* output, size_t m, size_t k,
                                wh_stream_t stream);

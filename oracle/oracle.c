@@ -100,6 +100,9 @@ size_t orc_block_size(int type) {
     case ORC_Q4_1:
     case ORC_Q8_0:
       return 32;
+    case ORC_Q4_K:
+    case ORC_Q6_K:
+      return 256;
     default:
       return 0;
   }
@@ -116,6 +119,10 @@ size_t orc_type_size(int type) {
       return 20;
     case ORC_Q8_0:
       return 34;
+    case ORC_Q4_K:
+      return 144;
+    case ORC_Q6_K:
+      return 210;
     default:
       return 0;
   }
@@ -157,6 +164,73 @@ static void dequant_block(int type, const uint8_t* b, float* out) {
   }
 }
 
+/* Q4_K as woolly_gguf decodes it (dequantize_q4_k_scalar, dequantize.rs:404-458;
+ * the x86 path: the NEON variant is aarch64-only).  This is woolly's own
+ * layout, not ggml's: 12 bytes of packed 6-bit scales first (bytes 0..11),
+ * then f16 d (12..13) and f16 dmin (14..15), then 128 bytes of quants.
+ * Scales: for i < 8, src = 3i/2; even i: s = b[src] & 63; odd i:
+ * s = ((b[src] >> 6) | ((b[src+1] & 15) << 2)) & 63.  Element i (0..255):
+ * q = qs[i/2] & 15 for even i, qs[i/2] >> 4 for odd i, value
+ * d * scale[i/32] * q + dmin, evaluated left to right in f32. */
+static void dequant_q4_k_block(const uint8_t* b, float* out) {
+  uint8_t scales[16] = {0};
+  for (int i = 0; i < 8; i++) {
+    int src = (i * 3) / 2;
+    if (i % 2 == 0) scales[i] = (uint8_t)(b[src] & 63);
+    else scales[i] = (uint8_t)(((b[src] >> 6) | ((b[src + 1] & 15) << 2)) & 63);
+  }
+  float d = orc_f16_to_f32(rd16(b + 12));
+  float dmin = orc_f16_to_f32(rd16(b + 14));
+  const uint8_t* qs = b + 16;
+  for (int i = 0; i < 256; i++) {
+    int q = (i % 2 == 0) ? (qs[i / 2] & 0x0F) : ((qs[i / 2] >> 4) & 0x0F);
+    float scale = (float)scales[i / 32];
+    float t = d * scale;
+    float u = t * (float)q;
+    out[i] = u + dmin;
+  }
+}
+
+/* Q6_K as woolly_gguf decodes it (dequantize_q6_k, dequantize.rs:460-536):
+ * ql = bytes 0..127, qh = 128..191, scales = 192..207 (read as u8), f16 d at
+ * 208..209.  Element i: is = i/16,
+ *   ql_idx = 64(i/128) + 32((i%128)/64) + 16((i%64)/32) + i%16,
+ *   qh_idx = 32(i/128) + 16((i%128)/64) + 8((i%64)/32) + (i%32)/4,
+ *   shift = 2((i%32)%4), e1 = (qh[qh_idx] >> shift) & 3,
+ *   e2 = shift < 6 ? (qh[qh_idx] >> (shift+2)) & 3 : (qh_idx+1 < 64 ? qh[qh_idx+1] & 3 : 0),
+ *   q = i < 128 ? (ql[ql_idx] & 15) | (e1 << 4) : (ql[ql_idx] >> 4) | (e2 << 4),
+ * value ((d * scales[is]) * (q - 32)) / 64, left to right in f32. */
+static void dequant_q6_k_block(const uint8_t* b, float* out) {
+  const uint8_t* ql = b;
+  const uint8_t* qh = b + 128;
+  const uint8_t* sc = b + 192;
+  float d = orc_f16_to_f32(rd16(b + 208));
+  for (int i = 0; i < 256; i++) {
+    int is = i / 16;
+    int ql_idx = 64 * (i / 128) + 32 * ((i % 128) / 64) + 16 * ((i % 64) / 32) + (i % 16);
+    int qh_idx = 32 * (i / 128) + 16 * ((i % 128) / 64) + 8 * ((i % 64) / 32) + (i % 32) / 4;
+    int shift = 2 * ((i % 32) % 4);
+    uint8_t qhv = qh[qh_idx];
+    uint8_t e1 = (uint8_t)((qhv >> shift) & 3);
+    uint8_t e2;
+    if (shift < 6) e2 = (uint8_t)((qhv >> (shift + 2)) & 3);
+    else e2 = (uint8_t)(qh_idx + 1 < 64 ? (qh[qh_idx + 1] & 3) : 0);
+    uint8_t q1 = (uint8_t)((ql[ql_idx] & 0x0F) | (e1 << 4));
+    uint8_t q2 = (uint8_t)((ql[ql_idx] >> 4) | (e2 << 4));
+    uint8_t q = i < 128 ? q1 : q2;
+    float s = (float)sc[is];
+    float t = d * s;
+    float u = t * (float)((int)(int8_t)q - 32);
+    out[i] = u / 64.0f;
+  }
+}
+
+static void dequant_any_block(int type, const uint8_t* b, float* out) {
+  if (type == ORC_Q4_K) dequant_q4_k_block(b, out);
+  else if (type == ORC_Q6_K) dequant_q6_k_block(b, out);
+  else dequant_block(type, b, out);
+}
+
 /* woolly_gguf::dequantize(data, ggml_type, nelements), dequantize.rs:189-205:
  * nblocks = ceil(n / 32); BufferTooSmall when data is shorter than
  * nblocks * type_size; the output is truncated to n elements. */
@@ -174,22 +248,24 @@ int orc_dequantize(int type, const uint8_t* data, size_t nbytes, size_t nelement
     for (size_t i = 0; i < nelements; i++) out[i] = orc_f16_to_f32(rd16(data + 2 * i));
     return ORC_OK;
   }
-  size_t nb = (nelements + 31) / 32;
-  if (nbytes < nb * ts) return ORC_ERR_BUFFER_TOO_SMALL;
-  float tmp[32];
+  size_t bs = orc_block_size(type);
+  size_t nb = (nelements + bs - 1) / bs;
+  /* Q4_K / Q6_K report a short buffer as InvalidTensorInfo (dequantize.rs:416-418, 472-474) */
+  if (nbytes < nb * ts) return bs == 256 ? ORC_ERR_INVALID_TENSOR_INFO : ORC_ERR_BUFFER_TOO_SMALL;
+  float tmp[256];
   for (size_t b = 0; b < nb; b++) {
-    dequant_block(type, data + b * ts, tmp);
-    size_t base = b * 32;
-    size_t cnt = nelements - base < 32 ? nelements - base : 32;
+    dequant_any_block(type, data + b * ts, tmp);
+    size_t base = b * bs;
+    size_t cnt = nelements - base < bs ? nelements - base : bs;
     memcpy(out + base, tmp, cnt * sizeof(float));
   }
   return ORC_OK;
 }
 
 static int check_matvec_args(int type, size_t k) {
-  if (type != ORC_Q4_0 && type != ORC_Q4_1 && type != ORC_Q8_0)
+  if (type != ORC_Q4_0 && type != ORC_Q4_1 && type != ORC_Q8_0 && type != ORC_Q4_K && type != ORC_Q6_K)
     return ORC_ERR_UNSUPPORTED_TYPE;
-  if (k % 32 != 0) return ORC_ERR_INVALID_SHAPE;
+  if (k % orc_block_size(type) != 0) return ORC_ERR_INVALID_SHAPE;
   return ORC_OK;
 }
 
@@ -204,6 +280,24 @@ int orc_matvec_f32(int type, const uint8_t* w, const float* x, float* y, size_t 
                    size_t k) {
   int st = check_matvec_args(type, k);
   if (st) return st;
+  if (type == ORC_Q4_K || type == ORC_Q6_K) {
+    /* no reference kernel: dequantize (dequantize.rs:404-536) then the f32 dot
+     * in element order */
+    size_t nbk = k / 256, tsk = orc_type_size(type);
+    float deq[256];
+    for (size_t row = 0; row < m; row++) {
+      float sum = 0.0f;
+      for (size_t b = 0; b < nbk; b++) {
+        dequant_any_block(type, w + (row * nbk + b) * tsk, deq);
+        for (int j = 0; j < 256; j++) {
+          float p = deq[j] * x[b * 256 + j];
+          sum = sum + p;
+        }
+      }
+      y[row] = sum;
+    }
+    return ORC_OK;
+  }
   size_t nb = k / 32, ts = orc_type_size(type);
   for (size_t row = 0; row < m; row++) {
     float sum = 0.0f;
@@ -254,15 +348,15 @@ int orc_matvec_f64(int type, const uint8_t* w, const float* x, double* y, size_t
                    size_t k) {
   int st = check_matvec_args(type, k);
   if (st) return st;
-  size_t nb = k / 32, ts = orc_type_size(type);
-  float deq[32];
+  size_t bs = orc_block_size(type), nb = k / bs, ts = orc_type_size(type);
+  float deq[256];
   for (size_t row = 0; row < m; row++) {
     double sum = 0.0;
     const uint8_t* rp = w + row * nb * ts;
     for (size_t b = 0; b < nb; b++) {
-      dequant_block(type, rp + b * ts, deq);
-      const float* in = x + b * 32;
-      for (int j = 0; j < 32; j++) sum += (double)deq[j] * (double)in[j];
+      dequant_any_block(type, rp + b * ts, deq);
+      const float* in = x + b * bs;
+      for (size_t j = 0; j < bs; j++) sum += (double)deq[j] * (double)in[j];
     }
     y[row] = sum;
   }
@@ -270,9 +364,9 @@ int orc_matvec_f64(int type, const uint8_t* w, const float* x, double* y, size_t
 }
 
 static void dequant_row(int type, const uint8_t* w, size_t row, size_t k, float* out) {
-  size_t nb = k / 32, ts = orc_type_size(type);
+  size_t bs = orc_block_size(type), nb = k / bs, ts = orc_type_size(type);
   const uint8_t* rp = w + row * nb * ts;
-  for (size_t b = 0; b < nb; b++) dequant_block(type, rp + b * ts, out + b * 32);
+  for (size_t b = 0; b < nb; b++) dequant_any_block(type, rp + b * ts, out + b * bs);
 }
 
 /* Y[t, n] = sum_k X[t, k] * W[n, k] in double, for a subset of token rows.

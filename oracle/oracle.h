@@ -21,8 +21,15 @@
  *                         edge values.
  *   orc_dequantize        reference KATs (quantization.rs:1294-1386,
  *                         parallel_inference_integration.rs:159-210) and an
- *                         independent vectorised numpy decoder.
- *   orc_matvec_f32        closed forms on constant-nibble blocks, brute force
+ *                         independent vectorised numpy decoder.  Q4_K /
+ *                         Q6_K (the reference holds no vectors for them,
+ *                         tests/test_oracle_kquant.py): closed forms that
+ *                         isolate each layout rule (field offsets, nibble
+ *                         order, 6-bit scale packing, unsigned Q6_K scales,
+ *                         (q - 32) / 64, the qh wrap at element 255), a
+ *                         whole-array numpy decoder on random bytes, and
+ *                         planted mistakes that fail the closed forms.
+ *   orc_matvec_f32       closed forms on constant-nibble blocks, brute force
  *                         in f64 on tiny shapes, and a numpy float32
  *                         sequential emulation on tiny shapes (order).
  *   orc_matvec_f64 /
@@ -50,7 +57,7 @@ extern "C" {
 #endif
 
 /* GGMLType ids, crates/woolly-gguf/src/tensor_info.rs:15-30 */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
 
 /* Status codes mirror woolly's errors (quantization.rs:8-26, error.rs:11-64). */
 enum {
@@ -58,6 +65,7 @@ enum {
   ORC_ERR_UNSUPPORTED_TYPE = 1,
   ORC_ERR_INVALID_SHAPE = 2,
   ORC_ERR_BUFFER_TOO_SMALL = 3,
+  ORC_ERR_INVALID_TENSOR_INFO = 11, /* Error::InvalidTensorInfo ("Q4_K data too small") */
 };
 
 float orc_f16_to_f32(uint16_t h);

@@ -35,7 +35,11 @@ def test_library_is_gfx950_only():
 def test_format_queries():
     lib = _lib.load()
     assert lib.wh_type_size(2) == 18 and lib.wh_type_size(3) == 20 and lib.wh_type_size(8) == 34
-    assert lib.wh_block_size(2) == 32 and lib.wh_block_size(0) == 1 and lib.wh_block_size(12) == 0
+    assert lib.wh_block_size(2) == 32 and lib.wh_block_size(0) == 1 and lib.wh_block_size(6) == 0
+    # dequantize.rs:208-242: Q4_K / Q6_K are 256-element blocks of 144 / 210 bytes
+    assert lib.wh_block_size(12) == 256 and lib.wh_type_size(12) == 144
+    assert lib.wh_block_size(14) == 256 and lib.wh_type_size(14) == 210
+    assert gguf.data_size(gguf.GGMLType.Q6_K, 4096 + 1) == 17 * 210
     # tensor_info.rs:292-305: 64x64 Q4_0 -> 2304 bytes; 4x8 F32 -> 128 bytes
     assert gguf.data_size(gguf.GGMLType.Q4_0, 4096) == 2304
     assert gguf.data_size(gguf.GGMLType.F32, 32) == 128
@@ -52,9 +56,15 @@ def test_matvec_argument_errors_need_no_gpu():
     assert lib.wh_quantized_matvec(2, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
                                    2, 48, None) == _lib.WH_ERR_INVALID_SHAPE
     assert b"multiple of the block size" in lib.wh_last_error()
-    # unsupported scheme (Q4_K, id 12) -> UnsupportedScheme
-    assert lib.wh_quantized_matvec(12, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
+    # unsupported scheme (Q5_0, id 6) -> UnsupportedScheme
+    assert lib.wh_quantized_matvec(6, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
                                    2, 64, None) == _lib.WH_ERR_UNSUPPORTED_TYPE
+    # Q4_K rows are whole 256-element blocks
+    assert lib.wh_quantized_matvec(12, w.ctypes.data, w.nbytes, x.ctypes.data, y.ctypes.data,
+                                   2, 64, None) == _lib.WH_ERR_INVALID_SHAPE
+    assert b"block size 256" in lib.wh_last_error()
+    assert lib.wh_quantized_matvec(14, w.ctypes.data, 2 * 210 - 1, x.ctypes.data, y.ctypes.data,
+                                   2, 256, None) == _lib.WH_ERR_BUFFER_TOO_SMALL
     # too few weight bytes -> BufferTooSmall{needed, available}
     assert lib.wh_quantized_matvec(2, w.ctypes.data, 71, x.ctypes.data, y.ctypes.data,
                                    2, 64, None) == _lib.WH_ERR_BUFFER_TOO_SMALL
@@ -71,7 +81,12 @@ def test_dequant_argument_errors_need_no_gpu():
         gguf.dequantize(bytes(35), gguf.GGMLType.Q4_0, 64)
     assert e.value.needed == 36 and e.value.available == 35
     with pytest.raises(gguf.InvalidTensorType):
-        gguf.dequantize(bytes(144), gguf.GGMLType.Q4_K, 256)
+        gguf.dequantize(bytes(22), gguf.GGMLType.Q5_0, 32)
+    # a short K-quant block is InvalidTensorInfo (dequantize.rs:416-418, 472-474)
+    with pytest.raises(gguf.InvalidTensorInfo):
+        gguf.dequantize(bytes(143), gguf.GGMLType.Q4_K, 256)
+    with pytest.raises(gguf.InvalidTensorInfo):
+        gguf.dequantize(bytes(210), gguf.GGMLType.Q6_K, 257)
     with pytest.raises(gguf.BufferTooSmall):
         gguf.dequantize(bytes(10), gguf.GGMLType.F32, 4)   # F32 needs exactly 16 bytes
     assert gguf.dequantize(b"", gguf.GGMLType.Q4_0, 0).size == 0

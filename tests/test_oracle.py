@@ -204,7 +204,7 @@ def test_dequant_errors(orc):
     w = synth.quantized_weight(Q4_0, 1, 64, seed=1)
     st, _ = orc.dequantize(Q4_0, w[:35], 64)   # needs 36 bytes
     assert st == 3
-    st, _ = orc.dequantize(12, w, 64)          # Q4_K is not on this path
+    st, _ = orc.dequantize(6, w, 32)           # Q5_0 is not on this path
     assert st == 1
     st, out = orc.dequantize(Q4_0, w, 40)      # truncation to nelements
     assert st == 0 and out.size == 40
@@ -283,7 +283,8 @@ def test_gemv_errors(orc):
     w = synth.quantized_weight(Q4_0, 2, 64, seed=1)
     x = np.zeros(64, np.float32)
     assert orc.matvec_f32(Q4_0, w, x, 2, 48)[0] == 2   # k % 32 != 0
-    assert orc.matvec_f32(12, w, x, 2, 64)[0] == 1     # unsupported scheme
+    assert orc.matvec_f32(6, w, x, 2, 64)[0] == 1      # unsupported scheme (Q5_0)
+    assert orc.matvec_f32(12, w, x, 2, 64)[0] == 2     # Q4_K: k % 256 != 0
 
 
 # ------------------------------------------------------------------- GEMM KATs

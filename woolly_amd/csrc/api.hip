@@ -42,9 +42,18 @@ int check_block_args(const char* fn, int type, size_t k) {
   return WH_OK;
 }
 
+// The GEMV also takes the 256-element K-quant blocks.
+int check_gemv_args(const char* fn, int type, size_t k) {
+  if (!wh::is_kquant(type)) return check_block_args(fn, type, k);
+  if (k % 256 != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: k = %zu is not a multiple of the block size 256",
+                         fn, k);
+  return WH_OK;
+}
+
 int check_weight_bytes(const char* fn, int type, size_t rows, size_t k, size_t have) {
   const size_t ts = wh::type_size(type);
-  const size_t nb = k / 32;
+  const size_t nb = k / wh::block_elems(type);
   if (rows != 0 && nb != 0 && (rows > SIZE_MAX / nb || rows * nb > SIZE_MAX / ts))
     return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: %zu x %zu weight size overflows", fn, rows, k);
   const size_t need = rows * nb * ts;
@@ -311,16 +320,7 @@ WH_API int wh_graph_destroy(wh_graph_t graph) {
 }
 
 // -------------------------------------------------------------------- format
-WH_API size_t wh_block_size(int type) {
-  switch (type) {
-    case WH_TYPE_F32:
-    case WH_TYPE_F16: return 1;
-    case WH_TYPE_Q4_0:
-    case WH_TYPE_Q4_1:
-    case WH_TYPE_Q8_0: return 32;
-    default: return 0;
-  }
-}
+WH_API size_t wh_block_size(int type) { return wh::block_elems(type); }
 
 WH_API size_t wh_type_size(int type) { return wh::type_size(type); }
 
@@ -344,7 +344,14 @@ WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelem
                            "dequantize: buffer too small: needed %zu bytes, available %zu",
                            nelements * ts, nbytes);
   } else {
-    const size_t need = (nelements + 31) / 32 * ts;
+    const size_t bs = wh::block_elems(type);
+    const size_t need = (nelements / bs + (nelements % bs != 0)) * ts;
+    // The K-quant decoders report a short block as invalid tensor info
+    // (dequantize.rs:416-418, 472-474), the others as BufferTooSmall.
+    if (nbytes < need && wh::is_kquant(type))
+      return wh::set_error(WH_ERR_INVALID_METADATA,
+                           "dequantize: insufficient data for K-quant block: needed %zu bytes, available %zu",
+                           need, nbytes);
     if (nbytes < need)
       return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
                            "dequantize: buffer too small: needed %zu bytes, available %zu", need,
@@ -362,7 +369,7 @@ WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelem
 WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbytes,
                                const float* input, float* output, size_t m, size_t k,
                                wh_stream_t stream) {
-  int st = check_block_args("quantized_matvec", type, k);
+  int st = check_gemv_args("quantized_matvec", type, k);
   if (st) return st;
   st = check_weight_bytes("quantized_matvec", type, m, k, weight_nbytes);
   if (st) return st;
@@ -581,7 +588,9 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
   if (nelements == 0) return wh_dequantize(type, data, nbytes, 0, out, nullptr);
   if (!data || !out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "dequantize_host: null pointer");
   const size_t in_bytes =
-      (type == WH_TYPE_F32 || type == WH_TYPE_F16) ? nelements * ts : (nelements + 31) / 32 * ts;
+      (type == WH_TYPE_F32 || type == WH_TYPE_F16)
+          ? nelements * ts
+          : (nelements / wh::block_elems(type) + (nelements % wh::block_elems(type) != 0)) * ts;
   if (nbytes < in_bytes || ((type == WH_TYPE_F32 || type == WH_TYPE_F16) && nbytes != in_bytes))
     return wh_dequantize(type, data, nbytes, nelements, out, nullptr);
   DevBuf din, dout;
@@ -596,14 +605,14 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
 
 WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
                                     const float* input, float* output, size_t m, size_t k) {
-  int st = check_block_args("quantized_matvec", type, k);
+  int st = check_gemv_args("quantized_matvec", type, k);
   if (st) return st;
   st = check_weight_bytes("quantized_matvec", type, m, k, weight_nbytes);
   if (st) return st;
   if (m == 0) return WH_OK;
   if (!output || (k > 0 && (!weights || !input)))
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matvec_host: null pointer");
-  const size_t wbytes = m * (k / 32) * wh::type_size(type);
+  const size_t wbytes = m * (k / wh::block_elems(type)) * wh::type_size(type);
   DevBuf dw, dx, dy;
   if (wbytes) WH_HIP_TRY(hipMalloc(&dw.p, wbytes));
   if (k) WH_HIP_TRY(hipMalloc(&dx.p, k * sizeof(float)));

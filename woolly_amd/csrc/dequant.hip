@@ -169,6 +169,9 @@ int launch_dequantize(int type, const void* data, size_t n, float* out, hipStrea
     case WH_TYPE_Q8_0:
       launch_blocks<WH_TYPE_Q8_0>(p, n, out, s, grid_for((n + 3) / 4, 256, cap));
       break;
+    case WH_TYPE_Q4_K:
+    case WH_TYPE_Q6_K:
+      return launch_dequantize_kquant(type, data, n, out, s);
     default:
       return set_error(WH_ERR_UNSUPPORTED_TYPE, "dequantize: unsupported type %d", type);
   }

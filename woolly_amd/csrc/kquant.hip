@@ -1,0 +1,150 @@
+// kquant.hip -- the 256-element K-quant blocks (Q4_K, Q6_K) as woolly-gguf
+// decodes them, on gfx950: bit-exact dequantization and a GEMV defined as that
+// dequantization followed by the f32 dot product.
+//
+// Reference: woolly_gguf::dequantize (crates/woolly-gguf/src/dequantize.rs:189-205)
+// with dequantize_q4_k_scalar (:404-458, the x86 path) and dequantize_q6_k
+// (:460-536).  woolly reads these blocks its own way (not ggml's layout):
+//   Q4_K (144 B): bytes 0..11 pack eight 6-bit scales, scale i from byte
+//     src = 3i/2: even i -> b[src] & 63, odd i -> ((b[src] >> 6) |
+//     ((b[src+1] & 15) << 2)) & 63; f16 d at 12..13, f16 dmin at 14..15,
+//     quants at 16..143: element i is the low nibble of qs[i/2] for even i, the
+//     high nibble for odd i; value d * scale[i/32] * q + dmin.
+//   Q6_K (210 B): ql = 0..127, qh = 128..191, u8 scales = 192..207, f16 d at
+//     208..209; element i takes 4 bits from ql[64(i/128) + 32((i%128)/64) +
+//     16((i%64)/32) + i%16] (low nibble below 128, high nibble from 128 on) and
+//     2 bits from qh[32(i/128) + 16((i%128)/64) + 8((i%64)/32) + (i%32)/4]
+//     at shift 2((i%32)%4) (+2 for the upper half; at shift 6 that pair is the
+//     low bits of the next qh byte, 0 past the last one); value
+//     ((d * scale[i/16]) * (q - 32)) / 64.
+// Every product and sum is rounded in the reference's order with unfused
+// operations, so the results are bit-identical to the CPU.
+#include "wh_common.hpp"
+
+namespace {
+
+__device__ __forceinline__ uint32_t b16(const uint8_t* p) {
+  return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
+}
+
+// Element i (0..255) of a Q4_K block at b.
+__device__ __forceinline__ float q4k_elem(const uint8_t* b, int i, float d, float dmin) {
+  const int j = i >> 5;            // scale index
+  const int src = (3 * j) >> 1;
+  const uint32_t s = (j & 1) ? (((b[src] >> 6) | ((b[src + 1] & 15u) << 2)) & 63u) : (b[src] & 63u);
+  const uint32_t qb = b[16 + (i >> 1)];
+  const uint32_t q = (i & 1) ? ((qb >> 4) & 15u) : (qb & 15u);
+  return __fadd_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q)), dmin);
+}
+
+// Element i (0..255) of a Q6_K block at b.
+__device__ __forceinline__ float q6k_elem(const uint8_t* b, int i, float d) {
+  const uint8_t* ql = b;
+  const uint8_t* qh = b + 128;
+  const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
+  const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
+  const int shift = 2 * (i & 3);
+  const uint32_t qhv = qh[qh_idx];
+  uint32_t q;
+  if (i < 128) {
+    q = (ql[ql_idx] & 15u) | (((qhv >> shift) & 3u) << 4);
+  } else {
+    const uint32_t e2 = shift < 6 ? ((qhv >> (shift + 2)) & 3u) : (qh_idx + 1 < 64 ? (qh[qh_idx + 1] & 3u) : 0u);
+    q = (ql[ql_idx] >> 4) | (e2 << 4);
+  }
+  const float s = static_cast<float>(b[192 + (i >> 4)]);
+  return __fmul_rn(__fmul_rn(__fmul_rn(d, s), static_cast<float>(static_cast<int>(q) - 32)), 0.015625f);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void kq_quad(const uint8_t* b, int c, float v[4]) {
+  if constexpr (TYPE == WH_TYPE_Q4_K) {
+    const float d = whd::f16_bits_to_f32(b16(b + 12));
+    const float dmin = whd::f16_bits_to_f32(b16(b + 14));
+#pragma unroll
+    for (int t = 0; t < 4; t++) v[t] = q4k_elem(b, 4 * c + t, d, dmin);
+  } else {
+    const float d = whd::f16_bits_to_f32(b16(b + 208));
+#pragma unroll
+    for (int t = 0; t < 4; t++) v[t] = q6k_elem(b, 4 * c + t, d);
+  }
+}
+
+template <int TYPE>
+constexpr int kq_bytes() { return TYPE == WH_TYPE_Q4_K ? 144 : 210; }
+
+// One thread per quad of 4 consecutive outputs (64 quads per block), grid-stride.
+template <int TYPE>
+__global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restrict__ data, float* __restrict__ out,
+                                                         size_t n) {
+  const size_t nquads = (n + 3) / 4;
+  for (size_t qd = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; qd < nquads;
+       qd += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t blk = qd >> 6;
+    const int c = static_cast<int>(qd & 63);
+    float v[4];
+    kq_quad<TYPE>(data + blk * kq_bytes<TYPE>(), c, v);
+    const size_t e = 4 * qd;
+    if (e + 4 <= n && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+      *reinterpret_cast<float4*>(out + e) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int t = 0; t < 4 && e + t < n; t++) out[e + t] = v[t];
+    }
+  }
+}
+
+// y[row] = sum_k dequant(W)[row, k] * x[k]: one wave per row (grid-stride),
+// lane l takes quad l (elements 4l..4l+3) of every block of the row.
+template <int TYPE>
+__global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                      float* __restrict__ y, size_t n_rows, size_t nb) {
+  const int lane = threadIdx.x & 63;
+  const size_t waves = static_cast<size_t>(gridDim.x) * (blockDim.x >> 6);
+  for (size_t row = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6); row < n_rows;
+       row += waves) {
+    const uint8_t* rp = w + row * nb * kq_bytes<TYPE>();
+    float acc = 0.f;
+    for (size_t b = 0; b < nb; b++) {
+      float v[4];
+      kq_quad<TYPE>(rp + b * kq_bytes<TYPE>(), lane, v);
+      const float* xb = x + 256 * b + 4 * lane;
+#pragma unroll
+      for (int t = 0; t < 4; t++) acc = __builtin_fmaf(v[t], xb[t], acc);
+    }
+    acc = whd::wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+  }
+}
+
+unsigned kq_grid(size_t work, unsigned per_block) {
+  size_t g = (work + per_block - 1) / per_block;
+  const size_t cap = static_cast<size_t>(wh::cu_count()) * 16;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+namespace wh {
+
+int launch_dequantize_kquant(int type, const void* data, size_t n, float* out, hipStream_t s) {
+  if (n == 0) return WH_OK;
+  const uint8_t* p = static_cast<const uint8_t*>(data);
+  const unsigned grid = kq_grid((n + 3) / 4, 256);
+  if (type == WH_TYPE_Q4_K) kq_dequant_kernel<WH_TYPE_Q4_K><<<grid, 256, 0, s>>>(p, out, n);
+  else kq_dequant_kernel<WH_TYPE_Q6_K><<<grid, 256, 0, s>>>(p, out, n);
+  WH_LAUNCH_CHECK("dequantize (k-quant) kernel launch");
+  return WH_OK;
+}
+
+int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k, hipStream_t s) {
+  if (n_rows == 0) return WH_OK;
+  const uint8_t* p = static_cast<const uint8_t*>(w);
+  const unsigned grid = kq_grid(n_rows, 4);
+  if (type == WH_TYPE_Q4_K) kq_gemv_kernel<WH_TYPE_Q4_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
+  else kq_gemv_kernel<WH_TYPE_Q6_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
+  WH_LAUNCH_CHECK("gemv (k-quant) kernel launch");
+  return WH_OK;
+}
+
+}  // namespace wh

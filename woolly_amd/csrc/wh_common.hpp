@@ -37,12 +37,30 @@ inline size_t type_size(int type) {
     case WH_TYPE_Q4_0: return 18;
     case WH_TYPE_Q4_1: return 20;
     case WH_TYPE_Q8_0: return 34;
+    case WH_TYPE_Q4_K: return 144;
+    case WH_TYPE_Q6_K: return 210;
     default: return 0;
   }
 }
+// Elements per block (1 for the plain types, 0 for unknown ids).
+inline size_t block_elems(int type) {
+  switch (type) {
+    case WH_TYPE_F32:
+    case WH_TYPE_F16: return 1;
+    case WH_TYPE_Q4_0:
+    case WH_TYPE_Q4_1:
+    case WH_TYPE_Q8_0: return 32;
+    case WH_TYPE_Q4_K:
+    case WH_TYPE_Q6_K: return 256;
+    default: return 0;
+  }
+}
+// The 32-element block formats every kernel of the library takes.
 inline bool is_block_type(int type) {
   return type == WH_TYPE_Q4_0 || type == WH_TYPE_Q4_1 || type == WH_TYPE_Q8_0;
 }
+// The 256-element K-quant formats (dequantization and GEMV only).
+inline bool is_kquant(int type) { return type == WH_TYPE_Q4_K || type == WH_TYPE_Q6_K; }
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
@@ -53,6 +71,10 @@ size_t max_lds_per_block();
 // validated by the C ABI layer; these only choose kernels and launch them.
 int launch_dequantize(int type, const void* data, size_t nelements, float* out,
                       hipStream_t stream);
+// Q4_K / Q6_K (kquant.hip): bit-exact dequantization and dequantize-then-dot GEMV.
+int launch_dequantize_kquant(int type, const void* data, size_t nelements, float* out, hipStream_t stream);
+int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k,
+                       hipStream_t stream);
 int launch_fill_bytes(void* dst, int value, size_t nbytes, hipStream_t stream);
 int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows,
                 size_t k, hipStream_t stream);

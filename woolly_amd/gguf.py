@@ -142,6 +142,8 @@ def dequantize(data, ggml_type: GGMLType, nelements: int) -> np.ndarray:
         raise BufferTooSmall(int(m.group(1)), int(m.group(2))) if m else GgufError(_lib.last_error())
     if st == _lib.WH_ERR_UNSUPPORTED_TYPE:
         raise InvalidTensorType(int(ggml_type))
+    if st == _lib.WH_ERR_INVALID_METADATA:  # short K-quant data (dequantize.rs:416-418, 472-474)
+        raise InvalidTensorInfo(_lib.last_error())
     _lib.check(st)
     return out
 

@@ -12,6 +12,7 @@ from . import _lib
 from .device import DeviceBuffer, Stream
 
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q8_0 = 0, 1, 2, 3, 8
+GGML_Q4_K, GGML_Q6_K = 12, 14  # dequantization and GEMV only
 
 
 def _s(stream: Stream | None):

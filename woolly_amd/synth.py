@@ -11,6 +11,10 @@ Block layouts (crates/woolly-tensor/src/quantization.rs:98-151):
   Q4_0  {u16 d; u8 qs[16]}            18 B
   Q4_1  {u16 d; u16 m; u8 qs[16]}     20 B
   Q8_0  {u16 d; i8 qs[32]}            34 B
+and the 256-element K-quant blocks as woolly-gguf reads them
+(crates/woolly-gguf/src/dequantize.rs:404-536):
+  Q4_K  {u8 scales[12]; u16 d; u16 dmin; u8 qs[128]}              144 B
+  Q6_K  {u8 ql[128]; u8 qh[64]; u8 scales[16]; u16 d}              210 B
 """
 from __future__ import annotations
 
@@ -20,9 +24,10 @@ GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 M1 = np.uint64(0xBF58476D1CE4E5B9)
 M2 = np.uint64(0x94D049BB133111EB)
 
-GGML_Q4_0, GGML_Q4_1, GGML_Q8_0 = 2, 3, 8
-TYPE_SIZE = {GGML_Q4_0: 18, GGML_Q4_1: 20, GGML_Q8_0: 34}
-TYPE_NAME = {GGML_Q4_0: "Q4_0", GGML_Q4_1: "Q4_1", GGML_Q8_0: "Q8_0"}
+GGML_Q4_0, GGML_Q4_1, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 2, 3, 8, 12, 14
+TYPE_SIZE = {GGML_Q4_0: 18, GGML_Q4_1: 20, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
+BLOCK_ELEMS = {GGML_Q4_0: 32, GGML_Q4_1: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+TYPE_NAME = {GGML_Q4_0: "Q4_0", GGML_Q4_1: "Q4_1", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K", GGML_Q6_K: "Q6_K"}
 
 
 def _mix(z: np.ndarray) -> np.ndarray:
@@ -76,13 +81,29 @@ def quantized_weight(ggml_type: int, n_rows: int, k: int, seed: int, stream: int
     Q4_0: d = f16(|N(0, 0.02)|), qs bytes uniform 0..255 (two uniform nibbles).
     Q8_0: d = f16(|N(0, 0.02)|), qs int8 uniform in [-127, 127].
     Q4_1: d, m = f16(N(0, 0.01)), qs bytes uniform 0..255.
+    Q4_K: scale bytes uniform, d = f16(|N(0, 0.0005)|), dmin = f16(N(0, 0.01)), quant bytes uniform.
+    Q6_K: ql, qh, scale bytes uniform, d = f16(|N(0, 0.0001)|).
     """
-    if k % 32:
-        raise ValueError("k must be a multiple of 32")
-    nb = n_rows * (k // 32)
+    be = BLOCK_ELEMS.get(ggml_type, 0)
+    if be == 0:
+        raise ValueError(f"unsupported ggml type {ggml_type}")
+    if k % be:
+        raise ValueError(f"k must be a multiple of {be}")
+    nb = n_rows * (k // be)
     ts = TYPE_SIZE[ggml_type]
     out = np.empty((nb, ts), dtype=np.uint8)
     s0 = 16 * stream
+    if ggml_type == GGML_Q4_K:
+        out[:, :] = (u64(seed, s0 + 2, nb * ts) & np.uint64(0xFF)).astype(np.uint8).reshape(nb, ts)
+        d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.0005 if d_std is None else d_std))
+        out[:, 12:14] = f16_bits(d).view(np.uint8).reshape(nb, 2)
+        out[:, 14:16] = f16_bits(normal(seed, s0 + 3, nb, 0.0, 0.01)).view(np.uint8).reshape(nb, 2)
+        return out.reshape(-1)
+    if ggml_type == GGML_Q6_K:
+        out[:, :] = (u64(seed, s0 + 2, nb * ts) & np.uint64(0xFF)).astype(np.uint8).reshape(nb, ts)
+        d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.0001 if d_std is None else d_std))
+        out[:, 208:210] = f16_bits(d).view(np.uint8).reshape(nb, 2)
+        return out.reshape(-1)
     if ggml_type == GGML_Q4_0:
         d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.02 if d_std is None else d_std))
         out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
