@@ -55,11 +55,12 @@ WARM_S = 0.1          # untimed replays before each timed GEMV measurement (cloc
 TIMED_REPLAYS = 5     # timed graph replays per measurement; the median is reported
 
 
-TYPE_SIZE = {2: 18, 3: 20, 8: 34}
+TYPE_SIZE = {2: 18, 3: 20, 8: 34, 12: 144, 14: 210}
+BLOCK_ELEMS = {2: 32, 3: 32, 8: 32, 12: 256, 14: 256}
 
 
 def gemv_bytes(n: int, k: int, t: int = Q4_0) -> int:
-    return n * (k // 32) * TYPE_SIZE[t] + 4 * k + 4 * n
+    return n * (k // BLOCK_ELEMS[t]) * TYPE_SIZE[t] + 4 * k + 4 * n
 
 
 def log(msg: str) -> None:
@@ -372,6 +373,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
+    ap.add_argument("--gemv-shape", type=int, nargs=3, default=None, metavar=("TYPE", "N", "K"),
+                    help="ggml type id and shape of --only gemv (default Q4_0 14336 4096)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only device-to-device copies of 256 MiB (counter calibration)")
     args = ap.parse_args()
@@ -388,8 +391,11 @@ def main() -> int:
         print(json.dumps({"copy_probe_GBps": round(copy_probe(), 1), "bytes_per_copy": 256 << 20}))
         return 0
     if args.only == "gemv":
-        ms_step, _, _ = bench_gemv(args.steps, args.warmup)
-        print(json.dumps({"gemv_us": round(ms_step * 1e3, 3)}))
+        t, n, k = args.gemv_shape or (Q4_0, N_ROWS, K)
+        reps = max(1, -(-300_000_000 // gemv_bytes(n, k, t)))  # > 256 MB of weights in rotation
+        ms_step, _, _ = bench_gemv(args.steps, args.warmup, t, n, k, 3, reps)
+        print(json.dumps({"gemv_us": round(ms_step * 1e3, 3), "type": t, "n": n, "k": k,
+                          "GBps": round(gemv_bytes(n, k, t) / (ms_step * 1e-3) / 1e9, 1)}))
         return 0
     if args.only == "gemm":
         print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5), 2)}))
@@ -439,7 +445,12 @@ def main() -> int:
                                           # the Q8_0 output head
                                           ("attn_kv_q4_0_1024x4096", Q4_0, 1024, 4096, 6, 120),
                                           ("ffn_down_q4_0_4096x14336", Q4_0, 4096, 14336, 6, 10),
-                                          ("head_q8_0_128256x4096", 8, 128256, 4096, 6, 1)):
+                                          ("head_q8_0_128256x4096", 8, 128256, 4096, 6, 1),
+                                          # the K-quant blocks (woolly-gguf's Q4_K / Q6_K layout)
+                                          ("kq_q4_k_14336x4096", 12, 14336, 4096, 7, 10),
+                                          ("kq_q6_k_14336x4096", 14, 14336, 4096, 7, 7),
+                                          ("kq_q4_k_4096x14336", 12, 4096, 14336, 7, 10),
+                                          ("kq_q6_k_4096x14336", 14, 4096, 14336, 7, 7)):
             ms, _, _ = bench_gemv(100, 10, t, n, k, seed, reps)
             gbs = gemv_bytes(n, k, t) / (ms * 1e-3) / 1e9
             gemv_cfg[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),

@@ -108,3 +108,59 @@ def test_kquant_gemv_matches_dequantized_dot(gpu):
     deq = gpu_dequant(Q6_K, w, m * k).reshape(m, k).astype(np.float64)
     got = gemv(Q6_K, w, x, m, k)
     assert rel_l2(got, deq @ x.astype(np.float64)) <= 1e-6
+
+
+# K = 2048 .. 16384: 1 .. 4 K-segments of the matrix-core kernel (Q6_K at
+# K = 14336: four segments of 14 blocks that start 4, 8, 12 bytes past a
+# 16-byte boundary); K = 2560 and 5120 (Q6_K rows not a multiple of 16 bytes)
+# run on the simple kernel
+MFMA_K = [2048, 2560, 4096, 5120, 8192, 12288, 14336, 16384]
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("k", MFMA_K)
+def test_kquant_mfma_matches_simple_kernel(gpu, orc, t, k):
+    print(f"[case] kquant mfma type={t} k={k}", flush=True)
+    m = 200
+    w = synth.quantized_weight(t, m, k, seed=k + t)
+    x = synth.activations(k, seed=k + 1)
+    got = gemv(t, w, x, m, k)
+    prev = ops.gemv_select(ops.GEMV_STREAM)
+    try:
+        simple = gemv(t, w, x, m, k)
+    finally:
+        ops.gemv_select(prev)
+    ref = orc.matvec_f64(t, w, x, m, k)[1]
+    for name, y in (("auto", got), ("simple", simple)):
+        r, a = rel_l2(y, ref), max_abs(y, ref)
+        print(f"[result] kquant {name} t={t} k={k} rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+        assert r <= 1e-4 and a <= 1e-3
+    assert rel_l2(got, simple) <= 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("scale", [1e-30, 1e30])
+def test_kquant_mfma_activation_scales(gpu, orc, t, scale):
+    m, k = 256, 4096
+    w = synth.quantized_weight(t, m, k, seed=31)
+    x = (synth.activations(k, seed=32) * np.float32(scale)).astype(np.float32)
+    got = gemv(t, w, x, m, k)
+    ref = orc.matvec_f64(t, w, x, m, k)[1]
+    assert rel_l2(got, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_kquant_mfma_nonfinite_and_zero_chunks(gpu, orc, t):
+    m, k = 128, 4096
+    w = synth.quantized_weight(t, m, k, seed=33)
+    x = synth.activations(k, seed=34)
+    x[:512] = 0.0
+    got = gemv(t, w, x, m, k)
+    assert rel_l2(got, orc.matvec_f64(t, w, x, m, k)[1]) <= 1e-4
+    x[700] = np.inf
+    got = gemv(t, w, x, m, k)
+    ref = orc.matvec_f32(t, w, x, m, k)[1]
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(np.isinf(got[fin]), np.isinf(ref[fin]))
+    assert np.array_equal(np.sign(got[fin]), np.sign(ref[fin]))

@@ -912,7 +912,14 @@ int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows
     case WH_TYPE_Q4_1: return launch_typed<WH_TYPE_Q4_1>(wp, x, y, n_rows, k, s);
     case WH_TYPE_Q8_0: return launch_typed<WH_TYPE_Q8_0>(wp, x, y, n_rows, k, s);
     case WH_TYPE_Q4_K:
-    case WH_TYPE_Q6_K: return launch_gemv_kquant(type, w, x, y, n_rows, k, s);
+    case WH_TYPE_Q6_K:
+      if (use_mfma(type, n_rows, k)) {
+        const void* mats[1] = {w};
+        const size_t rows[1] = {n_rows};
+        const int st = launch_gemv_mfma(type, mats, rows, 1, false, x, nullptr, 0.f, nullptr, y, n_rows, k, s);
+        if (st != WH_ERR_INVALID_SHAPE) return st;
+      }
+      return launch_gemv_kquant(type, w, x, y, n_rows, k, s);
     default: return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "gemv: unsupported type %d", type);
   }
 }

@@ -38,6 +38,26 @@
 // chunk holds inf or NaN computes that chunk per element instead,
 // ((q - 8) * d) * x accumulated like the reference, so inf/NaN propagate as in
 // quantized_matvec_q4_0_scalar (quantization.rs:1121-1124).
+//
+// Q4_K (woolly_gguf's layout, dequantize.rs:404-458: 6-bit scales s_j at bytes
+// 0..11, f16 d and dmin at 12..15, element 2b / 2b+1 = low / high nibble of
+// quant byte b at 16 + b) is one 256-element block per chunk, 144 bytes like
+// four Q4_0 pairs: its eight 32-element scale groups take the place of the
+// eight blocks, with scale d * s_j (exact in f32) and the minimum entering as
+// dmin * sum(x) over the block.
+//
+// Q6_K (woolly_gguf's indexing, dequantize.rs:460-536) is one 210-byte block
+// per chunk.  Element i = 32 j + 8 g + t of K-step j takes the low (j < 4) or
+// high (j >= 4) nibble of quant byte 16 j + 8 (g & 1) + t and the two bits
+// 2 t + 2 (j >= 4) .. of the 24-bit word qh[8 j + 2 g .. 8 j + 2 g + 2] (the
+// byte past the last is 0), so one lane's eight B values are two dwords of
+// nibbles or-ed with spread 2-bit fields (q = 0..63); the -32 enters through
+// the accumulator input, -32 * (limb sums), the same for every weight row
+// and computed once per segment with MFMAs against a B operand of -32s.  Its scales are per
+// 16 elements: the limbs of the two halves of a 32-element step sit in
+// different A rows (rows 8 (j & 1) + 4 h + limb), so lane group G of
+// accumulator t holds the sums of 16-element group 4 t + G, scaled by
+// d * s / 64 (exact).
 #include "wh_blocks.hpp"
 
 typedef int mg_v4i __attribute__((ext_vector_type(4)));
@@ -61,9 +81,16 @@ __device__ __forceinline__ mg_v4i mg_rsrc(const void* base, uint32_t nbytes) {
 
 constexpr int kMgWaves = 16;                   // waves per workgroup
 constexpr int kMgSegMax = 16 * 64 * 4;        // bytes of one row segment (at most 4 loads)
-constexpr int kMgPad = 16;                     // LDS row padding (bank spread)
+// LDS row stride of a ring slot: the segment (and its lead room) rounded up
+// to an odd number of 16-byte units, so that the 16 rows of a step start in
+// 16 different bank quads.
+__host__ __device__ constexpr uint32_t mg_row_stride(uint32_t seg_bytes, uint32_t lead_room) {
+  return ((seg_bytes + 15u) & ~15u) + lead_room + (((((seg_bytes + 15u) & ~15u) + lead_room) >> 4) & 1u ? 0u : 16u);
+}
 constexpr int kMgLimbBytes = 4 * 32;            // four limbs of one block
-constexpr int kMgStage = 8 * kMgLimbBytes + 8 * 16;  // limb staging bytes per chunk (+ limb sums)
+// limb staging bytes per chunk: the limbs, then the limb sums of each
+// 32-element block
+constexpr int mg_stage_bytes(int type) { return 8 * kMgLimbBytes + (type == WH_TYPE_Q6_K ? 0 : 8 * 16); }
 constexpr int kMgNt = 2;                       // streaming (non-temporal) loads
 constexpr int kMgNorm = 1, kMgFfn = 2;         // kernel variants
 
@@ -81,6 +108,24 @@ template <>
 struct MgFmt<WH_TYPE_Q8_0> {
   static constexpr int PB = 68;
 };
+template <>
+struct MgFmt<WH_TYPE_Q4_K> {
+  static constexpr int PB = 0;  // not used: one 144-byte block per chunk
+};
+template <>
+struct MgFmt<WH_TYPE_Q6_K> {
+  static constexpr int PB = 0;  // not used: one 210-byte block per chunk
+};
+
+// bytes of one 256-weight chunk of a format the kernel takes; 0 otherwise
+constexpr int mg_chunk_bytes(int type) {
+  return type == WH_TYPE_Q4_0 ? 144
+         : type == WH_TYPE_Q4_1 ? 160
+         : type == WH_TYPE_Q8_0 ? 272
+         : type == WH_TYPE_Q4_K ? 144
+         : type == WH_TYPE_Q6_K ? 210
+                                : 0;
+}
 
 // Output rows [0, n_out).  Plain mode: row r is row r of the matrices W0, W1,
 // W2 stacked (n0 rows of W0, n1 of W1, the rest of W2).  FFN mode: W0 = gate,
@@ -101,10 +146,14 @@ struct MgArgs {
 
 // k-slot (0..7) of lane group g that element el (0..31) of a block feeds:
 // Q4: slots 0..3 = low nibbles of quant bytes 4g..4g+3 (elements 4g..4g+3),
-// slots 4..7 = their high nibbles (elements 16+4g..); Q8_0: element 8g + slot.
+// slots 4..7 = their high nibbles (elements 16+4g..); Q8_0 and Q6_K: element
+// 8g + slot.
+// Q4_K: quant byte 4g + b of a group holds elements 8g + 2b (low nibble, slot
+// b) and 8g + 2b + 1 (high nibble, slot 4 + b).
 template <int TYPE>
 __device__ __forceinline__ int mg_slot_offset(int el) {
-  if constexpr (TYPE == WH_TYPE_Q8_0) return el;
+  if constexpr (TYPE == WH_TYPE_Q8_0 || TYPE == WH_TYPE_Q6_K) return el;
+  if constexpr (TYPE == WH_TYPE_Q4_K) return 8 * (el >> 3) + ((el & 1) ? 4 : 0) + ((el & 7) >> 1);
   return 8 * ((el & 15) >> 2) + (el & 3) + (el >= 16 ? 4 : 0);
 }
 
@@ -168,6 +217,78 @@ __device__ float mg_pair_exact(const uint8_t* p, const float* x, const float* ga
   return s;
 }
 
+// 6-bit scale j (0..7) of a Q4_K block (dequantize.rs:423-431): src = 3j/2,
+// even j: b[src] & 63, odd j: ((b[src] >> 6) | ((b[src + 1] & 15) << 2)) & 63.
+__device__ __forceinline__ uint32_t mg_q4k_scale(const uint8_t* b, int j) {
+  const int src = (3 * j) >> 1;
+  return (j & 1) ? (((static_cast<uint32_t>(b[src]) >> 6) | ((static_cast<uint32_t>(b[src + 1]) & 15u) << 2)) & 63u)
+                 : (static_cast<uint32_t>(b[src]) & 63u);
+}
+
+// Q4_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block at
+// blk, w = ((d * s) * q) + dmin as dequantize_q4_k_scalar evaluates it.
+__device__ float mg_q4k_exact(const uint8_t* blk, int g, const float* x, const float* gamma, float rms) {
+  const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[12]) | (static_cast<uint32_t>(blk[13]) << 8));
+  const float dmin = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[14]) | (static_cast<uint32_t>(blk[15]) << 8));
+  float s = 0.f;
+#pragma unroll 2
+  for (int el = 0; el < 64; el++) {
+    const int i = 64 * g + el;
+    const float ds = __fmul_rn(d, static_cast<float>(mg_q4k_scale(blk, i >> 5)));
+    const uint32_t qb = blk[16 + (i >> 1)];
+    const float w = __fadd_rn(__fmul_rn(ds, static_cast<float>((i & 1) ? (qb >> 4) : (qb & 15u))), dmin);
+    float xv = x[el];
+    if (gamma) xv = (xv / rms) * gamma[el];
+    s = __builtin_fmaf(w, xv, s);
+  }
+  return s;
+}
+
+// Q6_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block
+// at blk, w = ((d * s) * (q - 32)) / 64 as dequantize_q6_k evaluates it.
+__device__ float mg_q6k_exact(const uint8_t* blk, int g, const float* x, const float* gamma, float rms) {
+  const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
+  float s = 0.f;
+#pragma unroll 2
+  for (int el = 0; el < 64; el++) {
+    const int i = 64 * g + el;
+    const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
+    const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
+    const int sh = 2 * (i & 3);
+    const uint32_t qhv = blk[128 + qh_idx];
+    uint32_t q;
+    if (i < 128) {
+      q = (blk[ql_idx] & 15u) | (((qhv >> sh) & 3u) << 4);
+    } else {
+      const uint32_t e2 = sh < 6 ? ((qhv >> (sh + 2)) & 3u) : (qh_idx + 1 < 64 ? (blk[129 + qh_idx] & 3u) : 0u);
+      q = (static_cast<uint32_t>(blk[ql_idx]) >> 4) | (e2 << 4);
+    }
+    const float w = __fmul_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(blk[192 + (i >> 4)])),
+                                        static_cast<float>(static_cast<int>(q) - 32)),
+                              0.015625f);
+    float xv = x[el];
+    if (gamma) xv = (xv / rms) * gamma[el];
+    s = __builtin_fmaf(w, xv, s);
+  }
+  return s;
+}
+
+// Two dwords of LDS bytes at p, which lies mis (0 or 2) bytes past a dword
+// boundary.  Pointer arithmetic only: an integer round trip would turn the
+// LDS reads into flat loads, which wait behind the global loads in flight.
+__device__ __forceinline__ void mg_lds_u64(const uint8_t* p, int mis, uint32_t& lo, uint32_t& hi) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(p - mis);
+  const uint32_t sh = static_cast<uint32_t>(mis) * 8u;
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+  lo = __builtin_amdgcn_alignbit(w1, w0, sh);
+  hi = __builtin_amdgcn_alignbit(w2, w1, sh);
+}
+
+// Bits 2t .. 2t + 1 of v (t = 0..3) moved to bits 4..5 of byte t.
+__device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
+  return ((v << 4) | (v << 10) | (v << 16) | (v << 22)) & 0x30303030u;
+}
+
 // NL: 16-byte loads per lane per step (row segments of up to 1024 NL bytes).
 template <int TYPE, int NSEG, int NL, int MODE>
 __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a) {
@@ -175,19 +296,27 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   constexpr bool FFN = (MODE & kMgFfn) != 0;
   constexpr bool NORM = (MODE & kMgNorm) != 0;
   constexpr bool Q41 = TYPE == WH_TYPE_Q4_1;
+  constexpr bool Q4K = TYPE == WH_TYPE_Q4_K;
+  constexpr bool Q6K = TYPE == WH_TYPE_Q6_K;
+  constexpr int CB = mg_chunk_bytes(TYPE);
+  constexpr int STG = mg_stage_bytes(TYPE);
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int S = a.seg_pairs;
-  const uint32_t seg_bytes = static_cast<uint32_t>(S) * PB;
-  const uint32_t rstr = seg_bytes + kMgPad;
+  const uint32_t seg_bytes = static_cast<uint32_t>(S >> 2) * CB;
+  // Segments that do not start on a 16-byte boundary (Q6_K's 210-byte chunks)
+  // are loaded from the boundary below, `lead` bytes early, into an LDS row
+  // whose data then starts `lead` bytes in (the writes stay 16-byte aligned).
+  constexpr uint32_t kLeadRoom = (CB & 15) ? 16u : 0u;
+  const uint32_t rstr = mg_row_stride(seg_bytes, kLeadRoom);
   const uint32_t slot_bytes = 16 * rstr;
-  const size_t row_bytes = static_cast<size_t>(a.ppr) * PB;
+  const size_t row_bytes = static_cast<size_t>(a.ppr >> 2) * CB;
   const int K = a.ppr * 64;
   uint8_t* ring = lds;
-  uint8_t* stage = lds + 2 * slot_bytes + wave * NSEG * kMgStage;  // per segment: limbs, block sums
-  float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * NSEG * kMgStage);  // [2][16][16]
+  uint8_t* stage = lds + 2 * slot_bytes + wave * NSEG * STG;  // per segment: limbs, block sums
+  float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * NSEG * STG);  // [2][16][16]
   float* misc = part + 2 * kMgWaves * 16;                                                    // [16] + [16]
   float* res_lds = misc + 32;                                                                 // residual rows
 
@@ -223,7 +352,8 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   auto load = [&](int q, int seg) {
     const uint8_t* base = a.W0;
     const bool ok = row_src(q, &base);
-    const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes, ok ? seg_bytes : 0u);
+    const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
+    const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes - lead, ok ? seg_bytes + lead : 0u);
 #pragma unroll
     for (int i = 0; i < NL; i++) buf[i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
   };
@@ -295,8 +425,8 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       e = 30 - ee;
     }
     ex[seg] = e;
-    int8_t* xop = reinterpret_cast<int8_t*>(stage + seg * kMgStage);
-    int* bs_lds = reinterpret_cast<int*>(stage + seg * kMgStage + 8 * kMgLimbBytes);
+    int8_t* xop = reinterpret_cast<int8_t*>(stage + seg * STG);
+    int* bs_lds = reinterpret_cast<int*>(stage + seg * STG + 8 * kMgLimbBytes);
     int bs[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -319,14 +449,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       bs[2] += l2;
       bs[3] += l3;
     }
-    // a block is 8 consecutive lanes
+    // a block is 8 consecutive lanes (Q6_K needs no sums: its bias is in the quants)
+    if constexpr (!Q6K) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      bs[r] += __shfl_xor(bs[r], 4, 64);
-      bs[r] += __shfl_xor(bs[r], 2, 64);
-      bs[r] += __shfl_xor(bs[r], 1, 64);
+      for (int r = 0; r < 4; r++) {
+        bs[r] += __shfl_xor(bs[r], 4, 64);
+        bs[r] += __shfl_xor(bs[r], 2, 64);
+        bs[r] += __shfl_xor(bs[r], 1, 64);
+      }
+      if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
     }
-    if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
@@ -334,15 +466,29 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   // zeros set here
   long xo[8];
   mg_v4i cin[2];  // Q4_0: -8 * limb sums of block 4t + g (accumulator input)
+  mg_v4i cq[Q6K ? 4 : 1];  // Q6_K: -32 * limb sums of 16-element group 4t + g
   float bsum[2];  // Q4_1: sum of the block's activations, in units of 2^-e
 #pragma unroll
   for (int lb = 0; lb < 8; lb++) xo[lb] = 0;
   auto get_x = [&](int seg) {
-    const int8_t* xop = reinterpret_cast<const int8_t*>(stage + seg * kMgStage);
-    const int* bs_lds = reinterpret_cast<const int*>(stage + seg * kMgStage + 8 * kMgLimbBytes);
+    const int8_t* xop = reinterpret_cast<const int8_t*>(stage + seg * STG);
+    const int* bs_lds = reinterpret_cast<const int*>(stage + seg * STG + 8 * kMgLimbBytes);
 #pragma unroll
-    for (int lb = 0; lb < 8; lb++)
-      if ((n >> 2) == (lb & 3)) xo[lb] = *reinterpret_cast<const long*>(xop + lb * kMgLimbBytes + 32 * (n & 3) + 8 * g);
+    for (int lb = 0; lb < 8; lb++) {
+      // Q6_K: rows 8 (lb & 1) + 4 h + limb carry half h of block lb (k groups 2h, 2h + 1)
+      const bool mine = Q6K ? ((n >> 2) == 2 * (lb & 1) + (g >> 1)) : ((n >> 2) == (lb & 3));
+      if (mine) xo[lb] = *reinterpret_cast<const long*>(xop + lb * kMgLimbBytes + 32 * (n & 3) + 8 * g);
+    }
+    if constexpr (Q6K) {
+      // -32 * (limb sums of each 16-element group): the same for every weight
+      // row, so one MFMA per K-step against a B operand of -32s
+#pragma unroll
+      for (int t = 0; t < 4; t++) cq[t] = (mg_v4i){0, 0, 0, 0};
+#pragma unroll
+      for (int lb = 0; lb < 8; lb++)
+        cq[lb >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[lb], static_cast<long>(0xE0E0E0E0E0E0E0E0ull), cq[lb >> 1], 0, 0, 0);
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
       const int4 v = *reinterpret_cast<const int4*>(bs_lds + 4 * (4 * t + g));
@@ -384,10 +530,11 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       uint8_t* slot = ring + (s & 1) * slot_bytes;
       {
         uint8_t* dst = slot + wave * rstr;
+        const uint32_t end = seg_bytes + ((static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u));
 #pragma unroll
         for (int i = 0; i < NL; i++) {
           const uint32_t o = 16u * (64 * i + lane);
-          if (o < seg_bytes) *reinterpret_cast<mg_v4i*>(dst + o) = buf[i];
+          if (o < end) *reinterpret_cast<mg_v4i*>(dst + o) = buf[i];
         }
       }
       if (seg + 1 < NSEG) load(q, seg + 1);
@@ -399,43 +546,121 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
       if (owns) {
         if constexpr (NSEG > 1) get_x(seg);
-        const uint8_t* rowp = slot + n * rstr + wave * 4 * PB;
-        if (!exact[seg]) {
-          // scale (and minimum) of block 4t + g
-          uint32_t dm[2];
+        const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
+        const uint8_t* rowp = slot + n * rstr + lead + wave * CB;
+        if constexpr (Q6K) {
+          if (!exact[seg]) {
+            mg_v4i C[4];
 #pragma unroll
-          for (int t = 0; t < 2; t++) {
-            const int blk = 4 * t + g;
-            const uint8_t* bp = rowp + (blk >> 1) * PB + (blk & 1) * (PB / 2);
-            if constexpr (Q41) dm[t] = *reinterpret_cast<const uint32_t*>(bp);
-            else dm[t] = *reinterpret_cast<const uint16_t*>(bp);
+            for (int t = 0; t < 4; t++) C[t] = cq[t];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+              uint32_t l0, l1;
+              // LDS rows start 16-byte aligned, the chunk `lead + 210 wave` bytes in
+              mg_lds_u64(rowp + 16 * j + 8 * (g & 1), static_cast<int>((lead + 2 * (wave & 1)) & 3u), l0, l1);
+              const uint8_t* hp = rowp + 128 + 8 * j + 2 * g;
+              uint32_t w = *reinterpret_cast<const uint16_t*>(hp);  // hp is even
+              if (j >= 4) {
+                // 8 j + 2 g + 2 == 64 only for j = 7, g = 3 (element 255)
+                if (j < 7 || g < 3) w |= static_cast<uint32_t>(hp[2]) << 16;
+                w >>= 2;
+                l0 >>= 4;
+                l1 >>= 4;
+              }
+              const uint32_t b0 = (l0 & 0x0F0F0F0Fu) | mg_spread2(w & 0xFFu);
+              const uint32_t b1 = (l1 & 0x0F0F0F0Fu) | mg_spread2((w >> 8) & 0xFFu);
+              const long qj = static_cast<long>(b0) | (static_cast<long>(b1) << 32);
+              C[j >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[j], qj, C[j >> 1], 0, 0, 0);
+            }
+            const float d64 = whd::f16_bits_to_f32(static_cast<uint32_t>(rowp[208]) |
+                                                   (static_cast<uint32_t>(rowp[209]) << 8)) * 0.015625f;
+            float sacc = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
+                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
+                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
+                                                                           static_cast<float>(C[t][3]))));
+              sacc = __builtin_fmaf(d64 * static_cast<float>(rowp[192 + 4 * t + g]), f, sacc);
+            }
+            acc += ldexpf(sacc, -ex[seg]);
+          } else {
+            // lane group g: elements 64 g .. 64 g + 63 of the block, row n
+            const int e0 = (seg * S + 4 * wave + g) * 64;
+            acc += mg_q6k_exact(rowp, g, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
           }
-          mg_v4i C[2];
+        } else if constexpr (Q4K) {
+          if (!exact[seg]) {
+            // the chunk is one block: groups j = 0..7 of 32 elements, group
+            // 4t + g's limb sums in lane group g of C[t]
+            const uint32_t* pw = reinterpret_cast<const uint32_t*>(rowp);
+            mg_v4i C[2];
 #pragma unroll
-          for (int t = 0; t < 2; t++) C[t] = cin[t];
+            for (int t = 0; t < 2; t++) C[t] = cin[t];
 #pragma unroll
-          for (int p = 0; p < 4; p++) {
-            long qa, qb;
-            mg_quants<TYPE>(reinterpret_cast<const uint32_t*>(rowp + p * PB), g, qa, qb);
-            C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p], qa, C[p >> 1], 0, 0, 0);
-            C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p + 1], qb, C[p >> 1], 0, 0, 0);
+            for (int j = 0; j < 8; j++) {
+              const uint32_t u = pw[4 + 4 * j + g];
+              const long qj = static_cast<long>(u & 0x0F0F0F0Fu) | (static_cast<long>((u >> 4) & 0x0F0F0F0Fu) << 32);
+              C[j >> 2] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[j], qj, C[j >> 2], 0, 0, 0);
+            }
+            const uint32_t dd = pw[3];
+            const float d = whd::f16_bits_to_f32(dd & 0xFFFFu);
+            const float dmin = whd::f16_bits_to_f32(dd >> 16);
+            float sacc = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
+                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
+                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
+                                                                           static_cast<float>(C[t][3]))));
+              const float ds = d * static_cast<float>(mg_q4k_scale(rowp, 4 * t + g));
+              sacc = __builtin_fmaf(ds, f, sacc);
+              sacc = __builtin_fmaf(dmin, bsum[t], sacc);
+            }
+            acc += ldexpf(sacc, -ex[seg]);
+          } else {
+            // lane group g: elements 64 g .. 64 g + 63 of the block, row n
+            const int e0 = (seg * S + 4 * wave + g) * 64;
+            acc += mg_q4k_exact(rowp, g, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
           }
-          float sacc = 0.f;
-#pragma unroll
-          for (int t = 0; t < 2; t++) {
-            const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
-                                           __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
-                                                          __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
-                                                                         static_cast<float>(C[t][3]))));
-            const float d = whd::f16_bits_to_f32(dm[t] & 0xFFFFu);
-            sacc = __builtin_fmaf(d, f, sacc);
-            if constexpr (Q41) sacc = __builtin_fmaf(whd::f16_bits_to_f32(dm[t] >> 16), bsum[t], sacc);
-          }
-          acc += ldexpf(sacc, -ex[seg]);
         } else {
-          // lane group g: pair g of the chunk, row n
-          const int e0 = (seg * S + 4 * wave + g) * 64;
-          acc += mg_pair_exact<TYPE>(rowp + g * PB, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+          if (!exact[seg]) {
+            // scale (and minimum) of block 4t + g
+            uint32_t dm[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+              const int blk = 4 * t + g;
+              const uint8_t* bp = rowp + (blk >> 1) * PB + (blk & 1) * (PB / 2);
+              if constexpr (Q41) dm[t] = *reinterpret_cast<const uint32_t*>(bp);
+              else dm[t] = *reinterpret_cast<const uint16_t*>(bp);
+            }
+            mg_v4i C[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) C[t] = cin[t];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+              long qa, qb;
+              mg_quants<TYPE>(reinterpret_cast<const uint32_t*>(rowp + p * PB), g, qa, qb);
+              C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p], qa, C[p >> 1], 0, 0, 0);
+              C[p >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[2 * p + 1], qb, C[p >> 1], 0, 0, 0);
+            }
+            float sacc = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
+                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
+                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
+                                                                           static_cast<float>(C[t][3]))));
+              const float d = whd::f16_bits_to_f32(dm[t] & 0xFFFFu);
+              sacc = __builtin_fmaf(d, f, sacc);
+              if constexpr (Q41) sacc = __builtin_fmaf(whd::f16_bits_to_f32(dm[t] >> 16), bsum[t], sacc);
+            }
+            acc += ldexpf(sacc, -ex[seg]);
+          } else {
+            // lane group g: pair g of the chunk, row n
+            const int e0 = (seg * S + 4 * wave + g) * 64;
+            acc += mg_pair_exact<TYPE>(rowp + g * PB, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+          }
         }
       }
       if (seg == NSEG - 1) {
@@ -453,20 +678,28 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
 }
 
 size_t mg_lds_bytes(int type, int seg_pairs, int nseg, int rows_per_wg) {
-  const int pb = type == WH_TYPE_Q4_0 ? 36 : (type == WH_TYPE_Q4_1 ? 40 : 68);
-  return 2u * 16u * static_cast<size_t>(seg_pairs * pb + kMgPad) + static_cast<size_t>(kMgWaves) * nseg * kMgStage +
+  const int cb = mg_chunk_bytes(type);
+  const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * cb);
+  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), (cb & 15) ? 16u : 0u);
+  return 2u * 16u * rstr +
+         static_cast<size_t>(kMgWaves) * nseg * mg_stage_bytes(type) +
          4u * (2 * kMgWaves * 16 + 32 + static_cast<size_t>(rows_per_wg));
 }
 
 // Segments: the fewest (1 .. 4) that split the row into whole 4-pair chunks,
-// at most 16 chunks and 4 KB per segment; 0 when none does.
+// at most 16 chunks and 4 KB per segment (with the up to 15 bytes loaded
+// ahead of a segment that does not start on a 16-byte boundary).  Rows must
+// be a multiple of 16 bytes (Q6_K: a multiple of 8 blocks), so that a load
+// range only ends inside a 16-byte piece in the middle of a row, never at the
+// end of the matrix.  0 when none does.
 int mg_segments(int type, size_t ppr) {
-  const size_t pb = type == WH_TYPE_Q4_0 ? 36 : (type == WH_TYPE_Q4_1 ? 40 : 68);
-  if (ppr == 0 || ppr % 4 != 0) return 0;
+  const size_t cb = mg_chunk_bytes(type);
+  if (cb == 0 || ppr == 0 || ppr % 4 != 0 || (ppr / 4 * cb) % 16 != 0) return 0;
+  const size_t lead = (cb & 15) ? 15 : 0;
   for (int ns = 1; ns <= 4; ns++) {
     if (ppr % ns != 0) continue;
     const size_t s = ppr / ns;
-    if (s % 4 == 0 && s / 4 <= kMgWaves && s * pb <= kMgSegMax) return ns;
+    if (s % 4 == 0 && s / 4 <= kMgWaves && s / 4 * cb + lead <= kMgSegMax) return ns;
   }
   return 0;
 }
@@ -493,7 +726,8 @@ int mg_dispatch_nl(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t 
 
 template <int TYPE, int MODE>
 int mg_dispatch(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t s) {
-  const int seg_bytes = a.seg_pairs * MgFmt<TYPE>::PB;
+  // bytes one lane group of 64 lanes loads per row: the segment and its lead
+  const int seg_bytes = a.seg_pairs / 4 * mg_chunk_bytes(TYPE) + ((mg_chunk_bytes(TYPE) & 15) ? 15 : 0);
   return seg_bytes <= 3072 ? mg_dispatch_nl<TYPE, 3, MODE>(a, nseg, grid, lds, s)
                            : mg_dispatch_nl<TYPE, 4, MODE>(a, nseg, grid, lds, s);
 }
@@ -512,7 +746,7 @@ int mg_typed(const MgArgs& a, int nseg, int mode, int grid, size_t lds, hipStrea
 namespace wh {
 
 bool gemv_mfma_ok(int type, size_t n_out, size_t k) {
-  if (!(type == WH_TYPE_Q4_0 || type == WH_TYPE_Q4_1 || type == WH_TYPE_Q8_0)) return false;
+  if (mg_chunk_bytes(type) == 0) return false;
   if (n_out == 0 || n_out >= (1u << 30) || k % 64 != 0) return false;
   return mg_segments(type, k / 64) > 0;
 }
@@ -557,6 +791,8 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   switch (type) {
     case WH_TYPE_Q4_0: return mg_typed<WH_TYPE_Q4_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
     case WH_TYPE_Q4_1: return mg_typed<WH_TYPE_Q4_1>(a, nseg, mode, static_cast<int>(grid), lds, s);
+    case WH_TYPE_Q4_K: return mg_typed<WH_TYPE_Q4_K>(a, nseg, mode, static_cast<int>(grid), lds, s);
+    case WH_TYPE_Q6_K: return mg_typed<WH_TYPE_Q6_K>(a, nseg, mode, static_cast<int>(grid), lds, s);
     default: return mg_typed<WH_TYPE_Q8_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
   }
 }
