@@ -254,6 +254,43 @@ __device__ __forceinline__ half8 unpack_q8(uint32_t u0, uint32_t u1) {
   return out;
 }
 
+// v_and_or_b32: (u & mask) | magic in one instruction (mask in an SGPR, magic
+// in a VGPR: gfx950's VOP3 takes no two literal constants).
+__device__ __forceinline__ uint32_t and_or(uint32_t u, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(u), "s"(mask), "v"(magic));
+  return r;
+}
+
+// Part p (0..3) of the B operand of one weight lane, i.e. its fp16 slots
+// 2p, 2p + 1, in the slot order of unpack_q4 / unpack_q8; the four parts can
+// be computed at different points of the schedule.
+template <int TYPE>
+__device__ __forceinline__ void unpack_part(int p, uint32_t u0, uint32_t u1, uint32_t magic, half8& out) {
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  half2v r;
+  if constexpr (TYPE == WH_TYPE_Q8_0) {
+    const half2v off = {static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
+    const uint32_t w = p < 2 ? u0 : u1;
+    const uint32_t sel = (p & 1) ? 0x0c030c02u : 0x0c010c00u;
+    r = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0u, w, sel) ^ 0x64806480u) + off;
+  } else {
+    constexpr float OFF_LO = TYPE == WH_TYPE_Q4_0 ? -1032.f : -1024.f;
+    constexpr float OFF_HI = TYPE == WH_TYPE_Q4_0 ? -72.f : -64.f;
+    const uint32_t w = (p & 1) ? (u0 >> 8) : u0;
+    if (p < 2) {
+      const half2v off_lo = {static_cast<_Float16>(OFF_LO), static_cast<_Float16>(OFF_LO)};
+      r = __builtin_bit_cast(half2v, and_or(w, 0x000F000Fu, magic)) + off_lo;
+    } else {
+      const half2v off_hi = {static_cast<_Float16>(OFF_HI), static_cast<_Float16>(OFF_HI)};
+      const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+      r = __builtin_elementwise_fma(__builtin_bit_cast(half2v, and_or(w, 0x00F000F0u, magic)), sixteenth, off_hi);
+    }
+  }
+  out[2 * p] = r[0];
+  out[2 * p + 1] = r[1];
+}
+
 // Global -> LDS copies (global_load_lds): lane l's 16 (or 4) bytes at
 // base + voff land at LDS address lds + 16 l (4 l).  Issued through inline asm
 // so that the compiler does not treat them as pending LDS writes (it would
@@ -386,6 +423,38 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   const int g = lane >> 4;       // k-group
   const int ln = lane & 15;      // token (A) / weight row (B) within a 16-tile
 
+  // Software pipeline over pairs of row groups (NT is even).  Per pair of a
+  // block: the hi MFMAs of both groups, then their lo MFMAs (a lo MFMA comes
+  // 2 IT MFMAs after the hi MFMA it depends on), with the block-scale FMAs of
+  // the previous pair (pending: possibly of the previous block or stage) and
+  // the unpacking of the next pair's weights spread over the 4 IT MFMA slots;
+  // scheduling fences keep that order, so the matrix pipe and the VALU work
+  // side by side within a wave.  The pending scales start as 0 * 0 (no-ops)
+  // and are flushed after the last stage.
+  static_assert(NT % 2 == 0 && (SB * (NT / 2)) % 2 == 0, "pairs of row groups alternate buffers");
+  float4v cc[2][2][IT];  // [current / pending pair][group of the pair][token group]
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int i = 0; i < IT; i++) cc[b][h][i] = float4v{0.f, 0.f, 0.f, 0.f};
+  float pd[2] = {0.f, 0.f}, pm[2] = {0.f, 0.f};  // pending block scales (and Q4_1 minima)
+  float4v psx[IT];                               // pending Q4_1 block sums
+#pragma unroll
+  for (int i = 0; i < IT; i++) psx[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  const uint32_t magic = 0x64006400u;  // fp16 1024 in both halves (held in a VGPR)
+
+  // acc[i][N] += pd[h] * cc[B][h][i] (+ pm[h] * psx[i]); constants after unrolling
+  auto scale_one = [&](int N, int B, int h, int i) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float v = __builtin_fmaf(pd[h], cc[B][h][i][r], acc[i][N][r]);
+      if constexpr (TYPE == WH_TYPE_Q4_1) v = __builtin_fmaf(pm[h], psx[i][r], v);
+      acc[i][N][r] = v;
+    }
+  };
+
 #pragma unroll
   for (int st = 0; st < NSTAGE - 1; st++) issue(st);
   for (int st = 0; st < n_stages; st++) {
@@ -395,81 +464,109 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     issue(st + NSTAGE - 1);         // into the slot of stage st - 1, which all waves finished
     const uint8_t* slot = smem + (st % NSTAGE) * STAGE;
     const uint8_t* bslot = slot + A_STAGE;
-#pragma unroll
-    for (int j = 0; j < SB; j++) {
-      half8 ah[IT], al[IT];
+    // every LDS operand of the stage, read up front
+    half8 ah[SB][IT], al[SB][IT];
+    uint32_t wq0[SB][NT], wq1[SB][NT], wdm[SB][NT];
+    float4v sx[SB][IT];
+    auto load_a = [&](int j) {
 #pragma unroll
       for (int i = 0; i < IT; i++) {
         const int grp = (wm >> 4) + i;
-        ah[i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp) * FRAG + 16 * lane);
-        al[i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp + 1) * FRAG + 16 * lane);
+        ah[j][i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp) * FRAG + 16 * lane);
+        al[j][i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp + 1) * FRAG + 16 * lane);
       }
-      float4v sx[IT];
-      if constexpr (TYPE == WH_TYPE_Q4_1) {
-        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * BM;
+    };
 #pragma unroll
-        for (int i = 0; i < IT; i++) sx[i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
-      }
-      // Software pipeline over the row groups: the MFMAs of group n + 1 are
-      // issued before the block-scale FMAs of group n, so the matrix pipe and
-      // the VALU work on independent data; each group's weight bytes are read
-      // from LDS one group ahead.
-      auto load_w = [&](int n, uint32_t& u0, uint32_t& u1, uint32_t& dm) {
+    for (int j = 0; j < SB; j++) {
+      load_a(j);
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
         const int row = wn + 16 * n + ln;
         const uint8_t* rb = bslot + row * (DWB * 4) + j * TS;     // this block's bytes
         const uint16_t* r16 = reinterpret_cast<const uint16_t*>(rb);
         if constexpr (TYPE == WH_TYPE_Q8_0) {
           const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rb + QOFF + 8 * g);
-          u0 = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
-          u1 = static_cast<uint32_t>(q16[2]) | (static_cast<uint32_t>(q16[3]) << 16);
+          wq0[j][n] = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
+          wq1[j][n] = static_cast<uint32_t>(q16[2]) | (static_cast<uint32_t>(q16[3]) << 16);
         } else {
           const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rb + QOFF + 4 * g);
-          u0 = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
-          u1 = 0u;
+          wq0[j][n] = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
+          wq1[j][n] = 0u;
         }
-        dm = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
-                                  : static_cast<uint32_t>(r16[0]);
-      };
-      auto mfmas = [&](uint32_t u0, uint32_t u1, float4v* c) {
-        half8 bw;
-        if constexpr (TYPE == WH_TYPE_Q8_0) bw = unpack_q8(u0, u1);
-        else bw = unpack_q4<TYPE>(u0);
+        wdm[j][n] = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
+                                         : static_cast<uint32_t>(r16[0]);
+      }
+      if constexpr (TYPE == WH_TYPE_Q4_1) {
+        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * BM;
 #pragma unroll
-        for (int i = 0; i < IT; i++) c[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        for (int i = 0; i < IT; i++) sx[j][i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
+      }
+    }
+    half8 bw[2];
 #pragma unroll
-        for (int i = 0; i < IT; i++) c[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw, c[i], 0, 0, 0);
-      };
-      auto scale = [&](int n, uint32_t dm, const float4v* c) {
-        // d in an f32 register: the FMAs below are then plain v_fmac_f32
-        float d = whd::f16_bits_to_f32(dm & 0xFFFFu);
-        asm("" : "+v"(d));
-        const float mm = TYPE == WH_TYPE_Q4_1 ? whd::f16_bits_to_f32(dm >> 16) : 0.f;
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int i = 0; i < IT; i++)
+      for (int part = 0; part < 4; part++) unpack_part<TYPE>(part, wq0[0][h], wq1[0][h], magic, bw[h]);
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            float v = __builtin_fmaf(d, c[i][r], acc[i][n][r]);
-            if constexpr (TYPE == WH_TYPE_Q4_1) v = __builtin_fmaf(mm, sx[i][r], v);
-            acc[i][n][r] = v;
+    for (int j = 0; j < SB; j++) {
+#pragma unroll
+      for (int np = 0; np < NT / 2; np++) {
+        // the pairs of a stage alternate between the two buffers (SB NT / 2 is even)
+        const int cur = (j * (NT / 2) + np) & 1, pend = cur ^ 1;
+        // the pending pair: groups 2 np - 2, 2 np - 1 of this block, or the last pair of the previous
+        const int pn = np == 0 ? NT - 2 : 2 * np - 2;
+        // the next pair's weights: pair np + 1 of this block, or pair 0 of the next block
+        const bool more = np + 1 < NT / 2 || j + 1 < SB;
+        const int jn = np + 1 < NT / 2 ? j : (j + 1 < SB ? j + 1 : j);
+        const int nn = np + 1 < NT / 2 ? 2 * np + 2 : 0;
+        half8 bn[2] = {bw[0], bw[1]};
+        // slot k of 4 IT: the pending pair's scales for (h, i) = (k / IT) % 2, k % IT
+        // in the first 2 IT slots, the next pair's unpacking in the last 2 IT
+        int k = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int i = 0; i < IT; i++) {
+            cc[cur][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j][i], bw[h], float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            scale_one(pn + h, pend, h, i);
+            k++;
+            __builtin_amdgcn_sched_barrier(0);
           }
-      };
-      float4v cc[2][IT];
-      uint32_t wq0[2], wq1[2], wdm[2];
-      load_w(0, wq0[0], wq1[0], wdm[0]);
-      if (NT > 1) load_w(1, wq0[1], wq1[1], wdm[1]);
-      mfmas(wq0[0], wq1[0], cc[0]);
 #pragma unroll
-      for (int n = 0; n < NT; n++) {
-        const int cur = n & 1, nxt = cur ^ 1;
-        const uint32_t dm_n = wdm[cur];
-        if (n + 1 < NT) {
-          mfmas(wq0[nxt], wq1[nxt], cc[nxt]);
-          if (n + 2 < NT) load_w(n + 2, wq0[cur], wq1[cur], wdm[cur]);
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int i = 0; i < IT; i++) {
+            cc[cur][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j][i], bw[h], cc[cur][h][i], 0, 0, 0);
+            if (more) {
+              // 8 parts (2 groups x 4) over 2 IT slots
+#pragma unroll
+              for (int q = (h * IT + i) * 8 / (2 * IT); q < (h * IT + i + 1) * 8 / (2 * IT); q++)
+                unpack_part<TYPE>(q % 4, wq0[jn][nn + q / 4], wq1[jn][nn + q / 4], magic, bn[q / 4]);
+            }
+            k++;
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        // this pair becomes the pending one
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          pd[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] & 0xFFFFu);
+          asm("" : "+v"(pd[h]));  // in a VGPR: the FMAs are then plain v_fmac_f32
+          if constexpr (TYPE == WH_TYPE_Q4_1) pm[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] >> 16);
         }
-        scale(n, dm_n, cc[cur]);
+        if constexpr (TYPE == WH_TYPE_Q4_1) {
+#pragma unroll
+          for (int i = 0; i < IT; i++) psx[i] = sx[j][i];
+        }
+        bw[0] = bn[0];
+        bw[1] = bn[1];
       }
     }
   }
+  // flush the pending scales (the last pair of the last block)
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int i = 0; i < IT; i++) scale_one(NT - 2 + h, (SB * (NT / 2) - 1) & 1, h, i);
   wait_vmcnt<0>();  // (no copies remain: every issued stage was consumed)
 
   // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
