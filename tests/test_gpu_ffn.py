@@ -96,6 +96,23 @@ def test_ffn_small(gpu, orc, t, hidden, n_ff, m):
     assert r <= REL_L2 and a <= max_abs_bar(ref)
 
 
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1])
+@pytest.mark.parametrize("hidden,n_ff,m", [(20480, 256, 3), (256, 20480, 5), (4096, 1024, 64)])
+def test_ffn_prefill_fused_packing(gpu, orc, t, hidden, n_ff, m):
+    """The prefill FFN packs RMSNorm(x) once for gate and up and forms the SwiGLU
+    while packing the down projection's activations; rows longer than 16384
+    elements (hidden or n_ff = 20480) take the packing's multi-chunk path."""
+    print(f"[case] ffn fused packing t={t} hidden={hidden} n_ff={n_ff} m={m}", flush=True)
+    L = synth.ffn_layer(t, hidden, n_ff, m, seed=hidden + n_ff + t)
+    got = run_ffn(t, L, hidden, n_ff, m)
+    rows = sorted({0, m // 2, m - 1})
+    ref = orc.ffn_rows_f64(t, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5, L["x"], rows)
+    g = got[rows]
+    r, a = rel_l2(g, ref), max_abs(g, ref)
+    print(f"[result] ffn fused t={t} {hidden}/{n_ff} m={m} rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
 def test_ffn_llama3_8b_m1(gpu, orc):
     """Config 3 at M=1: Llama-3-8B FFN shape, Q4_0, against the f64 oracle."""
     hidden, n_ff, m = 4096, 14336, 1

@@ -490,6 +490,12 @@ WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps,
     }
     if (fused) return wh::launch_gemm(w->type, w->down, H, F, h, m, out, gemm_ws, gemm_bytes, s);
   }
+  if (m > wh::kGemvTokenLimit) {
+    // prefill: the tiled MFMA kernel with RMSNorm and SwiGLU in its packing
+    st = wh::launch_ffn_tiled(w->type, w->gate, w->up, w->down, H, F, x, gamma, eps, m, g, u, out, gemm_ws,
+                              gemm_bytes, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   if ((st = wh::launch_rms_norm(x, gamma, eps, m, H, xh, s))) return st;
   if ((st = wh::launch_gemm(w->type, w->gate, F, H, xh, m, g, gemm_ws, gemm_bytes, s))) return st;
   if ((st = wh::launch_gemm(w->type, w->up, F, H, xh, m, u, gemm_ws, gemm_bytes, s))) return st;

@@ -116,14 +116,24 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 // elements of a pair are two float4 loads (slot_elem order), all issued
 // before the first use; a row of up to 256 * PPT pairs (k <= 64 * PPT) is
 // read once and packed from registers, longer rows are read a second time.
+// MODE: the row packed is x itself (kPackPlain); the RMSNorm of x,
+// (x / sqrt(sum x^2 / k + eps)) * gamma as rms_norm computes it
+// (tensor_utils.rs:446-480; kPackNorm); or the SwiGLU of two rows,
+// (g * (1 / (1 + exp(-g)))) * u with g = x, u = x2 (tensor_utils.rs:512-532;
+// kPackSwiglu).  The FFN's elementwise steps thereby never go through HBM.
 constexpr int PPT = 8;
-__global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, int n_tokens, int k,
-                                                     int type, int bm, _Float16* __restrict__ frag,
+constexpr int kPackPlain = 0, kPackNorm = 1, kPackSwiglu = 2;
+template <int MODE>
+__global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
+                                                     const float* __restrict__ gamma, float eps, int n_tokens,
+                                                     int k, int type, int bm, _Float16* __restrict__ frag,
                                                      float* __restrict__ rscale, float* __restrict__ bsum) {
   __shared__ float red[4];
+  __shared__ float red2[4];
   const int t = blockIdx.x;
   const bool live = t < n_tokens;
   const float* xr = x + static_cast<size_t>(live ? t : 0) * k;
+  const float* ur = MODE == kPackSwiglu ? x2 + static_cast<size_t>(live ? t : 0) * k : nullptr;
   const int nb = k / 32, npairs = nb * 4;
   const int nchunks = (npairs + 256 * PPT - 1) / (256 * PPT);
   const bool q8 = type == WH_TYPE_Q8_0;
@@ -138,12 +148,55 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
         const float* src = xr + 32 * b + (q8 ? 8 * g : 4 * g);
         va[i] = *reinterpret_cast<const float4*>(src);
         vb[i] = *reinterpret_cast<const float4*>(src + (q8 ? 4 : 16));
+        if constexpr (MODE == kPackSwiglu) {
+          const float* us = ur + (src - xr);
+          const float4 ua = *reinterpret_cast<const float4*>(us);
+          const float4 ub = *reinterpret_cast<const float4*>(us + (q8 ? 4 : 16));
+          auto h = [](float g, float u) { return (g * (1.0f / (1.0f + expf(-g)))) * u; };
+          va[i] = float4{h(va[i].x, ua.x), h(va[i].y, ua.y), h(va[i].z, ua.z), h(va[i].w, ua.w)};
+          vb[i] = float4{h(vb[i].x, ub.x), h(vb[i].y, ub.y), h(vb[i].z, ub.z), h(vb[i].w, ub.w)};
+        }
       }
     }
   };
+  // RMSNorm: the row's rms first, then x_hat = (x / rms) * gamma in place of x
+  float rms = 1.f;
+  auto normalise = [&](int c) {
+    if constexpr (MODE == kPackNorm) {
+#pragma unroll
+      for (int i = 0; i < PPT; i++) {
+        const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+        if (!live || p >= npairs) continue;
+        const int b = p >> 2, g = p & 3;
+        const float* gs = gamma + 32 * b + (q8 ? 8 * g : 4 * g);
+        const float4 ga = *reinterpret_cast<const float4*>(gs);
+        const float4 gb = *reinterpret_cast<const float4*>(gs + (q8 ? 4 : 16));
+        va[i] = float4{(va[i].x / rms) * ga.x, (va[i].y / rms) * ga.y, (va[i].z / rms) * ga.z, (va[i].w / rms) * ga.w};
+        vb[i] = float4{(vb[i].x / rms) * gb.x, (vb[i].y / rms) * gb.y, (vb[i].z / rms) * gb.z, (vb[i].w / rms) * gb.w};
+      }
+    }
+  };
+  if constexpr (MODE == kPackNorm) {
+    float ss = 0.f;
+    for (int c = 0; c < nchunks; c++) {
+      load(c);
+#pragma unroll
+      for (int i = 0; i < PPT; i++) {
+        ss = __builtin_fmaf(va[i].x, va[i].x, ss); ss = __builtin_fmaf(va[i].y, va[i].y, ss);
+        ss = __builtin_fmaf(va[i].z, va[i].z, ss); ss = __builtin_fmaf(va[i].w, va[i].w, ss);
+        ss = __builtin_fmaf(vb[i].x, vb[i].x, ss); ss = __builtin_fmaf(vb[i].y, vb[i].y, ss);
+        ss = __builtin_fmaf(vb[i].z, vb[i].z, ss); ss = __builtin_fmaf(vb[i].w, vb[i].w, ss);
+      }
+    }
+    ss = whd::wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red2[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    rms = sqrtf(((red2[0] + red2[1]) + (red2[2] + red2[3])) / static_cast<float>(k) + eps);
+  }
   float mx = 0.f;
   for (int c = 0; c < nchunks; c++) {
-    load(c);
+    if (MODE != kPackNorm || nchunks > 1) load(c);  // one chunk: still in registers
+    normalise(c);
 #pragma unroll
     for (int i = 0; i < PPT; i++)
       mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(va[i].x), fabsf(va[i].y)), fmaxf(fabsf(va[i].z), fabsf(va[i].w))),
@@ -165,7 +218,10 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
   if (threadIdx.x == 0) rscale[t] = ldexpf(1.f, e);
   const int T = t / bm, i16 = (t % bm) / 16, tl = t % 16, fpb = bm / 8;
   for (int c = 0; c < nchunks; c++) {
-    if (nchunks > 1) load(c);   // one chunk: its values are still in registers
+    if (nchunks > 1) {   // one chunk: its values are still in registers
+      load(c);
+      normalise(c);
+    }
 #pragma unroll
     for (int i = 0; i < PPT; i++) {
       const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
@@ -520,16 +576,14 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         const int jn = np + 1 < NT / 2 ? j : (j + 1 < SB ? j + 1 : j);
         const int nn = np + 1 < NT / 2 ? 2 * np + 2 : 0;
         half8 bn[2] = {bw[0], bw[1]};
-        // slot k of 4 IT: the pending pair's scales for (h, i) = (k / IT) % 2, k % IT
-        // in the first 2 IT slots, the next pair's unpacking in the last 2 IT
-        int k = 0;
+        // the pending pair's scales over the first 2 IT MFMA slots, the next
+        // pair's unpacking over the last 2 IT
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
           for (int i = 0; i < IT; i++) {
             cc[cur][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j][i], bw[h], float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             scale_one(pn + h, pend, h, i);
-            k++;
             __builtin_amdgcn_sched_barrier(0);
           }
 #pragma unroll
@@ -543,7 +597,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
               for (int q = (h * IT + i) * 8 / (2 * IT); q < (h * IT + i + 1) * 8 / (2 * IT); q++)
                 unpack_part<TYPE>(q % 4, wq0[jn][nn + q / 4], wq1[jn][nn + q / 4], magic, bn[q / 4]);
             }
-            k++;
             __builtin_amdgcn_sched_barrier(0);
           }
         // this pair becomes the pending one
@@ -687,43 +740,98 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
   return b;
 }
 
-int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
-                      float* y, void* workspace, hipStream_t s) {
-  const int bm = tile_bm(n_tokens);
-  const size_t tm = (n_tokens + bm - 1) / bm * bm;
+// Workspace of one tiled GEMM: packed activations, row scales, Q4_1 block
+// sums, split-K partial planes.
+struct TiledWs {
+  _Float16* frag;
+  float* rs;
+  float* bs;
+  float* part;  // null without split-K
+  int bm, splits;
+  size_t tm;
+};
+
+static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void* workspace) {
+  TiledWs t{};
+  t.bm = tile_bm(n_tokens);
+  t.tm = (n_tokens + t.bm - 1) / t.bm * t.bm;
   char* ws = static_cast<char*>(workspace);
-  _Float16* frag = reinterpret_cast<_Float16*>(ws);
-  ws += al256(tm * k * 4);
-  float* rs = reinterpret_cast<float*>(ws);
-  ws += al256(tm * 4);
-  float* bs = nullptr;
+  t.frag = reinterpret_cast<_Float16*>(ws);
+  ws += al256(t.tm * k * 4);
+  t.rs = reinterpret_cast<float*>(ws);
+  ws += al256(t.tm * 4);
   if (type == WH_TYPE_Q4_1) {
-    bs = reinterpret_cast<float*>(ws);
-    ws += al256(tm * (k / 32) * 4);
+    t.bs = reinterpret_cast<float*>(ws);
+    ws += al256(t.tm * (k / 32) * 4);
   }
-  const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
-  float* part = splits > 1 ? reinterpret_cast<float*>(ws) : y;
-  pack_a_kernel<<<static_cast<unsigned>(tm), 256, 0, s>>>(x, static_cast<int>(n_tokens), static_cast<int>(k),
-                                                          type, bm, frag, rs, bs);
+  t.splits = gemm_tiled_splits(n_rows, n_tokens, k);
+  t.part = t.splits > 1 ? reinterpret_cast<float*>(ws) : nullptr;
+  return t;
+}
+
+template <int MODE>
+static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x2, const float* gamma, float eps,
+                      size_t n_tokens, size_t k, hipStream_t s) {
+  pack_a_kernel<MODE><<<static_cast<unsigned>(t.tm), 256, 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
+                                                                  static_cast<int>(k), type, t.bm, t.frag, t.rs, t.bs);
   WH_LAUNCH_CHECK("pack kernel launch");
+  return WH_OK;
+}
+
+// The GEMM over packed activations (and the split-K reduce) into y.
+static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t, float* y,
+                     hipStream_t s) {
   const uint8_t* wp = static_cast<const uint8_t*>(w);
+  float* part = t.splits > 1 ? t.part : y;
   int st;
   switch (type) {
-    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
-    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
-    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, frag, rs, bs, part, splits, s); break;
+    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
+    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
+    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
     default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
   }
   if (st != WH_OK) return st;
-  if (splits > 1) {
+  if (t.splits > 1) {
     const size_t n = n_rows * n_tokens;
     size_t gsz = (n + 255) / 256;
     const size_t cap = static_cast<size_t>(cu_count()) * 8;
     if (gsz > cap) gsz = cap;
-    tiled_splitk_reduce_kernel<<<static_cast<unsigned>(gsz), 256, 0, s>>>(part, splits, n, y);
+    tiled_splitk_reduce_kernel<<<static_cast<unsigned>(gsz), 256, 0, s>>>(part, t.splits, n, y);
     WH_LAUNCH_CHECK("split-K reduce launch");
   }
   return WH_OK;
+}
+
+int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
+                      float* y, void* workspace, hipStream_t s) {
+  const TiledWs t = tiled_ws(type, n_rows, k, n_tokens, workspace);
+  int st = tiled_pack<kPackPlain>(type, t, x, nullptr, nullptr, 0.f, n_tokens, k, s);
+  if (st) return st;
+  return tiled_run(type, w, n_rows, k, n_tokens, t, y, s);
+}
+
+// The FFN for n_tokens rows on the tiled kernel: the RMSNorm of x is packed
+// once for both gate and up, the SwiGLU of their outputs is formed while the
+// down projection's activations are packed.  g, u: n_tokens x n_ff scratch.
+// WH_ERR_INVALID_SHAPE (nothing launched) when a product does not fit.
+int launch_ffn_tiled(int type, const void* gate, const void* up, const void* down, size_t hidden, size_t n_ff,
+                     const float* x, const float* gamma, float eps, size_t n_tokens, float* g, float* u, float* out,
+                     void* workspace, size_t workspace_bytes, hipStream_t s) {
+  if (!gemm_tiled_ok(type, gate, x, n_ff, hidden, n_tokens) || !gemm_tiled_ok(type, up, x, n_ff, hidden, n_tokens) ||
+      !gemm_tiled_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16))
+    return WH_ERR_INVALID_SHAPE;
+  if (workspace_bytes < gemm_tiled_workspace_bytes(type, n_ff, n_tokens, hidden) ||
+      workspace_bytes < gemm_tiled_workspace_bytes(type, hidden, n_tokens, n_ff))
+    return WH_ERR_INVALID_SHAPE;
+  const TiledWs t1 = tiled_ws(type, n_ff, hidden, n_tokens, workspace);
+  int st = tiled_pack<kPackNorm>(type, t1, x, nullptr, gamma, eps, n_tokens, hidden, s);
+  if (!st) st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s);
+  if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s);
+  if (st) return st;
+  const TiledWs t2 = tiled_ws(type, hidden, n_ff, n_tokens, workspace);
+  st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, s);
+  if (st) return st;
+  return tiled_run(type, down, hidden, n_ff, n_tokens, t2, out, s);
 }
 
 }  // namespace wh

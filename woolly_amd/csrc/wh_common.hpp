@@ -111,6 +111,12 @@ bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x,
                       size_t n_tokens, float* y, void* workspace, hipStream_t stream);
+// FFN for more than kGemvTokenLimit tokens on the tiled kernel, with the
+// RMSNorm and SwiGLU fused into its activation packing (g, u: scratch of
+// n_tokens x n_ff); WH_ERR_INVALID_SHAPE (nothing launched) when it does not fit.
+int launch_ffn_tiled(int type, const void* gate, const void* up, const void* down, size_t hidden, size_t n_ff,
+                     const float* x, const float* gamma, float eps, size_t n_tokens, float* g, float* u, float* out,
+                     void* workspace, size_t workspace_bytes, hipStream_t s);
 // Decode attention (attention.hip).
 size_t attention_workspace_bytes(size_t n_heads, size_t head_dim, size_t max_ctx, size_t n_kv_heads);
 bool attention_shape_ok(size_t n_heads, size_t n_kv_heads, size_t head_dim);
