@@ -16,10 +16,12 @@
 //
 // Data flow.
 //   pack_a_kernel writes the activations pre-swizzled into MFMA fragment order:
-//     fragment (token tile T, block b, 16-token group i, limb) = 64 lanes x 8
-//     halves = 1 KiB, lane l holding token 16i + l%16 and the 8 k-slots of
-//     k-group l/16.  The k-slots follow the order in which a weight lane
-//     unpacks its nibbles, so a straight copy feeds the MFMA.
+//     fragment (token tile T, block b, 16-token group i, limb) = 16 tokens x
+//     4 k-groups x 8 halves = 1 KiB, token-major (a token's 64 bytes are
+//     contiguous, so a packing workgroup writes whole segments); the copy into
+//     LDS reads them in MFMA lane order (lane l: token 16i + l%16, k-group
+//     l/16).  The k-slots follow the order in which a weight lane unpacks its
+//     nibbles, so the copied fragment feeds the MFMA directly.
 //   gemm_tiled_kernel: 512 threads, a BM-token x 256-row tile (BM = 16, 32,
 //     64 or 128 from the token count, so small batches do not multiply
 //     padding), two waves per SIMD.  Stages of two blocks are copied
@@ -112,36 +114,39 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 // rows).  Rows t >= n_tokens are written as zeros.  rscale[t] = 2^e with
 // max|x_t| * 2^-e in [2^13, 2^14); bsum (Q4_1 only) = per-block sums of
 // hi + lo, laid out [T][b][bm].
-// Thread p of a chunk owns the (block, k-group) pairs p, p + 256, ...: the 8
-// elements of a pair are two float4 loads (slot_elem order), all issued
-// before the first use; a row of up to 256 * PPT pairs (k <= 64 * PPT) is
-// read once and packed from registers, longer rows are read a second time.
+// Thread p of a chunk owns the (block, k-group) pairs p, p + NTH, ... (NTH =
+// blockDim.x, 256 .. 1024 by the row length): the 8 elements of a pair are
+// two float4 loads (slot_elem order), all issued before the first use; a row
+// of up to NTH * PPT pairs is read once and packed from registers, longer
+// rows are read again per pass.
 // MODE: the row packed is x itself (kPackPlain); the RMSNorm of x,
 // (x / sqrt(sum x^2 / k + eps)) * gamma as rms_norm computes it
 // (tensor_utils.rs:446-480; kPackNorm); or the SwiGLU of two rows,
 // (g * (1 / (1 + exp(-g)))) * u with g = x, u = x2 (tensor_utils.rs:512-532;
 // kPackSwiglu).  The FFN's elementwise steps thereby never go through HBM.
-constexpr int PPT = 8;
+constexpr int PPT = 2;
+constexpr int kPackMaxThreads = 1024;
 constexpr int kPackPlain = 0, kPackNorm = 1, kPackSwiglu = 2;
 template <int MODE>
-__global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
+__global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
                                                      const float* __restrict__ gamma, float eps, int n_tokens,
                                                      int k, int type, int bm, _Float16* __restrict__ frag,
                                                      float* __restrict__ rscale, float* __restrict__ bsum) {
-  __shared__ float red[4];
-  __shared__ float red2[4];
+  __shared__ float red[kPackMaxThreads / 64];
+  __shared__ float red2[kPackMaxThreads / 64];
+  const int NTH = static_cast<int>(blockDim.x), nw = NTH >> 6;
   const int t = blockIdx.x;
   const bool live = t < n_tokens;
   const float* xr = x + static_cast<size_t>(live ? t : 0) * k;
   const float* ur = MODE == kPackSwiglu ? x2 + static_cast<size_t>(live ? t : 0) * k : nullptr;
   const int nb = k / 32, npairs = nb * 4;
-  const int nchunks = (npairs + 256 * PPT - 1) / (256 * PPT);
+  const int nchunks = (npairs + NTH * PPT - 1) / (NTH * PPT);
   const bool q8 = type == WH_TYPE_Q8_0;
   float4 va[PPT], vb[PPT];
   auto load = [&](int c) {
 #pragma unroll
     for (int i = 0; i < PPT; i++) {
-      const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+      const int p = c * NTH * PPT + NTH * i + static_cast<int>(threadIdx.x);
       va[i] = vb[i] = float4{0.f, 0.f, 0.f, 0.f};
       if (live && p < npairs) {
         const int b = p >> 2, g = p & 3;
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
     if constexpr (MODE == kPackNorm) {
 #pragma unroll
       for (int i = 0; i < PPT; i++) {
-        const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+        const int p = c * NTH * PPT + NTH * i + static_cast<int>(threadIdx.x);
         if (!live || p >= npairs) continue;
         const int b = p >> 2, g = p & 3;
         const float* gs = gamma + 32 * b + (q8 ? 8 * g : 4 * g);
@@ -191,7 +196,9 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
     ss = whd::wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red2[threadIdx.x >> 6] = ss;
     __syncthreads();
-    rms = sqrtf(((red2[0] + red2[1]) + (red2[2] + red2[3])) / static_cast<float>(k) + eps);
+    float tot = 0.f;
+    for (int w = 0; w < nw; w++) tot += red2[w];
+    rms = sqrtf(tot / static_cast<float>(k) + eps);
   }
   float mx = 0.f;
   for (int c = 0; c < nchunks; c++) {
@@ -206,7 +213,8 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  mx = 0.f;
+  for (int w = 0; w < nw; w++) mx = fmaxf(mx, red[w]);
   int e = 0;
   if (mx > 0.f && mx <= 3.4e38f) {
     int ex;
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
     }
 #pragma unroll
     for (int i = 0; i < PPT; i++) {
-      const int p = c * 256 * PPT + 256 * i + static_cast<int>(threadIdx.x);
+      const int p = c * NTH * PPT + NTH * i + static_cast<int>(threadIdx.x);
       if (p >= npairs) break;   // uniform across the four lanes of a block
       const int b = p >> 2, g = p & 3;
       // slot order: 4-bit formats {0, 2, 1, 3} within each half, Q8_0 natural
@@ -247,8 +255,9 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ x
         lv[s] = l;
         part += static_cast<float>(h) + static_cast<float>(l);
       }
-      const int lane = 16 * g + tl;
-      const size_t base = ((static_cast<size_t>(T) * nb + b) * fpb + 2 * i16) * 512 + 8 * lane;
+      // token-major inside a fragment: token tl's four k-groups are 64
+      // contiguous bytes (the copy into LDS puts them in MFMA lane order)
+      const size_t base = ((static_cast<size_t>(T) * nb + b) * fpb + 2 * i16) * 512 + 8 * (4 * tl + g);
       *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
       *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
       if (bsum) {
@@ -441,6 +450,8 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     b_off[c] = static_cast<uint32_t>(static_cast<size_t>(row) * row_bytes) + 4u * static_cast<uint32_t>(gi % DWB);
   }
   const uint32_t smem_base = lds_addr(smem);
+  // MFMA lane l (k-group l / 16, token l % 16) of a fragment, stored token-major
+  const uint32_t frag_lane_off = 16u * (4u * (lane & 15) + (lane >> 4));
 
   auto issue = [&](int st) {
     if (st >= n_stages) return;
@@ -453,7 +464,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       const int fi = (wave * A_DMA + f) % A_FR;
       const int j = fi / FPB;
       const uint32_t off =
-          static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * FPB + fi % FPB) * FRAG) + 16u * lane;
+          static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * FPB + fi % FPB) * FRAG) + frag_lane_off;
       copy16_to_lds(frag, off, slot + fi * FRAG);
     }
     const uint32_t bslot = slot + A_STAGE;
@@ -772,7 +783,11 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
 template <int MODE>
 static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x2, const float* gamma, float eps,
                       size_t n_tokens, size_t k, hipStream_t s) {
-  pack_a_kernel<MODE><<<static_cast<unsigned>(t.tm), 256, 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
+  // threads per row: enough for PPT pairs each, 256 .. 1024
+  const size_t npairs = k / 8;
+  size_t threads = (npairs + PPT - 1) / PPT;
+  threads = threads < 256 ? 256 : (threads > kPackMaxThreads ? kPackMaxThreads : (threads + 63) / 64 * 64);
+  pack_a_kernel<MODE><<<static_cast<unsigned>(t.tm), static_cast<unsigned>(threads), 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
                                                                   static_cast<int>(k), type, t.bm, t.frag, t.rs, t.bs);
   WH_LAUNCH_CHECK("pack kernel launch");
   return WH_OK;
