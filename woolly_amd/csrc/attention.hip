@@ -59,15 +59,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   // K / V rows of positions [p0, p0 + np) except pos, f16 pairs
   const bool own = pos >= p0 && pos < p0 + chunk;
   const int nrow = own ? np - 1 : np;
-  for (int e = t; e < nrow * (D / 8); e += kAttnThreads) {  // 16-byte pieces
-    const int r = e / (D / 8), j = e % (D / 8);
-    const size_t off = (static_cast<size_t>(p0 + r) * n_kv_heads + kvh) * D + 8 * j;
-    const uint4 kk = *reinterpret_cast<const uint4*>(k_cache + off);
-    const uint4 vv = *reinterpret_cast<const uint4*>(v_cache + off);
-    uint32_t* kd = ks + r * RS + 4 * j;
-    uint32_t* vd = vs + r * RS + 4 * j;
-    kd[0] = kk.x, kd[1] = kk.y, kd[2] = kk.z, kd[3] = kk.w;
-    vd[0] = vv.x, vd[1] = vv.y, vd[2] = vv.z, vd[3] = vv.w;
+  // 16-byte pieces, kBatch per thread with every load issued before the first
+  // LDS store (a load-store loop would wait out the memory latency each time)
+  constexpr int kBatch = 8;
+  for (int e0 = 0; e0 < nrow * (D / 8); e0 += kBatch * kAttnThreads) {
+    uint4 kk[kBatch], vv[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int e = e0 + b * kAttnThreads + t;
+      if (e < nrow * (D / 8)) {
+        const int r = e / (D / 8), j = e % (D / 8);
+        const size_t off = (static_cast<size_t>(p0 + r) * n_kv_heads + kvh) * D + 8 * j;
+        kk[b] = *reinterpret_cast<const uint4*>(k_cache + off);
+        vv[b] = *reinterpret_cast<const uint4*>(v_cache + off);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int e = e0 + b * kAttnThreads + t;
+      if (e < nrow * (D / 8)) {
+        const int r = e / (D / 8), j = e % (D / 8);
+        uint32_t* kd = ks + r * RS + 4 * j;
+        uint32_t* vd = vs + r * RS + 4 * j;
+        kd[0] = kk[b].x, kd[1] = kk[b].y, kd[2] = kk[b].z, kd[3] = kk[b].w;
+        vd[0] = vv[b].x, vd[1] = vv[b].y, vd[2] = vv[b].z, vd[3] = vv[b].w;
+      }
+    }
   }
   if (own) {
     // the new token: rotate k, round k and v to f16, store them in the cache
@@ -98,25 +115,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   }
   __syncthreads();
 
-  // scores: thread -> position p, heads g = t / chunk, t / chunk + stride ...
-  for (int e = t; e < G * chunk; e += kAttnThreads) {
-    const int g = e / chunk, p = e % chunk;
-    float s = -INFINITY;
+  // scores: thread -> position p and a pair of heads, so each K row is read
+  // once per pair (q comes from LDS as a broadcast: one address per wave)
+  for (int e = t; e < ((G + 1) / 2) * chunk; e += kAttnThreads) {
+    const int g0 = 2 * (e / chunk), p = e % chunk;
+    const bool two = g0 + 1 < G;
+    float s0 = -INFINITY, s1 = -INFINITY;
     if (p < np) {
       const uint32_t* kr = ks + p * RS;
-      const float* q = qs + g * D;
-      float a0 = 0.f, a1 = 0.f;
+      const float* q0 = qs + g0 * D;
+      const float* q1 = qs + (two ? g0 + 1 : g0) * D;
+      float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll 8
       for (int j = 0; j < D / 2; j++) {
         const uint32_t w = kr[j];
         const float k0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu)));
         const float k1 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-        a0 = __builtin_fmaf(q[2 * j], k0, a0);
-        a1 = __builtin_fmaf(q[2 * j + 1], k1, a1);
+        a0 = __builtin_fmaf(q0[2 * j], k0, a0);
+        a1 = __builtin_fmaf(q0[2 * j + 1], k1, a1);
+        b0 = __builtin_fmaf(q1[2 * j], k0, b0);
+        b1 = __builtin_fmaf(q1[2 * j + 1], k1, b1);
       }
-      s = (a0 + a1) * scale;
+      s0 = (a0 + a1) * scale;
+      s1 = (b0 + b1) * scale;
     }
-    sc[g * chunk + p] = s;
+    sc[g0 * chunk + p] = s0;
+    if (two) sc[(g0 + 1) * chunk + p] = s1;
   }
   __syncthreads();
 
@@ -142,21 +166,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   }
   __syncthreads();
 
-  // acc[g][d] = sum_p e[g][p] v[p][d]
-  for (int e = t; e < G * D; e += kAttnThreads) {
-    const int g = e / D, d = e % D;
+  // acc[g][d] = sum_p e[g][p] v[p][d]: thread -> (head, pair of dims), V read
+  // as one dword per position (consecutive lanes, consecutive dwords)
+  for (int e = t; e < G * (D / 2); e += kAttnThreads) {
+    const int g = e / (D / 2), dp = e % (D / 2);
     const float* ev = sc + g * chunk;
-    const _Float16* vcol = reinterpret_cast<const _Float16*>(vs) + d;
+    const uint32_t* vcol = vs + dp;
     float a0 = 0.f, a1 = 0.f;
-    int p = 0;
-    for (; p + 1 < np; p += 2) {
-      a0 = __builtin_fmaf(ev[p], static_cast<float>(vcol[p * 2 * RS]), a0);
-      a1 = __builtin_fmaf(ev[p + 1], static_cast<float>(vcol[(p + 1) * 2 * RS]), a1);
+#pragma unroll 4
+    for (int p = 0; p < np; p++) {
+      const uint32_t w = vcol[p * RS];
+      const float e_p = ev[p];
+      a0 = __builtin_fmaf(e_p, static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu))), a0);
+      a1 = __builtin_fmaf(e_p, static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16))), a1);
     }
-    if (p < np) a0 = __builtin_fmaf(ev[p], static_cast<float>(vcol[p * 2 * RS]), a0);
     float* o = part + (static_cast<size_t>(kvh * G + g) * n_chunks + c) * (D + 2);
-    o[2 + d] = a0 + a1;
-    if (d == 0) {
+    o[2 + 2 * dp] = a0;
+    o[3 + 2 * dp] = a1;
+    if (dp == 0) {
       o[0] = ml[2 * g];
       o[1] = ml[2 * g + 1];
     }
@@ -199,14 +226,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
 #pragma unroll
   for (int w = 0; w < kAttnThreads / 64; w++) L += red[w];
   const int d = t % D, grp = t / D;
-  float a0 = 0.f, a1 = 0.f;
-  int c = grp;
-  for (; c + NG < n_chunks; c += 2 * NG) {
-    a0 = __builtin_fmaf(cw[c], ph[static_cast<size_t>(c) * (D + 2) + 2 + d], a0);
-    a1 = __builtin_fmaf(cw[c + NG], ph[static_cast<size_t>(c + NG) * (D + 2) + 2 + d], a1);
+  // chunks grp, grp + NG, ...: kBatch loads in flight per step (a load-use
+  // loop would wait out the memory latency per chunk), summed in chunk order
+  constexpr int kBatch = 16;
+  float a0 = 0.f;
+  for (int c0 = grp; c0 < n_chunks; c0 += kBatch * NG) {
+    float v[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int c = c0 + b * NG;
+      v[b] = c < n_chunks ? ph[static_cast<size_t>(c) * (D + 2) + 2 + d] : 0.f;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int c = c0 + b * NG;
+      if (c < n_chunks) a0 = __builtin_fmaf(cw[c], v[b], a0);
+    }
   }
-  if (c < n_chunks) a0 = __builtin_fmaf(cw[c], ph[static_cast<size_t>(c) * (D + 2) + 2 + d], a0);
-  accs[grp * D + d] = a0 + a1;
+  accs[grp * D + d] = a0;
   __syncthreads();
   if (grp == 0) {
     float acc = accs[d];

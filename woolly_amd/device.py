@@ -72,6 +72,8 @@ class DeviceBuffer:
     def fill(self, value: int = 0, stream: "Stream | None" = None) -> None:
         s = stream.handle if stream else None
         _lib.check(_lib.load().wh_fill_bytes(self.ptr, value, self.nbytes, s))
+        if stream is None:
+            synchronize()  # the library's streams do not wait for the null stream
 
     def free(self) -> None:
         if self.ptr:
