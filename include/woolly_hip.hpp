@@ -183,6 +183,9 @@ struct InvalidTensorType : Error {
   uint32_t type_id;
   explicit InvalidTensorType(uint32_t t) : Error("Invalid tensor type: " + std::to_string(t)), type_id(t) {}
 };
+struct InvalidTensorInfo : Error {
+  using Error::Error;
+};
 
 // woolly_gguf::dequantize(data, ggml_type, nelements) (dequantize.rs:189-205).
 inline std::vector<float> dequantize(const std::vector<uint8_t>& data, GGMLType type, size_t nelements) {
@@ -196,6 +199,8 @@ inline std::vector<float> dequantize(const std::vector<uint8_t>& data, GGMLType 
     throw BufferTooSmall(needed, data.size());
   }
   if (st == WH_ERR_UNSUPPORTED_TYPE) throw InvalidTensorType(static_cast<uint32_t>(type));
+  // short K-quant data (dequantize.rs:416-418, 472-474)
+  if (st == WH_ERR_INVALID_METADATA) throw InvalidTensorInfo(wh_last_error());
   if (st != WH_OK) throw Error(wh_last_error());
   return out;
 }

@@ -224,18 +224,23 @@ int main() {
   // error.rs:11-64 through dequantize.rs:189-205
   run("gguf_errors", [] {
     std::vector<uint8_t> bytes(18 * 2 - 1);
-    bool too_small = false, invalid = false;
+    bool too_small = false, invalid = false, short_k = false;
     try {
       gguf::dequantize(bytes, gguf::GGMLType::Q4_0, 64);
     } catch (const gguf::BufferTooSmall& e) {
       too_small = e.needed == 36 && e.available == 35;
     }
     try {
-      gguf::dequantize(bytes, gguf::GGMLType::Q4_K, 256);
+      gguf::dequantize(bytes, gguf::GGMLType::Q5_0, 32);
     } catch (const gguf::InvalidTensorType& e) {
-      invalid = e.type_id == 12;
+      invalid = e.type_id == 6;
     }
-    EXPECT(too_small && invalid);
+    try {
+      gguf::dequantize(bytes, gguf::GGMLType::Q4_K, 256);  // 35 of 144 bytes
+    } catch (const gguf::InvalidTensorInfo&) {
+      short_k = true;
+    }
+    EXPECT(too_small && invalid && short_k);
     // A partial trailing block decodes the elements asked for.
     std::vector<uint8_t> one(18, 0x00);
     one[0] = 0x00, one[1] = 0x3C;  // d = 1.0
