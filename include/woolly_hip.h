@@ -160,6 +160,9 @@ WH_API int wh_gemv_select(int mode, int* previous);
  *   (model/lazy_transformer.rs:1073-1123), with ggml's [N][K] weight layout
  *   instead of the [K][N] reshape at lazy_transformer.rs:1091-1101.
  * X is row-major [n_tokens][k] f32, Y is row-major [n_tokens][n_rows] f32.
+ * Types: Q4_0, Q4_1, Q8_0 (k % 32 == 0) and Q4_K, Q6_K (k % 256 == 0; with
+ * more than 2 tokens the matrix is first rewritten into the workspace as
+ * 32-element blocks with f32 scales, the values unchanged).
  * The MFMA path (more than 2 tokens) needs a device workspace of
  * wh_quantized_matmul_workspace_bytes(type, n_rows, k, n_tokens) bytes (256-byte
  * aligned); the call itself never allocates.  WH_ERR_BUFFER_TOO_SMALL if it
@@ -189,9 +192,11 @@ WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out,
  *   process_layer (lazy_transformer.rs:98-258); FeedForward::forward
  *   (model/feedforward.rs:93-127) and fused_rmsnorm_ffn
  *   (model/fused_kernels.rs:403-455) compute the same layer.
- * gate and up are [n_ff][hidden], down is [hidden][n_ff], all of `type`.
- * The workspace must hold wh_ffn_workspace_bytes(hidden, n_ff, m) bytes of
- * device memory (no allocation happens inside the call). */
+ * gate and up are [n_ff][hidden], down is [hidden][n_ff], all of `type`
+ * (Q4_0, Q4_1, Q8_0, or Q4_K / Q6_K with hidden and n_ff multiples of 256).
+ * The workspace must hold wh_ffn_workspace_bytes_for_type(type, hidden, n_ff, m)
+ * bytes of device memory (no allocation happens inside the call);
+ * wh_ffn_workspace_bytes(hidden, n_ff, m) is enough for Q4_0, Q4_1 and Q8_0. */
 typedef struct wh_ffn_weights {
   int type;
   const void* gate;
@@ -202,6 +207,7 @@ typedef struct wh_ffn_weights {
 } wh_ffn_weights;
 
 WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m);
+WH_API size_t wh_ffn_workspace_bytes_for_type(int type, size_t hidden, size_t n_ff, size_t m);
 WH_API int wh_ffn_swiglu(const wh_ffn_weights* weights, const float* gamma, float eps,
                          const float* x, size_t m, float* out, void* workspace,
                          size_t workspace_bytes, wh_stream_t stream);

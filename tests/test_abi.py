@@ -110,6 +110,13 @@ def test_ffn_and_weight_argument_errors_need_no_gpu():
     w = _lib.wh_ffn_weights(2, 1, 1, 1, 4010, 14336)
     assert lib.wh_ffn_swiglu(C.byref(w), 1, 1e-5, 1, 1, 1, 1, 1 << 40, None) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_ffn_workspace_bytes(4096, 14336, 1) >= 4 * (4096 + 3 * 14336)
+    # K-quant FFN and GEMM: whole 256-element blocks; no GEMM workspace for 1-2 tokens
+    w = _lib.wh_ffn_weights(14, 1, 1, 1, 4096 + 32, 14336)
+    assert lib.wh_ffn_swiglu(C.byref(w), 1, 1e-5, 1, 1, 1, 1, 1 << 40, None) == _lib.WH_ERR_INVALID_SHAPE
+    assert b"block size 256" in lib.wh_last_error()
+    assert lib.wh_ffn_workspace_bytes_for_type(12, 4096, 14336, 1) == lib.wh_ffn_workspace_bytes(4096, 14336, 1)
+    assert lib.wh_quantized_matmul_workspace_bytes(12, 4096, 4096, 2) == 0
+    assert lib.wh_quantized_matmul(12, 1, 1 << 40, 8, 64, 1, 4, 1, None, 0, None) == _lib.WH_ERR_INVALID_SHAPE
     h = C.c_void_p()
     assert lib.wh_weight_upload(2, 4, 48, None, 0, C.byref(h)) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_weight_upload(2, 4, 64, None, 10, C.byref(h)) == _lib.WH_ERR_BUFFER_TOO_SMALL

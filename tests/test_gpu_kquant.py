@@ -164,3 +164,70 @@ def test_kquant_mfma_nonfinite_and_zero_chunks(gpu, orc, t):
     fin = ~np.isnan(ref)
     assert np.array_equal(np.isinf(got[fin]), np.isinf(ref[fin]))
     assert np.array_equal(np.sign(got[fin]), np.sign(ref[fin]))
+
+
+# ---------------------------------------------------------------- prefill
+# More than two tokens: the matrix is repacked into 32-element blocks with f32
+# scales (Q4_K: (d * scale) q + dmin; Q6_K: 16-element halves, (d * scale / 64)
+# (q - 32), padded to 32 with zeros) and multiplied on the tiled MFMA kernel.
+# (m, n, k): one to 56 super-blocks per row, ragged token and row counts,
+# token tiles of 16 .. 128, split-K
+KQ_MATMUL = [(3, 300, 4096), (8, 1024, 2048), (17, 768, 256), (64, 129, 4096), (130, 200, 512),
+             (257, 384, 1024), (512, 256, 14336)]
+
+
+def kq_matmul(t, w, x, m, n, k):
+    wb, wp = up(w)
+    xb, xp = up(x)
+    yb = DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_workspace_bytes(t, n, k, m)
+    ws = DeviceBuffer(max(wsz, 1))
+    ops.quantized_matmul(t, wp, w.nbytes, n, k, xp, m, yb.ptr, ws, wsz)
+    return down(yb, np.float32, m * n).reshape(m, n)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("m,n,k", KQ_MATMUL)
+def test_kquant_matmul_parity(gpu, orc, t, m, n, k):
+    print(f"[case] kquant matmul type={t} m={m} n={n} k={k}", flush=True)
+    w = synth.quantized_weight(t, n, k, seed=n + k + t)
+    x = synth.activations(m * k, seed=m + t).reshape(m, k)
+    got = kq_matmul(t, w, x, m, n, k)
+    ref = orc.matmul_rows_f64(t, w, n, k, x, m, np.arange(m))
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    print(f"[result] kquant matmul t={t} rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+    assert r <= 1e-4 and a <= 1e-3
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_kquant_matmul_matches_gemv(gpu, t):
+    """The tiled path (5 tokens) and the per-token GEMV agree on every token."""
+    m, n, k = 5, 520, 4096
+    w = synth.quantized_weight(t, n, k, seed=77 + t)
+    x = synth.activations(m * k, seed=78).reshape(m, k)
+    got = kq_matmul(t, w, x, m, n, k)
+    for i in range(m):
+        assert rel_l2(got[i], gemv(t, w, x[i], n, k)) <= 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("hidden,n_ff,m", [(256, 512, 1), (512, 1024, 4), (4096, 1024, 64), (256, 20480, 5)])
+def test_kquant_ffn_parity(gpu, orc, t, hidden, n_ff, m):
+    """The SwiGLU FFN layer on K-quant weights: decode (fused gate/up GEMV) and
+    prefill (RMSNorm and SwiGLU packed into the tiled GEMM's activations, each
+    matrix repacked in turn into one workspace region)."""
+    print(f"[case] kquant ffn t={t} hidden={hidden} n_ff={n_ff} m={m}", flush=True)
+    L = synth.ffn_layer(t, hidden, n_ff, m, seed=hidden + n_ff + t)
+    bufs = {name: up(v) for name, v in L.items()}
+    ob = DeviceBuffer(4 * m * hidden)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m, ggml_type=t)
+    ws = DeviceBuffer(wsz)
+    ops.ffn_swiglu(t, bufs["gate"][1], bufs["up"][1], bufs["down"][1], hidden, n_ff,
+                   bufs["gamma"][1], 1e-5, bufs["x"][1], m, ob.ptr, ws.ptr, wsz)
+    got = down(ob, np.float32, m * hidden).reshape(m, hidden)
+    rows = sorted({0, m // 2, m - 1})
+    ref = orc.ffn_rows_f64(t, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5, L["x"], rows)
+    r, a = rel_l2(got[rows], ref), max_abs(got[rows], ref)
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    print(f"[result] kquant ffn rel_l2={r:.3e} max_abs={a:.3e} rms={rms:.3e}", flush=True)
+    assert r <= 1e-4 and a <= 1e-3 * max(1.0, rms / 300.0)

@@ -157,6 +157,7 @@ SIGNATURES = {
     "wh_rms_norm": (_int, [_f32p, _f32p, C.c_float, _sz, _sz, _f32p, _vp]),
     "wh_swiglu": (_int, [_f32p, _f32p, _sz, _f32p, _vp]),
     "wh_ffn_workspace_bytes": (_sz, [_sz, _sz, _sz]),
+    "wh_ffn_workspace_bytes_for_type": (_sz, [_int, _sz, _sz, _sz]),
     "wh_ffn_swiglu": (_int, [C.POINTER(wh_ffn_weights), _f32p, C.c_float, _f32p, _sz, _f32p,
                              _vp, _sz, _vp]),
     "wh_weight_upload": (_int, [_int, _sz, _sz, _vp, _sz, C.POINTER(_vp)]),

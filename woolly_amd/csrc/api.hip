@@ -387,14 +387,14 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
 // -------------------------------------------------------------------- GEMM
 WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_rows, size_t k,
                                                   size_t n_tokens) {
-  if (!wh::is_block_type(type) || n_tokens <= wh::kGemvTokenLimit || k == 0) return 0;
+  if (!(wh::is_block_type(type) || wh::is_kquant(type)) || n_tokens <= wh::kGemvTokenLimit || k == 0) return 0;
   return wh::gemm_workspace_bytes_for(type, n_rows, n_tokens, k);
 }
 
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes, size_t n_rows,
                                size_t k, const float* x, size_t n_tokens, float* y, void* workspace,
                                size_t workspace_bytes, wh_stream_t stream) {
-  int st = check_block_args("quantized_matmul", type, k);
+  int st = check_gemv_args("quantized_matmul", type, k);
   if (st) return st;
   st = check_weight_bytes("quantized_matmul", type, n_rows, k, weight_nbytes);
   if (st) return st;
@@ -437,24 +437,41 @@ WH_API int wh_swiglu(const float* gate, const float* up, size_t n, float* out, w
 }
 
 // ------------------------------------------------------------------- FFN
-WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m) {
-  const size_t g1 = wh::gemm_workspace_bytes_for(WH_TYPE_Q4_1, n_ff, m, hidden);
-  const size_t g2 = wh::gemm_workspace_bytes_for(WH_TYPE_Q4_1, hidden, m, n_ff);
-  const size_t gemm_ws = m <= wh::kGemvTokenLimit ? 0 : (g1 > g2 ? g1 : g2);
+WH_API size_t wh_ffn_workspace_bytes_for_type(int type, size_t hidden, size_t n_ff, size_t m) {
+  size_t gemm_ws = 0;
+  if (m > wh::kGemvTokenLimit) {
+    if (wh::is_kquant(type)) {
+      gemm_ws = wh::ffn_kquant_workspace_bytes(type, hidden, n_ff, m);
+    } else {
+      const size_t g1 = wh::gemm_workspace_bytes_for(type, n_ff, m, hidden);
+      const size_t g2 = wh::gemm_workspace_bytes_for(type, hidden, m, n_ff);
+      gemm_ws = g1 > g2 ? g1 : g2;
+    }
+  }
   return align_up(m * hidden * sizeof(float), 256) + 3 * align_up(m * n_ff * sizeof(float), 256) +
          gemm_ws;
+}
+
+// Enough for each of Q4_0, Q4_1 and Q8_0.
+WH_API size_t wh_ffn_workspace_bytes(size_t hidden, size_t n_ff, size_t m) {
+  size_t need = 0;
+  for (int type : {WH_TYPE_Q4_0, WH_TYPE_Q4_1, WH_TYPE_Q8_0}) {
+    const size_t b = wh_ffn_workspace_bytes_for_type(type, hidden, n_ff, m);
+    if (b > need) need = b;
+  }
+  return need;
 }
 
 WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps, const float* x,
                          size_t m, float* out, void* workspace, size_t workspace_bytes,
                          wh_stream_t stream) {
   if (!w) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "ffn_swiglu: null weights");
-  int st = check_block_args("ffn_swiglu", w->type, w->hidden);
+  int st = check_gemv_args("ffn_swiglu", w->type, w->hidden);
   if (st) return st;
-  st = check_block_args("ffn_swiglu", w->type, w->n_ff);
+  st = check_gemv_args("ffn_swiglu", w->type, w->n_ff);
   if (st) return st;
   if (m == 0 || w->hidden == 0) return WH_OK;
-  const size_t need = wh_ffn_workspace_bytes(w->hidden, w->n_ff, m);
+  const size_t need = wh_ffn_workspace_bytes_for_type(w->type, w->hidden, w->n_ff, m);
   if (workspace_bytes < need)
     return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
                          "ffn_swiglu: workspace too small: needed %zu bytes, available %zu", need,

@@ -432,6 +432,7 @@ static size_t splitk_bytes(size_t n_rows, size_t n_tokens, int splits) {
 }
 
 size_t gemm_workspace_bytes_for(int type, size_t n_rows, size_t n_tokens, size_t k) {
+  if (is_kquant(type)) return gemm_kquant_workspace_bytes(type, n_rows, n_tokens, k);
   // enough for either kernel (the choice also depends on the weights' alignment)
   const size_t a = gemm_workspace_bytes(type, n_tokens, k) +
                    splitk_bytes(n_rows, n_tokens, gemm_splits(n_rows, n_tokens, k));
@@ -490,10 +491,13 @@ int launch_gemm_mfma(int type, const void* w, size_t n_rows, size_t k, const flo
 }
 
 // Y[t, r] = sum_k X[t, k] W[r, k].  Few tokens: one streaming GEMV per token;
-// otherwise the MFMA kernel (needs the workspace).
+// otherwise the MFMA kernel (needs the workspace).  Q4_K / Q6_K take the
+// tiled kernel after repacking, or one GEMV per token where it does not fit.
 int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
                 float* y, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  if (n_tokens <= kGemvTokenLimit || k == 0 || !aligned(w, 2)) {
+  const bool kq = is_kquant(type);
+  if (n_tokens <= kGemvTokenLimit || k == 0 || !aligned(w, 2) ||
+      (kq && !gemm_kquant_ok(type, w, x, n_rows, k, n_tokens))) {
     for (size_t t = 0; t < n_tokens; t++) {
       int st = launch_gemv(type, w, x + t * k, y + t * n_rows, n_rows, k, s);
       if (st != WH_OK) return st;
@@ -505,6 +509,7 @@ int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x
     return set_error(WH_ERR_BUFFER_TOO_SMALL,
                      "quantized_matmul: workspace too small: needed %zu bytes, available %zu", need,
                      workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (kq) return launch_gemm_kquant(type, w, n_rows, k, x, n_tokens, y, workspace, s);
   if (gemm_tiled_ok(type, w, x, n_rows, k, n_tokens)) return launch_gemm_tiled(type, w, n_rows, k, x, n_tokens, y, workspace, s);
   return launch_gemm_mfma(type, w, n_rows, k, x, n_tokens, y, workspace, s);
 }

@@ -71,6 +71,25 @@ template <>
 struct TFmt<WH_TYPE_Q8_0> {
   static constexpr int TS = 34, QOFF = 2;
 };
+// the repacked K-quant formats (f32 scale, and minimum for Q4F)
+template <>
+struct TFmt<wh::kGemmQ4F> {
+  static constexpr int TS = 24, QOFF = 8;
+};
+template <>
+struct TFmt<wh::kGemmQ8H> {
+  static constexpr int TS = 20, QOFF = 4;
+};
+// block value d * q + m: block sums of the activations are needed
+template <int TYPE>
+constexpr bool has_min() { return TYPE == WH_TYPE_Q4_1 || TYPE == wh::kGemmQ4F; }
+// int8 quants in natural element order (else 4-bit quants in nibble order)
+template <int TYPE>
+constexpr bool q8_like() { return TYPE == WH_TYPE_Q8_0 || TYPE == wh::kGemmQ8H; }
+// f32 block scale (else f16)
+template <int TYPE>
+constexpr bool f32_scale() { return TYPE == wh::kGemmQ4F || TYPE == wh::kGemmQ8H; }
+inline bool has_min_rt(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
 // dwords per weight row per stage (SB whole blocks)
 template <int TYPE>
 constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
@@ -82,14 +101,14 @@ constexpr int b_dma_per_wave() { return (TBN * dwb<TYPE>() + TWAVES * 64 - 1) / 
 template <int TYPE>
 constexpr int b_stage_bytes() { return b_dma_per_wave<TYPE>() * TWAVES * 64 * 4; }
 template <int TYPE, int BM>
-constexpr int s_stage_bytes() { return TYPE == WH_TYPE_Q4_1 ? SB * BM * 4 : 0; }
+constexpr int s_stage_bytes() { return has_min<TYPE>() ? SB * BM * 4 : 0; }
 template <int TYPE, int BM>
 constexpr int stage_bytes() { return TCfg<BM>::A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE, BM>(); }
 // Copy instructions per wave per stage (the vmcnt of one stage): activation
 // fragments, raw weight dwords, Q4_1 block sums.
 template <int TYPE, int BM>
 constexpr int per_stage() {
-  return (SB * TCfg<BM>::FPB + TWAVES - 1) / TWAVES + b_dma_per_wave<TYPE>() + (TYPE == WH_TYPE_Q4_1 ? 1 : 0);
+  return (SB * TCfg<BM>::FPB + TWAVES - 1) / TWAVES + b_dma_per_wave<TYPE>() + (has_min<TYPE>() ? 1 : 0);
 }
 // Ring depth: as many stages as 160 KiB of LDS holds, 3 to 8 (a deeper ring
 // keeps more weight bytes in flight where a stage is small), with the copies
@@ -105,7 +124,7 @@ template <int TYPE, int BM>
 constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>()) * stage_bytes<TYPE, BM>(); }
 
 // K-slot order of an MFMA operand: k-slot s (0..7) of k-group g (0..3) holds
-// block element 8g + s for Q8_0, and for the 4-bit formats element
+// block element 8g + s for the int8 formats, and for the 4-bit formats element
 // (s < 4 ? 0 : 16) + 4g + {0, 2, 1, 3}[s % 4], the order unpack_q4 below
 // produces the quants in.
 
@@ -124,33 +143,38 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 // (tensor_utils.rs:446-480; kPackNorm); or the SwiGLU of two rows,
 // (g * (1 / (1 + exp(-g)))) * u with g = x, u = x2 (tensor_utils.rs:512-532;
 // kPackSwiglu).  The FFN's elementwise steps thereby never go through HBM.
+// Rows of x are kx long; k is the packed length: kx, or 2 kx for kGemmQ8H,
+// whose 32-element blocks hold 16 elements of x and 16 zeros.
 constexpr int PPT = 2;
 constexpr int kPackMaxThreads = 1024;
 constexpr int kPackPlain = 0, kPackNorm = 1, kPackSwiglu = 2;
 template <int MODE>
 __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
                                                      const float* __restrict__ gamma, float eps, int n_tokens,
-                                                     int k, int type, int bm, _Float16* __restrict__ frag,
+                                                     int k, int kx, int type, int bm, _Float16* __restrict__ frag,
                                                      float* __restrict__ rscale, float* __restrict__ bsum) {
   __shared__ float red[kPackMaxThreads / 64];
   __shared__ float red2[kPackMaxThreads / 64];
   const int NTH = static_cast<int>(blockDim.x), nw = NTH >> 6;
   const int t = blockIdx.x;
   const bool live = t < n_tokens;
-  const float* xr = x + static_cast<size_t>(live ? t : 0) * k;
-  const float* ur = MODE == kPackSwiglu ? x2 + static_cast<size_t>(live ? t : 0) * k : nullptr;
+  const float* xr = x + static_cast<size_t>(live ? t : 0) * kx;
+  const float* ur = MODE == kPackSwiglu ? x2 + static_cast<size_t>(live ? t : 0) * kx : nullptr;
   const int nb = k / 32, npairs = nb * 4;
   const int nchunks = (npairs + NTH * PPT - 1) / (NTH * PPT);
-  const bool q8 = type == WH_TYPE_Q8_0;
+  const bool q8 = type == WH_TYPE_Q8_0 || type == wh::kGemmQ8H;
+  const bool pad = type == wh::kGemmQ8H;
+  // offset in the row of x of pair (b, g)'s first element, -1 for padding
+  auto elem_off = [&](int b, int g) { return pad ? (g < 2 ? 16 * b + 8 * g : -1) : 32 * b + (q8 ? 8 * g : 4 * g); };
   float4 va[PPT], vb[PPT];
   auto load = [&](int c) {
 #pragma unroll
     for (int i = 0; i < PPT; i++) {
       const int p = c * NTH * PPT + NTH * i + static_cast<int>(threadIdx.x);
       va[i] = vb[i] = float4{0.f, 0.f, 0.f, 0.f};
-      if (live && p < npairs) {
-        const int b = p >> 2, g = p & 3;
-        const float* src = xr + 32 * b + (q8 ? 8 * g : 4 * g);
+      const int off = p < npairs ? elem_off(p >> 2, p & 3) : -1;
+      if (live && off >= 0) {
+        const float* src = xr + off;
         va[i] = *reinterpret_cast<const float4*>(src);
         vb[i] = *reinterpret_cast<const float4*>(src + (q8 ? 4 : 16));
         if constexpr (MODE == kPackSwiglu) {
@@ -171,9 +195,9 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
 #pragma unroll
       for (int i = 0; i < PPT; i++) {
         const int p = c * NTH * PPT + NTH * i + static_cast<int>(threadIdx.x);
-        if (!live || p >= npairs) continue;
-        const int b = p >> 2, g = p & 3;
-        const float* gs = gamma + 32 * b + (q8 ? 8 * g : 4 * g);
+        const int off = p < npairs ? elem_off(p >> 2, p & 3) : -1;
+        if (!live || off < 0) continue;
+        const float* gs = gamma + off;
         const float4 ga = *reinterpret_cast<const float4*>(gs);
         const float4 gb = *reinterpret_cast<const float4*>(gs + (q8 ? 4 : 16));
         va[i] = float4{(va[i].x / rms) * ga.x, (va[i].y / rms) * ga.y, (va[i].z / rms) * ga.z, (va[i].w / rms) * ga.w};
@@ -198,7 +222,7 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
     __syncthreads();
     float tot = 0.f;
     for (int w = 0; w < nw; w++) tot += red2[w];
-    rms = sqrtf(tot / static_cast<float>(k) + eps);
+    rms = sqrtf(tot / static_cast<float>(kx) + eps);
   }
   float mx = 0.f;
   for (int c = 0; c < nchunks; c++) {
@@ -334,7 +358,7 @@ template <int TYPE>
 __device__ __forceinline__ void unpack_part(int p, uint32_t u0, uint32_t u1, uint32_t magic, half8& out) {
   typedef _Float16 half2v __attribute__((ext_vector_type(2)));
   half2v r;
-  if constexpr (TYPE == WH_TYPE_Q8_0) {
+  if constexpr (q8_like<TYPE>()) {
     const half2v off = {static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
     const uint32_t w = p < 2 ? u0 : u1;
     const uint32_t sel = (p & 1) ? 0x0c030c02u : 0x0c010c00u;
@@ -413,7 +437,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   constexpr int B_DMA = b_dma_per_wave<TYPE>();
   constexpr int S_CH = SB * BM / 4;                                 // Q4_1 block-sum chunks per stage
   constexpr int S_PW = S_CH / TWAVES;                               // ... per wave (>= 1)
-  constexpr int S_DMA = TYPE == WH_TYPE_Q4_1 ? 1 : 0;
+  constexpr int S_DMA = has_min<TYPE>() ? 1 : 0;
   constexpr int PER_STAGE = A_DMA + B_DMA + S_DMA;                  // vmcnt per stage
   static_assert(PER_STAGE == per_stage<TYPE, BM>(), "copy count");
   static_assert((NSTAGE - 2) * PER_STAGE < 64, "vmcnt range");
@@ -471,7 +495,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint32_t kboff = static_cast<uint32_t>(kb) * TS;
 #pragma unroll
     for (int c = 0; c < B_DMA; c++) copy4_to_lds(W, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
-    if constexpr (TYPE == WH_TYPE_Q4_1) {
+    if constexpr (has_min<TYPE>()) {
       // block sums [SB][BM] of this token tile: S_CH chunks of 16 B, S_PW per
       // wave, copied by lanes 0 .. S_PW - 1 (one instruction per wave)
       const int ci = wave * S_PW + lane;
@@ -517,7 +541,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       float v = __builtin_fmaf(pd[h], cc[B][h][i][r], acc[i][N][r]);
-      if constexpr (TYPE == WH_TYPE_Q4_1) v = __builtin_fmaf(pm[h], psx[i][r], v);
+      if constexpr (has_min<TYPE>()) v = __builtin_fmaf(pm[h], psx[i][r], v);
       acc[i][N][r] = v;
     }
   };
@@ -534,6 +558,10 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     // every LDS operand of the stage, read up front
     half8 ah[SB][IT], al[SB][IT];
     uint32_t wq0[SB][NT], wq1[SB][NT], wdm[SB][NT];
+    // kGemmQ4F's minimum is its super-block's dmin, the same for every block of
+    // a stage (stages hold SB blocks of the 8 of a super-block, SB-aligned)
+    static_assert(8 % SB == 0, "a stage within one super-block");
+    uint32_t wmm[NT];
     float4v sx[SB][IT];
     auto load_a = [&](int j) {
 #pragma unroll
@@ -551,7 +579,12 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         const int row = wn + 16 * n + ln;
         const uint8_t* rb = bslot + row * (DWB * 4) + j * TS;     // this block's bytes
         const uint16_t* r16 = reinterpret_cast<const uint16_t*>(rb);
-        if constexpr (TYPE == WH_TYPE_Q8_0) {
+        if constexpr (TYPE == wh::kGemmQ8H) {
+          // 16 quants: k-groups 0, 1; groups 2, 3 are the zero padding
+          const uint32_t* q32 = reinterpret_cast<const uint32_t*>(rb + QOFF + 8 * (g & 1));
+          wq0[j][n] = g < 2 ? q32[0] : 0u;
+          wq1[j][n] = g < 2 ? q32[1] : 0u;
+        } else if constexpr (TYPE == WH_TYPE_Q8_0) {
           const uint16_t* q16 = reinterpret_cast<const uint16_t*>(rb + QOFF + 8 * g);
           wq0[j][n] = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
           wq1[j][n] = static_cast<uint32_t>(q16[2]) | (static_cast<uint32_t>(q16[3]) << 16);
@@ -560,10 +593,15 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
           wq0[j][n] = static_cast<uint32_t>(q16[0]) | (static_cast<uint32_t>(q16[1]) << 16);
           wq1[j][n] = 0u;
         }
-        wdm[j][n] = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
-                                         : static_cast<uint32_t>(r16[0]);
+        if constexpr (f32_scale<TYPE>()) {
+          wdm[j][n] = reinterpret_cast<const uint32_t*>(rb)[0];
+          if (j == 0) wmm[n] = has_min<TYPE>() ? reinterpret_cast<const uint32_t*>(rb)[1] : 0u;
+        } else {
+          wdm[j][n] = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
+                                           : static_cast<uint32_t>(r16[0]);
+        }
       }
-      if constexpr (TYPE == WH_TYPE_Q4_1) {
+      if constexpr (has_min<TYPE>()) {
         const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * BM;
 #pragma unroll
         for (int i = 0; i < IT; i++) sx[j][i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
@@ -613,11 +651,16 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         // this pair becomes the pending one
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          pd[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] & 0xFFFFu);
+          if constexpr (f32_scale<TYPE>()) {
+            pd[h] = __uint_as_float(wdm[j][2 * np + h]);
+            if constexpr (has_min<TYPE>()) pm[h] = __uint_as_float(wmm[2 * np + h]);
+          } else {
+            pd[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] & 0xFFFFu);
+            if constexpr (TYPE == WH_TYPE_Q4_1) pm[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] >> 16);
+          }
           asm("" : "+v"(pd[h]));  // in a VGPR: the FMAs are then plain v_fmac_f32
-          if constexpr (TYPE == WH_TYPE_Q4_1) pm[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] >> 16);
         }
-        if constexpr (TYPE == WH_TYPE_Q4_1) {
+        if constexpr (has_min<TYPE>()) {
 #pragma unroll
           for (int i = 0; i < IT; i++) psx[i] = sx[j][i];
         }
@@ -715,17 +758,34 @@ namespace wh {
 // aligned rows and weights, 16-byte aligned activations, byte offsets into the weights, the activation
 // fragments and the block sums that fit 32 bits, and an LDS budget the device
 // provides.
+// Bytes per 32-element block of a GEMM format.
+static size_t tiled_ts(int type) {
+  switch (type) {
+    case WH_TYPE_Q4_0: return TFmt<WH_TYPE_Q4_0>::TS;
+    case WH_TYPE_Q4_1: return TFmt<WH_TYPE_Q4_1>::TS;
+    case WH_TYPE_Q8_0: return TFmt<WH_TYPE_Q8_0>::TS;
+    case kGemmQ4F: return TFmt<kGemmQ4F>::TS;
+    case kGemmQ8H: return TFmt<kGemmQ8H>::TS;
+    default: return 0;
+  }
+}
+
 bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens) {
-  const size_t ts = type_size(type);
+  const size_t ts = tiled_ts(type);
   if (ts == 0 || k == 0 || k % (32 * SB) != 0 || !aligned(w, 4) || !aligned(x, 16) || ((k / 32) * ts) % 4 != 0) return false;
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;
   const size_t lim = static_cast<size_t>(1) << 32;
   if (n_rows * (k / 32) * ts >= lim || tm * k * 4 >= lim) return false;
   const int b = static_cast<int>(bm);
-  const size_t lds = type == WH_TYPE_Q4_0 ? lds_typed<WH_TYPE_Q4_0>(b)
-                                          : (type == WH_TYPE_Q4_1 ? lds_typed<WH_TYPE_Q4_1>(b)
-                                                                  : lds_typed<WH_TYPE_Q8_0>(b));
+  size_t lds;
+  switch (type) {
+    case WH_TYPE_Q4_0: lds = lds_typed<WH_TYPE_Q4_0>(b); break;
+    case WH_TYPE_Q4_1: lds = lds_typed<WH_TYPE_Q4_1>(b); break;
+    case WH_TYPE_Q8_0: lds = lds_typed<WH_TYPE_Q8_0>(b); break;
+    case kGemmQ4F: lds = lds_typed<kGemmQ4F>(b); break;
+    default: lds = lds_typed<kGemmQ8H>(b); break;
+  }
   return lds <= max_lds_per_block();
 }
 
@@ -745,7 +805,7 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;   // padded tokens
   size_t b = al256(tm * k * 4) + al256(tm * 4);
-  if (type == WH_TYPE_Q4_1) b += al256(tm * (k / 32) * 4);
+  if (has_min_rt(type)) b += al256(tm * (k / 32) * 4);
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
   if (splits > 1) b += al256(static_cast<size_t>(splits) * n_rows * n_tokens * 4);
   return b;
@@ -771,7 +831,7 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
   ws += al256(t.tm * k * 4);
   t.rs = reinterpret_cast<float*>(ws);
   ws += al256(t.tm * 4);
-  if (type == WH_TYPE_Q4_1) {
+  if (has_min_rt(type)) {
     t.bs = reinterpret_cast<float*>(ws);
     ws += al256(t.tm * (k / 32) * 4);
   }
@@ -782,13 +842,14 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
 
 template <int MODE>
 static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x2, const float* gamma, float eps,
-                      size_t n_tokens, size_t k, hipStream_t s) {
+                      size_t n_tokens, size_t k, size_t kx, hipStream_t s) {
   // threads per row: enough for PPT pairs each, 256 .. 1024
   const size_t npairs = k / 8;
   size_t threads = (npairs + PPT - 1) / PPT;
   threads = threads < 256 ? 256 : (threads > kPackMaxThreads ? kPackMaxThreads : (threads + 63) / 64 * 64);
   pack_a_kernel<MODE><<<static_cast<unsigned>(t.tm), static_cast<unsigned>(threads), 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
-                                                                  static_cast<int>(k), type, t.bm, t.frag, t.rs, t.bs);
+                                                                  static_cast<int>(k), static_cast<int>(kx), type, t.bm,
+                                                                  t.frag, t.rs, t.bs);
   WH_LAUNCH_CHECK("pack kernel launch");
   return WH_OK;
 }
@@ -803,6 +864,8 @@ static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_
     case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
     case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
     case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
+    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
+    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
     default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
   }
   if (st != WH_OK) return st;
@@ -820,9 +883,45 @@ static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
                       float* y, void* workspace, hipStream_t s) {
   const TiledWs t = tiled_ws(type, n_rows, k, n_tokens, workspace);
-  int st = tiled_pack<kPackPlain>(type, t, x, nullptr, nullptr, 0.f, n_tokens, k, s);
+  int st = tiled_pack<kPackPlain>(type, t, x, nullptr, nullptr, 0.f, n_tokens, k, k, s);
   if (st) return st;
   return tiled_run(type, w, n_rows, k, n_tokens, t, y, s);
+}
+
+// ------------------------------------------------------------- K-quants
+// The matrix is repacked (kquant.hip) into the front of the workspace, in the
+// GEMM format of kquant_gemm_type with reduction length kquant_gemm_k; the
+// packed activations and the rest of the GEMM's workspace follow it.
+bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens) {
+  if (!is_kquant(type) || k % 256 != 0 || !aligned(w, 16)) return false;
+  // the repacked matrix is 256-byte aligned; any such address stands for it
+  const void* repacked = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+  return gemm_tiled_ok(kquant_gemm_type(type), repacked, x, n_rows, kquant_gemm_k(type, k), n_tokens);
+}
+
+size_t gemm_kquant_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
+  return al256(kquant_repacked_bytes(type, n_rows, k)) +
+         gemm_tiled_workspace_bytes(kquant_gemm_type(type), n_rows, n_tokens, kquant_gemm_k(type, k));
+}
+
+int launch_gemm_kquant(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
+                       float* y, void* workspace, hipStream_t s) {
+  const int it = kquant_gemm_type(type);
+  const size_t kk = kquant_gemm_k(type, k);
+  char* rp = static_cast<char*>(workspace);
+  const TiledWs t = tiled_ws(it, n_rows, kk, n_tokens, rp + al256(kquant_repacked_bytes(type, n_rows, k)));
+  int st = launch_repack_kquant(type, w, n_rows, k, rp, s);
+  if (!st) st = tiled_pack<kPackPlain>(it, t, x, nullptr, nullptr, 0.f, n_tokens, kk, k, s);
+  if (st) return st;
+  return tiled_run(it, rp, n_rows, kk, n_tokens, t, y, s);
+}
+
+size_t ffn_kquant_workspace_bytes(int type, size_t hidden, size_t n_ff, size_t n_tokens) {
+  const int it = kquant_gemm_type(type);
+  const size_t r1 = kquant_repacked_bytes(type, n_ff, hidden), r2 = kquant_repacked_bytes(type, hidden, n_ff);
+  const size_t t1 = gemm_tiled_workspace_bytes(it, n_ff, n_tokens, kquant_gemm_k(type, hidden));
+  const size_t t2 = gemm_tiled_workspace_bytes(it, hidden, n_tokens, kquant_gemm_k(type, n_ff));
+  return al256(r1 > r2 ? r1 : r2) + (t1 > t2 ? t1 : t2);
 }
 
 // The FFN for n_tokens rows on the tiled kernel: the RMSNorm of x is packed
@@ -832,6 +931,31 @@ int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const fl
 int launch_ffn_tiled(int type, const void* gate, const void* up, const void* down, size_t hidden, size_t n_ff,
                      const float* x, const float* gamma, float eps, size_t n_tokens, float* g, float* u, float* out,
                      void* workspace, size_t workspace_bytes, hipStream_t s) {
+  if (is_kquant(type)) {
+    // one repacked matrix at a time in the front of the workspace (stream order
+    // keeps a GEMM's reads ahead of the next repack)
+    const int it = kquant_gemm_type(type);
+    const size_t H2 = kquant_gemm_k(type, hidden), F2 = kquant_gemm_k(type, n_ff);
+    const size_t r1 = kquant_repacked_bytes(type, n_ff, hidden), r2 = kquant_repacked_bytes(type, hidden, n_ff);
+    char* rp = static_cast<char*>(workspace);
+    char* ws = rp + al256(r1 > r2 ? r1 : r2);
+    if (!gemm_kquant_ok(type, gate, x, n_ff, hidden, n_tokens) || !aligned(up, 16) || !aligned(down, 16) ||
+        !gemm_kquant_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16) ||
+        !aligned(workspace, 256) || workspace_bytes < ffn_kquant_workspace_bytes(type, hidden, n_ff, n_tokens))
+      return WH_ERR_INVALID_SHAPE;
+    const TiledWs t1 = tiled_ws(it, n_ff, H2, n_tokens, ws);
+    int st = tiled_pack<kPackNorm>(it, t1, x, nullptr, gamma, eps, n_tokens, H2, hidden, s);
+    if (!st) st = launch_repack_kquant(type, gate, n_ff, hidden, rp, s);
+    if (!st) st = tiled_run(it, rp, n_ff, H2, n_tokens, t1, g, s);
+    if (!st) st = launch_repack_kquant(type, up, n_ff, hidden, rp, s);
+    if (!st) st = tiled_run(it, rp, n_ff, H2, n_tokens, t1, u, s);
+    if (st) return st;
+    const TiledWs t2 = tiled_ws(it, hidden, F2, n_tokens, ws);
+    st = tiled_pack<kPackSwiglu>(it, t2, g, u, nullptr, 0.f, n_tokens, F2, n_ff, s);
+    if (!st) st = launch_repack_kquant(type, down, hidden, n_ff, rp, s);
+    if (st) return st;
+    return tiled_run(it, rp, hidden, F2, n_tokens, t2, out, s);
+  }
   if (!gemm_tiled_ok(type, gate, x, n_ff, hidden, n_tokens) || !gemm_tiled_ok(type, up, x, n_ff, hidden, n_tokens) ||
       !gemm_tiled_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16))
     return WH_ERR_INVALID_SHAPE;
@@ -839,12 +963,12 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
       workspace_bytes < gemm_tiled_workspace_bytes(type, hidden, n_tokens, n_ff))
     return WH_ERR_INVALID_SHAPE;
   const TiledWs t1 = tiled_ws(type, n_ff, hidden, n_tokens, workspace);
-  int st = tiled_pack<kPackNorm>(type, t1, x, nullptr, gamma, eps, n_tokens, hidden, s);
+  int st = tiled_pack<kPackNorm>(type, t1, x, nullptr, gamma, eps, n_tokens, hidden, hidden, s);
   if (!st) st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s);
   if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s);
   if (st) return st;
   const TiledWs t2 = tiled_ws(type, hidden, n_ff, n_tokens, workspace);
-  st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, s);
+  st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
   if (st) return st;
   return tiled_run(type, down, hidden, n_ff, n_tokens, t2, out, s);
 }

@@ -27,31 +27,36 @@ __device__ __forceinline__ uint32_t b16(const uint8_t* p) {
   return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
 }
 
+// 6-bit scale j (0..7) of a Q4_K block at b.
+__device__ __forceinline__ uint32_t q4k_scale(const uint8_t* b, int j) {
+  const int src = (3 * j) >> 1;
+  return (j & 1) ? (((b[src] >> 6) | ((b[src + 1] & 15u) << 2)) & 63u) : (b[src] & 63u);
+}
+
 // Element i (0..255) of a Q4_K block at b.
 __device__ __forceinline__ float q4k_elem(const uint8_t* b, int i, float d, float dmin) {
-  const int j = i >> 5;            // scale index
-  const int src = (3 * j) >> 1;
-  const uint32_t s = (j & 1) ? (((b[src] >> 6) | ((b[src + 1] & 15u) << 2)) & 63u) : (b[src] & 63u);
+  const uint32_t s = q4k_scale(b, i >> 5);
   const uint32_t qb = b[16 + (i >> 1)];
   const uint32_t q = (i & 1) ? ((qb >> 4) & 15u) : (qb & 15u);
   return __fadd_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q)), dmin);
 }
 
-// Element i (0..255) of a Q6_K block at b.
-__device__ __forceinline__ float q6k_elem(const uint8_t* b, int i, float d) {
+// The 6-bit quant q (0..63) of element i (0..255) of a Q6_K block at b.
+__device__ __forceinline__ uint32_t q6k_quant(const uint8_t* b, int i) {
   const uint8_t* ql = b;
   const uint8_t* qh = b + 128;
   const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
   const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
   const int shift = 2 * (i & 3);
   const uint32_t qhv = qh[qh_idx];
-  uint32_t q;
-  if (i < 128) {
-    q = (ql[ql_idx] & 15u) | (((qhv >> shift) & 3u) << 4);
-  } else {
-    const uint32_t e2 = shift < 6 ? ((qhv >> (shift + 2)) & 3u) : (qh_idx + 1 < 64 ? (qh[qh_idx + 1] & 3u) : 0u);
-    q = (ql[ql_idx] >> 4) | (e2 << 4);
-  }
+  if (i < 128) return (ql[ql_idx] & 15u) | (((qhv >> shift) & 3u) << 4);
+  const uint32_t e2 = shift < 6 ? ((qhv >> (shift + 2)) & 3u) : (qh_idx + 1 < 64 ? (qh[qh_idx + 1] & 3u) : 0u);
+  return (ql[ql_idx] >> 4) | (e2 << 4);
+}
+
+// Element i (0..255) of a Q6_K block at b.
+__device__ __forceinline__ float q6k_elem(const uint8_t* b, int i, float d) {
+  const uint32_t q = q6k_quant(b, i);
   const float s = static_cast<float>(b[192 + (i >> 4)]);
   return __fmul_rn(__fmul_rn(__fmul_rn(d, s), static_cast<float>(static_cast<int>(q) - 32)), 0.015625f);
 }
@@ -116,6 +121,74 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict_
   }
 }
 
+// ------------------------------------------------------ prefill repacking
+// The tiled prefill GEMM takes 32-element blocks with one scale each, so a
+// K-quant matrix is rewritten once per call (same row order, same element
+// order within a row) into:
+//   Q4_K -> {f32 d * scale_j; f32 dmin; u8 qs[16]} per 32 elements j: the
+//     value (d * scale_j) * q + dmin, quants in Q4_0's nibble order (byte i:
+//     element i low, element i + 16 high);
+//   Q6_K -> {f32 (d * scale_j) / 64; i8 q[16] = q - 32} per 16 elements j
+//     (the GEMM pads each to a 32-element block, upper half zero).
+// The scale products are exact in f32 (11-bit times 6- or 8-bit integers).
+// Every thread writes one output block; 16-byte aligned input.
+__global__ __launch_bounds__(256) void kq_repack_q4k_kernel(const uint8_t* __restrict__ w, size_t n_groups,
+                                                            uint32_t* __restrict__ out) {
+  for (size_t gi = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < n_groups;
+       gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint8_t* b = w + (gi >> 3) * 144;
+    const int j = static_cast<int>(gi & 7);
+    const float d = whd::f16_bits_to_f32(b16(b + 12));
+    const float dmin = whd::f16_bits_to_f32(b16(b + 14));
+    const uint4 q = *reinterpret_cast<const uint4*>(b + 16 + 16 * j);  // elements 32j .. 32j + 31
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[6];
+    o[0] = __float_as_uint(__fmul_rn(d, static_cast<float>(q4k_scale(b, j))));
+    o[1] = __float_as_uint(dmin);
+    // element e is nibble e & 1 of byte e >> 1; output byte 2m = lo(byte m) |
+    // lo(byte m + 8) << 4, byte 2m + 1 = hi(byte m) | hi(byte m + 8) << 4
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int m = 2 * c + t;
+        const uint32_t lo = (qw[m >> 2] >> (8 * (m & 3))) & 0xFFu;
+        const uint32_t hi = (qw[(m + 8) >> 2] >> (8 * ((m + 8) & 3))) & 0xFFu;
+        const uint32_t b0 = (lo & 15u) | ((hi & 15u) << 4);
+        const uint32_t b1 = (lo >> 4) | (hi & 0xF0u);
+        v |= (b0 | (b1 << 8)) << (16 * t);
+      }
+      o[2 + c] = v;
+    }
+    uint32_t* dst = out + gi * 6;
+#pragma unroll
+    for (int c = 0; c < 6; c++) dst[c] = o[c];
+  }
+}
+
+__global__ __launch_bounds__(256) void kq_repack_q6k_kernel(const uint8_t* __restrict__ w, size_t n_halves,
+                                                            uint32_t* __restrict__ out) {
+  for (size_t gi = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < n_halves;
+       gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint8_t* b = w + (gi >> 4) * 210;
+    const int j = static_cast<int>(gi & 15);
+    const float d = whd::f16_bits_to_f32(b16(b + 208));
+    uint32_t o[5];
+    o[0] = __float_as_uint(__fmul_rn(__fmul_rn(d, static_cast<float>(b[192 + j])), 0.015625f));
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int t = 0; t < 4; t++) v |= ((q6k_quant(b, 16 * j + 4 * c + t) - 32u) & 0xFFu) << (8 * t);
+      o[1 + c] = v;
+    }
+    uint32_t* dst = out + gi * 5;
+#pragma unroll
+    for (int c = 0; c < 5; c++) dst[c] = o[c];
+  }
+}
+
 unsigned kq_grid(size_t work, unsigned per_block) {
   size_t g = (work + per_block - 1) / per_block;
   const size_t cap = static_cast<size_t>(wh::cu_count()) * 16;
@@ -144,6 +217,21 @@ int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t
   if (type == WH_TYPE_Q4_K) kq_gemv_kernel<WH_TYPE_Q4_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
   else kq_gemv_kernel<WH_TYPE_Q6_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
   WH_LAUNCH_CHECK("gemv (k-quant) kernel launch");
+  return WH_OK;
+}
+
+int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void* out, hipStream_t s) {
+  if (n_rows == 0 || k == 0) return WH_OK;
+  const uint8_t* p = static_cast<const uint8_t*>(w);
+  uint32_t* o = static_cast<uint32_t*>(out);
+  if (type == WH_TYPE_Q4_K) {
+    const size_t n = n_rows * (k / 32);
+    kq_repack_q4k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, o);
+  } else {
+    const size_t n = n_rows * (k / 16);
+    kq_repack_q6k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, o);
+  }
+  WH_LAUNCH_CHECK("k-quant repack kernel launch");
   return WH_OK;
 }
 

@@ -59,8 +59,23 @@ inline size_t block_elems(int type) {
 inline bool is_block_type(int type) {
   return type == WH_TYPE_Q4_0 || type == WH_TYPE_Q4_1 || type == WH_TYPE_Q8_0;
 }
-// The 256-element K-quant formats (dequantization and GEMV only).
+// The 256-element K-quant formats.
 inline bool is_kquant(int type) { return type == WH_TYPE_Q4_K || type == WH_TYPE_Q6_K; }
+
+// Block formats of the tiled prefill GEMM that K-quant matrices are repacked
+// into (internal ids, never seen at the C ABI):
+//   kGemmQ4F {f32 d; f32 m; u8 qs[16]}: 32 elements d * q + m, Q4_0 nibble order
+//   kGemmQ8H {f32 d; i8 q[16]}: 16 elements d * q, which the GEMM reads as a
+//            32-element block whose upper half is zero (activations packed to match)
+constexpr int kGemmQ4F = 256, kGemmQ8H = 257;
+inline int kquant_gemm_type(int type) { return type == WH_TYPE_Q4_K ? kGemmQ4F : kGemmQ8H; }
+// The GEMM's reduction length for a K-quant row of k elements.
+inline size_t kquant_gemm_k(int type, size_t k) { return type == WH_TYPE_Q4_K ? k : 2 * k; }
+inline size_t kquant_repacked_bytes(int type, size_t n_rows, size_t k) {
+  return n_rows * (type == WH_TYPE_Q4_K ? k / 32 * 24 : k / 16 * 20);
+}
+// Rewrites a Q4_K / Q6_K matrix (n_rows x k, 16-byte aligned) into the format above (kquant.hip).
+int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void* out, hipStream_t stream);
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
@@ -111,6 +126,14 @@ bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x,
                       size_t n_tokens, float* y, void* workspace, hipStream_t stream);
+// Q4_K / Q6_K on the tiled kernel: the matrix repacked into the front of the
+// workspace, then the GEMM.
+bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens);
+size_t gemm_kquant_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
+int launch_gemm_kquant(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
+                       float* y, void* workspace, hipStream_t stream);
+// Workspace of launch_ffn_tiled beyond its g / u scratch, for a K-quant FFN.
+size_t ffn_kquant_workspace_bytes(int type, size_t hidden, size_t n_ff, size_t n_tokens);
 // FFN for more than kGemvTokenLimit tokens on the tiled kernel, with the
 // RMSNorm and SwiGLU fused into its activation packing (g, u: scratch of
 // n_tokens x n_ff); WH_ERR_INVALID_SHAPE (nothing launched) when it does not fit.

@@ -12,7 +12,7 @@ from . import _lib
 from .device import DeviceBuffer, Stream
 
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q8_0 = 0, 1, 2, 3, 8
-GGML_Q4_K, GGML_Q6_K = 12, 14  # dequantization and GEMV only
+GGML_Q4_K, GGML_Q6_K = 12, 14
 
 
 def _s(stream: Stream | None):
@@ -85,8 +85,11 @@ def swiglu(gate, up, n: int, out, stream: Stream | None = None) -> None:
     _lib.check(_lib.load().wh_swiglu(_p(gate), _p(up), n, _p(out), _s(stream)))
 
 
-def ffn_workspace_bytes(hidden: int, n_ff: int, m: int) -> int:
-    return int(_lib.load().wh_ffn_workspace_bytes(hidden, n_ff, m))
+def ffn_workspace_bytes(hidden: int, n_ff: int, m: int, ggml_type: int | None = None) -> int:
+    """Workspace of ffn_swiglu; without a type, enough for Q4_0, Q4_1 and Q8_0."""
+    if ggml_type is None:
+        return int(_lib.load().wh_ffn_workspace_bytes(hidden, n_ff, m))
+    return int(_lib.load().wh_ffn_workspace_bytes_for_type(ggml_type, hidden, n_ff, m))
 
 
 def ffn_swiglu(ggml_type: int, gate, up, down, hidden: int, n_ff: int, gamma, eps: float, x,
