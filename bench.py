@@ -129,20 +129,20 @@ def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int =
     return ms_total / steps, float(np.median(durs)), float(np.mean(durs))
 
 
-def bench_ffn(m: int, iters: int) -> float:
+def bench_ffn(m: int, iters: int, t: int = Q4_0) -> float:
     from woolly_amd import ops, synth
     from woolly_amd.device import DeviceBuffer, Event, Stream
 
     hidden, n_ff = 4096, 14336
-    L = synth.ffn_layer(Q4_0, hidden, n_ff, m, seed=5)
+    L = synth.ffn_layer(t, hidden, n_ff, m, seed=5)
     stream = Stream()
     b = {k: DeviceBuffer.from_array(v) for k, v in L.items()}
     out = DeviceBuffer(4 * m * hidden)
-    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m, ggml_type=t)
     ws = DeviceBuffer(wsz)
 
     def run():
-        ops.ffn_swiglu(Q4_0, b["gate"], b["up"], b["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
+        ops.ffn_swiglu(t, b["gate"], b["up"], b["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
                        m, out, ws, wsz, stream)
 
     for _ in range(3):
@@ -157,21 +157,21 @@ def bench_ffn(m: int, iters: int) -> float:
     return e0.elapsed_ms(e1) / iters * 1000.0
 
 
-def bench_gemm(m: int, iters: int) -> float:
-    """Q4_0 prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2), µs per call."""
+def bench_gemm(m: int, iters: int, t: int = Q4_0) -> float:
+    """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t), µs per call."""
     from woolly_amd import ops, synth
     from woolly_amd.device import DeviceBuffer, Event, Stream
 
-    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=4)
+    w = synth.quantized_weight(t, N_ROWS, K, seed=4)
     x = np.concatenate([synth.activations(K, seed=400 + t) for t in range(min(m, 64))])
     x = np.resize(x, m * K).astype(np.float32)
     stream = Stream()
     wb, xb, yb = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer(4 * m * N_ROWS)
-    wsz = ops.matmul_workspace_bytes(Q4_0, N_ROWS, K, m)
+    wsz = ops.matmul_workspace_bytes(t, N_ROWS, K, m)
     ws = DeviceBuffer(max(wsz, 256))
 
     def run():
-        ops.quantized_matmul(Q4_0, wb, w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
+        ops.quantized_matmul(t, wb, w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
 
     for _ in range(3):
         run()
@@ -373,6 +373,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
+    ap.add_argument("--type", type=int, default=Q4_0,
+                    help="ggml type id of --only gemm / ffn1 / ffn512 (default Q4_0)")
     ap.add_argument("--gemv-shape", type=int, nargs=3, default=None, metavar=("TYPE", "N", "K"),
                     help="ggml type id and shape of --only gemv (default Q4_0 14336 4096)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -398,14 +400,16 @@ def main() -> int:
                           "GBps": round(gemv_bytes(n, k, t) / (ms_step * 1e-3) / 1e9, 1)}))
         return 0
     if args.only == "gemm":
-        print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5), 2)}))
+        print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5, args.type), 2),
+                          "type": args.type}))
         return 0
     if args.only == "decode":
         print(json.dumps({"decode_step": bench_decode(10)}))
         return 0
     if args.only in ("ffn1", "ffn512"):
         m = 1 if args.only == "ffn1" else 512
-        print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3), 2)}))
+        print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3, args.type), 2),
+                          "type": args.type}))
         return 0
     ms_step, med_ms, mean_ms = bench_gemv(args.steps, args.warmup)
     nbytes = gemv_bytes(N_ROWS, K)
@@ -423,7 +427,7 @@ def main() -> int:
         ffn["m512"] = round(bench_ffn(512, 3), 2)
         log(f"[bench] ffn m=512: {ffn['m512']} us")
 
-    gemm = {}
+    gemm, gemm_kq = {}, {}
     if not args.no_gemm:
         # M sweep of config 2 (GEMV -> MFMA crossover).  tflops = 2*M*N*K / time;
         # the MFMA path issues two fp16 products per multiply-add (activation
@@ -433,6 +437,19 @@ def main() -> int:
             tf = 2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12
             gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}
             log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s")
+        # K-quant weights at M=512: the call includes rewriting the matrix into
+        # 32-element f32-scale blocks (Q6_K: zero-padded 16-element halves)
+        for name, t in (("q4_k", 12), ("q6_k", 14)):
+            us = bench_gemm(512, 5, t)
+            tf = 2.0 * 512 * N_ROWS * K / (us * 1e-6) / 1e12
+            gemm_kq[f"gemm_{name}_m512"] = {"us": round(us, 2), "tflops": round(tf, 2)}
+            log(f"[bench] gemm {name} m=512: {us:.2f} us, {tf:.1f} TFLOP/s")
+        if not args.no_ffn:
+            for name, t in (("q4_k", 12), ("q6_k", 14)):
+                gemm_kq[f"ffn_{name}_m1_us"] = round(bench_ffn(1, 50, t), 2)
+                gemm_kq[f"ffn_{name}_m512_us"] = round(bench_ffn(512, 3, t), 2)
+                log(f"[bench] ffn {name}: m=1 {gemm_kq[f'ffn_{name}_m1_us']} us, "
+                    f"m=512 {gemm_kq[f'ffn_{name}_m512_us']} us")
 
     # the other decode GEMV configurations (config 0, 1a, 1b); replicas keep
     # each timed set of weights above the 256 MB Infinity Cache
@@ -502,6 +519,7 @@ def main() -> int:
         },
         "ffn_layer_us": ffn or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,
+        "prefill_kquant_14336x4096": gemm_kq or None,
         "gemv_other_configs": gemv_cfg or None,
         "decode_step_llama3_8b_q4_0": decode,
         "cpu_baseline": cpu,

@@ -71,25 +71,27 @@ template <>
 struct TFmt<WH_TYPE_Q8_0> {
   static constexpr int TS = 34, QOFF = 2;
 };
-// the repacked K-quant formats (f32 scale, and minimum for Q4F)
+// the repacked K-quant formats (f32 scale)
 template <>
 struct TFmt<wh::kGemmQ4F> {
-  static constexpr int TS = 24, QOFF = 8;
+  static constexpr int TS = 20, QOFF = 4;
 };
 template <>
 struct TFmt<wh::kGemmQ8H> {
   static constexpr int TS = 20, QOFF = 4;
 };
-// block value d * q + m: block sums of the activations are needed
+// block value d * q + m: the kernel adds m times the activations' block sums
 template <int TYPE>
-constexpr bool has_min() { return TYPE == WH_TYPE_Q4_1 || TYPE == wh::kGemmQ4F; }
+constexpr bool has_min() { return TYPE == WH_TYPE_Q4_1; }
 // int8 quants in natural element order (else 4-bit quants in nibble order)
 template <int TYPE>
 constexpr bool q8_like() { return TYPE == WH_TYPE_Q8_0 || TYPE == wh::kGemmQ8H; }
 // f32 block scale (else f16)
 template <int TYPE>
 constexpr bool f32_scale() { return TYPE == wh::kGemmQ4F || TYPE == wh::kGemmQ8H; }
-inline bool has_min_rt(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
+// block sums of the activations are written by the packing (kGemmQ4F: for the
+// dmin pass after the GEMM)
+inline bool needs_bsum(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
 // dwords per weight row per stage (SB whole blocks)
 template <int TYPE>
 constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
@@ -558,10 +560,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     // every LDS operand of the stage, read up front
     half8 ah[SB][IT], al[SB][IT];
     uint32_t wq0[SB][NT], wq1[SB][NT], wdm[SB][NT];
-    // kGemmQ4F's minimum is its super-block's dmin, the same for every block of
-    // a stage (stages hold SB blocks of the 8 of a super-block, SB-aligned)
-    static_assert(8 % SB == 0, "a stage within one super-block");
-    uint32_t wmm[NT];
     float4v sx[SB][IT];
     auto load_a = [&](int j) {
 #pragma unroll
@@ -595,7 +593,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         }
         if constexpr (f32_scale<TYPE>()) {
           wdm[j][n] = reinterpret_cast<const uint32_t*>(rb)[0];
-          if (j == 0) wmm[n] = has_min<TYPE>() ? reinterpret_cast<const uint32_t*>(rb)[1] : 0u;
         } else {
           wdm[j][n] = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
                                            : static_cast<uint32_t>(r16[0]);
@@ -653,7 +650,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         for (int h = 0; h < 2; h++) {
           if constexpr (f32_scale<TYPE>()) {
             pd[h] = __uint_as_float(wdm[j][2 * np + h]);
-            if constexpr (has_min<TYPE>()) pm[h] = __uint_as_float(wmm[2 * np + h]);
           } else {
             pd[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] & 0xFFFFu);
             if constexpr (TYPE == WH_TYPE_Q4_1) pm[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] >> 16);
@@ -701,6 +697,68 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* _
     float v = part[i];
     for (int s = 1; s < splits; s++) v += part[static_cast<size_t>(s) * n + i];
     y[i] = v;
+  }
+}
+
+// Q4_K's minimum: y[t, r] += sum over super-blocks sb of dmin[sb][r] * S[t, sb],
+// S the activations' sum over the super-block (rscale[t] times the packing's
+// eight block sums of hi + lo, the scaling the GEMM's epilogue undoes).  A
+// thread owns kDminRows rows (256 apart) for kDminTokens tokens; the tokens'
+// sums are staged in LDS as [sb][token] and read four tokens at a time.
+constexpr int kDminTokens = 16, kDminRows = 2;
+__global__ __launch_bounds__(256) void kq_dmin_kernel(float* __restrict__ y, const float* __restrict__ dmin_t,
+                                                      const float* __restrict__ bsum, const float* __restrict__ rscale,
+                                                      int n_tokens, int n_rows, int nb, int bm) {
+  extern __shared__ float4 ssum4[];  // [nsb][kDminTokens / 4]
+  float* ssum = reinterpret_cast<float*>(ssum4);
+  const int nsb = nb / 8;
+  const int t0 = blockIdx.y * kDminTokens;
+  for (int i = threadIdx.x; i < kDminTokens * nsb; i += blockDim.x) {
+    const int sb = i / kDminTokens, tt = i % kDminTokens, t = t0 + tt;
+    float v = 0.f;
+    if (t < n_tokens) {
+      const float* bs = bsum + (static_cast<size_t>(t / bm) * nb + 8 * sb) * bm + (t % bm);
+#pragma unroll
+      for (int j = 0; j < 8; j++) v += bs[static_cast<size_t>(j) * bm];
+      v *= rscale[t];
+    }
+    ssum[i] = v;
+  }
+  __syncthreads();
+  const int r0 = blockIdx.x * (kDminRows * 256) + threadIdx.x;
+  float acc[kDminRows][kDminTokens];
+#pragma unroll
+  for (int q = 0; q < kDminRows; q++)
+#pragma unroll
+    for (int tt = 0; tt < kDminTokens; tt++) acc[q][tt] = 0.f;
+  for (int sb = 0; sb < nsb; sb++) {
+    float dm[kDminRows];
+#pragma unroll
+    for (int q = 0; q < kDminRows; q++) {
+      const int r = r0 + 256 * q;
+      dm[q] = r < n_rows ? dmin_t[static_cast<size_t>(sb) * n_rows + r] : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < kDminTokens / 4; c++) {
+      const float4 sv = ssum4[sb * (kDminTokens / 4) + c];
+#pragma unroll
+      for (int q = 0; q < kDminRows; q++) {
+        acc[q][4 * c + 0] = __builtin_fmaf(dm[q], sv.x, acc[q][4 * c + 0]);
+        acc[q][4 * c + 1] = __builtin_fmaf(dm[q], sv.y, acc[q][4 * c + 1]);
+        acc[q][4 * c + 2] = __builtin_fmaf(dm[q], sv.z, acc[q][4 * c + 2]);
+        acc[q][4 * c + 3] = __builtin_fmaf(dm[q], sv.w, acc[q][4 * c + 3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kDminRows; q++) {
+    const int r = r0 + 256 * q;
+    if (r >= n_rows) continue;
+#pragma unroll
+    for (int tt = 0; tt < kDminTokens; tt++) {
+      const int t = t0 + tt;
+      if (t < n_tokens) y[static_cast<size_t>(t) * n_rows + r] += acc[q][tt];
+    }
   }
 }
 
@@ -805,7 +863,7 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;   // padded tokens
   size_t b = al256(tm * k * 4) + al256(tm * 4);
-  if (has_min_rt(type)) b += al256(tm * (k / 32) * 4);
+  if (needs_bsum(type)) b += al256(tm * (k / 32) * 4);
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
   if (splits > 1) b += al256(static_cast<size_t>(splits) * n_rows * n_tokens * 4);
   return b;
@@ -831,7 +889,7 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
   ws += al256(t.tm * k * 4);
   t.rs = reinterpret_cast<float*>(ws);
   ws += al256(t.tm * 4);
-  if (has_min_rt(type)) {
+  if (needs_bsum(type)) {
     t.bs = reinterpret_cast<float*>(ws);
     ws += al256(t.tm * (k / 32) * 4);
   }
@@ -899,6 +957,25 @@ bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size
   return gemm_tiled_ok(kquant_gemm_type(type), repacked, x, n_rows, kquant_gemm_k(type, k), n_tokens);
 }
 
+// GEMM on a repacked K-quant matrix rp (n_rows x kk in its GEMM format) over
+// packed activations t, then for Q4_K the dmin pass (k: the row length).
+static int kquant_run(int type, const char* rp, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t,
+                      float* y, hipStream_t s) {
+  const int it = kquant_gemm_type(type);
+  const size_t kk = kquant_gemm_k(type, k);
+  int st = tiled_run(it, rp, n_rows, kk, n_tokens, t, y, s);
+  if (st || type != WH_TYPE_Q4_K) return st;
+  const float* dmin_t = reinterpret_cast<const float*>(rp + n_rows * (k / 32) * 20);
+  const int nb = static_cast<int>(k / 32);
+  dim3 grid(static_cast<unsigned>((n_rows + kDminRows * 256 - 1) / (kDminRows * 256)),
+            static_cast<unsigned>((n_tokens + kDminTokens - 1) / kDminTokens));
+  const size_t lds = static_cast<size_t>(kDminTokens) * (nb / 8) * sizeof(float);
+  kq_dmin_kernel<<<grid, 256, lds, s>>>(y, dmin_t, t.bs, t.rs, static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
+                                        t.bm);
+  WH_LAUNCH_CHECK("k-quant dmin kernel launch");
+  return WH_OK;
+}
+
 size_t gemm_kquant_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
   return al256(kquant_repacked_bytes(type, n_rows, k)) +
          gemm_tiled_workspace_bytes(kquant_gemm_type(type), n_rows, n_tokens, kquant_gemm_k(type, k));
@@ -913,7 +990,7 @@ int launch_gemm_kquant(int type, const void* w, size_t n_rows, size_t k, const f
   int st = launch_repack_kquant(type, w, n_rows, k, rp, s);
   if (!st) st = tiled_pack<kPackPlain>(it, t, x, nullptr, nullptr, 0.f, n_tokens, kk, k, s);
   if (st) return st;
-  return tiled_run(it, rp, n_rows, kk, n_tokens, t, y, s);
+  return kquant_run(type, rp, n_rows, k, n_tokens, t, y, s);
 }
 
 size_t ffn_kquant_workspace_bytes(int type, size_t hidden, size_t n_ff, size_t n_tokens) {
@@ -946,15 +1023,15 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
     const TiledWs t1 = tiled_ws(it, n_ff, H2, n_tokens, ws);
     int st = tiled_pack<kPackNorm>(it, t1, x, nullptr, gamma, eps, n_tokens, H2, hidden, s);
     if (!st) st = launch_repack_kquant(type, gate, n_ff, hidden, rp, s);
-    if (!st) st = tiled_run(it, rp, n_ff, H2, n_tokens, t1, g, s);
+    if (!st) st = kquant_run(type, rp, n_ff, hidden, n_tokens, t1, g, s);
     if (!st) st = launch_repack_kquant(type, up, n_ff, hidden, rp, s);
-    if (!st) st = tiled_run(it, rp, n_ff, H2, n_tokens, t1, u, s);
+    if (!st) st = kquant_run(type, rp, n_ff, hidden, n_tokens, t1, u, s);
     if (st) return st;
     const TiledWs t2 = tiled_ws(it, hidden, F2, n_tokens, ws);
     st = tiled_pack<kPackSwiglu>(it, t2, g, u, nullptr, 0.f, n_tokens, F2, n_ff, s);
     if (!st) st = launch_repack_kquant(type, down, hidden, n_ff, rp, s);
     if (st) return st;
-    return tiled_run(it, rp, hidden, F2, n_tokens, t2, out, s);
+    return kquant_run(type, rp, hidden, n_ff, n_tokens, t2, out, s);
   }
   if (!gemm_tiled_ok(type, gate, x, n_ff, hidden, n_tokens) || !gemm_tiled_ok(type, up, x, n_ff, hidden, n_tokens) ||
       !gemm_tiled_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16))

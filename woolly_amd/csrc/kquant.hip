@@ -125,26 +125,27 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict_
 // The tiled prefill GEMM takes 32-element blocks with one scale each, so a
 // K-quant matrix is rewritten once per call (same row order, same element
 // order within a row) into:
-//   Q4_K -> {f32 d * scale_j; f32 dmin; u8 qs[16]} per 32 elements j: the
-//     value (d * scale_j) * q + dmin, quants in Q4_0's nibble order (byte i:
-//     element i low, element i + 16 high);
+//   Q4_K -> {f32 d * scale_j; u8 qs[16]} per 32 elements j (quants in Q4_0's
+//     nibble order: byte i holds element i low, element i + 16 high), and the
+//     super-block's dmin as f32 in a [k / 256][n_rows] table after the blocks;
+//     the value (d * scale_j) * q + dmin is then the GEMM's d * q plus dmin
+//     times the super-block's activation sum;
 //   Q6_K -> {f32 (d * scale_j) / 64; i8 q[16] = q - 32} per 16 elements j
 //     (the GEMM pads each to a 32-element block, upper half zero).
 // The scale products are exact in f32 (11-bit times 6- or 8-bit integers).
 // Every thread writes one output block; 16-byte aligned input.
 __global__ __launch_bounds__(256) void kq_repack_q4k_kernel(const uint8_t* __restrict__ w, size_t n_groups,
-                                                            uint32_t* __restrict__ out) {
+                                                            size_t groups_per_row, size_t n_rows,
+                                                            uint32_t* __restrict__ out, float* __restrict__ dmin_t) {
   for (size_t gi = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < n_groups;
        gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const uint8_t* b = w + (gi >> 3) * 144;
     const int j = static_cast<int>(gi & 7);
     const float d = whd::f16_bits_to_f32(b16(b + 12));
-    const float dmin = whd::f16_bits_to_f32(b16(b + 14));
     const uint4 q = *reinterpret_cast<const uint4*>(b + 16 + 16 * j);  // elements 32j .. 32j + 31
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    uint32_t o[6];
+    uint32_t o[5];
     o[0] = __float_as_uint(__fmul_rn(d, static_cast<float>(q4k_scale(b, j))));
-    o[1] = __float_as_uint(dmin);
     // element e is nibble e & 1 of byte e >> 1; output byte 2m = lo(byte m) |
     // lo(byte m + 8) << 4, byte 2m + 1 = hi(byte m) | hi(byte m + 8) << 4
 #pragma unroll
@@ -159,33 +160,51 @@ __global__ __launch_bounds__(256) void kq_repack_q4k_kernel(const uint8_t* __res
         const uint32_t b1 = (lo >> 4) | (hi & 0xF0u);
         v |= (b0 | (b1 << 8)) << (16 * t);
       }
-      o[2 + c] = v;
-    }
-    uint32_t* dst = out + gi * 6;
-#pragma unroll
-    for (int c = 0; c < 6; c++) dst[c] = o[c];
-  }
-}
-
-__global__ __launch_bounds__(256) void kq_repack_q6k_kernel(const uint8_t* __restrict__ w, size_t n_halves,
-                                                            uint32_t* __restrict__ out) {
-  for (size_t gi = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < n_halves;
-       gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    const uint8_t* b = w + (gi >> 4) * 210;
-    const int j = static_cast<int>(gi & 15);
-    const float d = whd::f16_bits_to_f32(b16(b + 208));
-    uint32_t o[5];
-    o[0] = __float_as_uint(__fmul_rn(__fmul_rn(d, static_cast<float>(b[192 + j])), 0.015625f));
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int t = 0; t < 4; t++) v |= ((q6k_quant(b, 16 * j + 4 * c + t) - 32u) & 0xFFu) << (8 * t);
       o[1 + c] = v;
     }
     uint32_t* dst = out + gi * 5;
 #pragma unroll
     for (int c = 0; c < 5; c++) dst[c] = o[c];
+    if (j == 0) {
+      const size_t row = gi / groups_per_row, sb = (gi % groups_per_row) >> 3;
+      dmin_t[sb * n_rows + row] = whd::f16_bits_to_f32(b16(b + 14));
+    }
+  }
+}
+
+// Q6_K: a workgroup stages 32 consecutive blocks (6720 B, a 16-byte aligned
+// run) in LDS with coalesced 16-byte loads, then each thread rewrites halves.
+constexpr int kQ6Blocks = 32;
+__global__ __launch_bounds__(256) void kq_repack_q6k_kernel(const uint8_t* __restrict__ w, size_t n_blocks,
+                                                            uint32_t* __restrict__ out) {
+  __shared__ uint4 stage[kQ6Blocks * 210 / 16];
+  uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
+  for (size_t b0 = static_cast<size_t>(blockIdx.x) * kQ6Blocks; b0 < n_blocks;
+       b0 += static_cast<size_t>(gridDim.x) * kQ6Blocks) {
+    const int nblk = static_cast<int>(n_blocks - b0 < kQ6Blocks ? n_blocks - b0 : kQ6Blocks);
+    const int bytes = nblk * 210;
+    const uint8_t* src = w + b0 * 210;
+    for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) stage[i] = reinterpret_cast<const uint4*>(src)[i];
+    for (int i = bytes / 16 * 16 + threadIdx.x; i < bytes; i += blockDim.x) sb[i] = src[i];
+    __syncthreads();
+    for (int h = threadIdx.x; h < nblk * 16; h += blockDim.x) {
+      const uint8_t* b = sb + (h >> 4) * 210;
+      const int j = h & 15;
+      const float d = whd::f16_bits_to_f32(b16(b + 208));
+      uint32_t o[5];
+      o[0] = __float_as_uint(__fmul_rn(__fmul_rn(d, static_cast<float>(b[192 + j])), 0.015625f));
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) v |= ((q6k_quant(b, 16 * j + 4 * c + t) - 32u) & 0xFFu) << (8 * t);
+        o[1 + c] = v;
+      }
+      uint32_t* dst = out + (b0 * 16 + static_cast<size_t>(h)) * 5;
+#pragma unroll
+      for (int c = 0; c < 5; c++) dst[c] = o[c];
+    }
+    __syncthreads();
   }
 }
 
@@ -226,10 +245,11 @@ int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void*
   uint32_t* o = static_cast<uint32_t*>(out);
   if (type == WH_TYPE_Q4_K) {
     const size_t n = n_rows * (k / 32);
-    kq_repack_q4k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, o);
+    float* dmin_t = reinterpret_cast<float*>(static_cast<char*>(out) + n * 20);
+    kq_repack_q4k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, k / 32, n_rows, o, dmin_t);
   } else {
-    const size_t n = n_rows * (k / 16);
-    kq_repack_q6k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, o);
+    const size_t n = n_rows * (k / 256);
+    kq_repack_q6k_kernel<<<kq_grid(n, kQ6Blocks), 256, 0, s>>>(p, n, o);
   }
   WH_LAUNCH_CHECK("k-quant repack kernel launch");
   return WH_OK;
