@@ -252,7 +252,8 @@ WH_API int wh_rope_inv_freq(float base, size_t head_dim, float* out_host);
 /* Fused RMSNorm + Q/K/V projection of one token (the rms_norm of process_layer,
  * :130-134, then simd_attention_projections, tensor_utils_simd.rs:455-602):
  * qkv = [Wq; Wk; Wv] * rms_norm(x, gamma, eps), laid out q (q_rows) | k | v
- * (kv_rows each), all three matrices of one block type with K = hidden.
+ * (kv_rows each), all three matrices of one block type with K = hidden
+ * (Q4_0, Q4_1, Q8_0, or Q4_K / Q6_K with hidden a multiple of 256).
  * The workspace (wh_attention_qkv_workspace_bytes) is only used by shapes the
  * fused kernel does not take. */
 WH_API size_t wh_attention_qkv_workspace_bytes(size_t hidden);
@@ -278,7 +279,7 @@ WH_API int wh_attention_decode(const float* qkv, void* k_cache, void* v_cache, s
 
 /* y = residual + W x for one token (the attention output projection and the
  * FFN down projection with process_layer's residual adds, :186-188, 245-247).
- * y may be the residual buffer itself. */
+ * y may be the residual buffer itself.  Types as wh_quantized_matvec. */
 WH_API int wh_quantized_matvec_residual(int type, const void* weights, size_t weight_nbytes,
                                         const float* input, const float* residual, float* output,
                                         size_t m, size_t k, wh_stream_t stream);
@@ -296,10 +297,14 @@ typedef struct wh_llama_layer {
   const void* w_down;      /* [hidden][n_ff] */
   void* k_cache;           /* f16 [max_ctx][n_kv_heads][head_dim] */
   void* v_cache;           /* f16 [max_ctx][n_kv_heads][head_dim] */
+  /* Block type of each matrix; 0 (zero-initialised) = the model's type.  GGUF
+   * files such as Q4_K_M mix types per tensor (attn_v and ffn_down in Q6_K,
+   * the rest in Q4_K).  K-quant matrices need their K a multiple of 256. */
+  int wq_type, wk_type, wv_type, wo_type, w_gate_type, w_up_type, w_down_type;
 } wh_llama_layer;
 
 typedef struct wh_llama_model {
-  int type;                    /* block type of the layer matrices */
+  int type;                    /* block type of the layer matrices (see wh_llama_layer) */
   size_t n_layers, hidden, n_heads, n_kv_heads, head_dim, n_ff, max_ctx, vocab;
   float eps;                   /* RMSNorm epsilon (model/mod.rs:193: 1e-5) */
   const float* rope_inv_freq;  /* device [head_dim / 2], see wh_rope_inv_freq */

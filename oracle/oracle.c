@@ -667,16 +667,20 @@ static void rms_norm_dd(const double* x, const float* g, double eps, size_t n, d
  * (lazy_transformer.rs:98-258): x += Wo attn(qkv(rms_norm(x, attn_norm)));
  * x += Wd (silu(Wg x_hat) * (Wu x_hat)), x_hat = rms_norm(x, ffn_norm).  x in
  * f64, updated in place; the caches are updated at row pos. */
-int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
-                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
-                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
-                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
-                               double eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
-                               size_t pos, int store_new, double* x) {
-  int st = check_matvec_args(type, hidden);
-  if (st) return st;
-  if ((n_heads * d) % 32 || n_ff % 32) return ORC_ERR_INVALID_SHAPE;
+int orc_llama_layer_decode_types_f64(const int* types, const uint8_t* wq, const uint8_t* wk,
+                                     const uint8_t* wv, const uint8_t* wo, const float* attn_norm,
+                                     const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                                     const float* ffn_norm, size_t hidden, size_t n_heads, size_t n_kv,
+                                     size_t d, size_t n_ff, double eps, const float* inv_freq,
+                                     uint16_t* k_cache, uint16_t* v_cache, size_t pos, int store_new,
+                                     double* x) {
   size_t qd = n_heads * d, kvd = n_kv * d;
+  /* reduction length of each projection: q, k, v, gate, up read x_hat; o reads
+   * the attention output, down the SwiGLU */
+  const size_t kdim[7] = {hidden, hidden, hidden, qd, hidden, hidden, n_ff};
+  int st = ORC_OK;
+  for (int i = 0; i < 7; i++)
+    if ((st = check_matvec_args(types[i], kdim[i]))) return st;
   size_t big = hidden > n_ff ? hidden : n_ff;
   double* xn = (double*)malloc(big * sizeof(double));
   double* qkv = (double*)malloc((qd + 2 * kvd) * sizeof(double));
@@ -689,18 +693,18 @@ int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, c
     goto done;
   }
   rms_norm_dd(x, attn_norm, eps, hidden, xn);
-  if ((st = matvec_dd(type, wq, xn, qkv, qd, hidden))) goto done;
-  if ((st = matvec_dd(type, wk, xn, qkv + qd, kvd, hidden))) goto done;
-  if ((st = matvec_dd(type, wv, xn, qkv + qd + kvd, kvd, hidden))) goto done;
+  if ((st = matvec_dd(types[0], wq, xn, qkv, qd, hidden))) goto done;
+  if ((st = matvec_dd(types[1], wk, xn, qkv + qd, kvd, hidden))) goto done;
+  if ((st = matvec_dd(types[2], wv, xn, qkv + qd + kvd, kvd, hidden))) goto done;
   if ((st = orc_attention_decode_f64(qkv, k_cache, v_cache, pos, n_heads, n_kv, d, inv_freq, store_new, att)))
     goto done;
-  if ((st = matvec_dd(type, wo, att, y, hidden, qd))) goto done;
+  if ((st = matvec_dd(types[3], wo, att, y, hidden, qd))) goto done;
   for (size_t i = 0; i < hidden; i++) x[i] += y[i];
   rms_norm_dd(x, ffn_norm, eps, hidden, xn);
-  if ((st = matvec_dd(type, wg, xn, g, n_ff, hidden))) goto done;
-  if ((st = matvec_dd(type, wu, xn, u, n_ff, hidden))) goto done;
+  if ((st = matvec_dd(types[4], wg, xn, g, n_ff, hidden))) goto done;
+  if ((st = matvec_dd(types[5], wu, xn, u, n_ff, hidden))) goto done;
   orc_swiglu_f64(g, u, n_ff, g);
-  if ((st = matvec_dd(type, wd, g, y, hidden, n_ff))) goto done;
+  if ((st = matvec_dd(types[6], wd, g, y, hidden, n_ff))) goto done;
   for (size_t i = 0; i < hidden; i++) x[i] += y[i];
 done:
   free(xn);
@@ -710,6 +714,18 @@ done:
   free(u);
   free(y);
   return st;
+}
+
+int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
+                               const uint8_t* wo, const float* attn_norm, const uint8_t* wg,
+                               const uint8_t* wu, const uint8_t* wd, const float* ffn_norm,
+                               size_t hidden, size_t n_heads, size_t n_kv, size_t d, size_t n_ff,
+                               double eps, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache,
+                               size_t pos, int store_new, double* x) {
+  const int types[7] = {type, type, type, type, type, type, type};
+  return orc_llama_layer_decode_types_f64(types, wq, wk, wv, wo, attn_norm, wg, wu, wd, ffn_norm, hidden,
+                                          n_heads, n_kv, d, n_ff, eps, inv_freq, k_cache, v_cache, pos,
+                                          store_new, x);
 }
 
 /* logits = W rms_norm(x, norm) with f64 x (the end of forward,

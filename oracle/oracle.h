@@ -125,6 +125,15 @@ int orc_llama_layer_decode_f64(int type, const uint8_t* wq, const uint8_t* wk, c
                                size_t pos, int store_new, double* x);
 int orc_output_head_f64(int type, const uint8_t* w, const float* norm, double eps, const double* x,
                         size_t hidden, size_t vocab, double* logits);
+/* The same layer with a block type per projection, types = {q, k, v, o, gate,
+ * up, down} (GGUF files such as Q4_K_M mix Q4_K and Q6_K tensors). */
+int orc_llama_layer_decode_types_f64(const int* types, const uint8_t* wq, const uint8_t* wk,
+                                     const uint8_t* wv, const uint8_t* wo, const float* attn_norm,
+                                     const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                                     const float* ffn_norm, size_t hidden, size_t n_heads, size_t n_kv,
+                                     size_t d, size_t n_ff, double eps, const float* inv_freq,
+                                     uint16_t* k_cache, uint16_t* v_cache, size_t pos, int store_new,
+                                     double* x);
 /* The same layer in the reference's own f32 evaluation order (x f32 in place). */
 int orc_llama_layer_decode_f32(int type, const uint8_t* wq, const uint8_t* wk, const uint8_t* wv,
                                const uint8_t* wo, const float* attn_norm, const uint8_t* wg,

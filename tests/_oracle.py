@@ -54,6 +54,9 @@ class Oracle:
             "orc_llama_layer_decode_f64": (C.c_int, [C.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
                                                      _sz, _sz, _sz, _sz, C.c_double, _p, _p, _p, _sz,
                                                      C.c_int, _p]),
+            "orc_llama_layer_decode_types_f64": (C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
+                                                           _sz, _sz, _sz, _sz, C.c_double, _p, _p, _p, _sz,
+                                                           C.c_int, _p]),
             "orc_output_head_f64": (C.c_int, [C.c_int, _p, _p, C.c_double, _p, _sz, _sz, _p]),
             "orc_llama_layer_decode_f32": (C.c_int, [C.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
                                                      _sz, _sz, _sz, _sz, C.c_float, _p, _p, _p, _sz,
@@ -123,13 +126,14 @@ class Oracle:
     def llama_layer_decode_f64(self, t, L, dims, inv_freq, k_cache, v_cache, pos, x, store_new=True):
         """One layer on x (f64, updated copy returned); L: dict of the layer's
         weights (uint8 blocks) and norms (f32); dims: hidden, n_heads, n_kv, d,
-        n_ff, eps."""
+        n_ff, eps; t: one block type, or seven (q, k, v, o, gate, up, down)."""
         hidden, n_heads, n_kv, d, n_ff, eps = dims
         xx = np.array(x, dtype=np.float64, copy=True)
         a = {k: np.ascontiguousarray(v) for k, v in L.items()}
         f = np.ascontiguousarray(inv_freq, dtype=np.float32)
-        st = self.lib.orc_llama_layer_decode_f64(
-            t, _ptr(a["wq"]), _ptr(a["wk"]), _ptr(a["wv"]), _ptr(a["wo"]), _ptr(a["attn_norm"]),
+        types = np.ascontiguousarray(np.broadcast_to(np.asarray(t, dtype=np.int32), (7,)))
+        st = self.lib.orc_llama_layer_decode_types_f64(
+            _ptr(types), _ptr(a["wq"]), _ptr(a["wk"]), _ptr(a["wv"]), _ptr(a["wo"]), _ptr(a["attn_norm"]),
             _ptr(a["w_gate"]), _ptr(a["w_up"]), _ptr(a["w_down"]), _ptr(a["ffn_norm"]), hidden, n_heads,
             n_kv, d, n_ff, eps, _ptr(f), _ptr(k_cache), _ptr(v_cache), pos, int(store_new), _ptr(xx))
         assert st == 0, st

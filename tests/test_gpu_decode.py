@@ -8,12 +8,12 @@ import pytest
 
 from tests._gpu import down, up
 from tests._oracle import max_abs, rel_l2
-from tests.test_oracle_decode import small_layer
+from tests.test_oracle_decode import MIXED, PROJ, mixed_layer, small_layer
 from woolly_amd import ops, synth
 from woolly_amd.device import DeviceBuffer
 
 pytestmark = pytest.mark.gpu
-Q4_0, Q4_1, Q8_0 = 2, 3, 8
+Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
 REL_L2 = 1e-4
 
 
@@ -206,3 +206,93 @@ def test_layer_llama3_8b_shape_ctx4096(gpu, orc):
     # input if that is larger (the output is cancellation-limited: sum |w h| of
     # the down projection is ~10x the result)
     check(got, ref, "layer 8B ctx4096", abs_bar=max(1e-3, ref32_err))
+
+
+# K-quant models: every matrix Q4_K, every matrix Q6_K, or the per-tensor mix of
+# a Q4_K_M file (attn_v and ffn_down Q6_K); the model's type is Q4_K and the
+# layers name their own types where they differ
+KQ_MODELS = {"q4_k": {n: Q4_K for n in PROJ}, "q6_k": {n: Q6_K for n in PROJ}, "q4_k_m": MIXED}
+
+
+def kq_model(types, dims, ctx, vocab, inv, n_layers, head, onorm, rng, seed):
+    hidden, n_heads, n_kv, d, n_ff, _ = dims
+    Ls, devs, caches = [], [], []
+    for i in range(n_layers):
+        L = mixed_layer(types, hidden, n_heads, n_kv, d, n_ff, seed=seed + i)
+        dev, kc, vc = upload_layer(None, L, ctx, n_kv, d, rng)
+        for name in PROJ:
+            dev[name + "_type"] = types[name] if types[name] != Q4_K else 0   # 0: the model's type
+        Ls.append(L)
+        devs.append(dev)
+        caches.append((kc, vc))
+    model = ops.LlamaModel(Q4_K, dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff,
+                                      max_ctx=ctx, vocab=vocab, eps=1e-5),
+                           devs, up(inv)[0], up(onorm)[0] if onorm is not None else None,
+                           up(head)[0] if head is not None else None, Q6_K)
+    return model, Ls, devs, caches
+
+
+@pytest.mark.parametrize("kind", list(KQ_MODELS))
+def test_kquant_model_steps(gpu, orc, kind):
+    """Two K-quant layers and a Q6_K head, three steps on ~N(0,1) caches,
+    against the f64 oracle with each tensor's own type."""
+    types = KQ_MODELS[kind]
+    tl = [types[n] for n in PROJ]
+    hidden, n_heads, n_kv, d, n_ff, vocab, ctx = 512, 4, 2, 128, 768, 300, 8
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    rng = np.random.default_rng(1)
+    inv = orc.rope_inv_freq(500000.0, d)
+    head = synth.quantized_weight(Q6_K, vocab, hidden, seed=40)
+    onorm = np.linspace(0.8, 1.2, hidden).astype(np.float32)
+    model, Ls, devs, caches = kq_model(types, dims, ctx, vocab, inv, 2, head, onorm, rng, seed=50)
+    ws = DeviceBuffer(model.workspace_bytes())
+    xb, lb = DeviceBuffer(4 * hidden), DeviceBuffer(4 * vocab)
+    for pos in range(3):
+        print(f"[case] kquant model {kind} pos={pos}", flush=True)
+        x0 = synth.activations(hidden, seed=200 + pos)
+        xb.upload(x0)
+        model.decode_step(pos, xb, lb, ws, model.workspace_bytes())
+        got_x = down(xb, np.float32, hidden)
+        got_l = down(lb, np.float32, vocab)
+        gcache = [(down(dv["k_cache"], np.uint16, kc.size).reshape(kc.shape),
+                   down(dv["v_cache"], np.uint16, vc.size).reshape(vc.shape)) for dv, (kc, vc) in zip(devs, caches)]
+        x = x0.astype(np.float64)
+        for li, (L, (kc, vc), (kg, vg)) in enumerate(zip(Ls, caches, gcache)):
+            x = orc.llama_layer_decode_f64(tl, L, dims, inv, kc, vc, pos, x)
+            slack = 0.0 if li == 0 else 1e-4
+            assert f16_ulp_close(kg[pos], kc[pos], slack) and f16_ulp_close(vg[pos], vc[pos], slack), (pos, li)
+        x = x0.astype(np.float64)
+        for L, (kg, vg) in zip(Ls, gcache):
+            x = orc.llama_layer_decode_f64(tl, L, dims, inv, kg.copy(), vg.copy(), pos, x, store_new=False)
+        logits = orc.output_head_f64(Q6_K, head, onorm, 1e-5, x, hidden, vocab)
+        check(got_x, x, f"kquant {kind} pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
+        check(got_l, logits, f"kquant {kind} pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+        for (kc, vc), (kg, vg) in zip(caches, gcache):
+            kc[:] = kg
+            vc[:] = vg
+
+
+def test_kquant_m_layer_llama3_8b_shape(gpu, orc):
+    """One Llama-3-8B-shaped layer with Q4_K_M's per-tensor types at position
+    1000: the matrix-core GEMVs on K-quants with RMSNorm, residual and the
+    fused gate/up + SwiGLU, q / k / v as separate GEMVs (v is Q6_K)."""
+    hidden, n_heads, n_kv, d, n_ff, ctx, pos = 4096, 32, 8, 128, 14336, 1024, 1000
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    rng = np.random.default_rng(8)
+    inv = orc.rope_inv_freq(500000.0, d)
+    model, Ls, devs, caches = kq_model(MIXED, dims, ctx, 0, inv, 1, None, None, rng, seed=60)
+    ws = DeviceBuffer(model.workspace_bytes())
+    x0 = synth.activations(hidden, seed=9)
+    xb = up(x0)[0]
+    model.layer_decode(0, pos, xb, ws, model.workspace_bytes())
+    got = down(xb, np.float32, hidden)
+    kc, vc = caches[0]
+    kg = down(devs[0]["k_cache"], np.uint16, kc.size).reshape(kc.shape)
+    vg = down(devs[0]["v_cache"], np.uint16, vc.size).reshape(vc.shape)
+    tl = [MIXED[n] for n in PROJ]
+    kr, vr = kc.copy(), vc.copy()
+    orc.llama_layer_decode_f64(tl, Ls[0], dims, inv, kr, vr, pos, x0.astype(np.float64))
+    assert f16_ulp_close(kg[pos], kr[pos]) and f16_ulp_close(vg[pos], vr[pos])
+    ref = orc.llama_layer_decode_f64(tl, Ls[0], dims, inv, kg.copy(), vg.copy(), pos, x0.astype(np.float64),
+                                     store_new=False)
+    check(got, ref, "kquant q4_k_m layer 8B", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(ref))))

@@ -12,9 +12,10 @@ import numpy as np
 import pytest
 
 from tests.test_oracle import np_dequant
+from tests.test_oracle_kquant import np_q4_k, np_q6_k
 from woolly_amd import synth
 
-Q4_0, Q4_1, Q8_0 = 2, 3, 8
+Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
 
 
 def np_rope(x: np.ndarray, pos: int, inv_freq: np.ndarray) -> np.ndarray:
@@ -140,9 +141,22 @@ def small_layer(t, hidden, n_heads, n_kv, d, n_ff, seed):
     }
 
 
+PROJ = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+
+
+def np_dequant_any(t, blocks, n):
+    if t == Q4_K:
+        return np_q4_k(blocks)[:n]
+    if t == Q6_K:
+        return np_q6_k(blocks)[:n]
+    return np_dequant(t, blocks, n)
+
+
 def np_layer(t, L, dims, inv, kc, vc, pos, x):
+    """t: one block type, or a dict of types per projection."""
     hidden, n_heads, n_kv, d, n_ff, eps = dims
-    dq = lambda name, n, k: np_dequant(t, L[name], n * k).astype(np.float64).reshape(n, k)
+    ty = t if isinstance(t, dict) else {name: t for name in PROJ}
+    dq = lambda name, n, k: np_dequant_any(ty[name], L[name], n * k).astype(np.float64).reshape(n, k)
     xn = np_rms(x, L["attn_norm"], eps)
     qkv = np.concatenate([dq("wq", n_heads * d, hidden) @ xn, dq("wk", n_kv * d, hidden) @ xn,
                           dq("wv", n_kv * d, hidden) @ xn])
@@ -169,6 +183,44 @@ def test_layer_matches_numpy(orc, t):
     got = orc.llama_layer_decode_f64(t, L, dims, inv, kb, vb, pos, x)
     assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-12
     assert np.array_equal(kb[pos], krow.view(np.uint16))
+
+
+# the tensor types of a Q4_K_M file: attn_v and ffn_down in Q6_K, the rest Q4_K
+MIXED = {"wq": Q4_K, "wk": Q4_K, "wv": Q6_K, "wo": Q4_K, "w_gate": Q4_K, "w_up": Q4_K, "w_down": Q6_K}
+
+
+def mixed_layer(types, hidden, n_heads, n_kv, d, n_ff, seed):
+    shapes = {"wq": (n_heads * d, hidden), "wk": (n_kv * d, hidden), "wv": (n_kv * d, hidden),
+              "wo": (hidden, n_heads * d), "w_gate": (n_ff, hidden), "w_up": (n_ff, hidden),
+              "w_down": (hidden, n_ff)}
+    rng = np.random.default_rng(seed)
+    L = {name: synth.quantized_weight(types[name], *shapes[name], seed=seed * 10 + i)
+         for i, name in enumerate(PROJ)}
+    L["attn_norm"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    L["ffn_norm"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    return L
+
+
+def test_layer_mixed_types_matches_numpy(orc):
+    """A block type per projection (orc_llama_layer_decode_types_f64) against
+    the numpy layer over each tensor's own dequantization."""
+    hidden, n_heads, n_kv, d, n_ff, pos = 512, 4, 2, 128, 768, 5
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    L = mixed_layer(MIXED, hidden, n_heads, n_kv, d, n_ff, seed=9)
+    inv = orc.rope_inv_freq(500000.0, d)
+    rng = np.random.default_rng(10)
+    kc, vc = rand_cache(rng, 8, n_kv, d)
+    x = rng.standard_normal(hidden)
+    ref, krow, vrow = np_layer(MIXED, L, dims, inv, kc, vc, pos, x)
+    kb, vb = kc.view(np.uint16).copy(), vc.view(np.uint16).copy()
+    got = orc.llama_layer_decode_f64([MIXED[n] for n in PROJ], L, dims, inv, kb, vb, pos, x)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-12
+    assert np.array_equal(vb[pos], vrow.view(np.uint16))
+    # each projection is read with its own type: v's Q6_K bytes read as Q4_K differ
+    wrong = dict(MIXED, wv=Q4_K)
+    bad = orc.llama_layer_decode_f64([wrong[n] for n in PROJ], L, dims, inv, kc.view(np.uint16).copy(),
+                                     vc.view(np.uint16).copy(), pos, x)
+    assert not np.allclose(bad, ref, rtol=1e-3, atol=1e-3)
 
 
 def test_output_head_matches_numpy(orc):

@@ -95,7 +95,9 @@ class wh_gguf_tensor(C.Structure):
 
 class wh_llama_layer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate",
-                                          "w_up", "w_down", "k_cache", "v_cache")]
+                                          "w_up", "w_down", "k_cache", "v_cache")] + \
+               [(n, C.c_int) for n in ("wq_type", "wk_type", "wv_type", "wo_type", "w_gate_type",
+                                       "w_up_type", "w_down_type")]
 
 
 class wh_llama_model(C.Structure):

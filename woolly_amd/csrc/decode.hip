@@ -23,12 +23,28 @@ hipStream_t hs(wh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 
-int check_type(const char* fn, int type) {
-  if (!wh::is_block_type(type))
+// A matrix of `type` with rows of k elements: the 32-element formats, or the
+// K-quants with k a multiple of 256.
+int check_type(const char* fn, int type, size_t k) {
+  if (!wh::is_block_type(type) && !wh::is_kquant(type))
     return wh::set_error(WH_ERR_UNSUPPORTED_TYPE,
-                         "%s: unsupported quantization scheme (ggml type %d); supported: Q4_0 (2), Q4_1 (3), Q8_0 (8)",
+                         "%s: unsupported quantization scheme (ggml type %d); supported: Q4_0 (2), Q4_1 (3), "
+                         "Q8_0 (8), Q4_K (12), Q6_K (14)",
                          fn, type);
+  const size_t be = wh::block_elems(type);
+  if (k % be != 0)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: k = %zu is not a multiple of the block size %zu", fn, k, be);
   return WH_OK;
+}
+
+// The block types of a layer's matrices, q k v o gate up down (0: the model's type).
+struct LayerTypes {
+  int q, k, v, o, g, u, d;
+};
+LayerTypes layer_types(const wh_llama_model* m, const wh_llama_layer& L) {
+  auto t = [&](int v) { return v ? v : m->type; };
+  return {t(L.wq_type), t(L.wk_type), t(L.wv_type), t(L.wo_type), t(L.w_gate_type), t(L.w_up_type),
+          t(L.w_down_type)};
 }
 
 // Fused GEMV with the RMSNorm done separately when the fused kernel does not
@@ -79,8 +95,6 @@ StepWs step_layout(const wh_llama_model* m, void* base) {
 int check_model(const char* fn, const wh_llama_model* m) {
   if (!m || !m->layers || !m->rope_inv_freq)
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: null model, layers or rope_inv_freq", fn);
-  int st = check_type(fn, m->type);
-  if (st) return st;
   if (m->hidden == 0 || m->hidden % 32 != 0 || m->n_ff % 32 != 0 || (m->n_heads * m->head_dim) % 32 != 0)
     return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: hidden, n_ff and n_heads * head_dim must be multiples of 32",
                          fn);
@@ -95,6 +109,14 @@ int check_model(const char* fn, const wh_llama_model* m) {
     if (!L.k_cache || !L.v_cache || !wh::aligned(L.k_cache, 16) || !wh::aligned(L.v_cache, 16))
       return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: layer %zu KV caches must be non-null and 16-byte aligned",
                            fn, l);
+    const LayerTypes t = layer_types(m, L);
+    const size_t qd = m->n_heads * m->head_dim;
+    const int types[7] = {t.q, t.k, t.v, t.o, t.g, t.u, t.d};
+    const size_t ks[7] = {m->hidden, m->hidden, m->hidden, qd, m->hidden, m->hidden, m->n_ff};
+    for (int i = 0; i < 7; i++) {
+      const int st = check_type(fn, types[i], ks[i]);
+      if (st) return st;
+    }
   }
   return WH_OK;
 }
@@ -102,10 +124,24 @@ int check_model(const char* fn, const wh_llama_model* m) {
 int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, float* x, const StepWs& w,
                hipStream_t s) {
   const size_t D = m->head_dim, qd = m->n_heads * D, kvd = m->n_kv_heads * D;
-  // 1. qkv
-  const void* mats[3] = {L.wq, L.wk, L.wv};
-  const size_t rows[3] = {qd, kvd, kvd};
-  int st = gemv_fused_or_split(m->type, mats, rows, 3, x, L.attn_norm, m->eps, nullptr, w.qkv, m->hidden, w.xn, s);
+  const LayerTypes t = layer_types(m, L);
+  // 1. qkv: one stacked GEMV when q, k and v share a type, else the RMSNorm
+  // once and a GEMV per matrix
+  int st;
+  if (t.q == t.k && t.q == t.v) {
+    const void* mats[3] = {L.wq, L.wk, L.wv};
+    const size_t rows[3] = {qd, kvd, kvd};
+    st = gemv_fused_or_split(t.q, mats, rows, 3, x, L.attn_norm, m->eps, nullptr, w.qkv, m->hidden, w.xn, s);
+  } else {
+    st = wh::launch_rms_norm(x, L.attn_norm, m->eps, 1, m->hidden, w.xn, s);
+    const void* mq[1] = {L.wq};
+    const void* mk[1] = {L.wk};
+    const void* mv[1] = {L.wv};
+    const size_t rq[1] = {qd}, rk[1] = {kvd};
+    if (!st) st = wh::launch_gemv_fused(t.q, mq, rq, 1, w.xn, nullptr, 0.f, nullptr, w.qkv, m->hidden, s);
+    if (!st) st = wh::launch_gemv_fused(t.k, mk, rk, 1, w.xn, nullptr, 0.f, nullptr, w.qkv + qd, m->hidden, s);
+    if (!st) st = wh::launch_gemv_fused(t.v, mv, rk, 1, w.xn, nullptr, 0.f, nullptr, w.qkv + qd + kvd, m->hidden, s);
+  }
   if (st) return st;
   // 2-3. attention
   st = wh::launch_attention_decode(w.qkv, L.k_cache, L.v_cache, pos, m->n_heads, m->n_kv_heads, D,
@@ -114,21 +150,22 @@ int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, flo
   // 4. x += Wo attn
   const void* wo[1] = {L.wo};
   const size_t hr[1] = {m->hidden};
-  st = wh::launch_gemv_fused(m->type, wo, hr, 1, w.attn, nullptr, 0.f, x, x, qd, s);
+  st = wh::launch_gemv_fused(t.o, wo, hr, 1, w.attn, nullptr, 0.f, x, x, qd, s);
   if (st) return st;
   // 5. h = silu(gate) * up of rms_norm(x)
-  st = wh::launch_ffn_gate_up(m->type, L.w_gate, L.w_up, x, L.ffn_norm, m->eps, w.h, m->n_ff, m->hidden, s);
+  st = t.g == t.u ? wh::launch_ffn_gate_up(t.g, L.w_gate, L.w_up, x, L.ffn_norm, m->eps, w.h, m->n_ff, m->hidden, s)
+                  : WH_ERR_INVALID_SHAPE;
   if (st == WH_ERR_INVALID_SHAPE) {
     // unfused: rms_norm -> gate, up -> swiglu
     st = wh::launch_rms_norm(x, L.ffn_norm, m->eps, 1, m->hidden, w.xn, s);
-    if (!st) st = wh::launch_gemv(m->type, L.w_gate, w.xn, w.h, m->n_ff, m->hidden, s);
-    if (!st) st = wh::launch_gemv(m->type, L.w_up, w.xn, w.u, m->n_ff, m->hidden, s);
+    if (!st) st = wh::launch_gemv(t.g, L.w_gate, w.xn, w.h, m->n_ff, m->hidden, s);
+    if (!st) st = wh::launch_gemv(t.u, L.w_up, w.xn, w.u, m->n_ff, m->hidden, s);
     if (!st) st = wh::launch_swiglu(w.h, w.u, m->n_ff, w.h, s);
   }
   if (st) return st;
   // 6. x += Wd h
   const void* wd[1] = {L.w_down};
-  return wh::launch_gemv_fused(m->type, wd, hr, 1, w.h, nullptr, 0.f, x, x, m->n_ff, s);
+  return wh::launch_gemv_fused(t.d, wd, hr, 1, w.h, nullptr, 0.f, x, x, m->n_ff, s);
 }
 
 }  // namespace
@@ -150,10 +187,8 @@ WH_API size_t wh_attention_qkv_workspace_bytes(size_t hidden) { return 4 * hidde
 WH_API int wh_attention_qkv(int type, const void* wq, const void* wk, const void* wv, size_t q_rows,
                             size_t kv_rows, size_t hidden, const float* gamma, float eps, const float* x,
                             float* qkv, void* workspace, size_t workspace_bytes, wh_stream_t stream) {
-  int st = check_type("attention_qkv", type);
+  int st = check_type("attention_qkv", type, hidden);
   if (st) return st;
-  if (hidden % 32 != 0)
-    return wh::set_error(WH_ERR_INVALID_SHAPE, "attention_qkv: hidden = %zu is not a multiple of 32", hidden);
   if (!wq || !wk || !wv || !gamma || !x || !qkv)
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "attention_qkv: null pointer");
   if (q_rows + 2 * kv_rows == 0) return WH_OK;
@@ -190,11 +225,9 @@ WH_API int wh_attention_decode(const float* qkv, void* k_cache, void* v_cache, s
 WH_API int wh_quantized_matvec_residual(int type, const void* weights, size_t weight_nbytes, const float* input,
                                         const float* residual, float* output, size_t m, size_t k,
                                         wh_stream_t stream) {
-  int st = check_type("quantized_matvec_residual", type);
+  int st = check_type("quantized_matvec_residual", type, k);
   if (st) return st;
-  if (k % 32 != 0)
-    return wh::set_error(WH_ERR_INVALID_SHAPE, "quantized_matvec_residual: k = %zu is not a multiple of 32", k);
-  const size_t need = m * (k / 32) * wh::type_size(type);
+  const size_t need = m * (k / wh::block_elems(type)) * wh::type_size(type);
   if (weight_nbytes < need)
     return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
                          "quantized_matvec_residual: buffer too small: needed %zu bytes, available %zu", need,
@@ -250,7 +283,7 @@ WH_API int wh_llama_decode_step(const wh_llama_model* model, size_t pos, float* 
     if (st) return st;
   }
   if (!logits) return WH_OK;
-  st = check_type("llama_decode_step (output head)", model->output_type);
+  st = check_type("llama_decode_step (output head)", model->output_type, model->hidden);
   if (st) return st;
   if (!model->output || !model->output_norm)
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_decode_step: null output head or output_norm");

@@ -885,6 +885,17 @@ int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int
     const int st = launch_gemv_mfma(type, mats, rows, n_mats, false, x, gamma, eps, residual, y, n, k, s);
     if (st != WH_ERR_INVALID_SHAPE) return st;
   }
+  if (is_kquant(type)) {
+    // the dequantize-then-dot kernel per matrix (the caller normalises x first)
+    if (gamma) return WH_ERR_INVALID_SHAPE;
+    size_t off = 0;
+    for (int i = 0; i < n_mats; i++) {
+      const int st = launch_gemv_kquant(type, mats[i], x, y + off, rows[i], k, s, residual ? residual + off : nullptr);
+      if (st) return st;
+      off += rows[i];
+    }
+    return WH_OK;
+  }
   // Without the normalisation the generic kernel takes every shape; with it,
   // the caller normalises x first when the streaming kernels do not apply.
   const int mode = (gamma ? kNorm : 0) | (residual ? kResid : 0) | (n_mats > 1 ? kStack : 0);

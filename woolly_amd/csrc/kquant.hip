@@ -98,11 +98,12 @@ __global__ __launch_bounds__(256) void kq_dequant_kernel(const uint8_t* __restri
   }
 }
 
-// y[row] = sum_k dequant(W)[row, k] * x[k]: one wave per row (grid-stride),
-// lane l takes quad l (elements 4l..4l+3) of every block of the row.
+// y[row] = sum_k dequant(W)[row, k] * x[k] (+ residual[row]): one wave per row
+// (grid-stride), lane l takes quad l (elements 4l..4l+3) of every block of the
+// row.  y may be the residual itself (each row is read, then written, by one lane).
 template <int TYPE>
 __global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                      float* __restrict__ y, size_t n_rows, size_t nb) {
+                                                      const float* residual, float* y, size_t n_rows, size_t nb) {
   const int lane = threadIdx.x & 63;
   const size_t waves = static_cast<size_t>(gridDim.x) * (blockDim.x >> 6);
   for (size_t row = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6); row < n_rows;
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict_
       for (int t = 0; t < 4; t++) acc = __builtin_fmaf(v[t], xb[t], acc);
     }
     acc = whd::wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    if (lane == 0) y[row] = residual ? residual[row] + acc : acc;
   }
 }
 
@@ -229,12 +230,13 @@ int launch_dequantize_kquant(int type, const void* data, size_t n, float* out, h
   return WH_OK;
 }
 
-int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k, hipStream_t s) {
+int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k, hipStream_t s,
+                       const float* residual) {
   if (n_rows == 0) return WH_OK;
   const uint8_t* p = static_cast<const uint8_t*>(w);
   const unsigned grid = kq_grid(n_rows, 4);
-  if (type == WH_TYPE_Q4_K) kq_gemv_kernel<WH_TYPE_Q4_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
-  else kq_gemv_kernel<WH_TYPE_Q6_K><<<grid, 256, 0, s>>>(p, x, y, n_rows, k / 256);
+  if (type == WH_TYPE_Q4_K) kq_gemv_kernel<WH_TYPE_Q4_K><<<grid, 256, 0, s>>>(p, x, residual, y, n_rows, k / 256);
+  else kq_gemv_kernel<WH_TYPE_Q6_K><<<grid, 256, 0, s>>>(p, x, residual, y, n_rows, k / 256);
   WH_LAUNCH_CHECK("gemv (k-quant) kernel launch");
   return WH_OK;
 }

@@ -88,10 +88,11 @@ size_t max_lds_per_block();
 // validated by the C ABI layer; these only choose kernels and launch them.
 int launch_dequantize(int type, const void* data, size_t nelements, float* out,
                       hipStream_t stream);
-// Q4_K / Q6_K (kquant.hip): bit-exact dequantization and dequantize-then-dot GEMV.
+// Q4_K / Q6_K (kquant.hip): bit-exact dequantization and dequantize-then-dot GEMV
+// (y = residual + W x when residual is not null; y may be the residual).
 int launch_dequantize_kquant(int type, const void* data, size_t nelements, float* out, hipStream_t stream);
 int launch_gemv_kquant(int type, const void* w, const float* x, float* y, size_t n_rows, size_t k,
-                       hipStream_t stream);
+                       hipStream_t stream, const float* residual = nullptr);
 int launch_fill_bytes(void* dst, int value, size_t nbytes, hipStream_t stream);
 int launch_gemv(int type, const void* w, const float* x, float* y, size_t n_rows,
                 size_t k, hipStream_t stream);

@@ -191,7 +191,8 @@ def quantized_matvec_residual(ggml_type: int, weights, weight_nbytes: int, x, re
 class LlamaModel:
     """A Llama-shaped model on the device for the decode step: `layers` is a
     list of dicts of device buffers (attn_norm, wq, wk, wv, wo, ffn_norm,
-    w_gate, w_up, w_down, k_cache, v_cache); wraps wh_llama_model."""
+    w_gate, w_up, w_down, k_cache, v_cache) and optionally a block type per
+    matrix (wq_type .. w_down_type; absent or 0: ggml_type); wraps wh_llama_model."""
 
     def __init__(self, ggml_type: int, dims: dict, layers: list, inv_freq_dev, output_norm=None,
                  output=None, output_type: int = GGML_Q8_0) -> None:
@@ -199,7 +200,10 @@ class LlamaModel:
         arr = (_lib.wh_llama_layer * len(layers))()
         for i, L in enumerate(layers):
             for name, _ in _lib.wh_llama_layer._fields_:
-                setattr(arr[i], name, _p(L[name]) or None)
+                if name.endswith("_type"):
+                    setattr(arr[i], name, int(L.get(name, 0)))
+                else:
+                    setattr(arr[i], name, _p(L[name]) or None)
         self._layers = arr
         m = _lib.wh_llama_model()
         m.type = ggml_type
