@@ -190,30 +190,44 @@ L8B = dict(hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, n_ff=14336, voca
            n_layers=32, ctx=4096, rope_base=500000.0, eps=1e-5)
 
 
-def decode_bytes(c: dict = L8B) -> int:
+# per-matrix block types of a Q4_K_M file (attn_v and ffn_down in Q6_K, the
+# other projections in Q4_K; its output head is Q6_K)
+Q4_K_M = {"wq": 12, "wk": 12, "wv": 14, "wo": 12, "w_gate": 12, "w_up": 12, "w_down": 14}
+
+
+def decode_shapes(c: dict) -> dict:
+    h, nh, nkv, d, f = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["n_ff"]
+    return {"wq": (nh * d, h), "wk": (nkv * d, h), "wv": (nkv * d, h), "wo": (h, nh * d),
+            "w_gate": (f, h), "w_up": (f, h), "w_down": (h, f)}
+
+
+def decode_bytes(c: dict = L8B, types: dict | None = None, head_type: int = 8) -> int:
     """Algorithmic HBM bytes of one decode step at context c['ctx']: every
     weight once, the whole KV cache of every layer once, norms, x and logits."""
-    h, q, kv, f = c["hidden"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"], c["n_ff"]
-    per_layer = (2 * q * h + 2 * kv * h + 3 * f * h) // 32 * 18 + 2 * 4 * h
+    h, kv = c["hidden"], c["n_kv_heads"] * c["head_dim"]
+    types = types or {k: Q4_0 for k in decode_shapes(c)}
+    per_layer = sum(gemv_bytes(n, k, types[name]) - 4 * (n + k) for name, (n, k) in decode_shapes(c).items())
+    per_layer += 2 * 4 * h
     kv_read = c["n_layers"] * 2 * c["ctx"] * kv * 2
-    head = c["vocab"] * h // 32 * 34 + 4 * h
+    head = gemv_bytes(c["vocab"], h, head_type) - 4 * c["vocab"]
     return c["n_layers"] * per_layer + kv_read + head + 4 * h + 4 * c["vocab"]
 
 
-def bench_decode(steps: int, c: dict = L8B) -> dict:
-    """One decode step of a random-init 32-layer Llama-3-8B-shaped Q4_0 model
-    with a Q8_0 output head, f16 KV cache filled ~N(0,1), at position
-    ctx - 1 (attention over ctx positions).  The step (all layers + head) is
-    captured once into a HIP graph and replayed; returns timings."""
+def bench_decode(steps: int, c: dict = L8B, types: dict | None = None, head_type: int = 8) -> dict:
+    """One decode step of a random-init 32-layer Llama-3-8B-shaped model (Q4_0
+    matrices and a Q8_0 output head unless types / head_type say otherwise),
+    f16 KV cache filled ~N(0,1), at position ctx - 1 (attention over ctx
+    positions).  The step (all layers + head) is captured once into a HIP graph
+    and replayed; returns timings."""
     from woolly_amd import ops, synth
     from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
 
     h, nh, nkv, d, f = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["n_ff"]
     rng = np.random.default_rng(6)
+    mats = decode_shapes(c)
+    types = types or {k: Q4_0 for k in mats}
     # one layer's weights, uploaded to every layer's own buffers
-    mats = {"wq": (nh * d, h), "wk": (nkv * d, h), "wv": (nkv * d, h), "wo": (h, nh * d),
-            "w_gate": (f, h), "w_up": (f, h), "w_down": (h, f)}
-    host = {k: synth.quantized_weight(Q4_0, n, kk, seed=60 + i) for i, (k, (n, kk)) in enumerate(mats.items())}
+    host = {k: synth.quantized_weight(types[k], n, kk, seed=60 + i) for i, (k, (n, kk)) in enumerate(mats.items())}
     kc = rng.standard_normal((c["ctx"], nkv, d)).astype(np.float16)
     vc = rng.standard_normal((c["ctx"], nkv, d)).astype(np.float16)
     layers = []
@@ -223,17 +237,19 @@ def bench_decode(steps: int, c: dict = L8B) -> dict:
         L["ffn_norm"] = DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
         L["k_cache"] = DeviceBuffer.from_array(kc)
         L["v_cache"] = DeviceBuffer.from_array(vc)
+        for k in mats:
+            L[k + "_type"] = types[k]
         layers.append(L)
-    # Q8_0 head: 1/8 of the rows generated, tiled into the full matrix
-    part = synth.quantized_weight(8, c["vocab"] // 8, h, seed=70)
+    # head: 1/8 of the rows generated, tiled into the full matrix
+    part = synth.quantized_weight(head_type, c["vocab"] // 8, h, seed=70)
     head = DeviceBuffer(part.nbytes * 8)
     for i in range(8):
         head.upload(part, offset=i * part.nbytes)
     onorm = DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
     inv = DeviceBuffer.from_array(ops.rope_inv_freq(c["rope_base"], d))
-    model = ops.LlamaModel(Q4_0, dict(hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=d, n_ff=f,
-                                      max_ctx=c["ctx"], vocab=c["vocab"], eps=c["eps"]),
-                           layers, inv, onorm, head, 8)
+    model = ops.LlamaModel(types["wq"], dict(hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=d, n_ff=f,
+                                             max_ctx=c["ctx"], vocab=c["vocab"], eps=c["eps"]),
+                           layers, inv, onorm, head, head_type)
     wsz = model.workspace_bytes()
     ws = DeviceBuffer(wsz)
     x0 = synth.activations(h, seed=6)
@@ -256,7 +272,7 @@ def bench_decode(steps: int, c: dict = L8B) -> dict:
     ms = e0.elapsed_ms(e1) / steps
     graph.destroy()
     logits = lb.download(np.float32, c["vocab"])
-    nb = decode_bytes(c)
+    nb = decode_bytes(c, types, head_type)
     return {"tokens_per_s": round(1000.0 / ms, 1), "ms_per_token": round(ms, 4), "bytes_per_token": nb,
             "GBps": round(nb / (ms * 1e-3) / 1e9, 1), "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "ctx": c["ctx"], "layers": c["n_layers"], "logits_finite": bool(np.all(np.isfinite(logits)))}
@@ -370,7 +386,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other decode GEMV configurations (4096x4096 Q4_0, Q8_0, Q4_1)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode step")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode"], default=None,
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode", "decode_q4_k_m"], default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
     ap.add_argument("--type", type=int, default=Q4_0,
@@ -405,6 +421,9 @@ def main() -> int:
         return 0
     if args.only == "decode":
         print(json.dumps({"decode_step": bench_decode(10)}))
+        return 0
+    if args.only == "decode_q4_k_m":
+        print(json.dumps({"decode_step_q4_k_m": bench_decode(10, types=Q4_K_M, head_type=14)}))
         return 0
     if args.only in ("ffn1", "ffn512"):
         m = 1 if args.only == "ffn1" else 512
@@ -474,11 +493,14 @@ def main() -> int:
                               "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t)}
             log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
 
-    decode = None
+    decode = decode_km = None
     if not args.no_decode:
         decode = bench_decode(20)
         log(f"[bench] decode step (config 4, ctx {decode['ctx']}): {decode['ms_per_token']} ms/token, "
             f"{decode['tokens_per_s']} tokens/s, {decode['GBps']} GB/s")
+        decode_km = bench_decode(10, types=Q4_K_M, head_type=14)
+        log(f"[bench] decode step Q4_K_M types (ctx {decode_km['ctx']}): {decode_km['ms_per_token']} ms/token, "
+            f"{decode_km['tokens_per_s']} tokens/s, {decode_km['GBps']} GB/s")
 
     cpu, cpu_scalar = (None, None) if args.no_cpu else cpu_baselines()
     if cpu:
@@ -522,6 +544,7 @@ def main() -> int:
         "prefill_kquant_14336x4096": gemm_kq or None,
         "gemv_other_configs": gemv_cfg or None,
         "decode_step_llama3_8b_q4_0": decode,
+        "decode_step_llama3_8b_q4_k_m": decode_km,
         "cpu_baseline": cpu,
         "cpu_baseline_scalar": cpu_scalar,
     }

@@ -125,22 +125,23 @@ int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, flo
                hipStream_t s) {
   const size_t D = m->head_dim, qd = m->n_heads * D, kvd = m->n_kv_heads * D;
   const LayerTypes t = layer_types(m, L);
-  // 1. qkv: one stacked GEMV when q, k and v share a type, else the RMSNorm
-  // once and a GEMV per matrix
-  int st;
-  if (t.q == t.k && t.q == t.v) {
+  // 1. qkv: consecutive matrices of one type stacked into one GEMV with the
+  // RMSNorm fused (all three for a single-type model; q + k, then v, for
+  // Q4_K_M's Q6_K attn_v)
+  int st = WH_OK;
+  {
     const void* mats[3] = {L.wq, L.wk, L.wv};
     const size_t rows[3] = {qd, kvd, kvd};
-    st = gemv_fused_or_split(t.q, mats, rows, 3, x, L.attn_norm, m->eps, nullptr, w.qkv, m->hidden, w.xn, s);
-  } else {
-    st = wh::launch_rms_norm(x, L.attn_norm, m->eps, 1, m->hidden, w.xn, s);
-    const void* mq[1] = {L.wq};
-    const void* mk[1] = {L.wk};
-    const void* mv[1] = {L.wv};
-    const size_t rq[1] = {qd}, rk[1] = {kvd};
-    if (!st) st = wh::launch_gemv_fused(t.q, mq, rq, 1, w.xn, nullptr, 0.f, nullptr, w.qkv, m->hidden, s);
-    if (!st) st = wh::launch_gemv_fused(t.k, mk, rk, 1, w.xn, nullptr, 0.f, nullptr, w.qkv + qd, m->hidden, s);
-    if (!st) st = wh::launch_gemv_fused(t.v, mv, rk, 1, w.xn, nullptr, 0.f, nullptr, w.qkv + qd + kvd, m->hidden, s);
+    const int ty[3] = {t.q, t.k, t.v};
+    size_t off = 0;
+    for (int i = 0; i < 3 && !st;) {
+      int n = 1;
+      while (i + n < 3 && ty[i + n] == ty[i]) n++;
+      st = gemv_fused_or_split(ty[i], mats + i, rows + i, n, x, L.attn_norm, m->eps, nullptr, w.qkv + off, m->hidden,
+                               w.xn, s);
+      for (int j = 0; j < n; j++) off += rows[i + j];
+      i += n;
+    }
   }
   if (st) return st;
   // 2-3. attention
