@@ -176,8 +176,8 @@ KQ_MATMUL = [(3, 300, 4096), (8, 1024, 2048), (17, 768, 256), (64, 129, 4096), (
              (257, 384, 1024), (512, 256, 14336)]
 
 
-def kq_matmul(t, w, x, m, n, k):
-    wb, wp = up(w)
+def kq_matmul(t, w, x, m, n, k, w_offset=0):
+    wb, wp = up(w, offset=w_offset)
     xb, xp = up(x)
     yb = DeviceBuffer(4 * m * n)
     wsz = ops.matmul_workspace_bytes(t, n, k, m)
@@ -231,3 +231,16 @@ def test_kquant_ffn_parity(gpu, orc, t, hidden, n_ff, m):
     rms = float(np.sqrt(np.mean(ref ** 2)))
     print(f"[result] kquant ffn rel_l2={r:.3e} max_abs={a:.3e} rms={rms:.3e}", flush=True)
     assert r <= 1e-4 and a <= 1e-3 * max(1.0, rms / 300.0)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_kquant_matmul_unaligned_weights(gpu, orc, t):
+    """Weights 4 bytes past a 16-byte boundary cannot be repacked with 16-byte
+    loads: the call takes one GEMV per token instead, same results."""
+    m, n, k = 6, 256, 2048
+    w = synth.quantized_weight(t, n, k, seed=91 + t)
+    x = synth.activations(m * k, seed=92).reshape(m, k)
+    got = kq_matmul(t, w, x, m, n, k, w_offset=4)
+    ref = orc.matmul_rows_f64(t, w, n, k, x, m, np.arange(m))
+    assert rel_l2(got, ref) <= 1e-4 and max_abs(got, ref) <= 1e-3
+    assert rel_l2(got, kq_matmul(t, w, x, m, n, k)) <= 1e-5

@@ -89,9 +89,10 @@ constexpr bool q8_like() { return TYPE == WH_TYPE_Q8_0 || TYPE == wh::kGemmQ8H; 
 // f32 block scale (else f16)
 template <int TYPE>
 constexpr bool f32_scale() { return TYPE == wh::kGemmQ4F || TYPE == wh::kGemmQ8H; }
-// block sums of the activations are written by the packing (kGemmQ4F: for the
-// dmin pass after the GEMM)
+// block sums of the activations are written by the packing ([T][b][bm]; for
+// kGemmQ4F per 256-element super-block, [T][sb][bm], for its dmin term)
 inline bool needs_bsum(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
+inline size_t bsum_groups(int type, size_t k) { return type == wh::kGemmQ4F ? k / 256 : k / 32; }
 // dwords per weight row per stage (SB whole blocks)
 template <int TYPE>
 constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
@@ -290,7 +291,16 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
         // the four k-groups of a block are adjacent lanes (p = 4b + g)
         part += __shfl_xor(part, 1, 64);
         part += __shfl_xor(part, 2, 64);
-        if (g == 0) bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
+        if (type == wh::kGemmQ4F) {
+          // per 256-element super-block: its 8 blocks are 32 adjacent lanes
+          // (p = 32 sb + ..; rows are whole super-blocks, so all 32 are live)
+          part += __shfl_xor(part, 4, 64);
+          part += __shfl_xor(part, 8, 64);
+          part += __shfl_xor(part, 16, 64);
+          if ((p & 31) == 0) bsum[(static_cast<size_t>(T) * (nb / 8) + (b >> 3)) * bm + (t % bm)] = part;
+        } else if (g == 0) {
+          bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
+        }
       }
     }
   }
@@ -426,8 +436,8 @@ __device__ __forceinline__ void wait_stages(int n) {
 template <int TYPE, int BM>
 __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint8_t* __restrict__ W, const _Float16* __restrict__ frag, const float* __restrict__ rscale,
-    const float* __restrict__ bsum, float* __restrict__ y, int n_tokens, int n_rows, int nb,
-    int blocks_per_split, int tiles_n, int n_tiles) {
+    const float* __restrict__ bsum, const float* __restrict__ dmin, float* __restrict__ y, int n_tokens,
+    int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles) {
   using C = TCfg<BM>;
   constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = nstage<TYPE, BM>();
   constexpr int A_STAGE = C::A_STAGE;
@@ -672,6 +682,26 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     for (int i = 0; i < IT; i++) scale_one(NT - 2 + h, (SB * (NT / 2) - 1) & 1, h, i);
   wait_vmcnt<0>();  // (no copies remain: every issued stage was consumed)
 
+  if constexpr (TYPE == wh::kGemmQ4F) {
+    // Q4_K's dmin: acc += dmin[sb][row] * S[sb][token] over this split's
+    // super-blocks (split bounds are multiples of 8 blocks), S the packing's
+    // super-block sums in the same scaled domain as acc
+    const int nsb = nb / 8;
+    for (int sb = kb0 / 8; sb < kb1 / 8; sb++) {
+      float dm[NT];
+#pragma unroll
+      for (int n = 0; n < NT; n++) dm[n] = dmin[static_cast<size_t>(sb) * n_rows + min(r0 + wn + 16 * n + ln, n_rows - 1)];
+#pragma unroll
+      for (int i = 0; i < IT; i++) {
+        const float4v sv = *reinterpret_cast<const float4v*>(bsum + (static_cast<size_t>(T) * nsb + sb) * BM + wm + 16 * i + 4 * g);
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][n][r] = __builtin_fmaf(dm[n], sv[r], acc[i][n][r]);
+      }
+    }
+  }
+
   // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
   float* out = y + static_cast<size_t>(blockIdx.y) * n_tokens * n_rows;
 #pragma unroll
@@ -700,85 +730,24 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* _
   }
 }
 
-// Q4_K's minimum: y[t, r] += sum over super-blocks sb of dmin[sb][r] * S[t, sb],
-// S the activations' sum over the super-block (rscale[t] times the packing's
-// eight block sums of hi + lo, the scaling the GEMM's epilogue undoes).  A
-// thread owns kDminRows rows (256 apart) for kDminTokens tokens; the tokens'
-// sums are staged in LDS as [sb][token] and read four tokens at a time.
-constexpr int kDminTokens = 16, kDminRows = 2;
-__global__ __launch_bounds__(256) void kq_dmin_kernel(float* __restrict__ y, const float* __restrict__ dmin_t,
-                                                      const float* __restrict__ bsum, const float* __restrict__ rscale,
-                                                      int n_tokens, int n_rows, int nb, int bm) {
-  extern __shared__ float4 ssum4[];  // [nsb][kDminTokens / 4]
-  float* ssum = reinterpret_cast<float*>(ssum4);
-  const int nsb = nb / 8;
-  const int t0 = blockIdx.y * kDminTokens;
-  for (int i = threadIdx.x; i < kDminTokens * nsb; i += blockDim.x) {
-    const int sb = i / kDminTokens, tt = i % kDminTokens, t = t0 + tt;
-    float v = 0.f;
-    if (t < n_tokens) {
-      const float* bs = bsum + (static_cast<size_t>(t / bm) * nb + 8 * sb) * bm + (t % bm);
-#pragma unroll
-      for (int j = 0; j < 8; j++) v += bs[static_cast<size_t>(j) * bm];
-      v *= rscale[t];
-    }
-    ssum[i] = v;
-  }
-  __syncthreads();
-  const int r0 = blockIdx.x * (kDminRows * 256) + threadIdx.x;
-  float acc[kDminRows][kDminTokens];
-#pragma unroll
-  for (int q = 0; q < kDminRows; q++)
-#pragma unroll
-    for (int tt = 0; tt < kDminTokens; tt++) acc[q][tt] = 0.f;
-  for (int sb = 0; sb < nsb; sb++) {
-    float dm[kDminRows];
-#pragma unroll
-    for (int q = 0; q < kDminRows; q++) {
-      const int r = r0 + 256 * q;
-      dm[q] = r < n_rows ? dmin_t[static_cast<size_t>(sb) * n_rows + r] : 0.f;
-    }
-#pragma unroll
-    for (int c = 0; c < kDminTokens / 4; c++) {
-      const float4 sv = ssum4[sb * (kDminTokens / 4) + c];
-#pragma unroll
-      for (int q = 0; q < kDminRows; q++) {
-        acc[q][4 * c + 0] = __builtin_fmaf(dm[q], sv.x, acc[q][4 * c + 0]);
-        acc[q][4 * c + 1] = __builtin_fmaf(dm[q], sv.y, acc[q][4 * c + 1]);
-        acc[q][4 * c + 2] = __builtin_fmaf(dm[q], sv.z, acc[q][4 * c + 2]);
-        acc[q][4 * c + 3] = __builtin_fmaf(dm[q], sv.w, acc[q][4 * c + 3]);
-      }
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < kDminRows; q++) {
-    const int r = r0 + 256 * q;
-    if (r >= n_rows) continue;
-#pragma unroll
-    for (int tt = 0; tt < kDminTokens; tt++) {
-      const int t = t0 + tt;
-      if (t < n_tokens) y[static_cast<size_t>(t) * n_rows + r] += acc[q][tt];
-    }
-  }
-}
-
 // Token-tile height for a token count: the smallest of 16, 32, 64, 128 that
 // holds it (one tile) or 128 beyond.
 int tile_bm(size_t n_tokens) { return n_tokens <= 16 ? 16 : (n_tokens <= 32 ? 32 : (n_tokens <= 64 ? 64 : 128)); }
 
 template <int TYPE, int BM>
 int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
-              const float* rs, const float* bs, float* part, int splits, hipStream_t s) {
+              const float* rs, const float* bs, const float* dmin, float* part, int splits, hipStream_t s) {
   const int nb = static_cast<int>(k / 32);
   const int tiles_n = static_cast<int>((n_rows + TBN - 1) / TBN);
   const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
   int bps = (nb + splits - 1) / splits;
-  bps = (bps + SB - 1) / SB * SB;
+  constexpr int ALIGN = TYPE == wh::kGemmQ4F ? 8 : SB;   // kGemmQ4F: whole super-blocks per split
+  bps = (bps + ALIGN - 1) / ALIGN * ALIGN;
   const size_t lds = tiled_lds_bytes<TYPE, BM>();
   WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
-  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, part, static_cast<int>(n_tokens),
+  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, dmin, part, static_cast<int>(n_tokens),
                                                            static_cast<int>(n_rows), nb, bps, tiles_n,
                                                            tiles_m * tiles_n);
   WH_LAUNCH_CHECK("tiled gemm kernel launch");
@@ -787,12 +756,12 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
 
 template <int TYPE>
 int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
-                 const float* rs, const float* bs, float* part, int splits, hipStream_t s) {
+                 const float* rs, const float* bs, const float* dmin, float* part, int splits, hipStream_t s) {
   switch (tile_bm(n_tokens)) {
-    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
-    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
-    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
-    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, part, splits, s);
+    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
+    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
+    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
+    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
   }
 }
 
@@ -863,7 +832,7 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;   // padded tokens
   size_t b = al256(tm * k * 4) + al256(tm * 4);
-  if (needs_bsum(type)) b += al256(tm * (k / 32) * 4);
+  if (needs_bsum(type)) b += al256(tm * bsum_groups(type, k) * 4);
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
   if (splits > 1) b += al256(static_cast<size_t>(splits) * n_rows * n_tokens * 4);
   return b;
@@ -891,7 +860,7 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
   ws += al256(t.tm * 4);
   if (needs_bsum(type)) {
     t.bs = reinterpret_cast<float*>(ws);
-    ws += al256(t.tm * (k / 32) * 4);
+    ws += al256(t.tm * bsum_groups(type, k) * 4);
   }
   t.splits = gemm_tiled_splits(n_rows, n_tokens, k);
   t.part = t.splits > 1 ? reinterpret_cast<float*>(ws) : nullptr;
@@ -914,16 +883,16 @@ static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x
 
 // The GEMM over packed activations (and the split-K reduce) into y.
 static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t, float* y,
-                     hipStream_t s) {
+                     hipStream_t s, const float* dmin = nullptr) {
   const uint8_t* wp = static_cast<const uint8_t*>(w);
   float* part = t.splits > 1 ? t.part : y;
   int st;
   switch (type) {
-    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
-    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
-    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
-    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
-    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, part, t.splits, s); break;
+    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
+    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
+    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
+    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
+    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
     default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
   }
   if (st != WH_OK) return st;
@@ -957,23 +926,13 @@ bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size
   return gemm_tiled_ok(kquant_gemm_type(type), repacked, x, n_rows, kquant_gemm_k(type, k), n_tokens);
 }
 
-// GEMM on a repacked K-quant matrix rp (n_rows x kk in its GEMM format) over
-// packed activations t, then for Q4_K the dmin pass (k: the row length).
+// GEMM on a repacked K-quant matrix rp (its GEMM format, rows of k elements)
+// over packed activations t; Q4_K's dmin table follows the blocks.
 static int kquant_run(int type, const char* rp, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t,
                       float* y, hipStream_t s) {
-  const int it = kquant_gemm_type(type);
-  const size_t kk = kquant_gemm_k(type, k);
-  int st = tiled_run(it, rp, n_rows, kk, n_tokens, t, y, s);
-  if (st || type != WH_TYPE_Q4_K) return st;
-  const float* dmin_t = reinterpret_cast<const float*>(rp + n_rows * (k / 32) * 20);
-  const int nb = static_cast<int>(k / 32);
-  dim3 grid(static_cast<unsigned>((n_rows + kDminRows * 256 - 1) / (kDminRows * 256)),
-            static_cast<unsigned>((n_tokens + kDminTokens - 1) / kDminTokens));
-  const size_t lds = static_cast<size_t>(kDminTokens) * (nb / 8) * sizeof(float);
-  kq_dmin_kernel<<<grid, 256, lds, s>>>(y, dmin_t, t.bs, t.rs, static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
-                                        t.bm);
-  WH_LAUNCH_CHECK("k-quant dmin kernel launch");
-  return WH_OK;
+  const float* dmin_t =
+      type == WH_TYPE_Q4_K ? reinterpret_cast<const float*>(rp + n_rows * (k / 32) * 20) : nullptr;
+  return tiled_run(kquant_gemm_type(type), rp, n_rows, kquant_gemm_k(type, k), n_tokens, t, y, s, dmin_t);
 }
 
 size_t gemm_kquant_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {

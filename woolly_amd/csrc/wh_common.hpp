@@ -65,8 +65,8 @@ inline bool is_kquant(int type) { return type == WH_TYPE_Q4_K || type == WH_TYPE
 // Block formats of the tiled prefill GEMM that K-quant matrices are repacked
 // into (internal ids, never seen at the C ABI):
 //   kGemmQ4F {f32 d; u8 qs[16]}: 32 elements d * q, Q4_0 nibble order, followed
-//            by the super-blocks' dmin as f32 [k / 256][n_rows] (the GEMM adds
-//            dmin * sum(x) per super-block in a separate pass)
+//            by the super-blocks' dmin as f32 [k / 256][n_rows] (the GEMM's
+//            epilogue adds dmin * sum(x) per super-block)
 //   kGemmQ8H {f32 d; i8 q[16]}: 16 elements d * q, which the GEMM reads as a
 //            32-element block whose upper half is zero (activations packed to match)
 constexpr int kGemmQ4F = 256, kGemmQ8H = 257;
