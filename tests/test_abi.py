@@ -120,6 +120,9 @@ def test_ffn_and_weight_argument_errors_need_no_gpu():
     h = C.c_void_p()
     assert lib.wh_weight_upload(2, 4, 48, None, 0, C.byref(h)) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_weight_upload(2, 4, 64, None, 10, C.byref(h)) == _lib.WH_ERR_BUFFER_TOO_SMALL
+    # K-quants: 256-element blocks, 144 / 210 bytes each
+    assert lib.wh_weight_upload(12, 4, 64, None, 0, C.byref(h)) == _lib.WH_ERR_INVALID_SHAPE
+    assert lib.wh_weight_upload(14, 4, 256, None, 4 * 210 - 1, C.byref(h)) == _lib.WH_ERR_BUFFER_TOO_SMALL
     assert h.value is None
 
 

@@ -379,3 +379,32 @@ def test_upload_from_mapping_matches_host_weight(tmp_path):
     ops.quantized_matvec(2, dw.ptr, w.nbytes, xb, y1, n, k)
     ops.quantized_matvec(2, ref.ptr, w.nbytes, xb, y2, n, k)
     assert np.array_equal(y1.download(np.float32, n), y2.download(np.float32, n))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [GGMLType.Q4_K, GGMLType.Q6_K])
+def test_upload_kquant_tensor(tmp_path, t):
+    """Q4_K / Q6_K tensors (a Q4_K_M file's types) upload from the mapping with
+    their 256-element block sizes and compute the same GEMV as host uploads."""
+    from woolly_amd import _lib, ops, synth
+    from woolly_amd.device import DeviceBuffer
+
+    n, k = 80, 1024
+    w = synth.quantized_weight(int(t), n, k, seed=13)
+    data = (MockGGUFBuilder()
+            .add_metadata("general.architecture", VT.String, "llama")
+            .add_tensor("blk.0.ffn_down.weight", [k, n], t, w.tobytes())
+            .build())
+    ld = load(data, tmp_path)
+    dw = ld.upload("blk.0.ffn_down.weight")
+    assert (dw.ggml_type, dw.n_rows, dw.k, dw.nbytes) == (int(t), n, k, w.nbytes)
+    back = np.empty(w.nbytes, np.uint8)
+    _lib.check(_lib.load().wh_memcpy_d2h(back.ctypes.data, dw.ptr, w.nbytes, None))
+    _lib.check(_lib.load().wh_device_synchronize())
+    assert np.array_equal(back, np.frombuffer(w.tobytes(), np.uint8))
+    x = synth.activations(k, seed=14)
+    xb, y1, y2 = DeviceBuffer.from_array(x), DeviceBuffer(4 * n), DeviceBuffer(4 * n)
+    ref = ops.Weight(int(t), n, k, w)
+    ops.quantized_matvec(int(t), dw.ptr, w.nbytes, xb, y1, n, k)
+    ops.quantized_matvec(int(t), ref.ptr, w.nbytes, xb, y2, n, k)
+    assert np.array_equal(y1.download(np.float32, n), y2.download(np.float32, n))

@@ -536,11 +536,11 @@ WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_
       return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
                            "weight_upload: buffer too small: needed %zu bytes, available %zu", need, nbytes);
   } else {
-    int st = check_block_args("weight_upload", type, k);
+    int st = check_gemv_args("weight_upload", type, k);
     if (st) return st;
     st = check_weight_bytes("weight_upload", type, n_rows, k, nbytes);
     if (st) return st;
-    need = n_rows * (k / 32) * wh::type_size(type);
+    need = n_rows * (k / wh::block_elems(type)) * wh::type_size(type);
   }
   if (need > 0 && !host_bytes)
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_upload: null host bytes");
