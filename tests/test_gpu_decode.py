@@ -296,3 +296,56 @@ def test_kquant_m_layer_llama3_8b_shape(gpu, orc):
     ref = orc.llama_layer_decode_f64(tl, Ls[0], dims, inv, kg.copy(), vg.copy(), pos, x0.astype(np.float64),
                                      store_new=False)
     check(got, ref, "kquant q4_k_m layer 8B", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(ref))))
+
+
+def test_llama_model_from_gguf_q4_k_m(gpu, orc, tmp_path):
+    """A two-layer Q4_K_M-typed model written as a GGUF file (llama.* metadata,
+    blk.N.* tensors, Q6_K output head), loaded with LlamaModel.from_gguf and
+    stepped three times from empty caches, against the f64 oracle."""
+    from tests.test_gguf import MockGGUFBuilder, load
+    from woolly_amd.gguf import GGMLType, MetadataValueType as VT
+
+    hidden, n_heads, n_kv, d, n_ff, vocab, ctx = 512, 4, 2, 128, 768, 300, 8
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    Ls = [mixed_layer(MIXED, hidden, n_heads, n_kv, d, n_ff, seed=70 + i) for i in range(2)]
+    head = synth.quantized_weight(Q6_K, vocab, hidden, seed=72)
+    onorm = np.linspace(0.9, 1.1, hidden).astype(np.float32)
+    b = MockGGUFBuilder().add_metadata("general.architecture", VT.String, "llama")
+    for key, vt, v in (("embedding_length", VT.UInt32, hidden), ("block_count", VT.UInt32, 2),
+                       ("attention.head_count", VT.UInt32, n_heads), ("attention.head_count_kv", VT.UInt32, n_kv),
+                       ("feed_forward_length", VT.UInt32, n_ff), ("context_length", VT.UInt32, ctx),
+                       ("rope.freq_base", VT.Float32, 500000.0), ("attention.layer_norm_epsilon", VT.Float32, 1e-5)):
+        b.add_metadata("llama." + key, vt, v)
+    gnames = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "w_gate": "ffn_gate",
+              "w_up": "ffn_up", "w_down": "ffn_down"}
+    shapes = {"wq": (n_heads * d, hidden), "wk": (n_kv * d, hidden), "wv": (n_kv * d, hidden),
+              "wo": (hidden, n_heads * d), "w_gate": (n_ff, hidden), "w_up": (n_ff, hidden), "w_down": (hidden, n_ff)}
+    for i, L in enumerate(Ls):
+        b.add_tensor(f"blk.{i}.attn_norm.weight", [hidden], GGMLType.F32, L["attn_norm"].tobytes())
+        b.add_tensor(f"blk.{i}.ffn_norm.weight", [hidden], GGMLType.F32, L["ffn_norm"].tobytes())
+        for key, nm in gnames.items():
+            n, k = shapes[key]
+            b.add_tensor(f"blk.{i}.{nm}.weight", [k, n], GGMLType(MIXED[key]), L[key].tobytes())
+    b.add_tensor("output_norm.weight", [hidden], GGMLType.F32, onorm.tobytes())
+    b.add_tensor("output.weight", [hidden, vocab], GGMLType.Q6_K, head.tobytes())
+    ld = load(b.build(), tmp_path)
+    model = ops.LlamaModel.from_gguf(ld)
+    assert model.dims == dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff, max_ctx=ctx,
+                              vocab=vocab, eps=float(np.float32(1e-5)))
+    ws = DeviceBuffer(model.workspace_bytes())
+    xb, lb = DeviceBuffer(4 * hidden), DeviceBuffer(4 * vocab)
+    tl = [MIXED[n] for n in PROJ]
+    inv = orc.rope_inv_freq(500000.0, d)
+    caches = [(np.zeros((ctx, n_kv, d), np.uint16), np.zeros((ctx, n_kv, d), np.uint16)) for _ in Ls]
+    for pos in range(3):
+        print(f"[case] gguf q4_k_m model pos={pos}", flush=True)
+        x0 = synth.activations(hidden, seed=300 + pos)
+        xb.upload(x0)
+        model.decode_step(pos, xb, lb, ws, model.workspace_bytes())
+        got_x, got_l = down(xb, np.float32, hidden), down(lb, np.float32, vocab)
+        x = x0.astype(np.float64)
+        for L, (kc, vc) in zip(Ls, caches):
+            x = orc.llama_layer_decode_f64(tl, L, dims, inv, kc, vc, pos, x)
+        logits = orc.output_head_f64(Q6_K, head, onorm, 1e-5, x, hidden, vocab)
+        check(got_x, x, f"gguf q4_k_m pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
+        check(got_l, logits, f"gguf q4_k_m pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))

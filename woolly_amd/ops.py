@@ -20,9 +20,11 @@ def _s(stream: Stream | None):
 
 
 def _p(buf) -> int:
+    """Device address of a DeviceBuffer, a Weight handle or a plain integer."""
     if buf is None:
         return 0
-    return buf.ptr if isinstance(buf, DeviceBuffer) else int(buf)
+    ptr = getattr(buf, "ptr", None)
+    return int(ptr) if ptr is not None else int(buf)
 
 
 def type_size(ggml_type: int) -> int:
@@ -217,6 +219,68 @@ class LlamaModel:
         m.output_type = output_type
         m.output = _p(output) or None
         self.model = m
+
+    @classmethod
+    def from_gguf(cls, ld, max_ctx: int | None = None) -> "LlamaModel":
+        """The decode model of a GGUF file (gguf.GGUFLoader): the config from the
+        `{arch}.*` metadata keys GGUFModelLoader reads (model/loader.rs:110-150:
+        embedding_length, block_count, attention.head_count[_kv],
+        feed_forward_length, context_length, rope.freq_base,
+        attention.layer_norm_epsilon, default 1e-5) and the tensors
+        load_layer_weights / load_model_weights name (loader.rs:370-520:
+        blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate,
+        ffn_up, ffn_down}.weight, output_norm.weight, output.weight).  Every
+        matrix is uploaded from the mapping with its own block type (Q4_K_M
+        files mix Q4_K and Q6_K); the f16 KV caches (max_ctx rows, default the
+        context length) start zeroed."""
+        import numpy as np
+
+        from .device import DeviceBuffer
+
+        md = ld.metadata()
+        arch = md.get_string("general.architecture") or "llama"
+
+        def u32(key, default=None):
+            v = md.get_u32(f"{arch}.{key}")
+            if v is None and default is None:
+                raise ValueError(f"GGUF metadata {arch}.{key} missing")
+            return int(v if v is not None else default)
+
+        hidden, n_layers, n_heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
+        n_kv = u32("attention.head_count_kv", n_heads)
+        n_ff = u32("feed_forward_length", 4 * hidden)
+        ctx = int(max_ctx) if max_ctx else u32("context_length", 2048)
+        base = md.get_f32(f"{arch}.rope.freq_base")
+        base = float(base) if base is not None else 10000.0
+        eps = md.get_f32(f"{arch}.attention.layer_norm_epsilon")
+        if eps is None:
+            eps = md.get_f32(f"{arch}.layer_norm_epsilon")
+        eps = float(eps) if eps is not None else 1e-5
+        d = hidden // n_heads
+        names = {"attn_norm": "attn_norm", "wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output",
+                 "ffn_norm": "ffn_norm", "w_gate": "ffn_gate", "w_up": "ffn_up", "w_down": "ffn_down"}
+        layers = []
+        for i in range(n_layers):
+            L = {}
+            for key, nm in names.items():
+                name = f"blk.{i}.{nm}.weight"
+                L[key] = ld.upload(name)
+                if key.startswith("w"):
+                    L[key + "_type"] = int(ld.tensor_info(name).ggml_type)
+            for key in ("k_cache", "v_cache"):
+                L[key] = DeviceBuffer(ctx * n_kv * d * 2)
+                L[key].fill(0)
+            layers.append(L)
+        inv = DeviceBuffer.from_array(rope_inv_freq(base, d))
+        out_norm = ld.upload("output_norm.weight")
+        head = ld.upload("output.weight")
+        head_info = ld.tensor_info("output.weight")
+        dims = dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff, max_ctx=ctx,
+                    vocab=int(head_info.shape()[1]), eps=eps)
+        m = cls(layers[0]["wq_type"] if layers else GGML_Q4_0, dims, layers, inv, out_norm, head,
+                int(head_info.ggml_type))
+        m.dims = dims
+        return m
 
     def workspace_bytes(self) -> int:
         return int(_lib.load().wh_llama_decode_workspace_bytes(C.byref(self.model)))
