@@ -71,12 +71,13 @@ def test_matvec_residual_in_place(gpu, orc, t, m, k):
     check(got, ref, f"residual t={t} {m}x{k}")
 
 
-@pytest.mark.parametrize("n_heads,n_kv,d", [(32, 8, 128), (8, 2, 64), (4, 4, 64), (16, 2, 128)])
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1000, 4095])
+# (8, 1, 128) at 8191: 128 chunks per head, so each combine lane merges two load batches
+@pytest.mark.parametrize("n_heads,n_kv,d", [(32, 8, 128), (8, 2, 64), (4, 4, 64), (16, 2, 128), (8, 1, 128)])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1000, 4095, 8191])
 def test_attention_decode(gpu, orc, n_heads, n_kv, d, pos):
     print(f"[case] attention heads={n_heads}/{n_kv} d={d} pos={pos}", flush=True)
     rng = np.random.default_rng(pos + d)
-    ctx = 4096
+    ctx = max(4096, pos + 1)
     inv = orc.rope_inv_freq(500000.0, d)
     qkv = rng.standard_normal((n_heads + 2 * n_kv) * d).astype(np.float32)
     kc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)

@@ -191,65 +191,61 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 }
 
 // out[h][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c.
-// One workgroup per query head: the chunk maxima and weights are reduced by
-// all threads (weights kept in LDS), then 256 / D thread groups each sum a
-// fixed subset of the chunks for every d and meet in LDS in a fixed order.
+// One pass: a workgroup covers 64 dims of one head with four chunk groups (one
+// wave each, chunks grp, grp + 4, ...); every lane loads kBatch chunks' (m, l,
+// acc[d]) at once and merges them into its running (M, L, A) in chunk order
+// (M' = max(M, m_c), L' = L e^{M - M'} + l_c e^{m_c - M'}, likewise A), then
+// the four groups merge the same way in fixed order through LDS.
+constexpr int kCombDims = 64, kCombGroups = kAttnThreads / kCombDims;
+__device__ __forceinline__ void softmax_merge(float& M, float& L, float& A, float m, float l, float a) {
+  const float mn = fmaxf(M, m);
+  const float so = expf(M - mn), sn = expf(m - mn);
+  L = __builtin_fmaf(L, so, l * sn);
+  A = __builtin_fmaf(A, so, a * sn);
+  M = mn;
+}
+
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                     float* __restrict__ out, int n_chunks) {
-  constexpr int NG = kAttnThreads / D;  // chunk groups
-  extern __shared__ float cw[];         // [n_chunks] weights, then [NG][D] partial sums, [8] reduction
-  float* accs = cw + n_chunks;
-  float* red = accs + NG * D;
-  const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  __shared__ float sm[kCombGroups][kCombDims], sl[kCombGroups][kCombDims], sa[kCombGroups][kCombDims];
+  const int h = blockIdx.x, lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int d = blockIdx.y * kCombDims + lane;
   const float* ph = part + static_cast<size_t>(h) * n_chunks * (D + 2);
-  float m = -INFINITY;
-  for (int c = t; c < n_chunks; c += kAttnThreads) m = fmaxf(m, ph[static_cast<size_t>(c) * (D + 2)]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  float M = red[0];
-#pragma unroll
-  for (int w = 1; w < kAttnThreads / 64; w++) M = fmaxf(M, red[w]);
-  __syncthreads();
-  float l = 0.f;
-  for (int c = t; c < n_chunks; c += kAttnThreads) {
-    const float w = expf(ph[static_cast<size_t>(c) * (D + 2)] - M);
-    cw[c] = w;
-    l = __builtin_fmaf(ph[static_cast<size_t>(c) * (D + 2) + 1], w, l);
-  }
-  l = whd::wave_sum(l);
-  if (lane == 0) red[wave] = l;
-  __syncthreads();
-  float L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kAttnThreads / 64; w++) L += red[w];
-  const int d = t % D, grp = t / D;
-  // chunks grp, grp + NG, ...: kBatch loads in flight per step (a load-use
-  // loop would wait out the memory latency per chunk), summed in chunk order
   constexpr int kBatch = 16;
-  float a0 = 0.f;
-  for (int c0 = grp; c0 < n_chunks; c0 += kBatch * NG) {
-    float v[kBatch];
+  float M = -INFINITY, L = 0.f, A = 0.f;
+  bool any = false;
+  for (int c0 = grp; c0 < n_chunks; c0 += kBatch * kCombGroups) {
+    float mv[kBatch], lv[kBatch], av[kBatch];
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
-      const int c = c0 + b * NG;
-      v[b] = c < n_chunks ? ph[static_cast<size_t>(c) * (D + 2) + 2 + d] : 0.f;
+      const int c = c0 + b * kCombGroups;
+      const float* pc = ph + static_cast<size_t>(c < n_chunks ? c : 0) * (D + 2);
+      mv[b] = pc[0];
+      lv[b] = pc[1];
+      av[b] = pc[2 + d];
     }
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
-      const int c = c0 + b * NG;
-      if (c < n_chunks) a0 = __builtin_fmaf(cw[c], v[b], a0);
+      if (c0 + b * kCombGroups >= n_chunks) break;
+      if (!any) {
+        M = mv[b], L = lv[b], A = av[b];
+        any = true;
+      } else {
+        softmax_merge(M, L, A, mv[b], lv[b], av[b]);
+      }
     }
   }
-  accs[grp * D + d] = a0;
+  sm[grp][lane] = M;
+  sl[grp][lane] = L;
+  sa[grp][lane] = A;
   __syncthreads();
   if (grp == 0) {
-    float acc = accs[d];
+    // groups with no chunk (n_chunks < 4) hold M = -inf and are skipped
 #pragma unroll
-    for (int g = 1; g < NG; g++) acc += accs[g * D + d];
-    out[h * D + d] = acc / L;
+    for (int g = 1; g < kCombGroups; g++)
+      if (g < n_chunks) softmax_merge(M, L, A, sm[g][lane], sl[g][lane], sa[g][lane]);
+    out[h * D + d] = A / L;
   }
 }
 
@@ -264,10 +260,6 @@ int attn_chunk(size_t ctx, size_t n_kv_heads) {
   if (c < 64) c = 64;
   if (c > 256) c = 256;
   return static_cast<int>(c);
-}
-
-size_t combine_lds(int D, int n_chunks) {
-  return 4u * (static_cast<size_t>(n_chunks) + static_cast<size_t>(kAttnThreads / D) * D + 8);
 }
 
 template <int D>
@@ -299,14 +291,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
   const int G = static_cast<int>(n_heads / n_kv_heads);
   float* part = static_cast<float*>(ws);
   const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
-  const size_t clds = combine_lds(static_cast<int>(head_dim), n_chunks);
-  if (clds > wh::max_lds_per_block())
-    return wh::set_error(WH_ERR_INVALID_SHAPE, "attention: context of %zu positions exceeds the combine's LDS", pos + 1);
-  if (clds > 65536) {
-    WH_HIP_TRY(hipFuncSetAttribute(head_dim == 128 ? reinterpret_cast<const void*>(&attn_combine_kernel<128>)
-                                                   : reinterpret_cast<const void*>(&attn_combine_kernel<64>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(clds)));
-  }
+  const dim3 cgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(head_dim / kCombDims));
   dim3 grid(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(n_chunks));
   if (head_dim == 128) {
     const size_t lds = partial_lds<128>(G, chunk);
@@ -316,8 +301,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<128><<<static_cast<unsigned>(n_heads), kAttnThreads, clds, s>>>(
-        part, out, n_chunks);
+    attn_combine_kernel<128><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
   } else {
     const size_t lds = partial_lds<64>(G, chunk);
     WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<64>),
@@ -326,8 +310,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<64><<<static_cast<unsigned>(n_heads), kAttnThreads, clds, s>>>(
-        part, out, n_chunks);
+    attn_combine_kernel<64><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
   }
   WH_LAUNCH_CHECK("attention combine launch");
   return WH_OK;
