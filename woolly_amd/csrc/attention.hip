@@ -45,25 +45,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   const int t = threadIdx.x;
   const float fpos = static_cast<float>(pos);
 
-  // q heads of this group, rotated: thread -> (head, pair i)
-  for (int e = t; e < G * D / 2; e += kAttnThreads) {
-    const int g = e / (D / 2), i = e % (D / 2);
-    const float* q = qkv + (kvh * G + g) * D;
-    const float ang = fpos * inv_freq[i];
-    float sn, cs;
-    sincosf(ang, &sn, &cs);
-    const float x1 = q[i], x2 = q[i + D / 2];
-    qs[g * D + i] = x1 * cs - x2 * sn;
-    qs[g * D + i + D / 2] = x1 * sn + x2 * cs;
-  }
-  // K / V rows of positions [p0, p0 + np) except pos, f16 pairs
+  // K / V rows of positions [p0, p0 + np) except pos, f16 pairs, as 16-byte
+  // pieces, kBatch per thread: every load of a batch is issued before the
+  // first LDS store (a load-store loop would wait out the memory latency each
+  // time), and the first batch is in flight while q is rotated
   const bool own = pos >= p0 && pos < p0 + chunk;
   const int nrow = own ? np - 1 : np;
-  // 16-byte pieces, kBatch per thread with every load issued before the first
-  // LDS store (a load-store loop would wait out the memory latency each time)
   constexpr int kBatch = 8;
-  for (int e0 = 0; e0 < nrow * (D / 8); e0 += kBatch * kAttnThreads) {
-    uint4 kk[kBatch], vv[kBatch];
+  uint4 kk[kBatch], vv[kBatch];
+  auto kv_load = [&](int e0) {
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const int e = e0 + b * kAttnThreads + t;
@@ -74,6 +64,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         vv[b] = *reinterpret_cast<const uint4*>(v_cache + off);
       }
     }
+  };
+  auto kv_store = [&](int e0) {
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const int e = e0 + b * kAttnThreads + t;
@@ -85,6 +77,39 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         vd[0] = vv[b].x, vd[1] = vv[b].y, vd[2] = vv[b].z, vd[3] = vv[b].w;
       }
     }
+  };
+  // q heads of this group, rotated: thread -> (head, pair i), at most
+  // 8 * D / 2 / 256 pairs per thread.  Their loads go out before the K / V
+  // loads (loads complete in order, so waiting for q then leaves K / V in flight).
+  constexpr int QI = 8 * D / 2 / kAttnThreads;
+  float qx1[QI], qx2[QI], qf[QI];
+#pragma unroll
+  for (int u = 0; u < QI; u++) {
+    const int e = t + u * kAttnThreads;
+    if (e < G * D / 2) {
+      const int g = e / (D / 2), i = e % (D / 2);
+      const float* q = qkv + (kvh * G + g) * D;
+      qx1[u] = q[i];
+      qx2[u] = q[i + D / 2];
+      qf[u] = inv_freq[i];
+    }
+  }
+  kv_load(0);
+#pragma unroll
+  for (int u = 0; u < QI; u++) {
+    const int e = t + u * kAttnThreads;
+    if (e < G * D / 2) {
+      const int g = e / (D / 2), i = e % (D / 2);
+      float sn, cs;
+      sincosf(fpos * qf[u], &sn, &cs);
+      qs[g * D + i] = qx1[u] * cs - qx2[u] * sn;
+      qs[g * D + i + D / 2] = qx1[u] * sn + qx2[u] * cs;
+    }
+  }
+  kv_store(0);
+  for (int e0 = kBatch * kAttnThreads; e0 < nrow * (D / 8); e0 += kBatch * kAttnThreads) {
+    kv_load(e0);
+    kv_store(e0);
   }
   if (own) {
     // the new token: rotate k, round k and v to f16, store them in the cache
