@@ -58,7 +58,8 @@ typedef enum wh_type {
   WH_TYPE_Q4_1 = 3,
   WH_TYPE_Q8_0 = 8,
   /* 256-element K-quant blocks in woolly-gguf's layout (dequantize.rs:404-536,
-   * which differs from ggml's): dequantization and GEMV only. */
+   * which differs from ggml's): dequantization, GEMV, GEMM, the FFN layer and
+   * the decode step (rows a multiple of 256 elements). */
   WH_TYPE_Q4_K = 12,
   WH_TYPE_Q6_K = 14
 } wh_type;
