@@ -408,3 +408,32 @@ def test_upload_kquant_tensor(tmp_path, t):
     ops.quantized_matvec(int(t), dw.ptr, w.nbytes, xb, y1, n, k)
     ops.quantized_matvec(int(t), ref.ptr, w.nbytes, xb, y2, n, k)
     assert np.array_equal(y1.download(np.float32, n), y2.download(np.float32, n))
+
+
+def test_llama_config_from_gguf_metadata():
+    """LlamaModel.config_from_gguf reads GGUFModelLoader's keys
+    (model/loader.rs:110-150) with its defaults; no GPU needed."""
+    from woolly_amd import ops
+
+    def cfg(extra, arch="llama"):
+        b = MockGGUFBuilder().add_metadata("general.architecture", VT.String, arch)
+        for key, vt, v in extra:
+            b.add_metadata(f"{arch}.{key}", vt, v)
+        return ops.LlamaModel.config_from_gguf(load(b.build()))
+
+    full = cfg([("embedding_length", VT.UInt32, 4096), ("block_count", VT.UInt32, 32),
+                ("attention.head_count", VT.UInt32, 32), ("attention.head_count_kv", VT.UInt32, 8),
+                ("feed_forward_length", VT.UInt32, 14336), ("context_length", VT.UInt32, 8192),
+                ("rope.freq_base", VT.Float32, 500000.0), ("attention.layer_norm_epsilon", VT.Float32, 1e-6)])
+    assert full == dict(hidden=4096, n_layers=32, n_heads=32, n_kv_heads=8, head_dim=128, n_ff=14336,
+                        max_ctx=8192, rope_base=500000.0, eps=float(np.float32(1e-6)))
+    # defaults: n_kv = n_heads, n_ff = 4 hidden, context 2048, base 10000, eps 1e-5;
+    # the alternative epsilon key; another architecture name
+    small = cfg([("embedding_length", VT.UInt32, 256), ("block_count", VT.UInt32, 2),
+                 ("attention.head_count", VT.UInt32, 4), ("layer_norm_epsilon", VT.Float32, 2e-5)], arch="mistral")
+    assert small == dict(hidden=256, n_layers=2, n_heads=4, n_kv_heads=4, head_dim=64, n_ff=1024, max_ctx=2048,
+                         rope_base=10000.0, eps=float(np.float32(2e-5)))
+    assert cfg([("embedding_length", VT.UInt32, 256), ("block_count", VT.UInt32, 2),
+                ("attention.head_count", VT.UInt32, 4)])["eps"] == 1e-5
+    with pytest.raises(ValueError):
+        cfg([("block_count", VT.UInt32, 2), ("attention.head_count", VT.UInt32, 4)])

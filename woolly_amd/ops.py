@@ -220,23 +220,14 @@ class LlamaModel:
         m.output = _p(output) or None
         self.model = m
 
-    @classmethod
-    def from_gguf(cls, ld, max_ctx: int | None = None) -> "LlamaModel":
-        """The decode model of a GGUF file (gguf.GGUFLoader): the config from the
-        `{arch}.*` metadata keys GGUFModelLoader reads (model/loader.rs:110-150:
-        embedding_length, block_count, attention.head_count[_kv],
-        feed_forward_length, context_length, rope.freq_base,
-        attention.layer_norm_epsilon, default 1e-5) and the tensors
-        load_layer_weights / load_model_weights name (loader.rs:370-520:
-        blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate,
-        ffn_up, ffn_down}.weight, output_norm.weight, output.weight).  Every
-        matrix is uploaded from the mapping with its own block type (Q4_K_M
-        files mix Q4_K and Q6_K); the f16 KV caches (max_ctx rows, default the
-        context length) start zeroed."""
-        import numpy as np
-
-        from .device import DeviceBuffer
-
+    @staticmethod
+    def config_from_gguf(ld, max_ctx: int | None = None) -> dict:
+        """The model config of a GGUF file (gguf.GGUFLoader) from the
+        `{arch}.*` metadata keys GGUFModelLoader reads (model/loader.rs:110-150):
+        embedding_length, block_count, attention.head_count[_kv] (default: the
+        head count), feed_forward_length (default 4 x hidden), context_length
+        (default 2048; max_ctx overrides it), rope.freq_base (default 10000),
+        attention.layer_norm_epsilon or layer_norm_epsilon (default 1e-5)."""
         md = ld.metadata()
         arch = md.get_string("general.architecture") or "llama"
 
@@ -246,16 +237,35 @@ class LlamaModel:
                 raise ValueError(f"GGUF metadata {arch}.{key} missing")
             return int(v if v is not None else default)
 
+        def f32(keys, default):
+            for key in keys:
+                v = md.get_f32(f"{arch}.{key}")
+                if v is not None:
+                    return float(v)
+            return default
+
         hidden, n_layers, n_heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
-        n_kv = u32("attention.head_count_kv", n_heads)
-        n_ff = u32("feed_forward_length", 4 * hidden)
-        ctx = int(max_ctx) if max_ctx else u32("context_length", 2048)
-        base = md.get_f32(f"{arch}.rope.freq_base")
-        base = float(base) if base is not None else 10000.0
-        eps = md.get_f32(f"{arch}.attention.layer_norm_epsilon")
-        if eps is None:
-            eps = md.get_f32(f"{arch}.layer_norm_epsilon")
-        eps = float(eps) if eps is not None else 1e-5
+        return dict(hidden=hidden, n_layers=n_layers, n_heads=n_heads,
+                    n_kv_heads=u32("attention.head_count_kv", n_heads), head_dim=hidden // n_heads,
+                    n_ff=u32("feed_forward_length", 4 * hidden),
+                    max_ctx=int(max_ctx) if max_ctx else u32("context_length", 2048),
+                    rope_base=f32(["rope.freq_base"], 10000.0),
+                    eps=f32(["attention.layer_norm_epsilon", "layer_norm_epsilon"], 1e-5))
+
+    @classmethod
+    def from_gguf(cls, ld, max_ctx: int | None = None) -> "LlamaModel":
+        """The decode model of a GGUF file (gguf.GGUFLoader): the config of
+        config_from_gguf and the tensors load_layer_weights / load_model_weights
+        name (model/loader.rs:370-520: blk.N.{attn_norm, attn_q, attn_k, attn_v,
+        attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight,
+        output_norm.weight, output.weight).  Every matrix is uploaded from the
+        mapping with its own block type (Q4_K_M files mix Q4_K and Q6_K); the
+        f16 KV caches (max_ctx rows) start zeroed."""
+        from .device import DeviceBuffer
+
+        cfg = cls.config_from_gguf(ld, max_ctx)
+        hidden, n_layers, n_heads, n_kv = cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"]
+        n_ff, ctx, base, eps = cfg["n_ff"], cfg["max_ctx"], cfg["rope_base"], cfg["eps"]
         d = hidden // n_heads
         names = {"attn_norm": "attn_norm", "wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output",
                  "ffn_norm": "ffn_norm", "w_gate": "ffn_gate", "w_up": "ffn_up", "w_down": "ffn_down"}
