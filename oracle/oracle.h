@@ -43,8 +43,11 @@
  *   orc_attention_decode_f64  closed forms (pos 0: out = v; equal keys:
  *                         mean of V), RoPE norm preservation, an independent
  *                         numpy float64 implementation on small shapes.
- *   orc_llama_layer_decode_f64, orc_output_head_f64  numpy float64
- *                         composition on small shapes.
+ *   orc_llama_layer_decode_f64, orc_llama_layer_decode_types_f64,
+ *   orc_output_head_f64  numpy float64 composition on small shapes (the
+ *                         types variant with Q4_K_M's per-tensor Q4_K / Q6_K
+ *                         mix, each tensor dequantized with its own type; a
+ *                         planted type swap fails).
  */
 #ifndef WOOLLY_ORACLE_H
 #define WOOLLY_ORACLE_H
