@@ -13,13 +13,17 @@ Cache), so every launch streams its weights from HBM.
 Prints ONE JSON line with:
   value          algorithmic GB/s of the GEMV = bytes per launch / ms_per_step,
                  bytes = N*K/32*18 (weights) + 4K (x) + 4N (y) = 33,103,872 B
-  roofline       the GEMV kernel's average launch duration (the timed graph replay
-                 of K launches, HIP events on the launch stream, median of 5
-                 replays after ~0.1 s of clock settling) against the 8 TB/s HBM
-                 peak; traffic = HBM bytes per launch from the committed rocprofv3
-                 FETCH_SIZE / WRITE_SIZE summary
+  roofline       the GEMV kernel's average launch duration against the 8 TB/s HBM
+                 peak: the K launches are captured into one HIP graph, which is
+                 replayed back to back between two HIP events on the launch
+                 stream (at least 1000 launches per measurement, so a short
+                 graph's per-replay cost stays hidden), median of 5 measurements
+                 after ~0.1 s of clock settling; traffic = HBM bytes per launch
+                 from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary,
+                 null when that summary was taken from other kernel sources
   ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
-                 M=512, same run (the metric's second part)
+                 M=512, same run (the metric's second part; M=1 rotates 3 layers'
+                 weights, 297 MB, past the Infinity Cache)
   gemv_other_configs  the other decode GEMV configurations: Q4_0 4096x4096,
                  Q8_0 and Q4_1 14336x4096, and the other decode-step shapes (k/v
                  projections, FFN down, the Q8_0 128256x4096 output head):
@@ -52,7 +56,8 @@ Q4_0 = 2
 N_ROWS, K = 14336, 4096
 REPLICAS = 10
 WARM_S = 0.1          # untimed replays before each timed GEMV measurement (clock settling)
-TIMED_REPLAYS = 5     # timed graph replays per measurement; the median is reported
+TIMED_REPLAYS = 5     # timed measurements; the median is reported
+TIMED_LAUNCHES = 1000  # launches per measurement (back-to-back replays of the K-launch graph)
 
 
 TYPE_SIZE = {2: 18, 3: 20, 8: 34, 12: 144, 14: 210}
@@ -103,16 +108,22 @@ def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int =
     while time.perf_counter() - t0 < WARM_S:
         graph.launch(stream)
         stream.synchronize()
+    # each measurement: back-to-back replays of the graph between two events,
+    # at least TIMED_LAUNCHES launches, so that the per-replay cost of a short
+    # graph is hidden behind the previous replay's kernels
+    n_rep = max(1, -(-TIMED_LAUNCHES // steps))
     e0, e1 = Event(), Event()
     reps = []
     for _ in range(TIMED_REPLAYS):
         e0.record(stream)
-        graph.launch(stream)
+        for _ in range(n_rep):
+            graph.launch(stream)
         e1.record(stream)
         e1.synchronize()
-        reps.append(e0.elapsed_ms(e1))
+        reps.append(e0.elapsed_ms(e1) / n_rep)
     ms_total = float(np.median(reps))
     graph.destroy()
+    bench_gemv.launches_timed = n_rep * steps
 
     # per-launch kernel duration: an event pair around every launch
     n_pairs = min(steps, 200)
@@ -129,60 +140,89 @@ def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int =
     return ms_total / steps, float(np.median(durs)), float(np.mean(durs))
 
 
-def bench_ffn(m: int, iters: int, t: int = Q4_0) -> float:
+def bench_ffn(m: int, iters: int, t: int = Q4_0, replicas: int | None = None) -> float:
+    """The SwiGLU FFN layer (config 3, Llama-3-8B shape), µs per call.  The
+    weights of `replicas` layers (default: enough copies for > 256 MB, the
+    Infinity Cache, when the call streams its weights once, M <= 2) are
+    rotated, and the calls are captured into a HIP graph and replayed."""
     from woolly_amd import ops, synth
-    from woolly_amd.device import DeviceBuffer, Event, Stream
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
 
     hidden, n_ff = 4096, 14336
     L = synth.ffn_layer(t, hidden, n_ff, m, seed=5)
+    wbytes = L["gate"].nbytes + L["up"].nbytes + L["down"].nbytes
+    if replicas is None:
+        replicas = max(1, -(-300_000_000 // wbytes)) if m <= 2 else 1
     stream = Stream()
-    b = {k: DeviceBuffer.from_array(v) for k, v in L.items()}
+    copies = [{k: DeviceBuffer.from_array(L[k]) for k in ("gate", "up", "down")} for _ in range(replicas)]
+    b = {k: DeviceBuffer.from_array(L[k]) for k in ("gamma", "x")}
     out = DeviceBuffer(4 * m * hidden)
-    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m, ggml_type=t)
+    wsz = ops.ffn_workspace_bytes_for_type(t, hidden, n_ff, m)
     ws = DeviceBuffer(wsz)
 
-    def run():
-        ops.ffn_swiglu(t, b["gate"], b["up"], b["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
+    def run(i):
+        c = copies[i % replicas]
+        ops.ffn_swiglu(t, c["gate"], c["up"], c["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
                        m, out, ws, wsz, stream)
 
-    for _ in range(3):
-        run()
+    for i in range(3):
+        run(i)
+    stream.synchronize()
+    n = max(iters, replicas)
+    with Graph.capture(stream) as graph:
+        for i in range(n):
+            run(i)
+    graph.launch(stream)
     stream.synchronize()
     e0, e1 = Event(), Event()
     e0.record(stream)
-    for _ in range(iters):
-        run()
+    for _ in range(3):
+        graph.launch(stream)
     e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_ms(e1) / iters * 1000.0
+    graph.destroy()
+    return e0.elapsed_ms(e1) / (3 * n) * 1000.0
 
 
 def bench_gemm(m: int, iters: int, t: int = Q4_0) -> float:
-    """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t), µs per call."""
+    """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t), µs
+    per call.  For m <= 64, where the call streams its 33 MB of weights about
+    once, 10 weight copies (> 256 MB, the Infinity Cache) are rotated; the calls
+    are captured into a HIP graph and replayed."""
     from woolly_amd import ops, synth
-    from woolly_amd.device import DeviceBuffer, Event, Stream
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
 
     w = synth.quantized_weight(t, N_ROWS, K, seed=4)
-    x = np.concatenate([synth.activations(K, seed=400 + t) for t in range(min(m, 64))])
+    x = np.concatenate([synth.activations(K, seed=400 + i) for i in range(min(m, 64))])
     x = np.resize(x, m * K).astype(np.float32)
+    replicas = 10 if m <= 64 else 1
     stream = Stream()
-    wb, xb, yb = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer(4 * m * N_ROWS)
+    wbs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
+    xb = DeviceBuffer.from_array(x)
+    yb = DeviceBuffer(4 * m * N_ROWS)
     wsz = ops.matmul_workspace_bytes(t, N_ROWS, K, m)
     ws = DeviceBuffer(max(wsz, 256))
 
-    def run():
-        ops.quantized_matmul(t, wb, w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
+    def run(i):
+        ops.quantized_matmul(t, wbs[i % replicas], w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
 
-    for _ in range(3):
-        run()
+    for i in range(3):
+        run(i)
+    stream.synchronize()
+    n = max(iters, replicas)
+    with Graph.capture(stream) as graph:
+        for i in range(n):
+            run(i)
+    graph.launch(stream)
     stream.synchronize()
     e0, e1 = Event(), Event()
     e0.record(stream)
-    for _ in range(iters):
-        run()
+    for _ in range(3):
+        graph.launch(stream)
     e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_ms(e1) / iters * 1000.0
+    graph.destroy()
+    return e0.elapsed_ms(e1) / (3 * n) * 1000.0
 
 
 # config 4: Llama-3-8B-shaped decode step
@@ -299,17 +339,42 @@ def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
     return 2 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
 
 
-def traffic_from_profile() -> int | None:
+# The sources the headline GEMV kernel is built from: a committed profile
+# summary is current only if it records the same digest of them.
+GEMV_KERNEL_SOURCES = ("woolly_amd/csrc/gemv_mfma.hip", "woolly_amd/csrc/gemv.hip",
+                       "woolly_amd/csrc/wh_common.hpp", "woolly_amd/csrc/wh_blocks.hpp")
+PMC_PROFILE = ROOT / "profiles" / "gemv_q4_0_14336x4096_pmc.txt"
+
+
+def kernel_sources_digest() -> str:
+    """sha256 over the headline kernel's source files, in a fixed order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in GEMV_KERNEL_SOURCES:
+        h.update(rel.encode() + b"\0" + (ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def traffic_from_profile() -> tuple[int | None, str]:
     """HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
-    (scaled by the copy probe), as recorded in the committed profile summary."""
-    path = ROOT / "profiles" / "gemv_q4_0_14336x4096_pmc.txt"
+    (scaled by the copy probe), as recorded in the committed profile summary,
+    and its status: "current" when the summary's kernel_sources_sha256 matches
+    the sources in this tree, else "stale" (the traffic is then reported as
+    null) or "missing"."""
+    fields = {}
     try:
-        for line in path.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+        for line in PMC_PROFILE.read_text().splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return None
+        return None, "missing"
+    if "traffic_bytes_per_launch" not in fields:
+        return None, "missing"
+    if fields.get("kernel_sources_sha256") != kernel_sources_digest():
+        return None, "stale"
+    return int(float(fields["traffic_bytes_per_launch"])), "current"
 
 
 def _cpu_model() -> str:
@@ -395,7 +460,12 @@ def main() -> int:
                     help="ggml type id and shape of --only gemv (default Q4_0 14336 4096)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only device-to-device copies of 256 MiB (counter calibration)")
+    ap.add_argument("--sources-digest", action="store_true",
+                    help="print the digest of the headline GEMV kernel's sources and exit (no GPU)")
     args = ap.parse_args()
+    if args.sources_digest:
+        print(kernel_sources_digest())
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -431,6 +501,7 @@ def main() -> int:
                           "type": args.type}))
         return 0
     ms_step, med_ms, mean_ms = bench_gemv(args.steps, args.warmup)
+    traffic, traffic_status = traffic_from_profile()
     nbytes = gemv_bytes(N_ROWS, K)
     value = nbytes / (ms_step * 1e-3) / 1e9
     # the GEMV is the only kernel of a step: its average launch duration is the
@@ -533,10 +604,12 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profile(),
+            "traffic": traffic,
+            "traffic_profile": f"{PMC_PROFILE.relative_to(ROOT)} ({traffic_status})",
             "kernel": "gemv_mfma_kernel<Q4_0, 1 K-segment, 3 loads/step, plain> (int8 MFMA)",
             "profile": "profiles/gemv_q4_0_14336x4096_kernel_trace.txt",
             "launch_us_mean": round(ms_step * 1e3, 3),
+            "launches_timed": bench_gemv.launches_timed,
             "launch_us_eager_event_pairs": round(mean_ms * 1e3, 3),
         },
         "ffn_layer_us": ffn or None,

@@ -147,7 +147,8 @@ WH_API int wh_quantized_matvec(int type, const void* weights, size_t weight_nbyt
  * the activations) for the shapes it takes, the streaming VALU kernels
  * otherwise; WH_GEMV_STREAM: streaming kernels only.  Applies to
  * wh_quantized_matvec, the fused decode GEMVs and the M <= 2 FFN gate/up.
- * The previous setting is stored in *previous when it is not NULL.
+ * The setting belongs to the calling thread (other threads keep theirs); the
+ * previous setting is stored in *previous when it is not NULL.
  * WH_ERR_INVALID_ARGUMENT for an unknown mode (nothing changes). */
 enum { WH_GEMV_AUTO = 0, WH_GEMV_STREAM = 1 };
 WH_API int wh_gemv_select(int mode, int* previous);
@@ -313,6 +314,13 @@ typedef struct wh_llama_model {
   const float* output_norm;    /* f32 [hidden] */
   int output_type;             /* block type of the output head */
   const void* output;          /* [vocab][hidden] */
+  /* Token embeddings (token_embd.weight, [vocab][hidden] of token_embd_type:
+   * F32, F16 or a block type) for wh_llama_forward_token; may be NULL for the
+   * entry points that take an embedded x.  A GGUF file without output.weight
+   * ties the head to this table (lazy_transformer.rs:1301-1316): output =
+   * token_embd and output_type = token_embd_type. */
+  int token_embd_type;
+  const void* token_embd;
 } wh_llama_model;
 
 WH_API size_t wh_llama_decode_workspace_bytes(const wh_llama_model* model);
@@ -327,6 +335,25 @@ WH_API int wh_llama_layer_decode(const wh_llama_model* model, size_t layer, size
  * HIP graph with wh_graph_begin_capture. */
 WH_API int wh_llama_decode_step(const wh_llama_model* model, size_t pos, float* x, float* logits,
                                 void* workspace, size_t workspace_bytes, wh_stream_t stream);
+/* The step from a token id (forward, :1155-1230, for one token): x = the
+ * dequantized row *token of model->token_embd, then wh_llama_decode_step.
+ * `token` is device memory (a uint32 the caller or a sampler on the device
+ * writes before each step), so a captured step reads the current token at
+ * every replay.  An id >= vocab, which the reference rejects with
+ * TENSOR_EMBEDDING_TOKEN_OUT_OF_RANGE, makes x and the logits NaN. */
+WH_API int wh_llama_forward_token(const wh_llama_model* model, const uint32_t* token, size_t pos, float* x,
+                                  float* logits, void* workspace, size_t workspace_bytes,
+                                  wh_stream_t stream);
+
+/* embedding_lookup (crates/woolly-core/src/tensor_utils.rs:548-590) on the
+ * device: out[t, :] = the dequantized row ids[t] of table ([vocab][hidden] of
+ * `type`, e.g. token_embd.weight), bit-identical to wh_dequantize of that row,
+ * for t < n_tokens (at most 65535).  ids (uint32) and out are device memory,
+ * out 16-byte aligned, hidden a multiple of 4 and of the block size.  Rows of
+ * ids >= vocab are written as NaN (the reference returns
+ * TENSOR_EMBEDDING_TOKEN_OUT_OF_RANGE; the host mirrors check ids first). */
+WH_API int wh_embedding_lookup(int type, const void* table, size_t vocab, size_t hidden, const uint32_t* ids,
+                               size_t n_tokens, float* out, wh_stream_t stream);
 
 /* --------------------------------------------------------------- GGUF files */
 /* A parsed GGUF file: header, metadata key/values and the tensor table of

@@ -24,10 +24,15 @@ def _ptr(a: np.ndarray | None):
 
 
 class Oracle:
-    def __init__(self):
-        if not ORACLE_LIB.exists():
-            subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
-        lib = C.CDLL(str(ORACLE_LIB))
+    def __init__(self, lib_path: Path | None = None):
+        """The oracle library (oracle/_build/liboracle.so, built on demand), or
+        another build of the same sources at lib_path (the mutation tests load
+        copies with a planted mistake)."""
+        if lib_path is None:
+            if not ORACLE_LIB.exists():
+                subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+            lib_path = ORACLE_LIB
+        lib = C.CDLL(str(lib_path))
         sig = {
             "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
             "orc_f32_to_f16": (C.c_uint16, [C.c_float]),

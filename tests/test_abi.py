@@ -137,3 +137,67 @@ def test_cpp_mirror_header_compiles_and_links():
                    input=b'#include "woolly_hip.hpp"\n', check=True)
     subprocess.run(["make", "-s", "-C", str(root / "tests" / "cpp")], check=True)
     assert (root / "tests" / "cpp" / "_build" / "test_mirror").exists()
+
+
+def _fake_model(n_layers=2, null_field=None, output_type=8, logits_head=True):
+    """A wh_llama_model whose device pointers are fake non-null addresses: the
+    step's checks must reject it before any launch."""
+    layers = (_lib.wh_llama_layer * n_layers)()
+    for L in layers:
+        for name, _ in _lib.wh_llama_layer._fields_:
+            if not name.endswith("_type"):
+                setattr(L, name, 0x10000)
+    if null_field is not None:
+        setattr(layers[n_layers - 1], null_field, None)
+    m = _lib.wh_llama_model()
+    m.type = 2
+    m.n_layers, m.hidden, m.n_heads, m.n_kv_heads, m.head_dim = n_layers, 256, 4, 2, 64
+    m.n_ff, m.max_ctx, m.vocab, m.eps = 512, 16, 300, 1e-5
+    m.rope_inv_freq = 0x10000
+    m.layers = C.cast(layers, C.POINTER(_lib.wh_llama_layer))
+    m.output_norm = 0x10000 if logits_head else None
+    m.output_type = output_type
+    m.output = 0x10000
+    return m, layers
+
+
+@pytest.mark.parametrize("field", ["attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate", "w_up", "w_down"])
+def test_decode_step_rejects_null_layer_pointers(field):
+    """Every matrix and norm of every layer must be non-null: a null pointer is
+    WH_ERR_INVALID_ARGUMENT naming it, reported before anything is launched."""
+    lib = _lib.load()
+    m, keep = _fake_model(null_field=field)
+    st = lib.wh_llama_decode_step(C.byref(m), 0, 0x10000, 0x10000, 0x10000, 1 << 30, None)
+    assert st == _lib.WH_ERR_INVALID_ARGUMENT
+    assert f"layer 1 {field} is a null pointer".encode() in lib.wh_last_error()
+
+
+def test_decode_step_checks_the_head_before_any_layer():
+    """A bad output head (unsupported type, null output_norm) fails before the
+    first layer is launched, so x and the caches are left as they were: with
+    fake device pointers a launch would report a HIP error instead."""
+    lib = _lib.load()
+    m, keep = _fake_model(output_type=6)
+    assert lib.wh_llama_decode_step(C.byref(m), 0, 0x10000, 0x10000, 0x10000, 1 << 30, None) == \
+        _lib.WH_ERR_UNSUPPORTED_TYPE
+    assert b"output head" in lib.wh_last_error()
+    m, keep = _fake_model(logits_head=False)
+    assert lib.wh_llama_decode_step(C.byref(m), 0, 0x10000, 0x10000, 0x10000, 1 << 30, None) == \
+        _lib.WH_ERR_INVALID_ARGUMENT
+    assert b"output_norm" in lib.wh_last_error()
+    # forward_token without a token_embd table
+    m, keep = _fake_model()
+    assert lib.wh_llama_forward_token(C.byref(m), 0x10000, 0, 0x10000, 0x10000, 0x10000, 1 << 30, None) == \
+        _lib.WH_ERR_INVALID_ARGUMENT
+    assert b"token_embd" in lib.wh_last_error()
+
+
+def test_embedding_lookup_argument_errors_need_no_gpu():
+    lib = _lib.load()
+    assert lib.wh_embedding_lookup(6, 0x10000, 10, 256, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_UNSUPPORTED_TYPE
+    assert lib.wh_embedding_lookup(12, 0x10000, 10, 128, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_INVALID_SHAPE
+    assert lib.wh_embedding_lookup(2, None, 10, 256, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_INVALID_ARGUMENT
+    assert lib.wh_embedding_lookup(2, 0x10000, 10, 256, 0x10000, 0, 0x10000, None) == _lib.WH_OK
+    from woolly_amd import ops
+    with pytest.raises(ValueError, match="Token ID 10 exceeds vocabulary size 10"):
+        ops.embedding_lookup(2, 0x10000, 10, 256, [3, 10], 0x10000)

@@ -10,7 +10,7 @@ import struct
 import numpy as np
 import pytest
 
-from woolly_amd import gguf
+from woolly_amd import gguf, synth
 from woolly_amd.gguf import GGMLType, GGUFLoader, MetadataValue, MetadataValueType as VT
 
 _FMT = {VT.UInt8: "<B", VT.Int8: "<b", VT.UInt16: "<H", VT.Int16: "<h", VT.UInt32: "<I",
@@ -411,29 +411,95 @@ def test_upload_kquant_tensor(tmp_path, t):
 
 
 def test_llama_config_from_gguf_metadata():
-    """LlamaModel.config_from_gguf reads GGUFModelLoader's keys
-    (model/loader.rs:110-150) with its defaults; no GPU needed."""
+    """LlamaModel.config_from_gguf reads GGUFModelLoader::extract_config's keys
+    with their fallback keys and defaults (model/loader.rs:104-150); no GPU needed."""
     from woolly_amd import ops
 
-    def cfg(extra, arch="llama"):
-        b = MockGGUFBuilder().add_metadata("general.architecture", VT.String, arch)
+    def cfg(extra, arch="llama", top=()):
+        b = MockGGUFBuilder()
+        if arch is not None:
+            b.add_metadata("general.architecture", VT.String, arch)
         for key, vt, v in extra:
             b.add_metadata(f"{arch}.{key}", vt, v)
+        for key, vt, v in top:
+            b.add_metadata(key, vt, v)
         return ops.LlamaModel.config_from_gguf(load(b.build()))
 
     full = cfg([("embedding_length", VT.UInt32, 4096), ("block_count", VT.UInt32, 32),
                 ("attention.head_count", VT.UInt32, 32), ("attention.head_count_kv", VT.UInt32, 8),
                 ("feed_forward_length", VT.UInt32, 14336), ("context_length", VT.UInt32, 8192),
+                ("vocab_size", VT.UInt32, 128256),
                 ("rope.freq_base", VT.Float32, 500000.0), ("attention.layer_norm_epsilon", VT.Float32, 1e-6)])
     assert full == dict(hidden=4096, n_layers=32, n_heads=32, n_kv_heads=8, head_dim=128, n_ff=14336,
-                        max_ctx=8192, rope_base=500000.0, eps=float(np.float32(1e-6)))
-    # defaults: n_kv = n_heads, n_ff = 4 hidden, context 2048, base 10000, eps 1e-5;
-    # the alternative epsilon key; another architecture name
+                        max_ctx=8192, vocab=128256, rope_base=500000.0, eps=float(np.float32(1e-6)))
+    # defaults: n_kv = n_heads, n_ff = 4 hidden, context 2048, vocab 32000, base 10000,
+    # eps 1e-5; the alternative epsilon key; another architecture name
     small = cfg([("embedding_length", VT.UInt32, 256), ("block_count", VT.UInt32, 2),
                  ("attention.head_count", VT.UInt32, 4), ("layer_norm_epsilon", VT.Float32, 2e-5)], arch="mistral")
     assert small == dict(hidden=256, n_layers=2, n_heads=4, n_kv_heads=4, head_dim=64, n_ff=1024, max_ctx=2048,
-                         rope_base=10000.0, eps=float(np.float32(2e-5)))
+                         vocab=32000, rope_base=10000.0, eps=float(np.float32(2e-5)))
     assert cfg([("embedding_length", VT.UInt32, 256), ("block_count", VT.UInt32, 2),
                 ("attention.head_count", VT.UInt32, 4)])["eps"] == 1e-5
-    with pytest.raises(ValueError):
-        cfg([("block_count", VT.UInt32, 2), ("attention.head_count", VT.UInt32, 4)])
+    # the fallback keys: embed_dim, layer_count, tokenizer.ggml.context_length,
+    # attention.rope_theta, tokenizer.ggml.tokens.len
+    alt = cfg([("embed_dim", VT.UInt32, 512), ("layer_count", VT.UInt32, 3), ("attention.head_count", VT.UInt32, 8),
+               ("attention.rope_theta", VT.Float32, 1e6)],
+              top=[("tokenizer.ggml.context_length", VT.UInt32, 4096), ("tokenizer.ggml.tokens.len", VT.UInt32, 777)])
+    assert alt == dict(hidden=512, n_layers=3, n_heads=8, n_kv_heads=8, head_dim=64, n_ff=2048, max_ctx=4096,
+                       vocab=777, rope_base=1e6, eps=1e-5)
+    # the primary keys win over the fallbacks
+    both = cfg([("embedding_length", VT.UInt32, 256), ("embed_dim", VT.UInt32, 512), ("block_count", VT.UInt32, 2),
+                ("layer_count", VT.UInt32, 5), ("attention.head_count", VT.UInt32, 4),
+                ("rope.freq_base", VT.Float32, 5e5), ("attention.rope_theta", VT.Float32, 1e6)])
+    assert (both["hidden"], both["n_layers"], both["rope_base"]) == (256, 2, 5e5)
+    # nothing but the architecture: the reference's defaults (hidden 4096, 32 layers, 32 heads)
+    bare = cfg([])
+    assert (bare["hidden"], bare["n_layers"], bare["n_heads"], bare["n_ff"]) == (4096, 32, 32, 16384)
+    # no architecture: an error, as "No architecture specified in GGUF"
+    with pytest.raises(ValueError, match="architecture"):
+        cfg([], arch=None)
+
+
+def _llama_gguf(hidden=256, n_heads=4, n_kv=2, n_ff=512, vocab=64, kv_meta=True, ff_meta=None, output=True,
+                embd=True):
+    """A one-layer Q8_0 llama GGUF file's builder (no GPU needed to build it)."""
+    from woolly_amd.gguf import GGMLType
+
+    d = hidden // n_heads
+    b = MockGGUFBuilder().add_metadata("general.architecture", VT.String, "llama")
+    meta = [("embedding_length", hidden), ("block_count", 1), ("attention.head_count", n_heads),
+            ("feed_forward_length", ff_meta or n_ff)]
+    if kv_meta:
+        meta.append(("attention.head_count_kv", n_kv))
+    for key, v in meta:
+        b.add_metadata("llama." + key, VT.UInt32, v)
+    q8 = lambda n, k, s: synth.quantized_weight(8, n, k, seed=s).tobytes()
+    norm = np.ones(hidden, np.float32).tobytes()
+    b.add_tensor("blk.0.attn_norm.weight", [hidden], GGMLType.F32, norm)
+    b.add_tensor("blk.0.ffn_norm.weight", [hidden], GGMLType.F32, norm)
+    for nm, (n, k) in {"attn_q": (n_heads * d, hidden), "attn_k": (n_kv * d, hidden), "attn_v": (n_kv * d, hidden),
+                       "attn_output": (hidden, n_heads * d), "ffn_gate": (n_ff, hidden), "ffn_up": (n_ff, hidden),
+                       "ffn_down": (hidden, n_ff)}.items():
+        b.add_tensor(f"blk.0.{nm}.weight", [k, n], GGMLType.Q8_0, q8(n, k, len(nm)))
+    b.add_tensor("output_norm.weight", [hidden], GGMLType.F32, norm)
+    if embd:
+        b.add_tensor("token_embd.weight", [hidden, vocab], GGMLType.Q8_0, q8(vocab, hidden, 99))
+    if output:
+        b.add_tensor("output.weight", [hidden, vocab], GGMLType.Q8_0, q8(vocab, hidden, 98))
+    return b
+
+
+def test_llama_from_gguf_rejects_mismatched_dims():
+    """from_gguf compares every tensor's dims with the config before it uploads
+    anything: a GQA file without attention.head_count_kv (n_kv then defaults to
+    the head count) and a wrong feed_forward_length raise ValueError instead of
+    letting the kernels read past the weights; a file with neither output.weight
+    nor token_embd.weight has no head.  No GPU is touched."""
+    from woolly_amd import ops
+
+    with pytest.raises(ValueError, match="attn_k"):
+        ops.LlamaModel.from_gguf(load(_llama_gguf(kv_meta=False).build()))
+    with pytest.raises(ValueError, match="ffn_gate"):
+        ops.LlamaModel.from_gguf(load(_llama_gguf(ff_meta=1024).build()))
+    with pytest.raises(ValueError, match="neither"):
+        ops.LlamaModel.from_gguf(load(_llama_gguf(output=False, embd=False).build()))

@@ -1,0 +1,201 @@
+"""Every BASELINE configuration at its full size against the f64 oracle, with
+the achieved errors reported per configuration (tests/_gpu.report; set
+WH_PARITY_LOG to collect them as JSON lines).
+
+  config 0   Q4_0 GEMV 4096 x 4096                    quantization.rs:1100-1132
+  target     Q4_0 GEMV 14336 x 4096
+  config 1a  Q8_0 GEMV 14336 x 4096                    quantization.rs:1135-1163
+  config 1b  Q4_1 GEMV 14336 x 4096                    dequantize_q4_1 :490-511 + f32 dot
+  config 2   Q4_0 GEMM N=14336, K=4096, M = 1, 8, 64, 512, 2048
+                                                       ops/matmul.rs:83-259, 608-646
+  config 3   SwiGLU FFN layer, Llama-3-8B shape, M = 1, 512, 2048
+                                                       feedforward.rs:93-127
+  config 4   the whole 32-layer decode step with the Q8_0 128256 x 4096 head
+             at context 4096                           lazy_transformer.rs:98-456, 1155-1336
+
+Bars (north_star): rel-L2 <= 1e-4 and max-abs <= 1e-3 of the f64 oracle for
+matmul / FFN outputs and for the step's logits.  The step's hidden state is a
+residual sum with RMS ~1e3 after 32 layers, where one f32 ulp of its largest
+elements already exceeds 1e-3; it is held to rel-L2 <= 1e-4 and to max-abs
+<= 1e-3 per 300 of its RMS, the rule the FFN tests apply to large outputs.
+Token rows of a GEMM or FFN are independent, so for M >= 64 the oracle checks
+the first, a middle and the last token tile's rows."""
+import numpy as np
+import pytest
+
+from tests._gpu import down, report, up
+from tests._oracle import max_abs, rel_l2
+from tests.test_oracle_decode import small_layer
+from woolly_amd import ops, synth
+from woolly_amd.device import DeviceBuffer, Graph, Stream
+
+pytestmark = pytest.mark.gpu
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
+REL_L2, MAX_ABS = 1e-4, 1e-3
+
+
+def sample_rows(m: int) -> list[int]:
+    """First, middle and last 16-token tile (all rows when m <= 48)."""
+    if m <= 48:
+        return list(range(m))
+    mid = (m // 2) // 16 * 16
+    return sorted(set(range(16)) | set(range(mid, mid + 16)) | set(range(m - 16, m)))
+
+
+@pytest.mark.parametrize("tag,t,n,k,seed", [("config0_q4_0_4096x4096", Q4_0, 4096, 4096, 0),
+                                            ("target_q4_0_14336x4096", Q4_0, 14336, 4096, 3),
+                                            ("config1a_q8_0_14336x4096", Q8_0, 14336, 4096, 1),
+                                            ("config1b_q4_1_14336x4096", Q4_1, 14336, 4096, 2)])
+def test_gemv_configs(gpu, orc, tag, t, n, k, seed):
+    print(f"[case] {tag}", flush=True)
+    w = synth.quantized_weight(t, n, k, seed=seed)
+    x = synth.activations(k, seed=seed)
+    wb, xb, yb = up(w)[0], up(x)[0], DeviceBuffer(4 * n)
+    ops.quantized_matvec(t, wb, w.nbytes, xb, yb, n, k)
+    got = down(yb, np.float32, n)
+    ref = orc.matvec_f64(t, w, x, n, k)[1]
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    # the reference's own order-exact f32 scalar loop on the same input
+    ref32 = orc.matvec_f32(t, w, x, n, k)[1] if t != Q4_1 else None
+    extra = {} if ref32 is None else {"ref_f32_max_abs": max_abs(ref32, ref)}
+    report(tag, r, a, ref, **extra)
+    assert r <= REL_L2 and a <= MAX_ABS
+
+
+@pytest.mark.parametrize("m", [1, 8, 64, 512, 2048])
+def test_gemm_config2(gpu, orc, m):
+    """Config 2: X[m, 4096] ~ N(0,1) times the Q4_0 weight [14336, 4096]."""
+    n, k = 14336, 4096
+    print(f"[case] config2 m={m}", flush=True)
+    w = synth.quantized_weight(Q4_0, n, k, seed=4)
+    x = synth.activations(m * k, seed=4, stream=101).reshape(m, k)
+    wb, xb, yb = up(w)[0], up(x)[0], DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_workspace_bytes(Q4_0, n, k, m)
+    ws = DeviceBuffer(max(wsz, 256))
+    ops.quantized_matmul(Q4_0, wb, w.nbytes, n, k, xb, m, yb, ws, wsz)
+    got = down(yb, np.float32, m * n).reshape(m, n)
+    rows = sample_rows(m)
+    ref = orc.matmul_rows_f64(Q4_0, w, n, k, x, m, rows)
+    g = got[rows]
+    r, a = rel_l2(g, ref), max_abs(g, ref)
+    report(f"config2_q4_0_gemm_m{m}", r, a, ref, rows_checked=len(rows))
+    assert r <= REL_L2 and a <= MAX_ABS
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("m", [1, 512, 2048])
+def test_ffn_config3(gpu, orc, m):
+    """Config 3: RMSNorm + gate/up + SwiGLU + down, Llama-3-8B shape, Q4_0."""
+    hidden, n_ff = 4096, 14336
+    print(f"[case] config3 m={m}", flush=True)
+    L = synth.ffn_layer(Q4_0, hidden, n_ff, m, seed=5)
+    b = {kk: up(v)[0] for kk, v in L.items()}
+    out = DeviceBuffer(4 * m * hidden)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m)
+    ws = DeviceBuffer(wsz)
+    ops.ffn_swiglu(Q4_0, b["gate"], b["up"], b["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"], m, out, ws, wsz)
+    got = down(out, np.float32, m * hidden).reshape(m, hidden)
+    rows = sample_rows(m) if m > 1 else [0]
+    rows = rows if m <= 48 else [rows[0], rows[1], rows[len(rows) // 2], rows[-1]]
+    ref = orc.ffn_rows_f64(Q4_0, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5, L["x"], rows)
+    g = got[rows]
+    r, a = rel_l2(g, ref), max_abs(g, ref)
+    report(f"config3_ffn_q4_0_m{m}", r, a, ref, rows_checked=len(rows))
+    assert r <= REL_L2 and a <= MAX_ABS
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.timeout(900)
+def test_decode_step_config4_full(gpu, orc):
+    """Config 4: one decode step of a 32-layer Llama-3-8B-shaped Q4_0 model with
+    the Q8_0 128256 x 4096 output head, f16 KV caches of 4096 positions filled
+    ~N(0,1), at position 4095 (attention over all 4096 rows).  Two weight sets
+    alternate between even and odd layers and every layer has its own caches,
+    so a mix-up of layers fails.  The f64 oracle steps the same 32 layers on
+    the rows the GPU stored (each within one f16 ulp of the oracle's own), then
+    the head; a HIP-graph replay of the step reproduces the eager step bit for
+    bit, three times, with eager work in between."""
+    hidden, n_heads, n_kv, d, n_ff, vocab, ctx, n_layers = 4096, 32, 8, 128, 14336, 128256, 4096, 32
+    pos = ctx - 1
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    print("[case] config4 full step: generating weights", flush=True)
+    Ls = [small_layer(Q4_0, hidden, n_heads, n_kv, d, n_ff, seed=90 + i) for i in range(2)]
+    wdev = [{kk: up(v)[0] for kk, v in L.items()} for L in Ls]
+    rng = np.random.default_rng(6)
+    caches, devs = [], []
+    for li in range(n_layers):
+        kc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+        vc = rng.standard_normal((ctx, n_kv, d)).astype(np.float16).view(np.uint16)
+        dev = dict(wdev[li % 2])
+        dev["k_cache"], dev["v_cache"] = up(kc)[0], up(vc)[0]
+        caches.append((kc, vc))
+        devs.append(dev)
+    part = synth.quantized_weight(Q8_0, vocab // 8, hidden, seed=70)
+    head = np.concatenate([part] * 8)
+    onorm = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    inv = orc.rope_inv_freq(500000.0, d)
+    model = ops.LlamaModel(Q4_0, dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff,
+                                      max_ctx=ctx, vocab=vocab, eps=1e-5),
+                           devs, up(inv)[0], up(onorm)[0], up(head)[0], Q8_0)
+    wsz = model.workspace_bytes()
+    ws = DeviceBuffer(wsz)
+    x0 = synth.activations(hidden, seed=6)
+    xb, lb = up(x0)[0], DeviceBuffer(4 * vocab)
+    print("[case] config4 full step: eager step", flush=True)
+    model.decode_step(pos, xb, lb, ws, wsz)
+    got_x, got_l = down(xb, np.float32, hidden), down(lb, np.float32, vocab)
+    assert np.all(np.isfinite(got_l))
+
+    # graph replays == the eager step, bit for bit (x reset and the same rows
+    # rewritten at pos between replays)
+    stream = Stream()
+    xb.upload(x0)
+    with Graph.capture(stream) as graph:
+        model.decode_step(pos, xb, lb, ws, wsz, stream)
+    for rep in range(3):
+        xb.upload(x0)
+        graph.launch(stream)
+        stream.synchronize()
+        gx, gl = down(xb, np.float32, hidden), down(lb, np.float32, vocab)
+        assert np.array_equal(gx.view(np.uint32), got_x.view(np.uint32)), rep
+        assert np.array_equal(gl.view(np.uint32), got_l.view(np.uint32)), rep
+        # eager work between replays
+        ops.quantized_matvec(Q4_0, wdev[0]["wq"], Ls[0]["wq"].nbytes, xb, lb, n_heads * d, hidden)
+    graph.destroy()
+    stream.destroy()
+
+    print("[case] config4 full step: f64 oracle over 32 layers", flush=True)
+    x = x0.astype(np.float64)
+    for li in range(n_layers):
+        kc, vc = caches[li]
+        kg = down(devs[li]["k_cache"], np.uint16, n_kv * d, offset=pos * n_kv * d * 2)
+        vg = down(devs[li]["v_cache"], np.uint16, n_kv * d, offset=pos * n_kv * d * 2)
+        if li in (0, 1, n_layers - 1):
+            # the stored rows within one f16 ulp of the oracle's own (a few
+            # 1e-4 of slack after the first layer, whose inputs already differ)
+            kr, vr = kc.copy(), vc.copy()
+            orc.llama_layer_decode_f64(Q4_0, Ls[li % 2], dims, inv, kr, vr, pos, x)
+            slack = 0.0 if li == 0 else 1e-4
+            gk = kg.view(np.float16).astype(np.float64)
+            rk = kr[pos].reshape(-1).view(np.float16).astype(np.float64)
+            gv = vg.view(np.float16).astype(np.float64)
+            rv = vr[pos].reshape(-1).view(np.float16).astype(np.float64)
+            for gg, rr in ((gk, rk), (gv, rv)):
+                ulp = np.spacing(np.abs(rr).astype(np.float16)).astype(np.float64)
+                assert np.all(np.abs(gg - rr) <= ulp + slack * np.max(np.abs(rr))), li
+        # attend to the GPU's stored rows
+        kc2, vc2 = kc.copy(), vc.copy()
+        kc2[pos] = kg.reshape(n_kv, d)
+        vc2[pos] = vg.reshape(n_kv, d)
+        x = orc.llama_layer_decode_f64(Q4_0, Ls[li % 2], dims, inv, kc2, vc2, pos, x, store_new=False)
+        if li % 8 == 7:
+            print(f"[case] config4 oracle: layer {li + 1}/{n_layers}, rms(x)={np.sqrt(np.mean(x ** 2)):.1f}",
+                  flush=True)
+    logits = orc.output_head_f64(Q8_0, head, onorm, 1e-5, x, hidden, vocab)
+    rx, ax = rel_l2(got_x, x), max_abs(got_x, x)
+    rl, al = rel_l2(got_l, logits), max_abs(got_l, logits)
+    report("config4_decode_step_hidden", rx, ax, x)
+    report("config4_decode_step_logits", rl, al, logits)
+    rms_x = float(np.sqrt(np.mean(x ** 2)))
+    assert rx <= REL_L2 and ax <= MAX_ABS * max(1.0, rms_x / 300.0)
+    assert rl <= REL_L2 and al <= MAX_ABS

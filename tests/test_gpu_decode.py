@@ -6,7 +6,7 @@ output head.  Bars: rel-L2 <= 1e-4 and max-abs <= 1e-3 of the f64 oracle
 import numpy as np
 import pytest
 
-from tests._gpu import down, up
+from tests._gpu import down, report, up
 from tests._oracle import max_abs, rel_l2
 from tests.test_oracle_decode import MIXED, PROJ, mixed_layer, small_layer
 from woolly_amd import ops, synth
@@ -19,7 +19,7 @@ REL_L2 = 1e-4
 
 def check(got, ref, tag, abs_bar=1e-3):
     r, a = rel_l2(got, ref), max_abs(got, ref)
-    print(f"[result] {tag} rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+    report(tag, r, a, ref, abs_bar=float(abs_bar))
     assert r <= REL_L2 and a <= abs_bar, (tag, r, a)
 
 
@@ -350,3 +350,90 @@ def test_llama_model_from_gguf_q4_k_m(gpu, orc, tmp_path):
         logits = orc.output_head_f64(Q6_K, head, onorm, 1e-5, x, hidden, vocab)
         check(got_x, x, f"gguf q4_k_m pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
         check(got_l, logits, f"gguf q4_k_m pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+
+
+EMB_TYPES = [0, 1, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K]
+
+
+def emb_table(t, vocab, hidden, seed):
+    if t == 0:
+        return synth.activations(vocab * hidden, seed=seed).view(np.uint8)
+    if t == 1:
+        return synth.activations(vocab * hidden, seed=seed).astype(np.float16).view(np.uint8)
+    return synth.quantized_weight(t, vocab, hidden, seed=seed)
+
+
+@pytest.mark.parametrize("t", EMB_TYPES)
+def test_embedding_lookup_bit_exact(gpu, orc, t):
+    """embedding_lookup (tensor_utils.rs:548-590) on the device: every requested
+    row equals the oracle's dequantization of the table, bit for bit; an id past
+    the vocabulary gives a NaN row from the C ABI and ValueError from the host
+    mirror, as the reference's TENSOR_EMBEDDING_TOKEN_OUT_OF_RANGE."""
+    from woolly_amd import _lib
+
+    vocab, hidden = 300, 512
+    tab = emb_table(t, vocab, hidden, seed=40 + t)
+    st, full = orc.dequantize(t, tab, vocab * hidden)
+    assert st == 0
+    full = full.reshape(vocab, hidden)
+    ids = [0, 1, 299, 150, 7, 7]
+    tb = up(tab)[0]
+    out = DeviceBuffer(4 * len(ids) * hidden)
+    keep = ops.embedding_lookup(t, tb, vocab, hidden, ids, out)
+    got = down(out, np.float32, len(ids) * hidden).reshape(len(ids), hidden)
+    assert np.array_equal(got.view(np.uint32), full[ids].view(np.uint32)), t
+    del keep
+    with pytest.raises(ValueError):
+        ops.embedding_lookup(t, tb, vocab, hidden, [3, vocab], out)
+    idb = up(np.array([2, vocab, 5], np.uint32))[0]
+    _lib.check(_lib.load().wh_embedding_lookup(t, tb.ptr, vocab, hidden, idb.ptr, 3, out.ptr, None))
+    got = down(out, np.float32, 3 * hidden).reshape(3, hidden)
+    assert np.array_equal(got[0].view(np.uint32), full[2].view(np.uint32))
+    assert np.all(np.isnan(got[1]))
+    assert np.array_equal(got[2].view(np.uint32), full[5].view(np.uint32))
+
+
+def test_forward_token_tied_head_gguf(gpu, orc, tmp_path):
+    """A GGUF file without output.weight (the head tied to token_embd.weight,
+    lazy_transformer.rs:1301-1316), loaded with LlamaModel.from_gguf and run
+    from token ids held on the device (forward for one token, :1155-1230):
+    three steps against the f64 oracle starting from the dequantized embedding
+    rows, and each step equal bit for bit to decode_step on the uploaded row."""
+    from tests.test_gguf import _llama_gguf, load
+
+    hidden, n_heads, n_kv, d, n_ff, vocab = 256, 4, 2, 64, 512, 64
+    ld = load(_llama_gguf(hidden, n_heads, n_kv, n_ff, vocab, output=False).build(), tmp_path)
+    model = ops.LlamaModel.from_gguf(ld, max_ctx=8)
+    assert model.tied_head and model.dims["vocab"] == vocab
+    L = {k: np.array(ld.tensor_data(f"blk.0.{nm}.weight")) for k, nm in
+         {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "w_gate": "ffn_gate",
+          "w_up": "ffn_up", "w_down": "ffn_down"}.items()}
+    L["attn_norm"] = L["ffn_norm"] = np.ones(hidden, np.float32)
+    embd = np.array(ld.tensor_data("token_embd.weight"))
+    onorm = np.ones(hidden, np.float32)
+    st, rows = orc.dequantize(Q8_0, embd, vocab * hidden)
+    rows = rows.reshape(vocab, hidden)
+    inv = orc.rope_inv_freq(10000.0, d)
+    dims = (hidden, n_heads, n_kv, d, n_ff, 1e-5)
+    ws = DeviceBuffer(model.workspace_bytes())
+    xb, lb, x2, l2 = DeviceBuffer(4 * hidden), DeviceBuffer(4 * vocab), DeviceBuffer(4 * hidden), DeviceBuffer(4 * vocab)
+    tok = DeviceBuffer(4)
+    cache_dev = model._keep[0][0]
+    for pos, token in enumerate([5, 17, 63]):
+        print(f"[case] forward_token tied pos={pos} token={token}", flush=True)
+        tok.upload(np.array([token], np.uint32))
+        # decode_step on the uploaded row first (it writes the same cache row)
+        x2.upload(rows[token])
+        model.decode_step(pos, x2, l2, ws, model.workspace_bytes())
+        model.forward_token(tok, pos, xb, lb, ws, model.workspace_bytes())
+        got_x, got_l = down(xb, np.float32, hidden), down(lb, np.float32, vocab)
+        assert np.array_equal(got_x.view(np.uint32), down(x2, np.float32, hidden).view(np.uint32))
+        assert np.array_equal(got_l.view(np.uint32), down(l2, np.float32, vocab).view(np.uint32))
+        # the oracle attends to the rows the GPU stored (an f16 rounding flip of
+        # a new k or v is not an arithmetic difference)
+        kc = down(cache_dev["k_cache"], np.uint16, 8 * n_kv * d).reshape(8, n_kv, d)
+        vc = down(cache_dev["v_cache"], np.uint16, 8 * n_kv * d).reshape(8, n_kv, d)
+        x = orc.llama_layer_decode_f64(Q8_0, L, dims, inv, kc, vc, pos, rows[token].astype(np.float64),
+                                       store_new=False)
+        logits = orc.output_head_f64(Q8_0, embd, onorm, 1e-5, x, hidden, vocab)
+        check(got_l, logits, f"forward_token tied head pos={pos} logits")

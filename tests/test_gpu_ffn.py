@@ -4,7 +4,7 @@ lazy_transformer.rs:1073-1123 / feedforward.rs:93-127)."""
 import numpy as np
 import pytest
 
-from tests._gpu import down, up
+from tests._gpu import down, report, up
 from tests._oracle import max_abs, rel_l2
 from woolly_amd import ops, synth
 from woolly_amd.device import DeviceBuffer
@@ -69,7 +69,7 @@ def test_matmul_parity(gpu, orc, t, m, n, k):
     got = down(yb, np.float32, m * n).reshape(m, n)
     ref = orc.matmul_rows_f64(t, w, n, k, x, m, np.arange(m))
     r, a = rel_l2(got, ref), max_abs(got, ref)
-    print(f"[result] matmul rel_l2={r:.3e} max_abs={a:.3e}", flush=True)
+    report(f"matmul t={t} m={m} n={n} k={k}", r, a, ref)
     assert r <= REL_L2 and a <= max_abs_bar(ref)
 
 

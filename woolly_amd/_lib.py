@@ -112,6 +112,8 @@ class wh_llama_model(C.Structure):
         ("output_norm", C.c_void_p),
         ("output_type", C.c_int),
         ("output", C.c_void_p),
+        ("token_embd_type", C.c_int),
+        ("token_embd", C.c_void_p),
     ]
 
 
@@ -179,6 +181,8 @@ SIGNATURES = {
     "wh_llama_decode_workspace_bytes": (_sz, [C.POINTER(wh_llama_model)]),
     "wh_llama_layer_decode": (_int, [C.POINTER(wh_llama_model), _sz, _sz, _f32p, _vp, _sz, _vp]),
     "wh_llama_decode_step": (_int, [C.POINTER(wh_llama_model), _sz, _f32p, _f32p, _vp, _sz, _vp]),
+    "wh_llama_forward_token": (_int, [C.POINTER(wh_llama_model), _vp, _sz, _f32p, _f32p, _vp, _sz, _vp]),
+    "wh_embedding_lookup": (_int, [_int, _vp, _sz, _sz, _vp, _sz, _f32p, _vp]),
     "wh_gguf_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
     "wh_gguf_open_buffer": (_int, [_vp, _sz, C.POINTER(_vp)]),
     "wh_gguf_close": (_int, [_vp]),

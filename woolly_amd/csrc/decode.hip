@@ -14,6 +14,7 @@
 // RMSNorm).  Nothing here allocates or synchronises, so a caller can capture
 // the step into a HIP graph.
 #include <cmath>
+#include <cstdio>
 
 #include "wh_common.hpp"
 
@@ -109,6 +110,12 @@ int check_model(const char* fn, const wh_llama_model* m) {
     if (!L.k_cache || !L.v_cache || !wh::aligned(L.k_cache, 16) || !wh::aligned(L.v_cache, 16))
       return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: layer %zu KV caches must be non-null and 16-byte aligned",
                            fn, l);
+    const void* ptrs[9] = {L.attn_norm, L.wq, L.wk, L.wv, L.wo, L.ffn_norm, L.w_gate, L.w_up, L.w_down};
+    static const char* const names[9] = {"attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate", "w_up", "w_down"};
+    for (int i = 0; i < 9; i++)
+      if (!ptrs[i]) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: layer %zu %s is a null pointer", fn, l, names[i]);
+    if (!wh::aligned(L.attn_norm, 4) || !wh::aligned(L.ffn_norm, 4))
+      return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: layer %zu norm weights must be 4-byte aligned", fn, l);
     const LayerTypes t = layer_types(m, L);
     const size_t qd = m->n_heads * m->head_dim;
     const int types[7] = {t.q, t.k, t.v, t.o, t.g, t.u, t.d};
@@ -119,6 +126,28 @@ int check_model(const char* fn, const wh_llama_model* m) {
     }
   }
   return WH_OK;
+}
+
+// The output head of a step that writes logits: its type, pointers and vocab.
+int check_head(const char* fn, const wh_llama_model* m) {
+  char what[96];
+  std::snprintf(what, sizeof(what), "%s (output head)", fn);
+  const int st = check_type(what, m->output_type, m->hidden);
+  if (st) return st;
+  if (!m->output || !m->output_norm)
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: null output head or output_norm", fn);
+  if (m->vocab == 0 || m->vocab >= (static_cast<size_t>(1) << 30))
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: vocab = %zu out of range", fn, m->vocab);
+  return WH_OK;
+}
+
+// A status of INVALID_SHAPE from the kernels' layout checks, reported with the
+// entry point's name when no kernel takes the model's shapes.
+int shape_status(const char* fn, int st) {
+  if (st != WH_ERR_INVALID_SHAPE) return st;
+  char detail[256];
+  std::snprintf(detail, sizeof(detail), "%s", wh_last_error());
+  return wh::set_error(st, "%s: no kernel takes this layer shape (%s)", fn, detail);
 }
 
 int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, float* x, const StepWs& w,
@@ -263,33 +292,56 @@ WH_API int wh_llama_layer_decode(const wh_llama_model* model, size_t layer, size
                          "llama_layer_decode: workspace too small: needed %zu bytes, available %zu", w.bytes,
                          workspace ? workspace_bytes : static_cast<size_t>(0));
   if (!x) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_layer_decode: null x");
-  return layer_step(model, model->layers[layer], pos, x, w, hs(stream));
+  return shape_status("llama_layer_decode", layer_step(model, model->layers[layer], pos, x, w, hs(stream)));
 }
+
+namespace {
+
+// Checks and launches of one step (x already holds the token's embedding);
+// every check runs before the first launch, so a rejected call changes
+// neither x nor the caches.
+int decode_step(const char* fn, const wh_llama_model* model, const uint32_t* token, size_t pos, float* x,
+                float* logits, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  int st = check_model(fn, model);
+  if (st) return st;
+  if (pos >= model->max_ctx)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: position %zu beyond max_ctx %zu", fn, pos, model->max_ctx);
+  const StepWs w = step_layout(model, workspace);
+  if (!workspace || workspace_bytes < w.bytes)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL, "%s: workspace too small: needed %zu bytes, available %zu", fn,
+                         w.bytes, workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!x) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: null x", fn);
+  if (logits && (st = check_head(fn, model))) return st;
+  if (token) {
+    if (!model->token_embd)
+      return wh::set_error(WH_ERR_INVALID_ARGUMENT, "%s: the model has no token_embd table", fn);
+    if ((st = wh::check_embedding_args(fn, model->token_embd_type, model->token_embd, model->vocab, model->hidden,
+                                       token, x)))
+      return st;
+    if ((st = wh::launch_embedding_lookup(model->token_embd_type, model->token_embd, model->vocab, model->hidden,
+                                          token, 1, x, s)))
+      return st;
+  }
+  for (size_t l = 0; l < model->n_layers; l++) {
+    st = layer_step(model, model->layers[l], pos, x, w, s);
+    if (st) return shape_status(fn, st);
+  }
+  if (!logits) return WH_OK;
+  const void* head[1] = {model->output};
+  const size_t rows[1] = {model->vocab};
+  return shape_status(fn, gemv_fused_or_split(model->output_type, head, rows, 1, x, model->output_norm, model->eps,
+                                               nullptr, logits, model->hidden, w.xn, s));
+}
+
+}  // namespace
 
 WH_API int wh_llama_decode_step(const wh_llama_model* model, size_t pos, float* x, float* logits, void* workspace,
                                 size_t workspace_bytes, wh_stream_t stream) {
-  int st = check_model("llama_decode_step", model);
-  if (st) return st;
-  if (pos >= model->max_ctx)
-    return wh::set_error(WH_ERR_INVALID_SHAPE, "llama_decode_step: position %zu beyond max_ctx %zu", pos,
-                         model->max_ctx);
-  const StepWs w = step_layout(model, workspace);
-  if (!workspace || workspace_bytes < w.bytes)
-    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
-                         "llama_decode_step: workspace too small: needed %zu bytes, available %zu", w.bytes,
-                         workspace ? workspace_bytes : static_cast<size_t>(0));
-  if (!x) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_decode_step: null x");
-  for (size_t l = 0; l < model->n_layers; l++) {
-    st = layer_step(model, model->layers[l], pos, x, w, hs(stream));
-    if (st) return st;
-  }
-  if (!logits) return WH_OK;
-  st = check_type("llama_decode_step (output head)", model->output_type, model->hidden);
-  if (st) return st;
-  if (!model->output || !model->output_norm)
-    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_decode_step: null output head or output_norm");
-  const void* head[1] = {model->output};
-  const size_t rows[1] = {model->vocab};
-  return gemv_fused_or_split(model->output_type, head, rows, 1, x, model->output_norm, model->eps, nullptr, logits,
-                             model->hidden, w.xn, hs(stream));
+  return decode_step("llama_decode_step", model, nullptr, pos, x, logits, workspace, workspace_bytes, hs(stream));
+}
+
+WH_API int wh_llama_forward_token(const wh_llama_model* model, const uint32_t* token, size_t pos, float* x,
+                                  float* logits, void* workspace, size_t workspace_bytes, wh_stream_t stream) {
+  if (!token) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_forward_token: null token");
+  return decode_step("llama_forward_token", model, token, pos, x, logits, workspace, workspace_bytes, hs(stream));
 }

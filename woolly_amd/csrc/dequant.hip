@@ -14,61 +14,9 @@
 // 128-bit store; a wavefront writes 1 KiB contiguously.  Eight threads share
 // a block and read its scale and 4 quant bytes with 16-bit loads (blocks are
 // only 2-byte aligned in the stream); the repeated scale reads hit L1.
-#include "wh_common.hpp"
+#include "wh_blocks.hpp"
 
 namespace {
-
-template <int ALIGN>
-__device__ __forceinline__ uint32_t ld16(const uint8_t* p) {
-  if constexpr (ALIGN >= 2) {
-    return *reinterpret_cast<const uint16_t*>(p);
-  } else {
-    return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
-  }
-}
-
-template <int ALIGN>
-__device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
-  if constexpr (ALIGN >= 4) {
-    return *reinterpret_cast<const uint32_t*>(p);
-  } else {
-    return ld16<ALIGN>(p) | (ld16<ALIGN>(p + 2) << 16);
-  }
-}
-
-// Decodes quad c (0..7) of block `blk` into v[0..4).
-template <int TYPE, int ALIGN>
-__device__ __forceinline__ void decode_quad(const uint8_t* blk, int c, float v[4]) {
-  if constexpr (TYPE == WH_TYPE_Q4_0) {
-    const float d = whd::f16_bits_to_f32(ld16<ALIGN>(blk));
-    const uint32_t w = ld32<(ALIGN >= 2 ? 2 : 1)>(blk + 2 + 4 * (c & 3));
-    const uint32_t nib = (c >= 4) ? ((w >> 4) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = static_cast<int>((nib >> (8 * i)) & 0xFFu) - 8;
-      v[i] = static_cast<float>(q) * d;
-    }
-  } else if constexpr (TYPE == WH_TYPE_Q4_1) {
-    const uint32_t dm = ld32<ALIGN>(blk);
-    const float d = whd::f16_bits_to_f32(dm & 0xFFFFu);
-    const float m = whd::f16_bits_to_f32(dm >> 16);
-    const uint32_t w = ld32<ALIGN>(blk + 4 + 4 * (c & 3));
-    const uint32_t nib = (c >= 4) ? ((w >> 4) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float q = static_cast<float>((nib >> (8 * i)) & 0xFFu);
-      v[i] = __fadd_rn(__fmul_rn(q, d), m);
-    }
-  } else {  // Q8_0
-    const float d = whd::f16_bits_to_f32(ld16<ALIGN>(blk));
-    const uint32_t w = ld32<(ALIGN >= 2 ? 2 : 1)>(blk + 2 + 4 * c);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = static_cast<int>(static_cast<int8_t>((w >> (8 * i)) & 0xFFu));
-      v[i] = static_cast<float>(q) * d;
-    }
-  }
-}
 
 template <int TYPE, int ALIGN, bool OUT16>
 __global__ __launch_bounds__(256) void dequant_blocks_kernel(const uint8_t* __restrict__ data,
@@ -82,7 +30,7 @@ __global__ __launch_bounds__(256) void dequant_blocks_kernel(const uint8_t* __re
     const size_t b = q >> 3;
     const int c = static_cast<int>(q & 7);
     float v[4];
-    decode_quad<TYPE, ALIGN>(data + b * TS, c, v);
+    whd::decode_quad<TYPE, ALIGN>(data + b * TS, c, v);
     const size_t e = q * 4;
     if (OUT16 && e + 4 <= nelements) {
       *reinterpret_cast<float4*>(out + e) = make_float4(v[0], v[1], v[2], v[3]);

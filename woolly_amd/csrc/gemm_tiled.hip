@@ -396,17 +396,28 @@ __device__ __forceinline__ void unpack_part(int p, uint32_t u0, uint32_t u1, uin
 // base + voff land at LDS address lds + 16 l (4 l).  Issued through inline asm
 // so that the compiler does not treat them as pending LDS writes (it would
 // otherwise wait for every copy in flight before each LDS read); completion
-// is tracked explicitly with wait_vmcnt.  M0 is written here; the compiler
-// sets M0 itself before any instruction of its own that reads it.
+// is tracked explicitly with wait_vmcnt.  The copy reads its LDS address from
+// M0, a register the compiler reserves: the statement saves M0 in an SGPR of
+// its own, sets it (one wait state before the copy reads it, as GFX9-family
+// parts require after an SALU write of M0) and restores it, so M0 holds the
+// compiler's value again after every copy.
 __device__ __forceinline__ void copy16_to_lds(const void* base, uint32_t voff, uint32_t lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
-               : "memory");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory");
 }
 __device__ __forceinline__ void copy4_to_lds(const void* base, uint32_t voff, uint32_t lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(m0)
-               : "memory");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   // generic -> LDS address space (an address-space cast), then its 32-bit address

@@ -459,9 +459,14 @@ __device__ __forceinline__ void ring_copy16(const void* base, uint32_t voff, uin
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
   const uint64_t ub = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(reinterpret_cast<const void*>(ub)),
-               "s"(m0)
-               : "memory");
+  // M0 (reserved by the compiler) is saved in an SGPR, set for the copy after
+  // one wait state, and restored
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(reinterpret_cast<const void*>(ub)), "s"(m0)
+      : "memory");
 }
 template <int N>
 __device__ __forceinline__ void ring_wait() {
@@ -796,13 +801,15 @@ GemvArgs plain_args(const uint8_t* w, const float* x, float* y, size_t n_rows) {
   return a;
 }
 
-std::atomic<int> g_gemv_mode{WH_GEMV_AUTO};
+// wh_gemv_select's setting, per calling thread (like wh_last_error): a switch
+// on one thread never changes what another thread launches or captures.
+thread_local int t_gemv_mode = WH_GEMV_AUTO;
 
 // The matrix-core kernel pays for its activation preparation and its 16-row
 // steps on short rows and few rows; below these sizes the streaming kernels
 // are used.
 bool use_mfma(int type, size_t n_rows, size_t k) {
-  return g_gemv_mode.load(std::memory_order_relaxed) == WH_GEMV_AUTO && k >= 1024 && n_rows >= 64 &&
+  return t_gemv_mode == WH_GEMV_AUTO && k >= 1024 && n_rows >= 64 &&
          wh::gemv_mfma_ok(type, n_rows, k);
 }
 
@@ -829,12 +836,17 @@ namespace wh {
 // h = silu(W_gate x_hat) * (W_up x_hat), x_hat = rms_norm(x, gamma, eps).
 // Returns WH_ERR_INVALID_SHAPE without launching when the fused kernel's
 // layout conditions do not hold; the caller then runs the unfused sequence.
-int gemv_mode_exchange(int mode) { return g_gemv_mode.exchange(mode); }
+int gemv_mode_exchange(int mode) {
+  const int prev = t_gemv_mode;
+  t_gemv_mode = mode;
+  return prev;
+}
 
 int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* x, const float* gamma,
                        float eps, float* h, size_t n_ff, size_t hidden, hipStream_t s) {
   if (n_ff == 0) return WH_OK;
-  if (n_ff >= (1u << 30) || !gamma) return WH_ERR_INVALID_SHAPE;
+  if (n_ff >= (1u << 30) || !gamma)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "ffn gate/up: %zu rows (at most 2^30) or no RMSNorm weight", n_ff);
   if (use_mfma(type, n_ff, hidden)) {
     const void* mats[2] = {gate, up};
     const size_t rows[2] = {n_ff, n_ff};
@@ -847,16 +859,19 @@ int launch_ffn_gate_up(int type, const void* gate, const void* up, const float* 
   a.eps = eps;
   switch (type) {
     case WH_TYPE_Q4_0:
-      if (!stream_ok<WH_TYPE_Q4_0, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      if (!stream_ok<WH_TYPE_Q4_0, true>(a, hidden))
+        return wh::set_error(WH_ERR_INVALID_SHAPE, "ffn gate/up: layout not fused (hidden = %zu)", hidden);
       return launch_stream<WH_TYPE_Q4_0, true, kNorm>(a, hidden, s);
     case WH_TYPE_Q4_1:
-      if (!stream_ok<WH_TYPE_Q4_1, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      if (!stream_ok<WH_TYPE_Q4_1, true>(a, hidden))
+        return wh::set_error(WH_ERR_INVALID_SHAPE, "ffn gate/up: layout not fused (hidden = %zu)", hidden);
       return launch_stream<WH_TYPE_Q4_1, true, kNorm>(a, hidden, s);
     case WH_TYPE_Q8_0:
-      if (!stream_ok<WH_TYPE_Q8_0, true>(a, hidden)) return WH_ERR_INVALID_SHAPE;
+      if (!stream_ok<WH_TYPE_Q8_0, true>(a, hidden))
+        return wh::set_error(WH_ERR_INVALID_SHAPE, "ffn gate/up: layout not fused (hidden = %zu)", hidden);
       return launch_stream<WH_TYPE_Q8_0, true, kNorm>(a, hidden, s);
     default:
-      return WH_ERR_INVALID_SHAPE;
+      return wh::set_error(WH_ERR_INVALID_SHAPE, "ffn gate/up: type %d not fused", type);
   }
 }
 
@@ -872,7 +887,9 @@ int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int
   size_t n = 0;
   for (int i = 0; i < n_mats; i++) n += rows[i];
   if (n == 0) return WH_OK;
-  if (n >= (1u << 30) || n_mats < 1 || n_mats > 3) return WH_ERR_INVALID_SHAPE;
+  if (n >= (1u << 30) || n_mats < 1 || n_mats > 3)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "fused gemv: %zu rows (at most 2^30) over %d matrices (1 to 3)", n,
+                         n_mats);
   GemvArgs a = plain_args(static_cast<const uint8_t*>(mats[0]), x, y, n);
   a.n0 = static_cast<int>(rows[0]);
   a.n1 = n_mats > 1 ? static_cast<int>(rows[1]) : 0;
@@ -887,7 +904,8 @@ int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int
   }
   if (is_kquant(type)) {
     // the dequantize-then-dot kernel per matrix (the caller normalises x first)
-    if (gamma) return WH_ERR_INVALID_SHAPE;
+    if (gamma)
+      return wh::set_error(WH_ERR_INVALID_SHAPE, "fused gemv: RMSNorm not fused for this K-quant shape (k = %zu)", k);
     size_t off = 0;
     for (int i = 0; i < n_mats; i++) {
       const int st = launch_gemv_kquant(type, mats[i], x, y + off, rows[i], k, s, residual ? residual + off : nullptr);
@@ -902,13 +920,16 @@ int launch_gemv_fused(int type, const void* const* mats, const size_t* rows, int
   switch (type) {
     case WH_TYPE_Q4_0:
       if (stream_ok<WH_TYPE_Q4_0, false>(a, k)) return launch_fused_mode<WH_TYPE_Q4_0>(a, k, mode, s);
-      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q4_0>(a, k, s);
+      return gamma ? wh::set_error(WH_ERR_INVALID_SHAPE, "fused gemv: RMSNorm not fused for this shape (k = %zu)", k)
+                   : launch_generic<WH_TYPE_Q4_0>(a, k, s);
     case WH_TYPE_Q4_1:
       if (stream_ok<WH_TYPE_Q4_1, false>(a, k)) return launch_fused_mode<WH_TYPE_Q4_1>(a, k, mode, s);
-      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q4_1>(a, k, s);
+      return gamma ? wh::set_error(WH_ERR_INVALID_SHAPE, "fused gemv: RMSNorm not fused for this shape (k = %zu)", k)
+                   : launch_generic<WH_TYPE_Q4_1>(a, k, s);
     case WH_TYPE_Q8_0:
       if (stream_ok<WH_TYPE_Q8_0, false>(a, k)) return launch_fused_mode<WH_TYPE_Q8_0>(a, k, mode, s);
-      return gamma ? WH_ERR_INVALID_SHAPE : launch_generic<WH_TYPE_Q8_0>(a, k, s);
+      return gamma ? wh::set_error(WH_ERR_INVALID_SHAPE, "fused gemv: RMSNorm not fused for this shape (k = %zu)", k)
+                   : launch_generic<WH_TYPE_Q8_0>(a, k, s);
     default:
       return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "gemv: unsupported type %d", type);
   }

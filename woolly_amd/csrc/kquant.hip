@@ -19,61 +19,14 @@
 //     ((d * scale[i/16]) * (q - 32)) / 64.
 // Every product and sum is rounded in the reference's order with unfused
 // operations, so the results are bit-identical to the CPU.
-#include "wh_common.hpp"
+#include "wh_blocks.hpp"
 
 namespace {
 
-__device__ __forceinline__ uint32_t b16(const uint8_t* p) {
-  return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
-}
-
-// 6-bit scale j (0..7) of a Q4_K block at b.
-__device__ __forceinline__ uint32_t q4k_scale(const uint8_t* b, int j) {
-  const int src = (3 * j) >> 1;
-  return (j & 1) ? (((b[src] >> 6) | ((b[src + 1] & 15u) << 2)) & 63u) : (b[src] & 63u);
-}
-
-// Element i (0..255) of a Q4_K block at b.
-__device__ __forceinline__ float q4k_elem(const uint8_t* b, int i, float d, float dmin) {
-  const uint32_t s = q4k_scale(b, i >> 5);
-  const uint32_t qb = b[16 + (i >> 1)];
-  const uint32_t q = (i & 1) ? ((qb >> 4) & 15u) : (qb & 15u);
-  return __fadd_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q)), dmin);
-}
-
-// The 6-bit quant q (0..63) of element i (0..255) of a Q6_K block at b.
-__device__ __forceinline__ uint32_t q6k_quant(const uint8_t* b, int i) {
-  const uint8_t* ql = b;
-  const uint8_t* qh = b + 128;
-  const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
-  const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
-  const int shift = 2 * (i & 3);
-  const uint32_t qhv = qh[qh_idx];
-  if (i < 128) return (ql[ql_idx] & 15u) | (((qhv >> shift) & 3u) << 4);
-  const uint32_t e2 = shift < 6 ? ((qhv >> (shift + 2)) & 3u) : (qh_idx + 1 < 64 ? (qh[qh_idx + 1] & 3u) : 0u);
-  return (ql[ql_idx] >> 4) | (e2 << 4);
-}
-
-// Element i (0..255) of a Q6_K block at b.
-__device__ __forceinline__ float q6k_elem(const uint8_t* b, int i, float d) {
-  const uint32_t q = q6k_quant(b, i);
-  const float s = static_cast<float>(b[192 + (i >> 4)]);
-  return __fmul_rn(__fmul_rn(__fmul_rn(d, s), static_cast<float>(static_cast<int>(q) - 32)), 0.015625f);
-}
-
-template <int TYPE>
-__device__ __forceinline__ void kq_quad(const uint8_t* b, int c, float v[4]) {
-  if constexpr (TYPE == WH_TYPE_Q4_K) {
-    const float d = whd::f16_bits_to_f32(b16(b + 12));
-    const float dmin = whd::f16_bits_to_f32(b16(b + 14));
-#pragma unroll
-    for (int t = 0; t < 4; t++) v[t] = q4k_elem(b, 4 * c + t, d, dmin);
-  } else {
-    const float d = whd::f16_bits_to_f32(b16(b + 208));
-#pragma unroll
-    for (int t = 0; t < 4; t++) v[t] = q6k_elem(b, 4 * c + t, d);
-  }
-}
+using whd::b16;
+using whd::kq_quad;
+using whd::q4k_scale;
+using whd::q6k_quant;
 
 template <int TYPE>
 constexpr int kq_bytes() { return TYPE == WH_TYPE_Q4_K ? 144 : 210; }

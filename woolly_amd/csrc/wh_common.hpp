@@ -149,6 +149,12 @@ bool attention_shape_ok(size_t n_heads, size_t n_kv_heads, size_t head_dim);
 int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size_t pos, size_t n_heads,
                             size_t n_kv_heads, size_t head_dim, const float* inv_freq, float* out, void* ws,
                             hipStream_t stream);
+// Token-embedding rows (embed.hip): out[t] = dequantized row ids[t] of a
+// [vocab][hidden] table; NaN rows for ids >= vocab.
+int check_embedding_args(const char* fn, int type, const void* table, size_t vocab, size_t hidden,
+                         const uint32_t* ids, float* out);
+int launch_embedding_lookup(int type, const void* table, size_t vocab, size_t hidden, const uint32_t* ids,
+                            size_t n_tokens, float* out, hipStream_t stream);
 int launch_rms_norm(const float* x, const float* weight, float eps, size_t tokens,
                     size_t hidden, float* out, hipStream_t stream);
 int launch_swiglu(const float* gate, const float* up, size_t n, float* out,

@@ -415,6 +415,11 @@ class GGUFLoader:
     def tensor_info(self, name: str):
         return self.tensors().get(name)
 
+    def has_tensor(self, name: str) -> bool:
+        """Whether the file holds a tensor of this name (loader.has_tensor, used by
+        load_model_weights for the optional output.weight, loader.rs:384)."""
+        return name in self.tensors()
+
     def tensor_names(self) -> list[str]:
         return list(self.tensors())
 

@@ -190,6 +190,27 @@ def quantized_matvec_residual(ggml_type: int, weights, weight_nbytes: int, x, re
                                                         _p(residual), _p(y), m, k, _s(stream)))
 
 
+def embedding_lookup(ggml_type: int, table, vocab: int, hidden: int, input_ids, out,
+                     stream: Stream | None = None):
+    """embedding_lookup (crates/woolly-core/src/tensor_utils.rs:548-590) with the
+    table on the device: out (device, [len(input_ids)][hidden] f32) receives the
+    dequantized rows.  Token ids are checked on the host first and an id >=
+    vocab raises ValueError with the reference's message
+    (TENSOR_EMBEDDING_TOKEN_OUT_OF_RANGE); returns the device buffer of ids."""
+    import numpy as np
+
+    from .device import DeviceBuffer
+
+    ids = np.ascontiguousarray(np.asarray(input_ids, dtype=np.int64))
+    for t in ids.tolist():
+        if t < 0 or t >= vocab:
+            raise ValueError(f"Token ID {t} exceeds vocabulary size {vocab}")
+    idb = DeviceBuffer.from_array(ids.astype(np.uint32), stream)
+    _lib.check(_lib.load().wh_embedding_lookup(ggml_type, _p(table), vocab, hidden, idb.ptr, ids.size, _p(out),
+                                               _s(stream)))
+    return idb
+
+
 class LlamaModel:
     """A Llama-shaped model on the device for the decode step: `layers` is a
     list of dicts of device buffers (attn_norm, wq, wk, wv, wo, ffn_norm,
@@ -197,8 +218,8 @@ class LlamaModel:
     matrix (wq_type .. w_down_type; absent or 0: ggml_type); wraps wh_llama_model."""
 
     def __init__(self, ggml_type: int, dims: dict, layers: list, inv_freq_dev, output_norm=None,
-                 output=None, output_type: int = GGML_Q8_0) -> None:
-        self._keep = (layers, inv_freq_dev, output_norm, output)
+                 output=None, output_type: int = GGML_Q8_0, token_embd=None, token_embd_type: int = 0) -> None:
+        self._keep = (layers, inv_freq_dev, output_norm, output, token_embd)
         arr = (_lib.wh_llama_layer * len(layers))()
         for i, L in enumerate(layers):
             for name, _ in _lib.wh_llama_layer._fields_:
@@ -218,57 +239,105 @@ class LlamaModel:
         m.output_norm = _p(output_norm) or None
         m.output_type = output_type
         m.output = _p(output) or None
+        m.token_embd_type = token_embd_type
+        m.token_embd = _p(token_embd) or None
         self.model = m
 
     @staticmethod
     def config_from_gguf(ld, max_ctx: int | None = None) -> dict:
-        """The model config of a GGUF file (gguf.GGUFLoader) from the
-        `{arch}.*` metadata keys GGUFModelLoader reads (model/loader.rs:110-150):
-        embedding_length, block_count, attention.head_count[_kv] (default: the
-        head count), feed_forward_length (default 4 x hidden), context_length
-        (default 2048; max_ctx overrides it), rope.freq_base (default 10000),
-        attention.layer_norm_epsilon or layer_norm_epsilon (default 1e-5)."""
+        """The model config of a GGUF file (gguf.GGUFLoader), read as
+        GGUFModelLoader::extract_config does (model/loader.rs:104-150): the
+        architecture from general.architecture (ValueError when absent, like
+        the reference's "No architecture specified in GGUF"), then, each with
+        its fallback key and default:
+          hidden    {arch}.embedding_length, {arch}.embed_dim            4096
+          n_layers  {arch}.block_count, {arch}.layer_count               32
+          n_heads   {arch}.attention.head_count                          32
+          n_kv      {arch}.attention.head_count_kv                       n_heads
+          n_ff      {arch}.feed_forward_length                           4 x hidden
+          max_ctx   {arch}.context_length, tokenizer.ggml.context_length 2048 (max_ctx overrides)
+          vocab     {arch}.vocab_size, tokenizer.ggml.tokens.len         32000
+          rope_base {arch}.rope.freq_base, {arch}.attention.rope_theta   10000
+          eps       {arch}.attention.layer_norm_epsilon, {arch}.layer_norm_epsilon  1e-5"""
         md = ld.metadata()
-        arch = md.get_string("general.architecture") or "llama"
+        arch = md.get_string("general.architecture")
+        if not arch:
+            raise ValueError("No architecture specified in GGUF")
 
-        def u32(key, default=None):
-            v = md.get_u32(f"{arch}.{key}")
-            if v is None and default is None:
-                raise ValueError(f"GGUF metadata {arch}.{key} missing")
-            return int(v if v is not None else default)
-
-        def f32(keys, default):
+        def first(get, keys, default):
             for key in keys:
-                v = md.get_f32(f"{arch}.{key}")
+                v = get(key)
                 if v is not None:
-                    return float(v)
+                    return v
             return default
 
-        hidden, n_layers, n_heads = u32("embedding_length"), u32("block_count"), u32("attention.head_count")
-        return dict(hidden=hidden, n_layers=n_layers, n_heads=n_heads,
-                    n_kv_heads=u32("attention.head_count_kv", n_heads), head_dim=hidden // n_heads,
-                    n_ff=u32("feed_forward_length", 4 * hidden),
-                    max_ctx=int(max_ctx) if max_ctx else u32("context_length", 2048),
-                    rope_base=f32(["rope.freq_base"], 10000.0),
-                    eps=f32(["attention.layer_norm_epsilon", "layer_norm_epsilon"], 1e-5))
+        u32 = lambda keys, default: int(first(md.get_u32, keys, default))
+        f32 = lambda keys, default: float(first(md.get_f32, keys, default))
+        hidden = u32([f"{arch}.embedding_length", f"{arch}.embed_dim"], 4096)
+        n_heads = u32([f"{arch}.attention.head_count"], 32)
+        return dict(hidden=hidden, n_layers=u32([f"{arch}.block_count", f"{arch}.layer_count"], 32),
+                    n_heads=n_heads, n_kv_heads=u32([f"{arch}.attention.head_count_kv"], n_heads),
+                    head_dim=hidden // n_heads, n_ff=u32([f"{arch}.feed_forward_length"], 4 * hidden),
+                    max_ctx=int(max_ctx) if max_ctx else u32([f"{arch}.context_length",
+                                                              "tokenizer.ggml.context_length"], 2048),
+                    vocab=u32([f"{arch}.vocab_size", "tokenizer.ggml.tokens.len"], 32000),
+                    rope_base=f32([f"{arch}.rope.freq_base", f"{arch}.attention.rope_theta"], 10000.0),
+                    eps=f32([f"{arch}.attention.layer_norm_epsilon", f"{arch}.layer_norm_epsilon"], 1e-5))
 
     @classmethod
     def from_gguf(cls, ld, max_ctx: int | None = None) -> "LlamaModel":
         """The decode model of a GGUF file (gguf.GGUFLoader): the config of
         config_from_gguf and the tensors load_layer_weights / load_model_weights
-        name (model/loader.rs:370-520: blk.N.{attn_norm, attn_q, attn_k, attn_v,
-        attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight,
-        output_norm.weight, output.weight).  Every matrix is uploaded from the
-        mapping with its own block type (Q4_K_M files mix Q4_K and Q6_K); the
-        f16 KV caches (max_ctx rows) start zeroed."""
+        name (model/loader.rs:370-520: token_embd.weight, blk.N.{attn_norm,
+        attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_up,
+        ffn_down}.weight, output_norm.weight, output.weight).  Every matrix is
+        uploaded from the mapping with its own block type (Q4_K_M files mix Q4_K
+        and Q6_K) after its dims are checked against the config (ValueError on a
+        mismatch, before anything reads past a tensor); without output.weight
+        the head is token_embd.weight, tied as in lazy_transformer.rs:1301-1316.
+        The f16 KV caches (max_ctx rows) start zeroed."""
         from .device import DeviceBuffer
 
         cfg = cls.config_from_gguf(ld, max_ctx)
         hidden, n_layers, n_heads, n_kv = cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"]
         n_ff, ctx, base, eps = cfg["n_ff"], cfg["max_ctx"], cfg["rope_base"], cfg["eps"]
+        if n_heads == 0 or hidden % n_heads:
+            raise ValueError(f"hidden size {hidden} is not a multiple of {n_heads} heads")
         d = hidden // n_heads
+        # GGUF dims: [ne0 = K (fastest), ne1 = rows]
+        shapes = {"attn_norm": [hidden], "wq": [hidden, n_heads * d], "wk": [hidden, n_kv * d],
+                  "wv": [hidden, n_kv * d], "wo": [n_heads * d, hidden], "ffn_norm": [hidden],
+                  "w_gate": [hidden, n_ff], "w_up": [hidden, n_ff], "w_down": [n_ff, hidden]}
         names = {"attn_norm": "attn_norm", "wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output",
                  "ffn_norm": "ffn_norm", "w_gate": "ffn_gate", "w_up": "ffn_up", "w_down": "ffn_down"}
+
+        def info(name, want=None):
+            ti = ld.tensor_info(name)
+            if ti is None:
+                from .gguf import TensorNotFound
+                raise TensorNotFound(name)
+            got = [int(v) for v in ti.shape()]
+            if want is not None and got != want:
+                raise ValueError(f"tensor {name} has dims {got}, the config needs {want}")
+            return ti
+
+        for i in range(n_layers):
+            for key, nm in names.items():
+                info(f"blk.{i}.{nm}.weight", shapes[key])
+        embd = info("token_embd.weight") if ld.has_tensor("token_embd.weight") else None
+        if embd is not None and (len(embd.shape()) != 2 or int(embd.shape()[0]) != hidden):
+            raise ValueError(f"token_embd.weight has dims {list(embd.shape())}, the config needs [{hidden}, vocab]")
+        tied = not ld.has_tensor("output.weight")
+        if tied and embd is None:
+            raise ValueError("GGUF file has neither output.weight nor token_embd.weight")
+        head_info = embd if tied else info("output.weight")
+        if len(head_info.shape()) != 2 or int(head_info.shape()[0]) != hidden:
+            raise ValueError(f"output head has dims {list(head_info.shape())}, the config needs [{hidden}, vocab]")
+        vocab = int(head_info.shape()[1])
+        if embd is not None and int(embd.shape()[1]) != vocab:
+            raise ValueError(f"token_embd.weight has {int(embd.shape()[1])} rows, the head {vocab}")
+        info("output_norm.weight", [hidden])
+
         layers = []
         for i in range(n_layers):
             L = {}
@@ -283,13 +352,14 @@ class LlamaModel:
             layers.append(L)
         inv = DeviceBuffer.from_array(rope_inv_freq(base, d))
         out_norm = ld.upload("output_norm.weight")
-        head = ld.upload("output.weight")
-        head_info = ld.tensor_info("output.weight")
+        embd_dev = ld.upload("token_embd.weight") if embd is not None else None
+        head = embd_dev if tied else ld.upload("output.weight")
         dims = dict(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, n_ff=n_ff, max_ctx=ctx,
-                    vocab=int(head_info.shape()[1]), eps=eps)
+                    vocab=vocab, eps=eps)
         m = cls(layers[0]["wq_type"] if layers else GGML_Q4_0, dims, layers, inv, out_norm, head,
-                int(head_info.ggml_type))
+                int(head_info.ggml_type), embd_dev, int(embd.ggml_type) if embd is not None else 0)
         m.dims = dims
+        m.tied_head = tied
         return m
 
     def workspace_bytes(self) -> int:
@@ -299,6 +369,15 @@ class LlamaModel:
                      stream: Stream | None = None) -> None:
         _lib.check(_lib.load().wh_llama_layer_decode(C.byref(self.model), layer, pos, _p(x),
                                                      _p(workspace), workspace_bytes, _s(stream)))
+
+    def forward_token(self, token_dev, pos: int, x, logits, workspace, workspace_bytes: int,
+                      stream: Stream | None = None) -> None:
+        """The step from a token id held in device memory (uint32 at token_dev):
+        x = its embedding row, then decode_step (LazyTransformer::forward for
+        one token, lazy_transformer.rs:1155-1336)."""
+        _lib.check(_lib.load().wh_llama_forward_token(C.byref(self.model), _p(token_dev), pos, _p(x),
+                                                      _p(logits) or None, _p(workspace), workspace_bytes,
+                                                      _s(stream)))
 
     def decode_step(self, pos: int, x, logits, workspace, workspace_bytes: int,
                     stream: Stream | None = None) -> None:

@@ -46,10 +46,25 @@ def stream_seed(seed: int, stream: int) -> np.uint64:
 
 
 def u64(seed: int, stream: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start .. start + n - 1 of the stream, in cache-sized chunks with
+    in-place operations (the same values as _mix(base + idx * GOLDEN))."""
     base = stream_seed(seed, stream)
+    out = np.empty(n, np.uint64)
+    chunk = 1 << 16
+    tmp = np.empty(min(n, chunk), np.uint64)
     with np.errstate(over="ignore"):
-        idx = np.arange(start + 1, start + n + 1, dtype=np.uint64)
-        return _mix(base + idx * GOLDEN)
+        for c0 in range(0, n, chunk):
+            c1 = min(n, c0 + chunk)
+            z, t = out[c0:c1], tmp[: c1 - c0]
+            z[:] = np.arange(start + c0 + 1, start + c1 + 1, dtype=np.uint64)
+            np.multiply(z, GOLDEN, out=z)
+            np.add(z, base, out=z)
+            for sh, mul in ((30, M1), (27, M2), (31, None)):
+                np.right_shift(z, np.uint64(sh), out=t)
+                np.bitwise_xor(z, t, out=z)
+                if mul is not None:
+                    np.multiply(z, mul, out=z)
+    return out
 
 
 def uniform(seed: int, stream: int, n: int) -> np.ndarray:
@@ -117,7 +132,9 @@ def quantized_weight(ggml_type: int, n_rows: int, k: int, seed: int, stream: int
     elif ggml_type == GGML_Q8_0:
         d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.02 if d_std is None else d_std))
         out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
-        q = (u64(seed, s0 + 2, nb * 32) % np.uint64(255)).astype(np.int16) - 127
+        # u % 255 of each 64-bit draw, from the sum of its 8 bytes (2^8 = 1 mod 255)
+        u = u64(seed, s0 + 2, nb * 32)
+        q = (u.view(np.uint8).reshape(-1, 8).sum(axis=1, dtype=np.uint32) % np.uint32(255)).astype(np.int16) - 127
         out[:, 2:34] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
     else:
         raise ValueError(f"unsupported ggml type {ggml_type}")
