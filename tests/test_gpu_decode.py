@@ -2,7 +2,10 @@
 Q/K/V projection, single-token GQA attention over an f16 KV cache with RoPE,
 residual projections, one layer, several steps and the whole step with the
 output head.  Bars: rel-L2 <= 1e-4 and max-abs <= 1e-3 of the f64 oracle
-(north_star); cache rows written by the step within one f16 ulp of the oracle's."""
+(north_star) for projections, attention and logits; hidden states (residual
+sums, RMS up to ~2e4 here, where one f32 ulp of the largest elements exceeds
+1e-3) to max-abs <= 1e-3 per 300 of their RMS; cache rows written by the step
+within one f16 ulp of the oracle's."""
 import numpy as np
 import pytest
 
@@ -15,6 +18,14 @@ from woolly_amd.device import DeviceBuffer
 pytestmark = pytest.mark.gpu
 Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
 REL_L2 = 1e-4
+
+
+def hidden_bar(ref) -> float:
+    """max-abs bar of a hidden state (a residual sum): 1e-3 per 300 of its RMS,
+    the rule the FFN tests apply to outputs larger than config 3's (RMS ~ 300);
+    1e-3 for anything smaller.  Logits and projections use 1e-3 itself."""
+    rms = float(np.sqrt(np.mean(np.asarray(ref, np.float64) ** 2)))
+    return 1e-3 * max(1.0, rms / 300.0)
 
 
 def check(got, ref, tag, abs_bar=1e-3):
@@ -72,8 +83,11 @@ def test_matvec_residual_in_place(gpu, orc, t, m, k):
 
 
 # (8, 1, 128) at 8191: 128 chunks per head, so each combine lane merges two load batches
-@pytest.mark.parametrize("n_heads,n_kv,d", [(32, 8, 128), (8, 2, 64), (4, 4, 64), (16, 2, 128), (8, 1, 128)])
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1000, 4095, 8191])
+@pytest.mark.parametrize("n_heads,n_kv,d,pos", [(n, k, d, p) for (n, k, d) in
+                                                ((32, 8, 128), (8, 2, 64), (4, 4, 64), (16, 2, 128), (8, 1, 128))
+                                                for p in (0, 1, 63, 64, 200, 1000, 4095, 8191)] +
+                         # long contexts with 8 KV heads: 192- and 256-position chunks
+                         [(32, 8, 128, 12000), (32, 8, 128, 40000), (32, 8, 128, 64319), (16, 8, 64, 20000)])
 def test_attention_decode(gpu, orc, n_heads, n_kv, d, pos):
     print(f"[case] attention heads={n_heads}/{n_kv} d={d} pos={pos}", flush=True)
     rng = np.random.default_rng(pos + d)
@@ -160,8 +174,8 @@ def test_layers_and_steps_small_model(gpu, orc, t):
         logits = orc.output_head_f64(Q8_0, head, onorm, 1e-5, x, hidden, vocab)
         print(f"[info] step pos={pos} max|x|={np.max(np.abs(x)):.3e} max|logits|={np.max(np.abs(logits)):.3e}",
               flush=True)
-        check(got_x, x, f"step t={t} pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
-        check(got_l, logits, f"step t={t} pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+        check(got_x, x, f"step t={t} pos={pos} hidden", abs_bar=hidden_bar(x))
+        check(got_l, logits, f"step t={t} pos={pos} logits", abs_bar=1e-3)
         for (kc, vc), (kg, vg) in zip(caches, gcache):
             kc[:] = kg
             vc[:] = vg
@@ -203,10 +217,9 @@ def test_layer_llama3_8b_shape_ctx4096(gpu, orc):
     ref32_err = max_abs(ref32, ref)
     print(f"[info] layer 8B: reference-order f32 vs f64 max_abs={ref32_err:.3e} rel_l2={rel_l2(ref32, ref):.3e}; "
           f"GPU vs reference-order f32 max_abs={max_abs(got, ref32):.3e}", flush=True)
-    # bar: rel-L2 1e-4, max-abs 1e-3 or the reference's own f32 error on this
-    # input if that is larger (the output is cancellation-limited: sum |w h| of
-    # the down projection is ~10x the result)
-    check(got, ref, "layer 8B ctx4096", abs_bar=max(1e-3, ref32_err))
+    # bar: rel-L2 1e-4 and the hidden-state max-abs rule (the reference's own
+    # f32 order is several times further from f64 on this input: ref32_err)
+    check(got, ref, "layer 8B ctx4096", abs_bar=hidden_bar(ref))
 
 
 # K-quant models: every matrix Q4_K, every matrix Q6_K, or the per-tensor mix of
@@ -266,8 +279,8 @@ def test_kquant_model_steps(gpu, orc, kind):
         for L, (kg, vg) in zip(Ls, gcache):
             x = orc.llama_layer_decode_f64(tl, L, dims, inv, kg.copy(), vg.copy(), pos, x, store_new=False)
         logits = orc.output_head_f64(Q6_K, head, onorm, 1e-5, x, hidden, vocab)
-        check(got_x, x, f"kquant {kind} pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
-        check(got_l, logits, f"kquant {kind} pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+        check(got_x, x, f"kquant {kind} pos={pos} hidden", abs_bar=hidden_bar(x))
+        check(got_l, logits, f"kquant {kind} pos={pos} logits", abs_bar=1e-3)
         for (kc, vc), (kg, vg) in zip(caches, gcache):
             kc[:] = kg
             vc[:] = vg
@@ -296,7 +309,7 @@ def test_kquant_m_layer_llama3_8b_shape(gpu, orc):
     assert f16_ulp_close(kg[pos], kr[pos]) and f16_ulp_close(vg[pos], vr[pos])
     ref = orc.llama_layer_decode_f64(tl, Ls[0], dims, inv, kg.copy(), vg.copy(), pos, x0.astype(np.float64),
                                      store_new=False)
-    check(got, ref, "kquant q4_k_m layer 8B", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(ref))))
+    check(got, ref, "kquant q4_k_m layer 8B", abs_bar=hidden_bar(ref))
 
 
 def test_llama_model_from_gguf_q4_k_m(gpu, orc, tmp_path):
@@ -348,8 +361,8 @@ def test_llama_model_from_gguf_q4_k_m(gpu, orc, tmp_path):
         for L, (kc, vc) in zip(Ls, caches):
             x = orc.llama_layer_decode_f64(tl, L, dims, inv, kc, vc, pos, x)
         logits = orc.output_head_f64(Q6_K, head, onorm, 1e-5, x, hidden, vocab)
-        check(got_x, x, f"gguf q4_k_m pos={pos} hidden", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(x))))
-        check(got_l, logits, f"gguf q4_k_m pos={pos} logits", abs_bar=max(1e-3, 3e-6 * np.max(np.abs(logits))))
+        check(got_x, x, f"gguf q4_k_m pos={pos} hidden", abs_bar=hidden_bar(x))
+        check(got_l, logits, f"gguf q4_k_m pos={pos} logits", abs_bar=1e-3)
 
 
 EMB_TYPES = [0, 1, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K]
