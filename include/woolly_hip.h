@@ -345,6 +345,21 @@ WH_API int wh_llama_forward_token(const wh_llama_model* model, const uint32_t* t
                                   float* logits, void* workspace, size_t workspace_bytes,
                                   wh_stream_t stream);
 
+/* wh_llama_decode_step without a workspace argument and without any
+ * allocation (no counterpart in the reference: for callers that cannot
+ * allocate, such as code under HIP graph capture or a serving loop that
+ * forbids hipMalloc).  The step's workspace lives in a static device array of
+ * WH_LLAMA_DECODE_NOALLOC_MAX_BYTES bytes, one per device, held until the
+ * process ends; wh_init looks up its address.  A step whose
+ * workspace at this position exceeds it (about 64K positions for 32 heads of
+ * 128) fails with WH_ERR_BUFFER_TOO_SMALL before anything is launched.  All
+ * calls on one device share that array: calls that overlap on one device
+ * (concurrent streams or threads) race.  Results are identical to
+ * wh_llama_decode_step's. */
+#define WH_LLAMA_DECODE_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+WH_API int wh_llama_decode_step_noalloc(const wh_llama_model* model, size_t pos, float* x, float* logits,
+                                        wh_stream_t stream);
+
 /* embedding_lookup (crates/woolly-core/src/tensor_utils.rs:548-590) on the
  * device: out[t, :] = the dequantized row ids[t] of table ([vocab][hidden] of
  * `type`, e.g. token_embd.weight), bit-identical to wh_dequantize of that row,

@@ -28,6 +28,9 @@ WH_ERR_INVALID_METADATA = 11
 WH_ERR_NOT_FOUND = 12
 WH_ERR_TYPE_MISMATCH = 13
 
+# WH_LLAMA_DECODE_NOALLOC_MAX_BYTES: the static scratch of wh_llama_decode_step_noalloc
+LLAMA_DECODE_NOALLOC_MAX_BYTES = 16 << 20
+
 STATUS_NAMES = {
     0: "WH_OK",
     1: "WH_ERR_UNSUPPORTED_TYPE",
@@ -183,6 +186,7 @@ SIGNATURES = {
     "wh_llama_decode_step": (_int, [C.POINTER(wh_llama_model), _sz, _f32p, _f32p, _vp, _sz, _vp]),
     "wh_llama_forward_token": (_int, [C.POINTER(wh_llama_model), _vp, _sz, _f32p, _f32p, _vp, _sz, _vp]),
     "wh_embedding_lookup": (_int, [_int, _vp, _sz, _sz, _vp, _sz, _f32p, _vp]),
+    "wh_llama_decode_step_noalloc": (_int, [C.POINTER(wh_llama_model), _sz, _f32p, _f32p, _vp]),
     "wh_gguf_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
     "wh_gguf_open_buffer": (_int, [_vp, _sz, C.POINTER(_vp)]),
     "wh_gguf_close": (_int, [_vp]),

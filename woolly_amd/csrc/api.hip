@@ -176,7 +176,7 @@ WH_API int wh_init(int device) {
     return wh::set_error(WH_ERR_NO_DEVICE, "wh_init: device %d is %s; this library is built for gfx950",
                          device, prop.gcnArchName);
   (void)wh::cu_count();
-  return WH_OK;
+  return wh::init_step_scratch();
 }
 
 WH_API int wh_device_name(char* buf, size_t len) {

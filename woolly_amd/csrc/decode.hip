@@ -15,10 +15,44 @@
 // the step into a HIP graph.
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 
 #include "wh_common.hpp"
 
 namespace {
+
+// Scratch of wh_llama_decode_step_noalloc: the step's workspace (q/k/v, the
+// attention output and partials, the FFN hidden vector) for callers that
+// cannot allocate.  One copy per device, held until the process ends; every
+// call on a device shares it, so calls that overlap on one device race.  No
+// kernel of the step needs any of it zeroed: each one writes what it reads
+// later in the same step.  In host code `scratch` only names the symbol; the
+// device address of each device's copy comes from hipGetSymbolAddress.
+constexpr size_t kStepScratchBytes = WH_LLAMA_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kStepScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device.
+int step_scratch(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  WH_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices)
+    return wh::set_error(WH_ERR_NO_DEVICE, "decode step scratch: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return wh::hip_error(e, "hipGetSymbolAddress(decode step scratch)");
+    if (!p) return wh::set_error(WH_ERR_HIP, "hipGetSymbolAddress(decode step scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return WH_OK;
+}
 
 hipStream_t hs(wh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -344,4 +378,38 @@ WH_API int wh_llama_forward_token(const wh_llama_model* model, const uint32_t* t
                                   float* logits, void* workspace, size_t workspace_bytes, wh_stream_t stream) {
   if (!token) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "llama_forward_token: null token");
   return decode_step("llama_forward_token", model, token, pos, x, logits, workspace, workspace_bytes, hs(stream));
+}
+
+namespace wh {
+
+// Called by wh_init with the device current: looks up the device's copy of
+// the decode step's static scratch ahead of any call (and of any capture).
+int init_step_scratch() {
+  void* p = nullptr;
+  return step_scratch(&p);
+}
+
+}  // namespace wh
+
+WH_API int wh_llama_decode_step_noalloc(const wh_llama_model* model, size_t pos, float* x, float* logits,
+                                        wh_stream_t stream) {
+  static const char* const fn = "llama_decode_step_noalloc";
+  int st = check_model(fn, model);
+  if (st) return st;
+  if (pos >= model->max_ctx)
+    return wh::set_error(WH_ERR_INVALID_SHAPE, "%s: position %zu beyond max_ctx %zu", fn, pos, model->max_ctx);
+  // The step attends to positions 0..pos only, so its workspace is laid out
+  // for pos + 1 positions (the attention partials come last, every other
+  // offset is the same as for max_ctx).
+  wh_llama_model sized = *model;
+  sized.max_ctx = pos + 1;
+  const size_t need = step_layout(&sized, nullptr).bytes;
+  if (need > kStepScratchBytes)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "%s: the step at position %zu needs %zu bytes of scratch; the static scratch holds %zu "
+                         "(wh_llama_decode_step takes a workspace of any size)",
+                         fn, pos, need, kStepScratchBytes);
+  void* ws = nullptr;
+  if ((st = step_scratch(&ws))) return st;
+  return decode_step(fn, &sized, nullptr, pos, x, logits, ws, need, hs(stream));
 }

@@ -81,6 +81,9 @@ int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void*
 
 // Number of compute units of the current device (cached per device).
 int cu_count();
+// Looks up the current device's copy of the no-allocation decode step's
+// static scratch (decode.hip); called by wh_init.
+int init_step_scratch();
 // Largest LDS allocation one workgroup may use on the current device.
 size_t max_lds_per_block();
 
