@@ -157,7 +157,7 @@ def bench_ffn(m: int, iters: int, t: int = Q4_0, replicas: int | None = None) ->
     copies = [{k: DeviceBuffer.from_array(L[k]) for k in ("gate", "up", "down")} for _ in range(replicas)]
     b = {k: DeviceBuffer.from_array(L[k]) for k in ("gamma", "x")}
     out = DeviceBuffer(4 * m * hidden)
-    wsz = ops.ffn_workspace_bytes_for_type(t, hidden, n_ff, m)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m, ggml_type=t)
     ws = DeviceBuffer(wsz)
 
     def run(i):

@@ -83,7 +83,10 @@ constexpr int kMgWaves = 16;                   // waves per workgroup
 constexpr int kMgSegMax = 16 * 64 * 4;        // bytes of one row segment (at most 4 loads)
 // LDS row stride of a ring slot: the segment (and its lead room) rounded up
 // to an odd number of 16-byte units, so that the 16 rows of a step start in
-// 16 different bank quads.
+// 16 different bank quads.  Callers include 16 bytes of overflow room in
+// lead_room: lanes whose 16-byte piece lies past the segment store it there
+// (it is zeros: the buffer range ends at the segment), so that the copy into
+// LDS needs no branch.
 __host__ __device__ constexpr uint32_t mg_row_stride(uint32_t seg_bytes, uint32_t lead_room) {
   return ((seg_bytes + 15u) & ~15u) + lead_room + (((((seg_bytes + 15u) & ~15u) + lead_room) >> 4) & 1u ? 0u : 16u);
 }
@@ -93,6 +96,7 @@ constexpr int kMgLimbBytes = 4 * 32;            // four limbs of one block
 constexpr int mg_stage_bytes(int type) { return 8 * kMgLimbBytes + (type == WH_TYPE_Q6_K ? 0 : 8 * 16); }
 constexpr int kMgNt = 2;                       // streaming (non-temporal) loads
 constexpr int kMgNorm = 1, kMgFfn = 2;         // kernel variants
+constexpr int kMgDepth1 = 1;                   // steps in flight for one-segment rows
 
 template <int TYPE>
 struct MgFmt;
@@ -184,11 +188,12 @@ __device__ __forceinline__ void mg_quants(const uint32_t* pw, int g, long& qa, l
 }
 
 // Per-element dot product of one pair (64 weights at byte pointer p, in LDS)
-// with x[0..64) (global memory), normalised as x * inv * gamma when gamma is
-// set: w = (q - 8) * d, q * d + m or q * d as in dequantize_q4_0 / _q4_1 /
-// _q8_0, then w * x accumulated.  Used for chunks with non-finite activations.
-template <int TYPE>
-__device__ float mg_pair_exact(const uint8_t* p, const float* x, const float* gamma, float rms) {
+// with 64 activations (already RMS-normalised in the norm modes), xs(jj)
+// giving elements 4 jj .. 4 jj + 3: w = (q - 8) * d, q * d + m or q * d as in
+// dequantize_q4_0 / _q4_1 / _q8_0, then w * x accumulated in element order.
+// Used for chunks with non-finite activations.
+template <int TYPE, typename XS>
+__device__ float mg_pair_exact(const uint8_t* p, XS xs) {
   constexpr int BB = whd::BlockFmt<TYPE>::BYTES;
   float s = 0.f;
   for (int blk = 0; blk < 2; blk++) {
@@ -197,8 +202,12 @@ __device__ float mg_pair_exact(const uint8_t* p, const float* x, const float* ga
     float m = 0.f;
     if constexpr (TYPE == WH_TYPE_Q4_1)
       m = whd::f16_bits_to_f32(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
-#pragma unroll 2
-    for (int el = 0; el < 32; el++) {
+    for (int jj = 0; jj < 8; jj++) {
+      const float4 xq = xs(8 * blk + jj);
+      const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+      const int el = 4 * jj + c;
       float w;
       if constexpr (TYPE == WH_TYPE_Q4_0) {
         const uint32_t q = b[2 + (el & 15)];
@@ -209,9 +218,8 @@ __device__ float mg_pair_exact(const uint8_t* p, const float* x, const float* ga
       } else {
         w = static_cast<float>(static_cast<int8_t>(b[2 + el])) * d;
       }
-      float xv = x[32 * blk + el];
-      if (gamma) xv = (xv / rms) * gamma[32 * blk + el];
-      s = __builtin_fmaf(w, xv, s);
+      s = __builtin_fmaf(w, xa[c], s);
+      }
     }
   }
   return s;
@@ -227,30 +235,39 @@ __device__ __forceinline__ uint32_t mg_q4k_scale(const uint8_t* b, int j) {
 
 // Q4_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block at
 // blk, w = ((d * s) * q) + dmin as dequantize_q4_k_scalar evaluates it.
-__device__ float mg_q4k_exact(const uint8_t* blk, int g, const float* x, const float* gamma, float rms) {
+template <typename XS>
+__device__ float mg_q4k_exact(const uint8_t* blk, int g, XS xs) {
   const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[12]) | (static_cast<uint32_t>(blk[13]) << 8));
   const float dmin = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[14]) | (static_cast<uint32_t>(blk[15]) << 8));
   float s = 0.f;
-#pragma unroll 2
-  for (int el = 0; el < 64; el++) {
+  for (int jj = 0; jj < 16; jj++) {
+    const float4 xq = xs(jj);
+    const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+    const int el = 4 * jj + c;
     const int i = 64 * g + el;
     const float ds = __fmul_rn(d, static_cast<float>(mg_q4k_scale(blk, i >> 5)));
     const uint32_t qb = blk[16 + (i >> 1)];
     const float w = __fadd_rn(__fmul_rn(ds, static_cast<float>((i & 1) ? (qb >> 4) : (qb & 15u))), dmin);
-    float xv = x[el];
-    if (gamma) xv = (xv / rms) * gamma[el];
-    s = __builtin_fmaf(w, xv, s);
+    s = __builtin_fmaf(w, xa[c], s);
+    }
   }
   return s;
 }
 
 // Q6_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block
 // at blk, w = ((d * s) * (q - 32)) / 64 as dequantize_q6_k evaluates it.
-__device__ float mg_q6k_exact(const uint8_t* blk, int g, const float* x, const float* gamma, float rms) {
+template <typename XS>
+__device__ float mg_q6k_exact(const uint8_t* blk, int g, XS xs) {
   const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
   float s = 0.f;
-#pragma unroll 2
-  for (int el = 0; el < 64; el++) {
+  for (int jj = 0; jj < 16; jj++) {
+    const float4 xq = xs(jj);
+    const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+    const int el = 4 * jj + c;
     const int i = 64 * g + el;
     const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
     const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
@@ -266,9 +283,8 @@ __device__ float mg_q6k_exact(const uint8_t* blk, int g, const float* x, const f
     const float w = __fmul_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(blk[192 + (i >> 4)])),
                                         static_cast<float>(static_cast<int>(q) - 32)),
                               0.015625f);
-    float xv = x[el];
-    if (gamma) xv = (xv / rms) * gamma[el];
-    s = __builtin_fmaf(w, xv, s);
+    s = __builtin_fmaf(w, xa[c], s);
+    }
   }
   return s;
 }
@@ -290,8 +306,10 @@ __device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
 }
 
 // NL: 16-byte loads per lane per step (row segments of up to 1024 NL bytes).
-template <int TYPE, int NSEG, int NL, int MODE>
+// DEPTH: steps whose loads are in flight in registers (one-segment rows only).
+template <int TYPE, int NSEG, int NL, int MODE, int DEPTH>
 __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a) {
+  static_assert(DEPTH >= 1 && (DEPTH == 1 || NSEG == 1), "register prefetch of several steps needs one segment");
   constexpr int PB = MgFmt<TYPE>::PB;
   constexpr bool FFN = (MODE & kMgFfn) != 0;
   constexpr bool NORM = (MODE & kMgNorm) != 0;
@@ -310,7 +328,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   // are loaded from the boundary below, `lead` bytes early, into an LDS row
   // whose data then starts `lead` bytes in (the writes stay 16-byte aligned).
   constexpr uint32_t kLeadRoom = (CB & 15) ? 16u : 0u;
-  const uint32_t rstr = mg_row_stride(seg_bytes, kLeadRoom);
+  const uint32_t rstr = mg_row_stride(seg_bytes, kLeadRoom + 16u);
   const uint32_t slot_bytes = 16 * rstr;
   const size_t row_bytes = static_cast<size_t>(a.ppr >> 2) * CB;
   const int K = a.ppr * 64;
@@ -318,7 +336,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   uint8_t* stage = lds + 2 * slot_bytes + wave * NSEG * STG;  // per segment: limbs, block sums
   float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * NSEG * STG);  // [2][16][16]
   float* misc = part + 2 * kMgWaves * 16;                                                    // [16] + [16]
-  float* res_lds = misc + 32;                                                                 // residual rows
+  float* rows_lds = misc + 32;  // the workgroup's output rows (the residual, then += W x)
 
   const int r0 = blockIdx.x * a.rows_per_wg;
   const int r1 = min(a.n_out, r0 + a.rows_per_wg);
@@ -348,20 +366,27 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
     *base = w + static_cast<size_t>(local) * row_bytes;
     return true;
   };
-  mg_v4i buf[NL];
-  auto load = [&](int q, int seg) {
+  mg_v4i buf[DEPTH][NL];
+  auto load = [&](int q, int seg, int d) {
     const uint8_t* base = a.W0;
     const bool ok = row_src(q, &base);
     const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
     const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes - lead, ok ? seg_bytes + lead : 0u);
 #pragma unroll
-    for (int i = 0; i < NL; i++) buf[i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
+    for (int i = 0; i < NL; i++) buf[d][i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
   };
 
-  // The residual rows of the workgroup go to LDS first: inside the step loop a
-  // global load would make its consumer wait for every weight load in flight.
-  if (!FFN && a.residual) {
-    for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) res_lds[i] = a.residual[r0 + i];
+  // The workgroup's output rows are accumulated in LDS and stored to y after
+  // the step loop: a global store inside the loop would share the load
+  // counter with the weight loads, and the compiler then waits for every load
+  // in flight before each step.  They start as the residual (or 0).  Up to one
+  // row per thread the residual goes through a register, requested after x
+  // and before the weights (loads complete in order, so waiting for it does
+  // not wait for them); longer ranges are copied here.
+  const bool res_reg = r1 - r0 <= kMgWaves * 64;
+  if (!res_reg) {
+    for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64)
+      rows_lds[i] = (!FFN && a.residual) ? a.residual[r0 + i] : 0.f;
   }
   // ---- activations of this wave's chunks (4 consecutive per lane), then the first weights
   float xv[NSEG][4];
@@ -377,7 +402,13 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
     xv[seg][0] = xt.x, xv[seg][1] = xt.y, xv[seg][2] = xt.z, xv[seg][3] = xt.w;
     gv[seg][0] = gt.x, gv[seg][1] = gt.y, gv[seg][2] = gt.z, gv[seg][3] = gt.w;
   }
-  load(0, 0);
+  float resv = 0.f;
+  if (!FFN && a.residual && res_reg && static_cast<int>(threadIdx.x) < r1 - r0) resv = a.residual[r0 + threadIdx.x];
+#pragma unroll
+  for (int d = 0; d < DEPTH; d++) load(d, 0, d);
+  // Nothing that waits for x may be scheduled above the weight loads: the
+  // first step's weights must be requested before x's latency is waited out.
+  __builtin_amdgcn_sched_barrier(0);
 
   float rms = 1.f;
   if constexpr (NORM) {
@@ -460,6 +491,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
     }
   }
+  if (res_reg && static_cast<int>(threadIdx.x) < r1 - r0) rows_lds[threadIdx.x] = resv;
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
   // A operands of segment seg: lanes outside rows 4j..4j+3 of block j keep the
@@ -501,6 +533,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   };
   if constexpr (NSEG == 1) get_x(0);
 
+  // Elements 64 g + 4 jj .. + 3 of this wave's chunk of segment seg (the
+  // activations of the exact path, normalised like the limbs): lane 16 g + jj
+  // holds them (element 4 l + i of a chunk is xv[seg][i] of lane l).  The
+  // exact path is wave-uniform, so every lane takes part in the shuffles.
+  auto xquad = [&](int seg, int jj) -> float4 {
+    const int src = 16 * g + jj;
+    return make_float4(__shfl(xv[seg][0], src, 64), __shfl(xv[seg][1], src, 64), __shfl(xv[seg][2], src, 64),
+                       __shfl(xv[seg][3], src, 64));
+  };
+
   // Sum of group q over the 16 waves (fixed order), then the output row.
   auto finish = [&](int q) {
     if (lane >= 16) return;
@@ -516,35 +558,46 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
         return;
       }
       const float gt = misc[16 + n];
-      if (row < r1) a.y[row] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+      if (row < r1) rows_lds[row - r0] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
     } else {
-      if (row < r1) a.y[row] = (a.residual ? res_lds[row - r0] : 0.f) + v;
+      if (row < r1) rows_lds[row - r0] = rows_lds[row - r0] + v;
     }
   };
 
+  // With DEPTH > 1 the last pass may run up to DEPTH - 1 steps past GT: they
+  // copy (empty-range, so zero) loads and meet the barriers like any step but
+  // compute nothing.  No branch skips a load, so the compiler's wait counts
+  // stay exact (a skipped load merged into the loop header would make it wait
+  // for every load in flight).
   float acc = 0.f;
-  for (int q = 0; q < GT; q++) {
+  for (int q0 = 0; q0 < GT; q0 += DEPTH)
+#pragma unroll
+  for (int bb = 0; bb < DEPTH; bb++) {
+    const int q = q0 + bb;
+    const bool live = q < GT;
 #pragma unroll
     for (int seg = 0; seg < NSEG; seg++) {
       const int s = q * NSEG + seg;
       uint8_t* slot = ring + (s & 1) * slot_bytes;
       {
+        // every lane stores (pieces past the segment go to the overflow room)
         uint8_t* dst = slot + wave * rstr;
         const uint32_t end = seg_bytes + ((static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u));
+        const uint32_t end16 = (end + 15u) & ~15u;
 #pragma unroll
         for (int i = 0; i < NL; i++) {
           const uint32_t o = 16u * (64 * i + lane);
-          if (o < end) *reinterpret_cast<mg_v4i*>(dst + o) = buf[i];
+          *reinterpret_cast<mg_v4i*>(dst + (o < end16 ? o : end16)) = buf[bb][i];
         }
       }
-      if (seg + 1 < NSEG) load(q, seg + 1);
-      else load(q + 1, 0);
+      if (seg + 1 < NSEG) load(q, seg + 1, bb);
+      else load(q + DEPTH, 0, bb);
       // LDS-only barrier (a __syncthreads() would also wait for the loads in flight)
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
-      if (owns) {
+      if (seg == 0 && q > 0 && q < GT && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
+      if (owns && live) {
         if constexpr (NSEG > 1) get_x(seg);
         const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
         const uint8_t* rowp = slot + n * rstr + lead + wave * CB;
@@ -586,8 +639,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             acc += ldexpf(sacc, -ex[seg]);
           } else {
             // lane group g: elements 64 g .. 64 g + 63 of the block, row n
-            const int e0 = (seg * S + 4 * wave + g) * 64;
-            acc += mg_q6k_exact(rowp, g, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+            acc += mg_q6k_exact(rowp, g, [&](int jj) { return xquad(seg, jj); });
           }
         } else if constexpr (Q4K) {
           if (!exact[seg]) {
@@ -620,8 +672,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             acc += ldexpf(sacc, -ex[seg]);
           } else {
             // lane group g: elements 64 g .. 64 g + 63 of the block, row n
-            const int e0 = (seg * S + 4 * wave + g) * 64;
-            acc += mg_q4k_exact(rowp, g, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+            acc += mg_q4k_exact(rowp, g, [&](int jj) { return xquad(seg, jj); });
           }
         } else {
           if (!exact[seg]) {
@@ -658,12 +709,11 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             acc += ldexpf(sacc, -ex[seg]);
           } else {
             // lane group g: pair g of the chunk, row n
-            const int e0 = (seg * S + 4 * wave + g) * 64;
-            acc += mg_pair_exact<TYPE>(rowp + g * PB, a.x + e0, NORM ? a.gamma + e0 : nullptr, rms);
+            acc += mg_pair_exact<TYPE>(rowp + g * PB, [&](int jj) { return xquad(seg, jj); });
           }
         }
       }
-      if (seg == NSEG - 1) {
+      if (seg == NSEG - 1 && live) {
         float v = acc + __shfl_xor(acc, 16, 64);
         v += __shfl_xor(v, 32, 64);
         if (g == 0) part[(q & 1) * kMgWaves * 16 + wave * 16 + n] = v;
@@ -675,12 +725,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) a.y[r0 + i] = rows_lds[i];
 }
 
 size_t mg_lds_bytes(int type, int seg_pairs, int nseg, int rows_per_wg) {
   const int cb = mg_chunk_bytes(type);
   const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * cb);
-  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), (cb & 15) ? 16u : 0u);
+  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), ((cb & 15) ? 16u : 0u) + 16u);
   return 2u * 16u * rstr +
          static_cast<size_t>(kMgWaves) * nseg * mg_stage_bytes(type) +
          4u * (2 * kMgWaves * 16 + 32 + static_cast<size_t>(rows_per_wg));
@@ -704,9 +758,9 @@ int mg_segments(int type, size_t ppr) {
   return 0;
 }
 
-template <int TYPE, int NSEG, int NL, int MODE>
+template <int TYPE, int NSEG, int NL, int MODE, int DEPTH = 1>
 int mg_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
-  auto* fn = &gemv_mfma_kernel<TYPE, NSEG, NL, MODE>;
+  auto* fn = &gemv_mfma_kernel<TYPE, NSEG, NL, MODE, DEPTH>;
   WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  static_cast<int>(lds)));
   fn<<<grid, kMgWaves * 64, lds, s>>>(a);
@@ -717,7 +771,7 @@ int mg_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
 template <int TYPE, int NL, int MODE>
 int mg_dispatch_nl(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t s) {
   switch (nseg) {
-    case 1: return mg_launch<TYPE, 1, NL, MODE>(a, grid, lds, s);
+    case 1: return mg_launch<TYPE, 1, NL, MODE, kMgDepth1>(a, grid, lds, s);
     case 2: return mg_launch<TYPE, 2, NL, MODE>(a, grid, lds, s);
     case 3: return mg_launch<TYPE, 3, NL, MODE>(a, grid, lds, s);
     default: return mg_launch<TYPE, 4, NL, MODE>(a, grid, lds, s);
@@ -785,7 +839,7 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   size_t grid = groups < cus ? groups : cus;
   a.rows_per_wg = static_cast<int>((n_out + grid - 1) / grid);
   grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
-  const size_t lds = mg_lds_bytes(type, a.seg_pairs, nseg, a.residual ? a.rows_per_wg : 0);
+  const size_t lds = mg_lds_bytes(type, a.seg_pairs, nseg, a.rows_per_wg);
   if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
   const int mode = ffn ? (kMgNorm | kMgFfn) : (gamma ? kMgNorm : 0);
   switch (type) {
