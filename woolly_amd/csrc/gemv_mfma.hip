@@ -833,12 +833,15 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   a.n_out = static_cast<int>(n_out);
   a.ppr = static_cast<int>(ppr);
   a.seg_pairs = static_cast<int>(ppr / nseg);
-  // one workgroup per CU (or per 16 rows when there are fewer), rows split evenly
+  // at most one workgroup per CU, each with a whole number of 16-row groups:
+  // a half-empty last step costs about as much as a full one, so fewer
+  // workgroups with full steps finish sooner (Q4_0 K = 4096: 14336 rows in
+  // 224 x 64 take 8.55 us against 8.83 us in 256 x 56)
   const size_t groups = (n_out + 15) / 16;
   const size_t cus = static_cast<size_t>(cu_count());
-  size_t grid = groups < cus ? groups : cus;
-  a.rows_per_wg = static_cast<int>((n_out + grid - 1) / grid);
-  grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
+  const size_t grid0 = groups < cus ? groups : cus;
+  a.rows_per_wg = static_cast<int>((groups + grid0 - 1) / grid0 * 16);
+  const size_t grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
   const size_t lds = mg_lds_bytes(type, a.seg_pairs, nseg, a.rows_per_wg);
   if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
   const int mode = ffn ? (kMgNorm | kMgFfn) : (gamma ? kMgNorm : 0);
