@@ -300,6 +300,39 @@ __device__ __forceinline__ void mg_lds_u64(const uint8_t* p, int mis, uint32_t& 
   hi = __builtin_amdgcn_alignbit(w2, w1, sh);
 }
 
+// Cross-lane moves on the VALU (DPP) instead of ds_bpermute shuffles, which
+// go through the LDS pipe.
+template <int CTRL>
+__device__ __forceinline__ int mg_dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141, kDppMirror = 0x140;  // lane i <-> 7 - i (of 8), 15 - i (of 16)
+
+// Maximum of v over the 64 lanes (exact: max does not depend on the order).
+__device__ __forceinline__ float mg_wave_max(float v) {
+  auto step = [](float x, int y) { return fmaxf(x, __builtin_bit_cast(float, y)); };
+  const int b = __builtin_bit_cast(int, v);
+  v = step(v, mg_dpp<kDppXor1>(b));
+  v = step(v, mg_dpp<kDppXor2>(__builtin_bit_cast(int, v)));
+  v = step(v, mg_dpp<kDppHalfMirror>(__builtin_bit_cast(int, v)));
+  v = step(v, mg_dpp<kDppMirror>(__builtin_bit_cast(int, v)));  // every lane: the max of its 16-lane row
+  const int vi = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Sum over each group of 8 lanes (lanes 8k .. 8k + 7) of two small integers
+// packed as 16-bit fields, each in [0, 8192) after the sum (no carries).
+__device__ __forceinline__ int mg_sum8_packed(int v) {
+  v += mg_dpp<kDppXor1>(v);
+  v += mg_dpp<kDppXor2>(v);
+  return v + mg_dpp<kDppHalfMirror>(v);
+}
+
 // Bits 2t .. 2t + 1 of v (t = 0..3) moved to bits 4..5 of byte t.
 __device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
   return ((v << 4) | (v << 10) | (v << 16) | (v << 22)) & 0x30303030u;
@@ -447,8 +480,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       fin = fin && __builtin_isfinite(xv[seg][i]);  // fmaxf drops NaN
     }
     exact[seg] = __any(!fin);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = mg_wave_max(mx);
     int e = 0;
     if (mx > 0.f && !exact[seg]) {
       int ee;
@@ -458,36 +490,54 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
     ex[seg] = e;
     int8_t* xop = reinterpret_cast<int8_t*>(stage + seg * STG);
     int* bs_lds = reinterpret_cast<int*>(stage + seg * STG + 8 * kMgLimbBytes);
-    int bs[4] = {0, 0, 0, 0};
+    // Signed base-256 digits of xi = 2^24 l0 + 2^16 l1 + 2^8 l2 + l3 (l1..l3
+    // in [-128, 127]): adding 128 to each of the three low digits makes them
+    // bytes without carries, so the bytes of (xi + 0x808080) ^ 0x808080 are
+    // l3, l2, l1, l0 (|xi| < 2^30 keeps l0 within [-64, 64]).
+    uint32_t z[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int el_c = 4 * lane + i;  // element of the chunk
       // |x * 2^e| < 2^30: the conversion is exact for the chunk's larger elements
       const int xi = exact[seg] ? 0 : static_cast<int>(rintf(ldexpf(xv[seg][i], e)));
-      const int l3 = static_cast<int>(static_cast<int8_t>(xi & 0xFF));
-      int t = (xi - l3) >> 8;
-      const int l2 = static_cast<int>(static_cast<int8_t>(t & 0xFF));
-      t = (t - l2) >> 8;
-      const int l1 = static_cast<int>(static_cast<int8_t>(t & 0xFF));
-      const int l0 = (t - l1) >> 8;
-      int8_t* p = xop + (el_c >> 5) * kMgLimbBytes + mg_slot_offset<TYPE>(el_c & 31);
-      p[0] = static_cast<int8_t>(l0);
-      p[32] = static_cast<int8_t>(l1);
-      p[64] = static_cast<int8_t>(l2);
-      p[96] = static_cast<int8_t>(l3);
-      bs[0] += l0;
-      bs[1] += l1;
-      bs[2] += l2;
-      bs[3] += l3;
+      z[i] = static_cast<uint32_t>(xi + 0x808080) ^ 0x808080u;
     }
-    // a block is 8 consecutive lanes (Q6_K needs no sums: its bias is in the quants)
-    if constexpr (!Q6K) {
+    // the lane's four elements feed four consecutive k-slots (all but Q4_K):
+    // transpose the 4 x 4 bytes so that row[r] holds limb r of elements 0..3
+    uint32_t row[4];
+    {
+      const uint32_t a = __builtin_amdgcn_perm(z[1], z[0], 0x06020703u);  // z0.b3 z1.b3 z0.b2 z1.b2
+      const uint32_t b = __builtin_amdgcn_perm(z[1], z[0], 0x04000501u);  // z0.b1 z1.b1 z0.b0 z1.b0
+      const uint32_t c = __builtin_amdgcn_perm(z[3], z[2], 0x06020703u);
+      const uint32_t d = __builtin_amdgcn_perm(z[3], z[2], 0x04000501u);
+      row[0] = __builtin_amdgcn_perm(c, a, 0x05040100u);
+      row[1] = __builtin_amdgcn_perm(c, a, 0x07060302u);
+      row[2] = __builtin_amdgcn_perm(d, b, 0x05040100u);
+      row[3] = __builtin_amdgcn_perm(d, b, 0x07060302u);
+    }
+    int8_t* pb = xop + (lane >> 3) * kMgLimbBytes + mg_slot_offset<TYPE>(4 * (lane & 7));
+    if constexpr (Q4K) {
+      // elements 0..3 of the lane go to slots +0, +4, +1, +5
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        bs[r] += __shfl_xor(bs[r], 4, 64);
-        bs[r] += __shfl_xor(bs[r], 2, 64);
-        bs[r] += __shfl_xor(bs[r], 1, 64);
+        *reinterpret_cast<uint16_t*>(pb + 32 * r) = static_cast<uint16_t>(__builtin_amdgcn_perm(0u, row[r], 0x0c0c0200u));
+        *reinterpret_cast<uint16_t*>(pb + 32 * r + 4) = static_cast<uint16_t>(__builtin_amdgcn_perm(0u, row[r], 0x0c0c0301u));
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++) *reinterpret_cast<uint32_t*>(pb + 32 * r) = row[r];
+    }
+    int bs[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) bs[r] = __builtin_amdgcn_sdot4(static_cast<int>(row[r]), 0x01010101, 0, false);
+    // a block is 8 consecutive lanes (Q6_K needs no sums: its bias is in the quants)
+    if constexpr (!Q6K) {
+      // per lane each sum lies in [-512, 512): biased by 512, two per dword
+      const int p01 = mg_sum8_packed((bs[0] + 512) | ((bs[1] + 512) << 16));
+      const int p23 = mg_sum8_packed((bs[2] + 512) | ((bs[3] + 512) << 16));
+      bs[0] = (p01 & 0xFFFF) - 8 * 512;
+      bs[1] = (p01 >> 16) - 8 * 512;
+      bs[2] = (p23 & 0xFFFF) - 8 * 512;
+      bs[3] = (p23 >> 16) - 8 * 512;
       if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
     }
   }
