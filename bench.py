@@ -451,9 +451,10 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other decode GEMV configurations (4096x4096 Q4_0, Q8_0, Q4_1)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode step")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "gemm", "decode", "decode_q4_k_m"], default=None,
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "ffn", "gemm", "decode", "decode_q4_k_m"],
+                    default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
-    ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm")
+    ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm / --only ffn")
     ap.add_argument("--type", type=int, default=Q4_0,
                     help="ggml type id of --only gemm / ffn1 / ffn512 (default Q4_0)")
     ap.add_argument("--gemv-shape", type=int, nargs=3, default=None, metavar=("TYPE", "N", "K"),
@@ -495,8 +496,8 @@ def main() -> int:
     if args.only == "decode_q4_k_m":
         print(json.dumps({"decode_step_q4_k_m": bench_decode(10, types=Q4_K_M, head_type=14)}))
         return 0
-    if args.only in ("ffn1", "ffn512"):
-        m = 1 if args.only == "ffn1" else 512
+    if args.only in ("ffn1", "ffn512", "ffn"):
+        m = 1 if args.only == "ffn1" else 512 if args.only == "ffn512" else args.gemm_m
         print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3, args.type), 2),
                           "type": args.type}))
         return 0
@@ -514,6 +515,10 @@ def main() -> int:
     if not args.no_ffn:
         ffn["m1"] = round(bench_ffn(1, 50), 2)
         log(f"[bench] ffn m=1: {ffn['m1']} us")
+        # a few tokens (speculative / batched decode): one pass of the weights
+        for m in (2, 4):
+            ffn[f"m{m}"] = round(bench_ffn(m, 50), 2)
+            log(f"[bench] ffn m={m}: {ffn[f'm{m}']} us ({ffn[f'm{m}'] / ffn['m1']:.2f}x m=1)")
         ffn["m512"] = round(bench_ffn(512, 3), 2)
         log(f"[bench] ffn m=512: {ffn['m512']} us")
 
@@ -522,7 +527,7 @@ def main() -> int:
         # M sweep of config 2 (GEMV -> MFMA crossover).  tflops = 2*M*N*K / time;
         # the MFMA path issues two fp16 products per multiply-add (activation
         # hi and lo halves), so its MFMA work is twice that.
-        for m in (1, 8, 64, 512, 2048):
+        for m in (1, 2, 4, 8, 16, 64, 512, 2048):
             us = bench_gemm(m, 20 if m <= 64 else 5)
             tf = 2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12
             gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}

@@ -496,6 +496,14 @@ WH_API int wh_ffn_swiglu(const wh_ffn_weights* w, const float* gamma, float eps,
   const size_t gemm_bytes = need - static_cast<size_t>(ws - static_cast<char*>(workspace));
   hipStream_t s = hs(stream);
   if (F == 0) return wh::launch_fill_bytes(out, 0, m * H * sizeof(float), s);
+  if (m >= 2 && m <= 16 && wh::mt_allowed(F, H)) {
+    // a few tokens: RMSNorm, gate, up and SwiGLU for all of them in one pass
+    // of the gate / up weights, then the down projection
+    const void* gu[2] = {w->gate, w->up};
+    st = wh::launch_gemv_mt(w->type, gu, true, x, m, gamma, eps, h, F, F, H, s);
+    if (st == WH_OK) return wh::launch_gemm(w->type, w->down, H, F, h, m, out, gemm_ws, gemm_bytes, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   if (m <= wh::kGemvTokenLimit) {
     // decode: RMSNorm, gate, up and SwiGLU in one streaming kernel per token,
     // then the down GEMV; the unfused sequence below when the layout does not fit

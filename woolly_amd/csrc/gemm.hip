@@ -496,6 +496,15 @@ int launch_gemm_mfma(int type, const void* w, size_t n_rows, size_t k, const flo
 int launch_gemm(int type, const void* w, size_t n_rows, size_t k, const float* x, size_t n_tokens,
                 float* y, void* workspace, size_t workspace_bytes, hipStream_t s) {
   const bool kq = is_kquant(type);
+  // 2..16 tokens: one pass of the weights on the matrix-core GEMV (Q4_0 and
+  // Q8_0 shapes it takes); the workspace stays required as documented
+  if (n_tokens >= 2 && n_tokens <= 16 && k > 0 && mt_allowed(n_rows, k) &&
+      (n_tokens <= kGemvTokenLimit ||
+       (workspace && workspace_bytes >= gemm_workspace_bytes_for(type, n_rows, n_tokens, k)))) {
+    const void* mats[1] = {w};
+    const int st = launch_gemv_mt(type, mats, false, x, n_tokens, nullptr, 0.f, y, n_rows, n_rows, k, s);
+    if (st != WH_ERR_INVALID_SHAPE) return st;
+  }
   if (n_tokens <= kGemvTokenLimit || k == 0 || !aligned(w, 2) ||
       (kq && !gemm_kquant_ok(type, w, x, n_rows, k, n_tokens))) {
     for (size_t t = 0; t < n_tokens; t++) {

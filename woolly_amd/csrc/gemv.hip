@@ -836,6 +836,8 @@ namespace wh {
 // h = silu(W_gate x_hat) * (W_up x_hat), x_hat = rms_norm(x, gamma, eps).
 // Returns WH_ERR_INVALID_SHAPE without launching when the fused kernel's
 // layout conditions do not hold; the caller then runs the unfused sequence.
+bool mt_allowed(size_t n_rows, size_t k) { return t_gemv_mode == WH_GEMV_AUTO && k >= 1024 && n_rows >= 64; }
+
 int gemv_mode_exchange(int mode) {
   const int prev = t_gemv_mode;
   t_gemv_mode = mode;

@@ -146,6 +146,7 @@ struct MgArgs {
   const float* residual;
   float* y;
   int n_out, ppr, seg_pairs, rows_per_wg;
+  int m, ldy;  // several-token kernel: tokens (rows of x, K apart) and the row stride of y
 };
 
 // k-slot (0..7) of lane group g that element el (0..31) of a block feeds:
@@ -196,12 +197,14 @@ template <int TYPE, typename XS>
 __device__ float mg_pair_exact(const uint8_t* p, XS xs) {
   constexpr int BB = whd::BlockFmt<TYPE>::BYTES;
   float s = 0.f;
+#pragma unroll 1
   for (int blk = 0; blk < 2; blk++) {
     const uint8_t* b = p + blk * BB;
     const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
     float m = 0.f;
     if constexpr (TYPE == WH_TYPE_Q4_1)
       m = whd::f16_bits_to_f32(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
+#pragma unroll 1
     for (int jj = 0; jj < 8; jj++) {
       const float4 xq = xs(8 * blk + jj);
       const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
@@ -240,6 +243,7 @@ __device__ float mg_q4k_exact(const uint8_t* blk, int g, XS xs) {
   const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[12]) | (static_cast<uint32_t>(blk[13]) << 8));
   const float dmin = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[14]) | (static_cast<uint32_t>(blk[15]) << 8));
   float s = 0.f;
+#pragma unroll 1
   for (int jj = 0; jj < 16; jj++) {
     const float4 xq = xs(jj);
     const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
@@ -262,6 +266,7 @@ template <typename XS>
 __device__ float mg_q6k_exact(const uint8_t* blk, int g, XS xs) {
   const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
   float s = 0.f;
+#pragma unroll 1
   for (int jj = 0; jj < 16; jj++) {
     const float4 xq = xs(jj);
     const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
@@ -584,13 +589,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   if constexpr (NSEG == 1) get_x(0);
 
   // Elements 64 g + 4 jj .. + 3 of this wave's chunk of segment seg (the
-  // activations of the exact path, normalised like the limbs): lane 16 g + jj
-  // holds them (element 4 l + i of a chunk is xv[seg][i] of lane l).  The
-  // exact path is wave-uniform, so every lane takes part in the shuffles.
+  // activations of the exact path, normalised like the limbs), read again from
+  // x (and gamma) so that no register holds the activations past the limbs.
   auto xquad = [&](int seg, int jj) -> float4 {
-    const int src = 16 * g + jj;
-    return make_float4(__shfl(xv[seg][0], src, 64), __shfl(xv[seg][1], src, 64), __shfl(xv[seg][2], src, 64),
-                       __shfl(xv[seg][3], src, 64));
+    const int el = (seg * S + 4 * wave) * 64 + 64 * g + 4 * jj;
+    float4 v = *reinterpret_cast<const float4*>(a.x + el);
+    if constexpr (NORM) {
+      const float4 gm = *reinterpret_cast<const float4*>(a.gamma + el);
+      v = make_float4((v.x / rms) * gm.x, (v.y / rms) * gm.y, (v.z / rms) * gm.z, (v.w / rms) * gm.w);
+    }
+    return v;
   };
 
   // Sum of group q over the 16 waves (fixed order), then the output row.
@@ -781,6 +789,368 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) a.y[r0 + i] = rows_lds[i];
 }
 
+// ---------------------------------------------------------------- several tokens
+// The matrix-core GEMV for 2..16 tokens (Q4_0, Q8_0): Y[t] = W X[t] (plain
+// mode) or the FFN gate/up pair with each token's RMSNorm prologue and the
+// SwiGLU epilogue (FFN mode), in the data flow of gemv_mfma_kernel.  The A
+// operand of one MFMA carries the limbs of four tokens for ONE block (rows
+// 4 t + limb, t = token within its group of four), so each block's weights,
+// unpacked once, meet one MFMA per group of four tokens and stream from HBM
+// once for all tokens; lane group g of the result holds token 4 tg + g's four
+// limb sums of the block.  Q4_0's -8 goes into the B operand: nibble ^ 8 read
+// as a signed 4-bit number is q - 8, kept in the high half of each byte
+// (16 (q - 8), an exact int8), and the block scale enters as d / 16.  The A
+// operands of every segment stay in registers (TG * NSEG <= 4).
+// MS = 2 (two tokens): rows 8 (b & 1) + 4 t + limb, so blocks 2p and 2p + 1
+// share one accumulator and lane group g holds token g & 1 of block
+// 2p + (g >> 1), half the accumulator conversions of the four-token layout.
+template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS>
+__global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) {
+  static_assert(TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q8_0, "several-token GEMV: Q4_0 and Q8_0");
+  static_assert(TG * NSEG <= 4, "A operands of every segment in registers");
+  static_assert(MS == 4 || (MS == 2 && TG == 1), "two-token layout: one group");
+  constexpr int PB = MgFmt<TYPE>::PB;
+  constexpr int BB = PB / 2;  // bytes of one block
+  constexpr bool FFN = (MODE & kMgFfn) != 0;
+  constexpr bool NORM = (MODE & kMgNorm) != 0;
+  constexpr int CB = mg_chunk_bytes(TYPE);  // a multiple of 16: segments start 16-byte aligned
+  constexpr int STG = mg_stage_bytes(TYPE);
+  constexpr int MT = MS * TG;  // token slots
+  constexpr float kScale = TYPE == WH_TYPE_Q4_0 ? 0.0625f : 1.0f;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int S = a.seg_pairs;
+  const int M = a.m;
+  const uint32_t seg_bytes = static_cast<uint32_t>(S >> 2) * CB;
+  const uint32_t rstr = mg_row_stride(seg_bytes, 16u);
+  const uint32_t slot_bytes = 16 * rstr;
+  const size_t row_bytes = static_cast<size_t>(a.ppr >> 2) * CB;
+  const int K = a.ppr * 64;
+  const int R = a.rows_per_wg;
+  uint8_t* ring = lds;
+  uint8_t* stage = lds + 2 * slot_bytes + wave * STG;
+  float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * STG);  // [2][16 waves][MT][16]
+  float* misc = part + 2 * kMgWaves * MT * 16;  // [16 waves][MT] norm sums, later [MT][16] gate values
+  float* rms_lds = misc + kMgWaves * MT;        // [MT] RMSNorm scale of each token
+  float* rows_lds = rms_lds + MT;               // [MT][R] the workgroup's output rows
+
+  const int r0 = blockIdx.x * R;
+  const int r1 = min(a.n_out, r0 + R);
+  const int G = (r1 - r0 + 15) >> 4;
+  const int GT = FFN ? 2 * G : G;
+  const bool owns = wave < (S >> 2);
+
+  auto row_src = [&](int q, const uint8_t** base) -> bool {
+    const int gi = FFN ? (q >> 1) : q;
+    const int row = r0 + 16 * gi + wave;
+    if (q >= GT || row >= r1) return false;
+    *base = (FFN && (q & 1) ? a.W1 : a.W0) + static_cast<size_t>(row) * row_bytes;
+    return true;
+  };
+  mg_v4i buf[NL];
+  auto load = [&](int q, int seg) {
+    const uint8_t* base = a.W0;
+    const bool ok = row_src(q, &base);
+    const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes, ok ? seg_bytes : 0u);
+#pragma unroll
+    for (int i = 0; i < NL; i++) buf[i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
+  };
+  auto xload = [&](int t, int seg) -> float4 {
+    if (t >= M || !owns) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + (seg * S + 4 * wave) * 64 + 4 * lane);
+  };
+
+  // ---- each token's RMSNorm scale (a workgroup reduction of sum x^2)
+  float rms[MT];
+  float4 gv[NSEG];
+#pragma unroll
+  for (int t = 0; t < MT; t++) rms[t] = 1.f;
+  if constexpr (NORM) {
+#pragma unroll
+    for (int seg = 0; seg < NSEG; seg++)
+      gv[seg] = owns ? *reinterpret_cast<const float4*>(a.gamma + (seg * S + 4 * wave) * 64 + 4 * lane)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      float ss = 0.f;
+#pragma unroll
+      for (int seg = 0; seg < NSEG; seg++) {
+        const float4 v = xload(t, seg);
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+      }
+      ss = whd::wave_sum(ss);
+      if (lane == 0) misc[wave * MT + t] = ss;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMgWaves; w++) tot += misc[w * MT + t];
+      rms[t] = sqrtf(tot / static_cast<float>(K) + a.eps);
+    }
+    if (threadIdx.x < MT) rms_lds[threadIdx.x] = rms[threadIdx.x];
+  }
+  for (int i = threadIdx.x; i < MT * R; i += kMgWaves * 64) rows_lds[i] = 0.f;
+  load(0, 0);
+
+  // ---- limbs of every (segment, token) chunk -> A operands in registers
+  // two-token layout: a lane's rows belong to the even blocks (n < 8) or the
+  // odd ones, so one register per block pair holds its nonzero operand
+  constexpr int NA = MS == 4 ? 8 : 4;
+  long xa[NSEG][TG][NA];
+  int ex_u[NSEG][MT];       // chunk exponent (wave-uniform)
+  uint32_t exact_u[NSEG];   // bit t: token t's chunk holds inf / NaN (computed per element)
+#pragma unroll
+  for (int seg = 0; seg < NSEG; seg++)
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++)
+#pragma unroll
+      for (int b = 0; b < NA; b++) xa[seg][tg][b] = 0;
+  auto xnorm = [&](int t, int seg) -> float4 {
+    float4 v = xload(t, seg);
+    if constexpr (NORM) {
+      v.x = (v.x / rms[t]) * gv[seg].x;
+      v.y = (v.y / rms[t]) * gv[seg].y;
+      v.z = (v.z / rms[t]) * gv[seg].z;
+      v.w = (v.w / rms[t]) * gv[seg].w;
+    }
+    return v;
+  };
+#pragma unroll
+  for (int seg = 0; seg < NSEG; seg++) {
+    exact_u[seg] = 0u;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      const float4 v = xnorm(t, seg);
+      const float xv[4] = {v.x, v.y, v.z, v.w};
+      float mx = 0.f;
+      bool fin = true;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        mx = fmaxf(mx, fabsf(xv[i]));
+        fin = fin && __builtin_isfinite(xv[i]);
+      }
+      const bool exact = __any(!fin);
+      mx = mg_wave_max(mx);
+      int e = 0;
+      if (mx > 0.f && !exact) {
+        int ee;
+        frexpf(mx, &ee);
+        e = 30 - ee;
+      }
+      ex_u[seg][t] = __builtin_amdgcn_readfirstlane(e);
+      if (exact) exact_u[seg] |= 1u << t;
+      uint32_t z[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int xi = exact ? 0 : static_cast<int>(rintf(ldexpf(xv[i], e)));
+        z[i] = static_cast<uint32_t>(xi + 0x808080) ^ 0x808080u;
+      }
+      const uint32_t pa = __builtin_amdgcn_perm(z[1], z[0], 0x06020703u);
+      const uint32_t pb2 = __builtin_amdgcn_perm(z[1], z[0], 0x04000501u);
+      const uint32_t pc = __builtin_amdgcn_perm(z[3], z[2], 0x06020703u);
+      const uint32_t pd = __builtin_amdgcn_perm(z[3], z[2], 0x04000501u);
+      int8_t* pw = reinterpret_cast<int8_t*>(stage) + (lane >> 3) * kMgLimbBytes + mg_slot_offset<TYPE>(4 * (lane & 7));
+      *reinterpret_cast<uint32_t*>(pw) = __builtin_amdgcn_perm(pc, pa, 0x05040100u);
+      *reinterpret_cast<uint32_t*>(pw + 32) = __builtin_amdgcn_perm(pc, pa, 0x07060302u);
+      *reinterpret_cast<uint32_t*>(pw + 64) = __builtin_amdgcn_perm(pd, pb2, 0x05040100u);
+      *reinterpret_cast<uint32_t*>(pw + 96) = __builtin_amdgcn_perm(pd, pb2, 0x07060302u);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      // this token's rows of the A operands (four-token layout: rows 4 (t & 3)
+      // .. + 3 of token group t / 4; two-token layout: rows 8 (b & 1) + 4 t ..)
+      {
+        const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + 32 * (n & 3) + 8 * g;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+          const int slot = MS == 4 ? (t & 3) : 2 * (b & 1) + t;
+          if ((n >> 2) == slot)
+            xa[seg][MS == 4 ? t >> 2 : 0][MS == 4 ? b : b >> 1] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  // exponent of the token this lane's results belong to (4 tg + g; two-token layout: g & 1)
+  int ex_l[NSEG][TG];
+#pragma unroll
+  for (int seg = 0; seg < NSEG; seg++)
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) {
+      if constexpr (MS == 4) {
+        const int* e4 = &ex_u[seg][4 * tg];
+        ex_l[seg][tg] = g == 0 ? e4[0] : g == 1 ? e4[1] : g == 2 ? e4[2] : e4[3];
+      } else {
+        ex_l[seg][tg] = (g & 1) ? ex_u[seg][1] : ex_u[seg][0];
+      }
+    }
+
+  // B operand of lane group g for the two blocks of the pair at pw (LDS)
+  auto quants = [&](const uint32_t* pw, long& qa, long& qb) {
+    if constexpr (TYPE == WH_TYPE_Q4_0) {
+      auto split = [](uint32_t u) -> long {
+        const uint32_t v = u ^ 0x88888888u;  // nibble ^ 8: q - 8 as a signed 4-bit number
+        return static_cast<long>((v << 4) & 0xF0F0F0F0u) | (static_cast<long>(v & 0xF0F0F0F0u) << 32);
+      };
+      qa = split(__builtin_amdgcn_alignbit(pw[g + 1], pw[g], 16));
+      qb = split(pw[5 + g]);
+    } else {
+      const uint32_t w0 = pw[2 * g], w1 = pw[2 * g + 1], w2 = pw[2 * g + 2];
+      qa = static_cast<long>(__builtin_amdgcn_alignbit(w1, w0, 16)) |
+           (static_cast<long>(__builtin_amdgcn_alignbit(w2, w1, 16)) << 32);
+      qb = static_cast<long>(pw[9 + 2 * g]) | (static_cast<long>(pw[10 + 2 * g]) << 32);
+    }
+  };
+  auto combine = [](const mg_v4i& C) -> float {
+    return __builtin_fmaf(static_cast<float>(C[0]), 16777216.f,
+                          __builtin_fmaf(static_cast<float>(C[1]), 65536.f,
+                                         __builtin_fmaf(static_cast<float>(C[2]), 256.f, static_cast<float>(C[3]))));
+  };
+
+  // Sum of group q over the 16 waves (fixed order) for every token, then the output rows.
+  auto finish = [&](int q) {
+    const int gi = FFN ? (q >> 1) : q;
+    const int row = r0 + 16 * gi + n;
+    if (MS == 2 && g >= 2) return;
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) {
+      const int t = MS * tg + g;
+      const float* pp = part + ((q & 1) * kMgWaves * MT + t) * 16 + n;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMgWaves; w++) v += pp[w * MT * 16];
+      if constexpr (FFN) {
+        if ((q & 1) == 0) {
+          misc[t * 16 + n] = v;  // gate, combined with up one group later
+        } else if (row < r1) {
+          const float gt = misc[t * 16 + n];
+          rows_lds[t * R + row - r0] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+        }
+      } else if (row < r1) {
+        rows_lds[t * R + row - r0] = v;
+      }
+    }
+  };
+
+  float acc[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; tg++) acc[tg] = 0.f;
+  for (int q = 0; q < GT; q++) {
+#pragma unroll
+    for (int seg = 0; seg < NSEG; seg++) {
+      const int s = q * NSEG + seg;
+      uint8_t* slot = ring + (s & 1) * slot_bytes;
+      {
+        uint8_t* dst = slot + wave * rstr;
+        const uint32_t end16 = (seg_bytes + 15u) & ~15u;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+          const uint32_t o = 16u * (64 * i + lane);
+          *reinterpret_cast<mg_v4i*>(dst + (o < end16 ? o : end16)) = buf[i];
+        }
+      }
+      if (seg + 1 < NSEG) load(q, seg + 1);
+      else load(q + 1, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
+      if (owns) {
+        const uint8_t* rowp = slot + n * rstr + wave * CB;
+        float sacc[TG];
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) sacc[tg] = 0.f;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+          long qa, qb;
+          quants(reinterpret_cast<const uint32_t*>(rowp + p * PB), qa, qb);
+          const float da = whd::f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + p * PB)) * kScale;
+          const float db = whd::f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + p * PB + BB)) * kScale;
+#pragma unroll
+          for (int tg = 0; tg < TG; tg++) {
+            const mg_v4i zero = {0, 0, 0, 0};
+            if constexpr (MS == 4) {
+              const mg_v4i ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p], qa, zero, 0, 0, 0);
+              const mg_v4i cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p + 1], qb, zero, 0, 0, 0);
+              sacc[tg] = __builtin_fmaf(da, combine(ca), sacc[tg]);
+              sacc[tg] = __builtin_fmaf(db, combine(cb), sacc[tg]);
+            } else {
+              const long ae = n < 8 ? xa[seg][tg][p] : 0, ao = n < 8 ? 0 : xa[seg][tg][p];
+              mg_v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, qa, zero, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ao, qb, c, 0, 0, 0);
+              sacc[tg] = __builtin_fmaf((g >> 1) ? db : da, combine(c), sacc[tg]);
+            }
+          }
+        }
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) acc[tg] += ldexpf(sacc[tg], -ex_l[seg][tg]);
+        // tokens whose chunk is not finite: their limbs are zero, the lanes of
+        // the token add the chunk per element (the reference's order)
+        for (uint32_t em = exact_u[seg]; em != 0u; em &= em - 1u) {
+          const int t = __builtin_ctz(em);
+          if (g != (MS == 4 ? (t & 3) : t)) continue;
+          const float rt = NORM ? rms_lds[t] : 1.f;
+          float sx = 0.f;
+#pragma unroll 1
+          for (int p = 0; p < 4; p++)
+            sx += mg_pair_exact<TYPE>(rowp + p * PB, [&](int jj) {
+              const int el = (seg * S + 4 * wave) * 64 + 64 * p + 4 * jj;
+              float4 v = *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + el);
+              if constexpr (NORM) {
+                const float4 gm = *reinterpret_cast<const float4*>(a.gamma + el);
+                v = make_float4((v.x / rt) * gm.x, (v.y / rt) * gm.y, (v.z / rt) * gm.z, (v.w / rt) * gm.w);
+              }
+              return v;
+            });
+#pragma unroll
+          for (int tg = 0; tg < TG; tg++)
+            if (t / MS == tg) acc[tg] += sx;
+        }
+      }
+      if (seg == NSEG - 1) {
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+          if constexpr (MS == 4) {
+            part[(((q & 1) * kMgWaves + wave) * MT + 4 * tg + g) * 16 + n] = acc[tg];
+          } else {
+            // token g & 1: the even blocks' sum (lane group g) + the odd blocks' (g + 2)
+            const float v = acc[tg] + __shfl_xor(acc[tg], 32, 64);
+            if (g < 2) part[(((q & 1) * kMgWaves + wave) * MT + g) * 16 + n] = v;
+          }
+          acc[tg] = 0.f;
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  for (int i = threadIdx.x; i < M * (r1 - r0); i += kMgWaves * 64) {
+    const int t = i / (r1 - r0), r = i - t * (r1 - r0);
+    a.y[static_cast<size_t>(t) * a.ldy + r0 + r] = rows_lds[t * R + r];
+  }
+}
+
+size_t mt_lds_bytes(int type, int seg_pairs, int mt, int rows_per_wg) {
+  const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * mg_chunk_bytes(type));
+  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), 16u);
+  return 2u * 16u * rstr + static_cast<size_t>(kMgWaves) * mg_stage_bytes(type) +
+         4u * (2u * kMgWaves * mt * 16 + static_cast<size_t>(kMgWaves) * mt + mt + static_cast<size_t>(mt) * rows_per_wg);
+}
+
 size_t mg_lds_bytes(int type, int seg_pairs, int nseg, int rows_per_wg) {
   const int cb = mg_chunk_bytes(type);
   const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * cb);
@@ -832,6 +1202,8 @@ template <int TYPE, int MODE>
 int mg_dispatch(const MgArgs& a, int nseg, int grid, size_t lds, hipStream_t s) {
   // bytes one lane group of 64 lanes loads per row: the segment and its lead
   const int seg_bytes = a.seg_pairs / 4 * mg_chunk_bytes(TYPE) + ((mg_chunk_bytes(TYPE) & 15) ? 15 : 0);
+  if constexpr (TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q4_1 || TYPE == WH_TYPE_Q8_0)
+    if (nseg == 4 && seg_bytes <= 2048) return mg_launch<TYPE, 4, 2, MODE>(a, grid, lds, s);
   return seg_bytes <= 3072 ? mg_dispatch_nl<TYPE, 3, MODE>(a, nseg, grid, lds, s)
                            : mg_dispatch_nl<TYPE, 4, MODE>(a, nseg, grid, lds, s);
 }
@@ -843,6 +1215,46 @@ int mg_typed(const MgArgs& a, int nseg, int mode, int grid, size_t lds, hipStrea
     case kMgNorm: return mg_dispatch<TYPE, kMgNorm>(a, nseg, grid, lds, s);
     default: return mg_dispatch<TYPE, kMgNorm | kMgFfn>(a, nseg, grid, lds, s);
   }
+}
+
+template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS = 4>
+int mt_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
+  auto* fn = &gemv_mt_kernel<TYPE, NSEG, NL, MODE, TG, MS>;
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(lds)));
+  fn<<<grid, kMgWaves * 64, lds, s>>>(a);
+  WH_LAUNCH_CHECK("gemv (several tokens) kernel launch");
+  return WH_OK;
+}
+
+template <int TYPE, int NL, int MODE>
+int mt_dispatch_nl(const MgArgs& a, int nseg, int tg, int grid, size_t lds, hipStream_t s) {
+  if (a.m == 2) {
+    switch (nseg) {
+      case 1: return mt_launch<TYPE, 1, NL, MODE, 1, 2>(a, grid, lds, s);
+      case 2: return mt_launch<TYPE, 2, NL, MODE, 1, 2>(a, grid, lds, s);
+      default: return mt_launch<TYPE, 4, NL, MODE, 1, 2>(a, grid, lds, s);
+    }
+  }
+  if (nseg == 1) {
+    switch (tg) {
+      case 1: return mt_launch<TYPE, 1, NL, MODE, 1>(a, grid, lds, s);
+      case 2: return mt_launch<TYPE, 1, NL, MODE, 2>(a, grid, lds, s);
+      case 3: return mt_launch<TYPE, 1, NL, MODE, 3>(a, grid, lds, s);
+      default: return mt_launch<TYPE, 1, NL, MODE, 4>(a, grid, lds, s);
+    }
+  }
+  if (nseg == 2) return tg == 1 ? mt_launch<TYPE, 2, NL, MODE, 1>(a, grid, lds, s) : mt_launch<TYPE, 2, NL, MODE, 2>(a, grid, lds, s);
+  return mt_launch<TYPE, 4, NL, MODE, 1>(a, grid, lds, s);
+}
+
+template <int TYPE, int MODE>
+int mt_dispatch(const MgArgs& a, int nseg, int tg, int grid, size_t lds, hipStream_t s) {
+  const int seg_bytes = a.seg_pairs / 4 * mg_chunk_bytes(TYPE);
+  if (nseg == 4 && seg_bytes <= 2048)
+    return a.m == 2 ? mt_launch<TYPE, 4, 2, MODE, 1, 2>(a, grid, lds, s) : mt_launch<TYPE, 4, 2, MODE, 1>(a, grid, lds, s);
+  return seg_bytes <= 3072 ? mt_dispatch_nl<TYPE, 3, MODE>(a, nseg, tg, grid, lds, s)
+                           : mt_dispatch_nl<TYPE, 4, MODE>(a, nseg, tg, grid, lds, s);
 }
 
 }  // namespace
@@ -883,6 +1295,8 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   a.n_out = static_cast<int>(n_out);
   a.ppr = static_cast<int>(ppr);
   a.seg_pairs = static_cast<int>(ppr / nseg);
+  a.m = 1;
+  a.ldy = static_cast<int>(n_out);
   // at most one workgroup per CU, each with a whole number of 16-row groups:
   // a half-empty last step costs about as much as a full one, so fewer
   // workgroups with full steps finish sooner (Q4_0 K = 4096: 14336 rows in
@@ -902,6 +1316,53 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
     case WH_TYPE_Q6_K: return mg_typed<WH_TYPE_Q6_K>(a, nseg, mode, static_cast<int>(grid), lds, s);
     default: return mg_typed<WH_TYPE_Q8_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
   }
+}
+
+
+// Several tokens (2..16) on the matrix cores: plain Y[t] = W X[t] (mats =
+// {W}) or, with ffn, H[t] = silu(gate x_hat[t]) * (up x_hat[t]) (mats = {gate,
+// up}, x_hat the RMS-normalised x[t]).  x: [m][k]; y: row t at y + t * ldy.
+// WH_ERR_INVALID_SHAPE without launching when the shape does not fit.
+int launch_gemv_mt(int type, const void* const* mats, bool ffn, const float* x, size_t m, const float* gamma,
+                   float eps, float* y, size_t ldy, size_t n_out, size_t k, hipStream_t s) {
+  if (n_out == 0 || m == 0) return WH_OK;
+  if ((type != WH_TYPE_Q4_0 && type != WH_TYPE_Q8_0) || m < 2 || m > 16 || !gemv_mfma_ok(type, n_out, k) ||
+      (ffn && !gamma))
+    return WH_ERR_INVALID_SHAPE;
+  const size_t ppr = k / 64;
+  const int nseg = mg_segments(type, ppr);
+  const int tg = static_cast<int>((m + 3) / 4);
+  if (nseg == 3 || tg * nseg > 4) return WH_ERR_INVALID_SHAPE;
+  for (int i = 0; i < (ffn ? 2 : 1); i++)
+    if (!aligned(mats[i], 4)) return WH_ERR_INVALID_SHAPE;
+  if (!aligned(x, 16) || (gamma && !aligned(gamma, 16))) return WH_ERR_INVALID_SHAPE;
+  MgArgs a{};
+  a.W0 = static_cast<const uint8_t*>(mats[0]);
+  a.W1 = ffn ? static_cast<const uint8_t*>(mats[1]) : a.W0;
+  a.W2 = a.W1;
+  a.n0 = static_cast<int>(n_out);
+  a.x = x;
+  a.gamma = gamma;
+  a.eps = eps;
+  a.y = y;
+  a.n_out = static_cast<int>(n_out);
+  a.ppr = static_cast<int>(ppr);
+  a.seg_pairs = static_cast<int>(ppr / nseg);
+  a.m = static_cast<int>(m);
+  a.ldy = static_cast<int>(ldy);
+  const size_t groups = (n_out + 15) / 16;
+  const size_t cus = static_cast<size_t>(cu_count());
+  const size_t grid0 = groups < cus ? groups : cus;
+  a.rows_per_wg = static_cast<int>((groups + grid0 - 1) / grid0 * 16);
+  const size_t grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
+  const size_t lds = mt_lds_bytes(type, a.seg_pairs, m == 2 ? 2 : 4 * tg, a.rows_per_wg);
+  if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
+  const int g = static_cast<int>(grid);
+  if (type == WH_TYPE_Q4_0)
+    return ffn ? mt_dispatch<WH_TYPE_Q4_0, kMgNorm | kMgFfn>(a, nseg, tg, g, lds, s)
+               : mt_dispatch<WH_TYPE_Q4_0, 0>(a, nseg, tg, g, lds, s);
+  return ffn ? mt_dispatch<WH_TYPE_Q8_0, kMgNorm | kMgFfn>(a, nseg, tg, g, lds, s)
+             : mt_dispatch<WH_TYPE_Q8_0, 0>(a, nseg, tg, g, lds, s);
 }
 
 }  // namespace wh

@@ -118,6 +118,17 @@ bool gemv_mfma_ok(int type, size_t n_out, size_t k);
 int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
                      const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
                      hipStream_t stream);
+// 2..16 tokens on the matrix cores (gemv_mfma.hip, Q4_0 and Q8_0): plain
+// Y[t] = W X[t] (mats = {W}) or, with ffn, H[t] = silu(gate x_hat[t]) *
+// (up x_hat[t]) with each token's RMSNorm (mats = {gate, up}); x is [m][k], row
+// t of y starts at y + t * ldy.  WH_ERR_INVALID_SHAPE (nothing launched) when
+// the shape does not fit.
+int launch_gemv_mt(int type, const void* const* mats, bool ffn, const float* x, size_t m, const float* gamma,
+                   float eps, float* y, size_t ldy, size_t n_out, size_t k, hipStream_t stream);
+// Whether several-token products may take launch_gemv_mt: the calling
+// thread's wh_gemv_select mode and the sizes the single-token matrix-core
+// kernel needs (gemv.hip).
+bool mt_allowed(size_t n_rows, size_t k);
 // WH_GEMV_AUTO / WH_GEMV_STREAM (wh_gemv_select); returns the previous mode.
 int gemv_mode_exchange(int mode);
 // Token counts up to this use one streaming GEMV per token instead of MFMA.
