@@ -184,27 +184,34 @@ def bench_ffn(m: int, iters: int, t: int = Q4_0, replicas: int | None = None) ->
     return e0.elapsed_ms(e1) / (3 * n) * 1000.0
 
 
-def bench_gemm(m: int, iters: int, t: int = Q4_0) -> float:
-    """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t), µs
-    per call.  For m <= 64, where the call streams its 33 MB of weights about
-    once, 10 weight copies (> 256 MB, the Infinity Cache) are rotated; the calls
-    are captured into a HIP graph and replayed."""
+def bench_gemm(m: int, iters: int, t: int = Q4_0, bf16: bool = False) -> float:
+    """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t; X in
+    bfloat16 with bf16), µs per call.  For m <= 64, where the call streams its
+    33 MB of weights about once, 10 weight copies (> 256 MB, the Infinity
+    Cache) are rotated; the calls are captured into a HIP graph and replayed."""
     from woolly_amd import ops, synth
     from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
 
     w = synth.quantized_weight(t, N_ROWS, K, seed=4)
     x = np.concatenate([synth.activations(K, seed=400 + i) for i in range(min(m, 64))])
     x = np.resize(x, m * K).astype(np.float32)
+    if bf16:
+        x = (x.view(np.uint32) >> 16).astype(np.uint16)
     replicas = 10 if m <= 64 else 1
     stream = Stream()
     wbs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
     xb = DeviceBuffer.from_array(x)
     yb = DeviceBuffer(4 * m * N_ROWS)
-    wsz = ops.matmul_workspace_bytes(t, N_ROWS, K, m)
+    wsz = (ops.matmul_x_workspace_bytes(t, N_ROWS, K, m, ops.TYPE_BF16) if bf16
+           else ops.matmul_workspace_bytes(t, N_ROWS, K, m))
     ws = DeviceBuffer(max(wsz, 256))
 
     def run(i):
-        ops.quantized_matmul(t, wbs[i % replicas], w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
+        if bf16:
+            ops.quantized_matmul_x(t, wbs[i % replicas], w.nbytes, N_ROWS, K, xb, ops.TYPE_BF16, m, yb, ws, wsz,
+                                   stream)
+        else:
+            ops.quantized_matmul(t, wbs[i % replicas], w.nbytes, N_ROWS, K, xb, m, yb, ws, wsz, stream)
 
     for i in range(3):
         run(i)
@@ -532,6 +539,10 @@ def main() -> int:
             tf = 2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12
             gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}
             log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s")
+        for m in (8, 512):
+            us = bench_gemm(m, 20 if m <= 64 else 5, bf16=True)
+            gemm[f"m{m}_bf16"] = {"us": round(us, 2), "tflops": round(2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12, 2)}
+            log(f"[bench] gemm bf16 activations m={m}: {us:.2f} us")
         # K-quant weights at M=512: the call includes rewriting the matrix into
         # 32-element f32-scale blocks (Q6_K: zero-padded 16-element halves)
         for name, t in (("q4_k", 12), ("q6_k", 14)):

@@ -52,6 +52,7 @@ pub const WH_TYPE_Q4_1: c_int = 3;
 pub const WH_TYPE_Q8_0: c_int = 8;
 pub const WH_TYPE_Q4_K: c_int = 12;
 pub const WH_TYPE_Q6_K: c_int = 14;
+pub const WH_TYPE_BF16: c_int = 30;
 
 // ------------------------------------------------------- single-token GEMV kernels
 pub const WH_GEMV_AUTO: c_int = 0;
@@ -244,6 +245,12 @@ extern "C" {
     pub fn wh_quantized_matmul(r#type: c_int, weights: *const c_void, weight_nbytes: usize, n_rows: usize, k: usize,
                                x: *const c_float, n_tokens: usize, y: *mut c_float, workspace: *mut c_void,
                                workspace_bytes: usize, stream: wh_stream_t) -> c_int;
+
+    pub fn wh_quantized_matmul_x_workspace_bytes(r#type: c_int, n_rows: usize, k: usize, n_tokens: usize,
+                                                 x_dtype: c_int) -> usize;
+    pub fn wh_quantized_matmul_x(r#type: c_int, weights: *const c_void, weight_nbytes: usize, n_rows: usize, k: usize,
+                                 x: *const c_void, x_dtype: c_int, n_tokens: usize, y: *mut c_float,
+                                 workspace: *mut c_void, workspace_bytes: usize, stream: wh_stream_t) -> c_int;
 
     // elementwise (tensor_utils.rs:446-480, 512-532)
     pub fn wh_rms_norm(x: *const c_float, weight: *const c_float, eps: c_float, tokens: usize, hidden: usize,

@@ -61,7 +61,10 @@ typedef enum wh_type {
    * which differs from ggml's): dequantization, GEMV, GEMM, the FFN layer and
    * the decode step (rows a multiple of 256 elements). */
   WH_TYPE_Q4_K = 12,
-  WH_TYPE_Q6_K = 14
+  WH_TYPE_Q6_K = 14,
+  /* bfloat16 (GGMLType::BF16, tensor_info.rs:72-73): activations of
+   * wh_quantized_matmul_x only */
+  WH_TYPE_BF16 = 30
 } wh_type;
 
 typedef struct wh_stream_opaque* wh_stream_t; /* a hipStream_t */
@@ -175,6 +178,19 @@ WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbyt
                                size_t n_rows, size_t k, const float* x, size_t n_tokens,
                                float* y, void* workspace, size_t workspace_bytes,
                                wh_stream_t stream);
+
+/* The same product with the activations given as x_dtype: WH_TYPE_F32 (as
+ * wh_quantized_matmul) or WH_TYPE_BF16 (X row-major [n_tokens][k] bfloat16,
+ * 8-byte aligned), the activation type config 2 of the benchmark names
+ * ("f32/bf16"; SURVEY's wh_qgemm(.., X, x_dtype, ..)).  bf16 values are
+ * widened exactly to f32, so the result equals wh_quantized_matmul on the
+ * widened X.  The workspace (wh_quantized_matmul_x_workspace_bytes) is needed
+ * for bf16 at any token count; WH_ERR_UNSUPPORTED_TYPE for another x_dtype. */
+WH_API size_t wh_quantized_matmul_x_workspace_bytes(int type, size_t n_rows, size_t k, size_t n_tokens,
+                                                    int x_dtype);
+WH_API int wh_quantized_matmul_x(int type, const void* weights, size_t weight_nbytes, size_t n_rows, size_t k,
+                                 const void* x, int x_dtype, size_t n_tokens, float* y, void* workspace,
+                                 size_t workspace_bytes, wh_stream_t stream);
 
 /* --------------------------------------------------- elementwise / norms */
 /* rms_norm (crates/woolly-core/src/tensor_utils.rs:446-480):

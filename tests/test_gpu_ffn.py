@@ -166,3 +166,42 @@ def test_matmul_large_values_row_scaling(gpu, orc):
         r = rel_l2(got[t], ref[t])
         print(f"[result] row {t} rel_l2={r:.3e}", flush=True)
         assert r <= 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1, 12])
+@pytest.mark.parametrize("m,n,k", [(1, 300, 4096), (2, 300, 4096), (8, 300, 4096), (64, 300, 4096),
+                                   (512, 256, 4096), (33, 200, 1024)])
+def test_matmul_bf16_activations(gpu, orc, t, m, n, k):
+    """bf16 X (config 2's "f32/bf16"): the result equals the f32 product on the
+    exactly widened X bit for bit (the tiled kernel's packing reads bf16
+    itself; other paths widen first), and meets the bars against f64."""
+    print(f"[case] matmul bf16 type={t} m={m} n={n} k={k}", flush=True)
+    w = synth.quantized_weight(t, n, k, seed=n + k + 1)
+    xf = synth.activations(m * k, seed=m + 3).reshape(m, k)
+    xb16 = (xf.view(np.uint32) >> 16).astype(np.uint16)          # truncated to bf16
+    xw = (xb16.astype(np.uint32) << 16).view(np.float32)          # the exact widening
+    wb, wp = up(w)
+    xbb, xbp = up(xb16)
+    xwb, xwp = up(xw)
+    y_bf, y_f = DeviceBuffer(4 * m * n), DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_x_workspace_bytes(t, n, k, m, ops.TYPE_BF16)
+    ws = DeviceBuffer(max(wsz, 256))
+    ops.quantized_matmul_x(t, wp, w.nbytes, n, k, xbp, ops.TYPE_BF16, m, y_bf.ptr, ws, wsz)
+    wsz2 = ops.matmul_workspace_bytes(t, n, k, m)
+    ws2 = DeviceBuffer(max(wsz2, 256))
+    ops.quantized_matmul(t, wp, w.nbytes, n, k, xwp, m, y_f.ptr, ws2, wsz2)
+    got = down(y_bf, np.float32, m * n).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), down(y_f, np.float32, m * n).reshape(m, n).view(np.uint32))
+    rows = np.arange(m) if m <= 64 else np.array([0, 1, m // 2, m - 1])
+    ref = orc.matmul_rows_f64(t, w, n, k, xw, m, rows)
+    r, a = rel_l2(got[rows], ref), max_abs(got[rows], ref)
+    report(f"matmul bf16 t={t} m={m} n={n} k={k}", r, a, ref)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
+def test_matmul_x_rejects_other_activation_types(gpu):
+    w = synth.quantized_weight(Q4_0, 64, 256, seed=1)
+    wb, wp = up(w)
+    y = DeviceBuffer(4 * 64)
+    with pytest.raises(Exception, match="activation type"):
+        ops.quantized_matmul_x(Q4_0, wp, w.nbytes, 64, 256, wp, 1, 1, y.ptr, None, 0)

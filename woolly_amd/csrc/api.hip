@@ -412,6 +412,55 @@ WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbyt
                          hs(stream));
 }
 
+WH_API size_t wh_quantized_matmul_x_workspace_bytes(int type, size_t n_rows, size_t k, size_t n_tokens,
+                                                    int x_dtype) {
+  if (x_dtype != WH_TYPE_BF16) return wh_quantized_matmul_workspace_bytes(type, n_rows, k, n_tokens);
+  if (!(wh::is_block_type(type) || wh::is_kquant(type)) || k == 0) return 0;
+  // the widened activations, then the f32 product's workspace (the tiled
+  // kernel reads bf16 directly and needs only the latter)
+  return align_up(n_tokens * k * sizeof(float), 256) + wh_quantized_matmul_workspace_bytes(type, n_rows, k, n_tokens);
+}
+
+WH_API int wh_quantized_matmul_x(int type, const void* weights, size_t weight_nbytes, size_t n_rows, size_t k,
+                                 const void* x, int x_dtype, size_t n_tokens, float* y, void* workspace,
+                                 size_t workspace_bytes, wh_stream_t stream) {
+  if (x_dtype == WH_TYPE_F32)
+    return wh_quantized_matmul(type, weights, weight_nbytes, n_rows, k, static_cast<const float*>(x), n_tokens, y,
+                               workspace, workspace_bytes, stream);
+  if (x_dtype != WH_TYPE_BF16)
+    return wh::set_error(WH_ERR_UNSUPPORTED_TYPE, "quantized_matmul_x: activation type %d (f32 = 0 or bf16 = 30)",
+                         x_dtype);
+  int st = check_gemv_args("quantized_matmul_x", type, k);
+  if (st) return st;
+  st = check_weight_bytes("quantized_matmul_x", type, n_rows, k, weight_nbytes);
+  if (st) return st;
+  if (n_rows == 0 || n_tokens == 0) return WH_OK;
+  st = check_ptr("quantized_matmul_x", "y", y, 4);
+  if (st) return st;
+  hipStream_t s = hs(stream);
+  if (k == 0) return wh::launch_fill_bytes(y, 0, n_rows * n_tokens * sizeof(float), s);
+  if ((st = check_ptr("quantized_matmul_x", "weights", weights, 1)) || (st = check_ptr("quantized_matmul_x", "x", x, 8)))
+    return st;
+  const size_t need = wh_quantized_matmul_x_workspace_bytes(type, n_rows, k, n_tokens, x_dtype);
+  if (!workspace || workspace_bytes < need)
+    return wh::set_error(WH_ERR_BUFFER_TOO_SMALL,
+                         "quantized_matmul_x: workspace too small: needed %zu bytes, available %zu", need,
+                         workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!wh::aligned(workspace, 256))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matmul_x: workspace is not 256-byte aligned");
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  // many tokens: the tiled kernel's packing reads bf16 itself
+  if (n_tokens > 16 && wh::is_block_type(type) &&
+      wh::gemm_tiled_ok(type, weights, static_cast<const float*>(x), n_rows, k, n_tokens))
+    return wh::launch_gemm_tiled_bf16(type, weights, n_rows, k, xb, n_tokens, y, workspace, s);
+  // otherwise widen into the workspace and run the f32 product
+  float* xf = static_cast<float*>(workspace);
+  const size_t head = align_up(n_tokens * k * sizeof(float), 256);
+  if ((st = wh::launch_bf16_to_f32(xb, n_tokens * k, xf, s))) return st;
+  return wh::launch_gemm(type, weights, n_rows, k, xf, n_tokens, y, static_cast<char*>(workspace) + head,
+                         workspace_bytes - head, s);
+}
+
 // --------------------------------------------------------------- elementwise
 WH_API int wh_rms_norm(const float* x, const float* weight, float eps, size_t tokens, size_t hidden,
                        float* out, wh_stream_t stream) {

@@ -70,6 +70,14 @@ __global__ __launch_bounds__(256) void fill_bytes_kernel(uint8_t* __restrict__ d
     dst[i] = value;
 }
 
+// bfloat16 -> f32: the 16 bits become the high half of the f32 (exact).
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ x, size_t n,
+                                                          float* __restrict__ out) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = __builtin_bit_cast(float, static_cast<uint32_t>(x[i]) << 16);
+}
+
 unsigned grid_for(size_t items, unsigned per_block, unsigned cap) {
   size_t g = (items + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -124,6 +132,14 @@ int launch_dequantize(int type, const void* data, size_t n, float* out, hipStrea
       return set_error(WH_ERR_UNSUPPORTED_TYPE, "dequantize: unsupported type %d", type);
   }
   WH_LAUNCH_CHECK("dequantize kernel launch");
+  return WH_OK;
+}
+
+int launch_bf16_to_f32(const uint16_t* x, size_t n, float* out, hipStream_t s) {
+  if (n == 0) return WH_OK;
+  const unsigned cap = static_cast<unsigned>(cu_count()) * 8u;
+  bf16_to_f32_kernel<<<grid_for(n, 256, cap), 256, 0, s>>>(x, n, out);
+  WH_LAUNCH_CHECK("bf16 conversion kernel launch");
   return WH_OK;
 }
 

@@ -151,7 +151,8 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 constexpr int PPT = 2;
 constexpr int kPackMaxThreads = 1024;
 constexpr int kPackPlain = 0, kPackNorm = 1, kPackSwiglu = 2;
-template <int MODE>
+// XB: x holds bfloat16 values (plain mode), widened exactly to f32 on load.
+template <int MODE, bool XB = false>
 __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
                                                      const float* __restrict__ gamma, float eps, int n_tokens,
                                                      int k, int kx, int type, int bm, _Float16* __restrict__ frag,
@@ -178,8 +179,19 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
       const int off = p < npairs ? elem_off(p >> 2, p & 3) : -1;
       if (live && off >= 0) {
         const float* src = xr + off;
+        if constexpr (XB) {
+          // row t of bf16 x: element e at byte 2 (t kx + e)
+          const uint16_t* xb = reinterpret_cast<const uint16_t*>(x) + static_cast<size_t>(t) * kx + off;
+          auto widen = [](uint2 u) {
+            return float4{__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xFFFF0000u),
+                          __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xFFFF0000u)};
+          };
+          va[i] = widen(*reinterpret_cast<const uint2*>(xb));
+          vb[i] = widen(*reinterpret_cast<const uint2*>(xb + (q8 ? 4 : 16)));
+        } else {
         va[i] = *reinterpret_cast<const float4*>(src);
         vb[i] = *reinterpret_cast<const float4*>(src + (q8 ? 4 : 16));
+        }
         if constexpr (MODE == kPackSwiglu) {
           const float* us = ur + (src - xr);
           const float4 ua = *reinterpret_cast<const float4*>(us);
@@ -878,14 +890,14 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
   return t;
 }
 
-template <int MODE>
+template <int MODE, bool XB = false>
 static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x2, const float* gamma, float eps,
                       size_t n_tokens, size_t k, size_t kx, hipStream_t s) {
   // threads per row: enough for PPT pairs each, 256 .. 1024
   const size_t npairs = k / 8;
   size_t threads = (npairs + PPT - 1) / PPT;
   threads = threads < 256 ? 256 : (threads > kPackMaxThreads ? kPackMaxThreads : (threads + 63) / 64 * 64);
-  pack_a_kernel<MODE><<<static_cast<unsigned>(t.tm), static_cast<unsigned>(threads), 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
+  pack_a_kernel<MODE, XB><<<static_cast<unsigned>(t.tm), static_cast<unsigned>(threads), 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
                                                                   static_cast<int>(k), static_cast<int>(kx), type, t.bm,
                                                                   t.frag, t.rs, t.bs);
   WH_LAUNCH_CHECK("pack kernel launch");
@@ -922,6 +934,15 @@ int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const fl
                       float* y, void* workspace, hipStream_t s) {
   const TiledWs t = tiled_ws(type, n_rows, k, n_tokens, workspace);
   int st = tiled_pack<kPackPlain>(type, t, x, nullptr, nullptr, 0.f, n_tokens, k, k, s);
+  if (st) return st;
+  return tiled_run(type, w, n_rows, k, n_tokens, t, y, s);
+}
+
+int launch_gemm_tiled_bf16(int type, const void* w, size_t n_rows, size_t k, const uint16_t* x, size_t n_tokens,
+                           float* y, void* workspace, hipStream_t s) {
+  const TiledWs t = tiled_ws(type, n_rows, k, n_tokens, workspace);
+  int st = tiled_pack<kPackPlain, true>(type, t, reinterpret_cast<const float*>(x), nullptr, nullptr, 0.f, n_tokens,
+                                        k, k, s);
   if (st) return st;
   return tiled_run(type, w, n_rows, k, n_tokens, t, y, s);
 }

@@ -143,6 +143,11 @@ bool gemm_tiled_ok(int type, const void* w, const float* x, size_t n_rows, size_
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k);
 int launch_gemm_tiled(int type, const void* w, size_t n_rows, size_t k, const float* x,
                       size_t n_tokens, float* y, void* workspace, hipStream_t stream);
+// The tiled GEMM with bfloat16 activations, read directly by its packing.
+int launch_gemm_tiled_bf16(int type, const void* w, size_t n_rows, size_t k, const uint16_t* x, size_t n_tokens,
+                           float* y, void* workspace, hipStream_t s);
+// bfloat16 -> f32 (exact), n elements.
+int launch_bf16_to_f32(const uint16_t* x, size_t n, float* out, hipStream_t s);
 // Q4_K / Q6_K on the tiled kernel: the matrix repacked into the front of the
 // workspace, then the GEMM.
 bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size_t k, size_t n_tokens);

@@ -77,6 +77,22 @@ def quantized_matmul(ggml_type: int, weights, weight_nbytes: int, n_rows: int, k
                                                workspace_bytes, _s(stream)))
 
 
+TYPE_BF16 = 30  # activation type of quantized_matmul_x (GGMLType::BF16)
+
+
+def matmul_x_workspace_bytes(ggml_type: int, n_rows: int, k: int, n_tokens: int, x_dtype: int) -> int:
+    return int(_lib.load().wh_quantized_matmul_x_workspace_bytes(ggml_type, n_rows, k, n_tokens, x_dtype))
+
+
+def quantized_matmul_x(ggml_type: int, weights, weight_nbytes: int, n_rows: int, k: int, x, x_dtype: int,
+                       n_tokens: int, y, workspace=None, workspace_bytes: int = 0,
+                       stream: Stream | None = None) -> None:
+    """Y = X W^T with X of x_dtype (0: f32, TYPE_BF16: bfloat16 [n_tokens][k])."""
+    _lib.check(_lib.load().wh_quantized_matmul_x(ggml_type, _p(weights), weight_nbytes, n_rows, k, _p(x),
+                                                 x_dtype, n_tokens, _p(y), _p(workspace) or None,
+                                                 workspace_bytes, _s(stream)))
+
+
 def rms_norm(x, weight, eps: float, tokens: int, hidden: int, out,
              stream: Stream | None = None) -> None:
     _lib.check(_lib.load().wh_rms_norm(_p(x), _p(weight), eps, tokens, hidden, _p(out),
