@@ -374,7 +374,8 @@ def traffic_from_profile() -> tuple[int | None, str]:
         for line in PMC_PROFILE.read_text().splitlines():
             if ":" in line:
                 k, v = line.split(":", 1)
-                fields[k.strip()] = v.strip()
+                if v.split():
+                    fields[k.strip()] = v.split()[0]  # the value, without a trailing note
     except OSError:
         return None, "missing"
     if "traffic_bytes_per_launch" not in fields:

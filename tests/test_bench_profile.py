@@ -1,0 +1,32 @@
+"""bench.py's link to the committed rocprofv3 summaries: the HBM traffic of the
+headline GEMV is read from profiles/gemv_q4_0_14336x4096_pmc.txt only when that
+summary's kernel_sources_sha256 names the GEMV sources of this tree."""
+import bench
+
+
+def _write(tmp_path, digest, traffic="33299849"):
+    p = tmp_path / "pmc.txt"
+    p.write_text("# summary\n"
+                 f"kernel_sources_sha256: {digest}   (python bench.py --sources-digest)\n"
+                 f"traffic_bytes_per_launch: {traffic}\n")
+    return p
+
+
+def test_current_summary_gives_traffic(tmp_path, monkeypatch):
+    monkeypatch.setattr(bench, "PMC_PROFILE", _write(tmp_path, bench.kernel_sources_digest()))
+    assert bench.traffic_from_profile() == (33299849, "current")
+
+
+def test_stale_summary_gives_none(tmp_path, monkeypatch):
+    monkeypatch.setattr(bench, "PMC_PROFILE", _write(tmp_path, "0123456789abcdef"))
+    assert bench.traffic_from_profile() == (None, "stale")
+
+
+def test_missing_summary(tmp_path, monkeypatch):
+    monkeypatch.setattr(bench, "PMC_PROFILE", tmp_path / "absent.txt")
+    assert bench.traffic_from_profile() == (None, "missing")
+
+
+def test_digest_covers_every_gemv_source():
+    assert len(bench.kernel_sources_digest()) == 16
+    assert all((bench.ROOT / rel).is_file() for rel in bench.GEMV_KERNEL_SOURCES)
