@@ -49,6 +49,8 @@ pub const WH_TYPE_F32: c_int = 0;
 pub const WH_TYPE_F16: c_int = 1;
 pub const WH_TYPE_Q4_0: c_int = 2;
 pub const WH_TYPE_Q4_1: c_int = 3;
+pub const WH_TYPE_Q5_0: c_int = 6;
+pub const WH_TYPE_Q5_1: c_int = 7;
 pub const WH_TYPE_Q8_0: c_int = 8;
 pub const WH_TYPE_Q4_K: c_int = 12;
 pub const WH_TYPE_Q6_K: c_int = 14;

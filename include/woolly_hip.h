@@ -56,6 +56,11 @@ typedef enum wh_type {
   WH_TYPE_F16 = 1,
   WH_TYPE_Q4_0 = 2,
   WH_TYPE_Q4_1 = 3,
+  /* BlockQ5_0 {f16 d; u8 qh[4]; u8 qs[16]} (22 B) and BlockQ5_1 {f16 d; f16 m;
+   * u8 qh[4]; u8 qs[16]} (24 B), quantization.rs:117-140: dequantization only
+   * (dequantize_q5_0 / _q5_1, quantization.rs:515-575) */
+  WH_TYPE_Q5_0 = 6,
+  WH_TYPE_Q5_1 = 7,
   WH_TYPE_Q8_0 = 8,
   /* 256-element K-quant blocks in woolly-gguf's layout (dequantize.rs:404-536,
    * which differs from ggml's): dequantization, GEMV, GEMM, the FFN layer and
@@ -127,7 +132,10 @@ WH_API int wh_tensor_nbytes(int type, uint64_t nelements, uint64_t* nbytes);
  * nbytes < ceil(nelements/32) * type_size.
  * Q4_K and Q6_K (dequantize_q4_k_scalar / dequantize_q6_k, dequantize.rs:404-536)
  * decode 256-element blocks; a buffer shorter than ceil(nelements/256) *
- * type_size is Error::InvalidTensorInfo there, WH_ERR_INVALID_METADATA here. */
+ * type_size is Error::InvalidTensorInfo there, WH_ERR_INVALID_METADATA here.
+ * Q5_0 and Q5_1 decode as dequantize_q5_0 / dequantize_q5_1
+ * (quantization.rs:515-575); woolly_gguf's own Q5 functions (dequantize.rs:538-550)
+ * are stubs that return zeros, which this entry point does not reproduce. */
 WH_API int wh_dequantize(int type, const void* data, size_t nbytes, size_t nelements,
                          float* out, wh_stream_t stream);
 

@@ -4,7 +4,7 @@
 // Names, argument meaning and errors follow the Rust reference so code (and
 // tests) written against it read the same:
 //   woolly::tensor::quantization   crates/woolly-tensor/src/quantization.rs
-//     BlockQ4_0 / BlockQ4_1 / BlockQ8_0              :98-151
+//     BlockQ4_0 / BlockQ4_1 / BlockQ5_0 / BlockQ5_1 / BlockQ8_0   :98-151
 //     QuantizationError{UnsupportedScheme, InvalidParameters}   :8-26
 //     QuantizedStorage (Q4_0 / Q4_1 / Q8_0)           :154-170
 //     dequantize_q4_0 / dequantize_q4_1 / dequantize_q8_0       :466, 490, 576
@@ -74,6 +74,17 @@ struct BlockQ4_1 {
   f16 m;
   uint8_t qs[16];
 };
+struct BlockQ5_0 {
+  f16 d;
+  uint8_t qh[4];
+  uint8_t qs[16];
+};
+struct BlockQ5_1 {
+  f16 d;
+  f16 m;
+  uint8_t qh[4];
+  uint8_t qs[16];
+};
 struct BlockQ8_0 {
   f16 d;
   int8_t qs[32];
@@ -81,6 +92,7 @@ struct BlockQ8_0 {
 #pragma pack(pop)
 static_assert(sizeof(BlockQ4_0) == 18 && sizeof(BlockQ4_1) == 20 && sizeof(BlockQ8_0) == 34,
               "GGUF block sizes");
+static_assert(sizeof(BlockQ5_0) == 22 && sizeof(BlockQ5_1) == 24, "GGUF block sizes");
 
 // QuantizationError (quantization.rs:8-26); thrown, as Result::Err would be returned.
 struct QuantizationError : std::runtime_error {
@@ -99,14 +111,19 @@ inline void check_status(int st) {
   throw QuantizationError(QuantizationError::Kind::Backend, msg);
 }
 
-// QuantizedStorage (quantization.rs:154-170), restricted to the block formats on this path.
+// QuantizedStorage (quantization.rs:154-170), restricted to the 32-element block formats.
 struct QuantizedStorage {
-  std::variant<std::vector<BlockQ4_0>, std::vector<BlockQ4_1>, std::vector<BlockQ8_0>> blocks;
+  std::variant<std::vector<BlockQ4_0>, std::vector<BlockQ4_1>, std::vector<BlockQ8_0>, std::vector<BlockQ5_0>,
+               std::vector<BlockQ5_1>>
+      blocks;
   static QuantizedStorage Q4_0(std::vector<BlockQ4_0> b) { return {std::move(b)}; }
   static QuantizedStorage Q4_1(std::vector<BlockQ4_1> b) { return {std::move(b)}; }
   static QuantizedStorage Q8_0(std::vector<BlockQ8_0> b) { return {std::move(b)}; }
+  static QuantizedStorage Q5_0(std::vector<BlockQ5_0> b) { return {std::move(b)}; }
+  static QuantizedStorage Q5_1(std::vector<BlockQ5_1> b) { return {std::move(b)}; }
   int ggml_type() const {
-    return blocks.index() == 0 ? WH_TYPE_Q4_0 : (blocks.index() == 1 ? WH_TYPE_Q4_1 : WH_TYPE_Q8_0);
+    static const int ids[5] = {WH_TYPE_Q4_0, WH_TYPE_Q4_1, WH_TYPE_Q8_0, WH_TYPE_Q5_0, WH_TYPE_Q5_1};
+    return ids[blocks.index()];
   }
   const void* data() const {
     return std::visit([](const auto& v) { return static_cast<const void*>(v.data()); }, blocks);
@@ -136,10 +153,18 @@ inline std::vector<float> dequantize_q4_1(const std::vector<BlockQ4_1>& blocks) 
 inline std::vector<float> dequantize_q8_0(const std::vector<BlockQ8_0>& blocks) {
   return detail::dequantize(WH_TYPE_Q8_0, blocks.data(), blocks.size() * sizeof(BlockQ8_0), blocks.size());
 }
+// dequantize_q5_0 / dequantize_q5_1 (quantization.rs:515-575)
+inline std::vector<float> dequantize_q5_0(const std::vector<BlockQ5_0>& blocks) {
+  return detail::dequantize(WH_TYPE_Q5_0, blocks.data(), blocks.size() * sizeof(BlockQ5_0), blocks.size());
+}
+inline std::vector<float> dequantize_q5_1(const std::vector<BlockQ5_1>& blocks) {
+  return detail::dequantize(WH_TYPE_Q5_1, blocks.data(), blocks.size() * sizeof(BlockQ5_1), blocks.size());
+}
 
 namespace simd {
 // simd::quantized_matvec (quantization.rs:869-909), Q4_0 / Q8_0 like the
-// reference and Q4_1 in addition.  output[r] = sum_k W[r, k] * input[k].
+// reference and Q4_1 in addition (Q5 storage: UnsupportedScheme, as there).
+// output[r] = sum_k W[r, k] * input[k].
 inline void quantized_matvec(const QuantizedStorage& weights, const std::vector<float>& input,
                              std::vector<float>& output, size_t m, size_t k) {
   if (input.size() < k || output.size() < m)
@@ -150,6 +175,8 @@ inline void quantized_matvec(const QuantizedStorage& weights, const std::vector<
 inline std::vector<float> dequantize_q4_0_batch(const std::vector<BlockQ4_0>& b) { return dequantize_q4_0(b); }
 inline std::vector<float> dequantize_q4_1_batch(const std::vector<BlockQ4_1>& b) { return dequantize_q4_1(b); }
 inline std::vector<float> dequantize_q8_0_batch(const std::vector<BlockQ8_0>& b) { return dequantize_q8_0(b); }
+inline std::vector<float> dequantize_q5_0_batch(const std::vector<BlockQ5_0>& b) { return dequantize_q5_0(b); }
+inline std::vector<float> dequantize_q5_1_batch(const std::vector<BlockQ5_1>& b) { return dequantize_q5_1(b); }
 }  // namespace simd
 
 namespace optimized {
@@ -188,6 +215,8 @@ struct InvalidTensorInfo : Error {
 };
 
 // woolly_gguf::dequantize(data, ggml_type, nelements) (dequantize.rs:189-205).
+// Q5_0 / Q5_1 decode as dequantize_q5_0 / _q5_1 (quantization.rs:515-575); the
+// reference's gguf-level Q5 functions (dequantize.rs:538-550) return zeros.
 inline std::vector<float> dequantize(const std::vector<uint8_t>& data, GGMLType type, size_t nelements) {
   std::vector<float> out(nelements);
   const int st = wh_dequantize_host(static_cast<int>(type), data.data(), data.size(), nelements,

@@ -98,6 +98,8 @@ size_t orc_block_size(int type) {
       return 1;
     case ORC_Q4_0:
     case ORC_Q4_1:
+    case ORC_Q5_0:
+    case ORC_Q5_1:
     case ORC_Q8_0:
       return 32;
     case ORC_Q4_K:
@@ -117,6 +119,10 @@ size_t orc_type_size(int type) {
       return 18;
     case ORC_Q4_1:
       return 20;
+    case ORC_Q5_0:
+      return 22;
+    case ORC_Q5_1:
+      return 24;
     case ORC_Q8_0:
       return 34;
     case ORC_Q4_K:
@@ -134,6 +140,12 @@ static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); 
  *   Q4_0: quantization.rs:466-486 / dequantize.rs:286-327:
  *         element j<16 = ((qs[j] & 0xF) - 8) * d, element j+16 = ((qs[j] >> 4) - 8) * d
  *   Q4_1: quantization.rs:490-511 / dequantize.rs:337-378: q * d + m
+ *   Q5_0: quantization.rs:515-541 (BlockQ5_0 {d, qh[4], qs[16]}, :117-127):
+ *         qh = u32::from_le_bytes(qh); for j < 16:
+ *         xh_0 = ((qh >> j) << 4) & 0x10, xh_1 = (qh >> (j + 12)) & 0x10,
+ *         element j = ((qs[j] & 0xF) | xh_0) - 16) * d, element j+16 = ((qs[j] >> 4) | xh_1) - 16) * d
+ *   Q5_1: quantization.rs:545-573 (BlockQ5_1 {d, m, qh[4], qs[16]}, :129-140):
+ *         the same x0 / x1 without the -16, value x * d + m (mul, then add)
  *   Q8_0: quantization.rs:576-590 / dequantize.rs:553-586: (int8)qs[j] * d */
 static void dequant_block(int type, const uint8_t* b, float* out) {
   if (type == ORC_Q4_0) {
@@ -156,6 +168,28 @@ static void dequant_block(int type, const uint8_t* b, float* out) {
       float p1 = x1 * d;
       out[j] = p0 + m;
       out[j + 16] = p1 + m;
+    }
+  } else if (type == ORC_Q5_0 || type == ORC_Q5_1) {
+    const int q51 = type == ORC_Q5_1;
+    float d = orc_f16_to_f32(rd16(b));
+    float m = q51 ? orc_f16_to_f32(rd16(b + 2)) : 0.0f;
+    const uint8_t* qhp = b + (q51 ? 4 : 2);
+    const uint8_t* qs = qhp + 4;
+    uint32_t qh = (uint32_t)qhp[0] | ((uint32_t)qhp[1] << 8) | ((uint32_t)qhp[2] << 16) | ((uint32_t)qhp[3] << 24);
+    for (int j = 0; j < 16; j++) {
+      uint32_t xh_0 = ((qh >> j) << 4) & 0x10;
+      uint32_t xh_1 = (qh >> (j + 12)) & 0x10;
+      uint32_t x0 = (uint32_t)(qs[j] & 0x0F) | xh_0;
+      uint32_t x1 = (uint32_t)(qs[j] >> 4) | xh_1;
+      if (q51) {
+        float p0 = (float)x0 * d;
+        float p1 = (float)x1 * d;
+        out[j] = p0 + m;
+        out[j + 16] = p1 + m;
+      } else {
+        out[j] = (float)((int32_t)x0 - 16) * d;
+        out[j + 16] = (float)((int32_t)x1 - 16) * d;
+      }
     }
   } else { /* ORC_Q8_0 */
     float d = orc_f16_to_f32(rd16(b));

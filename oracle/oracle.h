@@ -60,7 +60,7 @@ extern "C" {
 #endif
 
 /* GGMLType ids, crates/woolly-gguf/src/tensor_info.rs:15-30 */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
 
 /* Status codes mirror woolly's errors (quantization.rs:8-26, error.rs:11-64). */
 enum {

@@ -126,10 +126,35 @@ int main() {
     for (int i = 2; i < 32; ++i) EXPECT(result[i] == 0.0f);
   });
 
-  // quantization.rs:1346-1356 (the block formats on this path)
+  // quantization.rs:1409-1427
+  run("test_q5_0_dequantization", [] {
+    BlockQ5_0 b;
+    b.d = f16::from_f32(0.5f);
+    std::memset(b.qh, 0xFF, sizeof b.qh);
+    std::memset(b.qs, 0xFF, sizeof b.qs);
+    const auto result = dequantize_q5_0({b});
+    EXPECT(result.size() == 32);
+    for (float v : result) EXPECT(std::fabs(v - 7.5f) < 1e-6f);
+  });
+
+  // quantization.rs:1429-1446
+  run("test_q5_1_dequantization", [] {
+    BlockQ5_1 b;
+    b.d = f16::from_f32(1.0f);
+    b.m = f16::from_f32(10.0f);
+    std::memset(b.qh, 0x00, sizeof b.qh);
+    std::memset(b.qs, 0x11, sizeof b.qs);
+    const auto result = optimized::dequantize_blocks(QuantizedStorage::Q5_1({b}));
+    EXPECT(result.size() == 32);
+    for (float v : result) EXPECT(std::fabs(v - 11.0f) < 1e-6f);
+  });
+
+  // quantization.rs:1346-1356
   run("test_block_sizes", [] {
     EXPECT(sizeof(BlockQ4_0) == 18);
     EXPECT(sizeof(BlockQ4_1) == 20);
+    EXPECT(sizeof(BlockQ5_0) == 22);
+    EXPECT(sizeof(BlockQ5_1) == 24);
     EXPECT(sizeof(BlockQ8_0) == 34);
   });
 
@@ -231,9 +256,9 @@ int main() {
       too_small = e.needed == 36 && e.available == 35;
     }
     try {
-      gguf::dequantize(bytes, gguf::GGMLType::Q5_0, 32);
+      gguf::dequantize(bytes, gguf::GGMLType::Q2_K, 256);
     } catch (const gguf::InvalidTensorType& e) {
-      invalid = e.type_id == 6;
+      invalid = e.type_id == 10;
     }
     try {
       gguf::dequantize(bytes, gguf::GGMLType::Q4_K, 256);  // 35 of 144 bytes

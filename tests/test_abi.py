@@ -35,7 +35,10 @@ def test_library_is_gfx950_only():
 def test_format_queries():
     lib = _lib.load()
     assert lib.wh_type_size(2) == 18 and lib.wh_type_size(3) == 20 and lib.wh_type_size(8) == 34
-    assert lib.wh_block_size(2) == 32 and lib.wh_block_size(0) == 1 and lib.wh_block_size(6) == 0
+    assert lib.wh_block_size(2) == 32 and lib.wh_block_size(0) == 1 and lib.wh_block_size(10) == 0
+    # dequantize.rs:213, 230-231: Q5_0 / Q5_1 are 32-element blocks of 22 / 24 bytes
+    assert lib.wh_block_size(6) == 32 and lib.wh_type_size(6) == 22
+    assert lib.wh_block_size(7) == 32 and lib.wh_type_size(7) == 24
     # dequantize.rs:208-242: Q4_K / Q6_K are 256-element blocks of 144 / 210 bytes
     assert lib.wh_block_size(12) == 256 and lib.wh_type_size(12) == 144
     assert lib.wh_block_size(14) == 256 and lib.wh_type_size(14) == 210
@@ -81,7 +84,14 @@ def test_dequant_argument_errors_need_no_gpu():
         gguf.dequantize(bytes(35), gguf.GGMLType.Q4_0, 64)
     assert e.value.needed == 36 and e.value.available == 35
     with pytest.raises(gguf.InvalidTensorType):
-        gguf.dequantize(bytes(22), gguf.GGMLType.Q5_0, 32)
+        gguf.dequantize(bytes(84), gguf.GGMLType.Q2_K, 256)
+    # Q5_0 / Q5_1 blocks are 22 / 24 bytes (quantization.rs:1353-1354)
+    with pytest.raises(gguf.BufferTooSmall) as e:
+        gguf.dequantize(bytes(43), gguf.GGMLType.Q5_0, 64)
+    assert e.value.needed == 44 and e.value.available == 43
+    with pytest.raises(gguf.BufferTooSmall) as e:
+        gguf.dequantize(bytes(23), gguf.GGMLType.Q5_1, 32)
+    assert e.value.needed == 24
     # a short K-quant block is InvalidTensorInfo (dequantize.rs:416-418, 472-474)
     with pytest.raises(gguf.InvalidTensorInfo):
         gguf.dequantize(bytes(143), gguf.GGMLType.Q4_K, 256)

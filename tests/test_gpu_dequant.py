@@ -3,12 +3,13 @@ import numpy as np
 import pytest
 
 from tests._gpu import down, up
-from tests.test_oracle import block_q4_0, block_q4_1, block_q8_0
+from tests.test_oracle import block_q4_0, block_q4_1, block_q5_0, block_q5_1, block_q8_0
 from woolly_amd import gguf, ops, quantization, synth
 from woolly_amd.device import DeviceBuffer
 
 pytestmark = pytest.mark.gpu
 Q4_0, Q4_1, Q8_0 = 2, 3, 8
+Q5_0, Q5_1 = 6, 7
 
 
 def same_bits(a, b):
@@ -41,6 +42,33 @@ def test_q8_0_dequantization(gpu):
     assert len(result) == 32 and abs(result[0] - 5.0) < 1e-6 and abs(result[1] + 2.5) < 1e-6
 
 
+def test_q5_0_dequantization(gpu):
+    # quantization.rs:1410-1427
+    blocks = np.frombuffer(block_q5_0(0.5, [0xFF] * 4, [0xFF] * 16).tobytes(), quantization.BlockQ5_0)
+    result = quantization.dequantize_q5_0(blocks)
+    assert len(result) == 32 and np.all(np.abs(result - 7.5) < 1e-6)
+
+
+def test_q5_1_dequantization(gpu):
+    # quantization.rs:1429-1446
+    blocks = np.frombuffer(block_q5_1(1.0, 10.0, [0] * 4, [0x11] * 16).tobytes(), quantization.BlockQ5_1)
+    result = quantization.dequantize_q5_1(blocks)
+    assert len(result) == 32 and np.all(np.abs(result - 11.0) < 1e-6)
+
+
+def test_q5_storage_dispatch(gpu, orc):
+    # optimized::dequantize_blocks takes Q5 storage (quantization.rs:1187-1200);
+    # simd::quantized_matvec does not (UnsupportedScheme, :905-907)
+    for t, make in ((Q5_0, quantization.QuantizedStorage.Q5_0), (Q5_1, quantization.QuantizedStorage.Q5_1)):
+        data = synth.quantized_weight(t, 1, 8 * 32, seed=t)
+        got = quantization.optimized.dequantize_blocks(make(data))
+        st, ref = orc.dequantize(t, data, 8 * 32)
+        assert st == 0 and same_bits(got, ref)
+        with pytest.raises(quantization.QuantizationError.UnsupportedScheme):
+            quantization.simd.quantized_matvec(make(data), np.zeros(256, np.float32), np.zeros(1, np.float32),
+                                               1, 256)
+
+
 def test_optimized_dispatcher(gpu):
     data = np.concatenate([block_q4_0(1.0, [0x11] * 16), block_q4_0(2.0, [0x22] * 16)])
     storage = quantization.QuantizedStorage.Q4_0(data)
@@ -67,7 +95,7 @@ def test_parallel_quantization_correctness(gpu, orc):
 
 
 # --- bit-exact parity with the oracle
-@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0, Q5_0, Q5_1])
 @pytest.mark.parametrize("n", [1, 4, 31, 32, 33, 100, 4096, 100003])
 @pytest.mark.parametrize("in_off,out_off", [(0, 0), (2, 4), (1, 8)])
 def test_dequant_bit_exact(gpu, orc, t, n, in_off, out_off):
@@ -81,14 +109,14 @@ def test_dequant_bit_exact(gpu, orc, t, n, in_off, out_off):
     assert st == 0 and same_bits(got, ref)
 
 
-@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0, Q5_0, Q5_1])
 def test_dequant_every_f16_scale(gpu, orc, t):
     nb = 65536
-    ts = {Q4_0: 18, Q4_1: 20, Q8_0: 34}[t]
+    ts = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q5_0: 22, Q5_1: 24}[t]
     rng = np.random.default_rng(t)
     data = rng.integers(0, 256, (nb, ts), dtype=np.uint8)
     data[:, 0:2] = np.arange(nb, dtype=np.uint16).view(np.uint8).reshape(nb, 2)
-    if t == Q4_1:  # every pattern as the min too
+    if t in (Q4_1, Q5_1):  # every pattern as the min too
         data[:, 2:4] = np.arange(nb, dtype=np.uint16)[::-1].copy().view(np.uint8).reshape(nb, 2)
     data = data.reshape(-1)
     got = gguf.dequantize(data, gguf.GGMLType(t), nb * 32)

@@ -17,6 +17,7 @@ from tests._oracle import max_abs, rel_l2
 from woolly_amd import synth
 
 Q4_0, Q4_1, Q8_0 = 2, 3, 8
+Q5_0, Q5_1 = 6, 7
 
 
 def f16(x):
@@ -38,6 +39,23 @@ def block_q4_1(d, m, qs):
     return b
 
 
+def block_q5_0(d, qh, qs):
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
+    b[2:6] = qh
+    b[6:] = qs
+    return b
+
+
+def block_q5_1(d, m, qh, qs):
+    b = np.zeros(24, np.uint8)
+    b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([f16(m)], np.uint16).view(np.uint8)
+    b[4:8] = qh
+    b[8:] = qs
+    return b
+
+
 def block_q8_0(d, qs):
     b = np.zeros(34, np.uint8)
     b[0:2] = np.array([f16(d)], np.uint16).view(np.uint8)
@@ -48,11 +66,22 @@ def block_q8_0(d, qs):
 # ----------------------------------------------------------------- numpy twins
 def np_dequant(t, data, n):
     """Independent vectorised decoder (numpy), written from the block layout."""
-    ts = {Q4_0: 18, Q4_1: 20, Q8_0: 34}[t]
+    ts = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34}[t]
     nb = (n + 31) // 32
     blk = np.asarray(data, np.uint8)[: nb * ts].reshape(nb, ts)
     d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
-    if t == Q4_0:
+    if t in (Q5_0, Q5_1):
+        # 32 fifth bits: the four qh bytes as one little-endian bit string
+        h = 2 if t == Q5_0 else 4
+        hi = np.unpackbits(blk[:, h:h + 4], axis=1, bitorder="little").astype(np.int32)
+        qs = blk[:, h + 4:h + 20].astype(np.int32)
+        q = np.concatenate([qs & 15, qs >> 4], axis=1) + 16 * hi
+        if t == Q5_0:
+            out = (q - 16).astype(np.float32) * d
+        else:
+            m = blk[:, 2:4].copy().view(np.float16).astype(np.float32)
+            out = (q.astype(np.float32) * d).astype(np.float32) + m
+    elif t == Q4_0:
         qs = blk[:, 2:18]
         q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32) - 8.0
         out = q * d
@@ -176,6 +205,76 @@ def test_kat_bench_generators(orc):
         assert np.array_equal(out.view(np.uint32), np_dequant(t, data, nb * 32).view(np.uint32))
 
 
+# ----------------------------------------------------- Q5_0 / Q5_1 (reference)
+def test_q5_block_sizes(orc):
+    # quantization.rs:1353-1354 (size_of 22 / 24), dequantize.rs:208-242
+    assert orc.type_size(Q5_0) == 22 and orc.type_size(Q5_1) == 24
+    assert orc.block_size(Q5_0) == 32 and orc.block_size(Q5_1) == 32
+
+
+def test_kat_q5_0_dequantization(orc):
+    # quantization.rs:1410-1427: all high bits and all low nibbles set: 31 - 16 = 15, times 0.5
+    st, out = orc.dequantize(Q5_0, block_q5_0(0.5, [0xFF] * 4, [0xFF] * 16), 32)
+    assert st == 0 and out.size == 32 and np.all(out == 7.5)
+
+
+def test_kat_q5_1_dequantization(orc):
+    # quantization.rs:1429-1446: no high bits, every nibble 1: 1 * 1.0 + 10.0
+    st, out = orc.dequantize(Q5_1, block_q5_1(1.0, 10.0, [0] * 4, [0x11] * 16), 32)
+    assert st == 0 and np.all(out == 11.0)
+
+
+@pytest.mark.parametrize("e", [0, 1, 7, 8, 12, 15, 16, 17, 19, 27, 28, 31])
+def test_q5_fifth_bit_position(orc, e):
+    # bit e of the little-endian qh is element e's fifth bit, for both halves
+    # of the block (element j < 16: bit j; element j + 16: bit j + 16), which
+    # a swapped byte order, a j + 12 shift taken as a bit index or a low/high
+    # nibble mix-up would all move
+    qh = np.array([(1 << e) >> (8 * i) & 0xFF for i in range(4)], np.uint8)
+    st, out = orc.dequantize(Q5_0, block_q5_0(1.0, qh, [0] * 16), 32)
+    exp = np.full(32, -16.0, np.float32)
+    exp[e] = 0.0
+    assert st == 0 and np.array_equal(out, exp)
+    st, out = orc.dequantize(Q5_1, block_q5_1(2.0, 0.25, qh, [0] * 16), 32)
+    exp = np.full(32, 0.25, np.float32)
+    exp[e] = 32.25
+    assert st == 0 and np.array_equal(out, exp)
+
+
+def test_q5_nibble_order(orc):
+    # element j: low nibble of qs[j]; element j + 16: high nibble (quantization.rs:528-536)
+    qs = np.array([(j & 15) | ((15 - j) << 4) for j in range(16)], np.uint8)
+    st, out = orc.dequantize(Q5_0, block_q5_0(1.0, [0] * 4, qs), 32)
+    assert st == 0
+    assert np.array_equal(out[:16], np.arange(16, dtype=np.float32) - 16)
+    assert np.array_equal(out[16:], 15 - np.arange(16, dtype=np.float32) - 16)
+
+
+@pytest.mark.parametrize("t", [Q5_0, Q5_1])
+@pytest.mark.parametrize("n", [32, 96, 1000, 4096])
+def test_q5_dequant_matches_numpy(orc, t, n):
+    w = synth.quantized_weight(t, 1, ((n + 31) // 32) * 32, seed=9)
+    st, out = orc.dequantize(t, w, n)
+    assert st == 0
+    assert np.array_equal(out.view(np.uint32), np_dequant(t, w, n).view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q5_0, Q5_1])
+def test_q5_dequant_all_f16_scales(orc, t):
+    nb = 65536
+    ts = 22 if t == Q5_0 else 24
+    data = np.random.default_rng(t).integers(0, 256, (nb, ts), dtype=np.uint8)
+    data[:, 0:2] = np.arange(nb, dtype=np.uint16).view(np.uint8).reshape(nb, 2)
+    if t == Q5_1:
+        data[:, 2:4] = np.arange(nb, dtype=np.uint16)[::-1].copy().view(np.uint8).reshape(nb, 2)
+    st, out = orc.dequantize(t, data.reshape(-1), nb * 32)
+    ref = np_dequant(t, data.reshape(-1), nb * 32)
+    assert st == 0
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
 # ---------------------------------------------- dequantization vs numpy twin
 @pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
 @pytest.mark.parametrize("n", [32, 96, 1000, 4096])
@@ -205,8 +304,10 @@ def test_dequant_errors(orc):
     w = synth.quantized_weight(Q4_0, 1, 64, seed=1)
     st, _ = orc.dequantize(Q4_0, w[:35], 64)   # needs 36 bytes
     assert st == 3
-    st, _ = orc.dequantize(6, w, 32)           # Q5_0 is not on this path
+    st, _ = orc.dequantize(10, w, 32)          # Q2_K: no block decoder
     assert st == 1
+    st, _ = orc.dequantize(Q5_0, w[:21], 32)   # Q5_0 needs 22 bytes
+    assert st == 3
     st, out = orc.dequantize(Q4_0, w, 40)      # truncation to nelements
     assert st == 0 and out.size == 40
 

@@ -44,6 +44,13 @@ MUTANTS = [
      "else scales[i] = (uint8_t)(((b[src] >> 6) | ((b[src + 1] & 15) << 2)) & 63);",
      "else scales[i] = (uint8_t)((b[src] >> 6) & 63);", 1),
     ("q6_k bias -31", "float u = t * (float)((int)(int8_t)q - 32);", "float u = t * (float)((int)(int8_t)q - 31);", 1),
+    ("q5 high half takes bit j + 12", "uint32_t xh_1 = (qh >> (j + 12)) & 0x10;",
+     "uint32_t xh_1 = ((qh >> (j + 12)) << 4) & 0x10;", 1),
+    ("q5 qh read big-endian",
+     "uint32_t qh = (uint32_t)qhp[0] | ((uint32_t)qhp[1] << 8) | ((uint32_t)qhp[2] << 16) | ((uint32_t)qhp[3] << 24);",
+     "uint32_t qh = (uint32_t)qhp[3] | ((uint32_t)qhp[2] << 8) | ((uint32_t)qhp[1] << 16) | ((uint32_t)qhp[0] << 24);", 1),
+    ("q5_0 -16 offset dropped", "out[j] = (float)((int32_t)x0 - 16) * d;", "out[j] = (float)((int32_t)x0) * d;", 1),
+    ("q5_1 minimum not added", "out[j + 16] = p1 + m;\n      } else {", "out[j + 16] = p1;\n      } else {", 1),
 ]
 
 MODULES = (test_oracle, test_oracle_decode, test_oracle_kquant)

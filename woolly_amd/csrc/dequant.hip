@@ -5,9 +5,11 @@
 //   Q4_0  {f16 d; u8 qs[16]}        e[j] = ((qs[j] & 15) - 8) * d, e[j+16] = ((qs[j] >> 4) - 8) * d
 //   Q4_1  {f16 d; f16 m; u8 qs[16]} e[j] = (qs[j] & 15) * d + m,   e[j+16] = (qs[j] >> 4) * d + m
 //   Q8_0  {f16 d; i8 qs[32]}        e[j] = qs[j] * d
+//   Q5_0  {f16 d; u8 qh[4]; u8 qs[16]}        x = nibble | (bit e of qh) << 4, e = (x - 16) * d
+//   Q5_1  {f16 d; f16 m; u8 qh[4]; u8 qs[16]} e = x * d + m  (quantization.rs:515-575)
 // Every product is exact in f32 (a <=8-bit integer times an 11-bit
 // significand), so the results are bit-identical to the CPU whatever the
-// rounding of the single Q4_1 addition (fused or not, it is one rounding).
+// rounding of the single Q4_1 / Q5_1 addition (fused or not, it is one rounding).
 //
 // Work mapping: the output dominates the traffic (128 B written per 18-34 B
 // read), so each thread produces one quad of 4 consecutive floats with one
@@ -22,7 +24,11 @@ template <int TYPE, int ALIGN, bool OUT16>
 __global__ __launch_bounds__(256) void dequant_blocks_kernel(const uint8_t* __restrict__ data,
                                                              float* __restrict__ out,
                                                              size_t nelements) {
-  constexpr int TS = TYPE == WH_TYPE_Q4_0 ? 18 : (TYPE == WH_TYPE_Q4_1 ? 20 : 34);
+  constexpr int TS = TYPE == WH_TYPE_Q4_0   ? 18
+                     : TYPE == WH_TYPE_Q4_1 ? 20
+                     : TYPE == WH_TYPE_Q5_0 ? 22
+                     : TYPE == WH_TYPE_Q5_1 ? 24
+                                            : 34;
   const size_t nquads = (nelements + 3) / 4;
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t q = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < nquads;
@@ -124,6 +130,12 @@ int launch_dequantize(int type, const void* data, size_t n, float* out, hipStrea
       break;
     case WH_TYPE_Q8_0:
       launch_blocks<WH_TYPE_Q8_0>(p, n, out, s, grid_for((n + 3) / 4, 256, cap));
+      break;
+    case WH_TYPE_Q5_0:
+      launch_blocks<WH_TYPE_Q5_0>(p, n, out, s, grid_for((n + 3) / 4, 256, cap));
+      break;
+    case WH_TYPE_Q5_1:
+      launch_blocks<WH_TYPE_Q5_1>(p, n, out, s, grid_for((n + 3) / 4, 256, cap));
       break;
     case WH_TYPE_Q4_K:
     case WH_TYPE_Q6_K:

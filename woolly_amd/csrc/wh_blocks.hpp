@@ -1,5 +1,5 @@
 // wh_blocks.hpp -- GGUF block formats on the device (BlockQ4_0 / BlockQ4_1 /
-// BlockQ8_0, crates/woolly-tensor/src/quantization.rs:98-151).
+// BlockQ5_0 / BlockQ5_1 / BlockQ8_0, crates/woolly-tensor/src/quantization.rs:98-151).
 #pragma once
 
 #include "wh_common.hpp"
@@ -50,7 +50,7 @@ __device__ __forceinline__ void decode_block_bytes(const uint8_t* b, float v[32]
 }
 
 // ---- per-quad decoders (4 consecutive elements of a block), bit-exact with
-// dequantize_q4_0 / _q4_1 / _q8_0 (quantization.rs:466-590) and
+// dequantize_q4_0 / _q4_1 / _q5_0 / _q5_1 / _q8_0 (quantization.rs:466-590) and
 // dequantize_q4_k_scalar / dequantize_q6_k (dequantize.rs:404-536).
 
 // Little-endian 16- / 32-bit loads at a pointer with ALIGN-byte alignment.
@@ -94,6 +94,30 @@ __device__ __forceinline__ void decode_quad(const uint8_t* blk, int c, float v[4
     for (int i = 0; i < 4; i++) {
       const float q = static_cast<float>((nib >> (8 * i)) & 0xFFu);
       v[i] = __fadd_rn(__fmul_rn(q, d), m);
+    }
+  } else if constexpr (TYPE == WH_TYPE_Q5_0 || TYPE == WH_TYPE_Q5_1) {
+    // quantization.rs:515-575: element e (< 16: low nibble of qs[e], >= 16: high
+    // nibble of qs[e - 16]) takes bit e of the little-endian qh as its 5th bit
+    // (((qh >> j) << 4) & 0x10 and (qh >> (j + 12)) & 0x10 are both bit e);
+    // Q5_0: (x - 16) * d, Q5_1: x * d + m
+    constexpr int QH = TYPE == WH_TYPE_Q5_0 ? 2 : 4;
+    const float d = f16_bits_to_f32(ld16<ALIGN>(blk));
+    const uint32_t qh = ld32<(ALIGN >= 2 ? 2 : 1)>(blk + QH) >> (4 * c);
+    const uint32_t w = ld32<(ALIGN >= 2 ? 2 : 1)>(blk + QH + 4 + 4 * (c & 3));
+    const uint32_t nib = (c >= 4) ? ((w >> 4) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+    if constexpr (TYPE == WH_TYPE_Q5_0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int q = static_cast<int>(((nib >> (8 * i)) & 0xFFu) | (((qh >> i) & 1u) << 4)) - 16;
+        v[i] = static_cast<float>(q) * d;
+      }
+    } else {
+      const float m = f16_bits_to_f32(ld16<ALIGN>(blk + 2));
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float q = static_cast<float>(((nib >> (8 * i)) & 0xFFu) | (((qh >> i) & 1u) << 4));
+        v[i] = __fadd_rn(__fmul_rn(q, d), m);
+      }
     }
   } else {  // Q8_0
     const float d = f16_bits_to_f32(ld16<ALIGN>(blk));

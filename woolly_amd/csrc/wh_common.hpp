@@ -36,6 +36,8 @@ inline size_t type_size(int type) {
     case WH_TYPE_F16: return 2;
     case WH_TYPE_Q4_0: return 18;
     case WH_TYPE_Q4_1: return 20;
+    case WH_TYPE_Q5_0: return 22;
+    case WH_TYPE_Q5_1: return 24;
     case WH_TYPE_Q8_0: return 34;
     case WH_TYPE_Q4_K: return 144;
     case WH_TYPE_Q6_K: return 210;
@@ -49,6 +51,8 @@ inline size_t block_elems(int type) {
     case WH_TYPE_F16: return 1;
     case WH_TYPE_Q4_0:
     case WH_TYPE_Q4_1:
+    case WH_TYPE_Q5_0:
+    case WH_TYPE_Q5_1:
     case WH_TYPE_Q8_0: return 32;
     case WH_TYPE_Q4_K:
     case WH_TYPE_Q6_K: return 256;

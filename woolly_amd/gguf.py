@@ -131,7 +131,10 @@ def data_size(t: GGMLType, n_elements: int) -> int:
 
 
 def dequantize(data, ggml_type: GGMLType, nelements: int) -> np.ndarray:
-    """woolly_gguf::dequantize (dequantize.rs:189-205) on the GPU."""
+    """woolly_gguf::dequantize (dequantize.rs:189-205) on the GPU.  Q5_0 / Q5_1
+    decode as woolly-tensor's dequantize_q5_0 / _q5_1 (quantization.rs:515-575):
+    the reference's gguf-level versions (dequantize.rs:538-550) are stubs that
+    return zeros, which this drop-in does not reproduce."""
     buf = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8)
                                if not isinstance(data, np.ndarray) else data.view(np.uint8))
     out = np.empty(nelements, dtype=np.float32)

@@ -4,10 +4,10 @@ Names, argument meaning and errors follow
 crates/woolly-tensor/src/quantization.rs so that tests read like the
 reference's own:
 
-  BlockQ4_0 / BlockQ4_1 / BlockQ8_0            quantization.rs:98-151
+  BlockQ4_0 / BlockQ4_1 / BlockQ5_0 / BlockQ5_1 / BlockQ8_0   quantization.rs:98-151
   QuantizationError.{UnsupportedScheme, InvalidParameters}   :8-26
-  QuantizedStorage.{Q4_0, Q4_1, Q8_0}           :154-170
-  dequantize_q4_0 / dequantize_q4_1 / dequantize_q8_0       :466, 490, 576
+  QuantizedStorage.{Q4_0, Q4_1, Q5_0, Q5_1, Q8_0}           :154-170
+  dequantize_q4_0 / _q4_1 / _q5_0 / _q5_1 / _q8_0  :466, 490, 515, 545, 576
   simd.quantized_matvec(weights, input, output, m, k)       :869-909
   optimized.dequantize_blocks(storage)          :1171-1210
 
@@ -24,8 +24,11 @@ from . import _lib
 
 BlockQ4_0 = np.dtype([("d", "<u2"), ("qs", "u1", (16,))])
 BlockQ4_1 = np.dtype([("d", "<u2"), ("m", "<u2"), ("qs", "u1", (16,))])
+BlockQ5_0 = np.dtype([("d", "<u2"), ("qh", "u1", (4,)), ("qs", "u1", (16,))])
+BlockQ5_1 = np.dtype([("d", "<u2"), ("m", "<u2"), ("qh", "u1", (4,)), ("qs", "u1", (16,))])
 BlockQ8_0 = np.dtype([("d", "<u2"), ("qs", "i1", (32,))])
 assert BlockQ4_0.itemsize == 18 and BlockQ4_1.itemsize == 20 and BlockQ8_0.itemsize == 34
+assert BlockQ5_0.itemsize == 22 and BlockQ5_1.itemsize == 24
 
 QK = 32
 
@@ -39,7 +42,11 @@ class QuantizationScheme(enum.Enum):
 
 
 _DTYPE = {QuantizationScheme.Q4_0: BlockQ4_0, QuantizationScheme.Q4_1: BlockQ4_1,
+          QuantizationScheme.Q5_0: BlockQ5_0, QuantizationScheme.Q5_1: BlockQ5_1,
           QuantizationScheme.Q8_0: BlockQ8_0}
+# the schemes simd::quantized_matvec takes (Q4_0 and Q8_0 in the reference,
+# quantization.rs:869-909, plus Q4_1 here); Q5 storage is dequantization only
+_MATVEC = (QuantizationScheme.Q4_0, QuantizationScheme.Q4_1, QuantizationScheme.Q8_0)
 
 
 class QuantizationError(Exception):
@@ -65,7 +72,7 @@ def _raise(status: int) -> None:
 
 
 class QuantizedStorage:
-    """QuantizedStorage::{Q4_0, Q4_1, Q8_0}(Vec<Block>) (quantization.rs:154-170)."""
+    """QuantizedStorage::{Q4_0, Q4_1, Q5_0, Q5_1, Q8_0}(Vec<Block>) (quantization.rs:154-170)."""
 
     def __init__(self, scheme: QuantizationScheme, blocks: np.ndarray):
         self.scheme = scheme
@@ -81,6 +88,14 @@ class QuantizedStorage:
     @classmethod
     def Q4_1(cls, blocks):
         return cls(QuantizationScheme.Q4_1, blocks)
+
+    @classmethod
+    def Q5_0(cls, blocks):
+        return cls(QuantizationScheme.Q5_0, blocks)
+
+    @classmethod
+    def Q5_1(cls, blocks):
+        return cls(QuantizationScheme.Q5_1, blocks)
 
     @classmethod
     def Q8_0(cls, blocks):
@@ -108,6 +123,16 @@ def dequantize_q4_1(blocks: np.ndarray) -> np.ndarray:
     return _dequantize(QuantizationScheme.Q4_1, np.asarray(blocks, dtype=BlockQ4_1))
 
 
+def dequantize_q5_0(blocks: np.ndarray) -> np.ndarray:
+    """dequantize_q5_0(&[BlockQ5_0]) -> Vec<f32> (quantization.rs:515-541)."""
+    return _dequantize(QuantizationScheme.Q5_0, np.asarray(blocks, dtype=BlockQ5_0))
+
+
+def dequantize_q5_1(blocks: np.ndarray) -> np.ndarray:
+    """dequantize_q5_1(&[BlockQ5_1]) -> Vec<f32> (quantization.rs:545-573)."""
+    return _dequantize(QuantizationScheme.Q5_1, np.asarray(blocks, dtype=BlockQ5_1))
+
+
 def dequantize_q8_0(blocks: np.ndarray) -> np.ndarray:
     """dequantize_q8_0(&[BlockQ8_0]) -> Vec<f32> (quantization.rs:576-590)."""
     return _dequantize(QuantizationScheme.Q8_0, np.asarray(blocks, dtype=BlockQ8_0))
@@ -122,7 +147,7 @@ class simd:  # noqa: N801 -- mirrors the reference's `quantization::simd` module
         output[r] = sum_k W[r, k] * input[k] for r < m.  Errors: UnsupportedScheme
         for other storage, InvalidParameters for k % 32 != 0 (the reference's
         assert_eq! panic) or too few blocks."""
-        if weights.scheme not in _DTYPE:
+        if weights.scheme not in _MATVEC:
             raise QuantizationError.UnsupportedScheme(
                 "Quantized matvec not implemented for this scheme")
         x = np.ascontiguousarray(input, dtype=np.float32)
@@ -140,6 +165,8 @@ class simd:  # noqa: N801 -- mirrors the reference's `quantization::simd` module
     dequantize_q8_0_simd = staticmethod(dequantize_q8_0)
     dequantize_q4_0_batch = staticmethod(dequantize_q4_0)
     dequantize_q4_1_batch = staticmethod(dequantize_q4_1)
+    dequantize_q5_0_batch = staticmethod(dequantize_q5_0)
+    dequantize_q5_1_batch = staticmethod(dequantize_q5_1)
     dequantize_q8_0_batch = staticmethod(dequantize_q8_0)
 
 

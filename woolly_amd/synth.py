@@ -25,8 +25,11 @@ M1 = np.uint64(0xBF58476D1CE4E5B9)
 M2 = np.uint64(0x94D049BB133111EB)
 
 GGML_Q4_0, GGML_Q4_1, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 2, 3, 8, 12, 14
-TYPE_SIZE = {GGML_Q4_0: 18, GGML_Q4_1: 20, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
-BLOCK_ELEMS = {GGML_Q4_0: 32, GGML_Q4_1: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+GGML_Q5_0, GGML_Q5_1 = 6, 7
+TYPE_SIZE = {GGML_Q4_0: 18, GGML_Q4_1: 20, GGML_Q5_0: 22, GGML_Q5_1: 24, GGML_Q8_0: 34, GGML_Q4_K: 144,
+             GGML_Q6_K: 210}
+BLOCK_ELEMS = {GGML_Q4_0: 32, GGML_Q4_1: 32, GGML_Q5_0: 32, GGML_Q5_1: 32, GGML_Q8_0: 32, GGML_Q4_K: 256,
+               GGML_Q6_K: 256}
 TYPE_NAME = {GGML_Q4_0: "Q4_0", GGML_Q4_1: "Q4_1", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K", GGML_Q6_K: "Q6_K"}
 
 
@@ -96,6 +99,8 @@ def quantized_weight(ggml_type: int, n_rows: int, k: int, seed: int, stream: int
     Q4_0: d = f16(|N(0, 0.02)|), qs bytes uniform 0..255 (two uniform nibbles).
     Q8_0: d = f16(|N(0, 0.02)|), qs int8 uniform in [-127, 127].
     Q4_1: d, m = f16(N(0, 0.01)), qs bytes uniform 0..255.
+    Q5_0: d = f16(|N(0, 0.02)|), qh and qs bytes uniform 0..255 (dequantization only).
+    Q5_1: d, m = f16(N(0, 0.01)), qh and qs bytes uniform 0..255 (dequantization only).
     Q4_K: scale bytes uniform, d = f16(|N(0, 0.0005)|), dmin = f16(N(0, 0.01)), quant bytes uniform.
     Q6_K: ql, qh, scale bytes uniform, d = f16(|N(0, 0.0001)|).
     """
@@ -129,6 +134,16 @@ def quantized_weight(ggml_type: int, n_rows: int, k: int, seed: int, stream: int
         out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
         out[:, 2:4] = f16_bits(m).view(np.uint8).reshape(nb, 2)
         out[:, 4:20] = u64(seed, s0 + 2, nb * 2).view(np.uint8).reshape(nb, 16)
+    elif ggml_type in (GGML_Q5_0, GGML_Q5_1):
+        # d (and m), then 20 random bytes: qh[4], qs[16]
+        h = 2 if ggml_type == GGML_Q5_0 else 4
+        if ggml_type == GGML_Q5_0:
+            d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.02 if d_std is None else d_std))
+        else:
+            d = normal(seed, s0 + 1, nb, 0.0, 0.01 if d_std is None else d_std)
+            out[:, 2:4] = f16_bits(normal(seed, s0 + 3, nb, 0.0, 0.01)).view(np.uint8).reshape(nb, 2)
+        out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
+        out[:, h:h + 20] = u64(seed, s0 + 2, nb * 3).view(np.uint8).reshape(nb, 24)[:, :20]
     elif ggml_type == GGML_Q8_0:
         d = np.abs(normal(seed, s0 + 1, nb, 0.0, 0.02 if d_std is None else d_std))
         out[:, 0:2] = f16_bits(d).view(np.uint8).reshape(nb, 2)
