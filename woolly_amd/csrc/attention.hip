@@ -14,16 +14,327 @@
 // attends to the stored values.
 //
 // Work split (flash-decoding): one workgroup per (KV head, chunk of C
-// positions); it applies RoPE to its G = n_heads / n_kv_heads query heads,
-// stages the chunk's K and V rows in LDS (the row of position pos comes from
-// the fresh k / v, which this workgroup also writes to the cache), and writes
-// per query head the chunk's running maximum m, sum l = sum exp(s - m) and
-// acc = sum exp(s - m) v.  attn_combine_kernel merges the chunks of each head.
+// positions); it applies RoPE to its G = n_heads / n_kv_heads query heads and
+// writes per query head the chunk's maximum m, sum l = sum exp(s - m) and
+// acc = sum exp(s - m) v (the row of position pos comes from the fresh k / v,
+// which the workgroup owning pos also writes to the cache).
+// attn_combine_kernel merges the chunks of each head.
+//
+// head_dim 128 (attn_partial_mfma_kernel): each wave owns 16-position tiles of
+// the chunk (tiles w, w + 4, ...).  Scores on the matrix cores: one
+// v_mfma_f32_16x16x32_f16 per 32 dims with A = the rotated queries (rows 0..G-1,
+// each query split exactly enough into f16 hi + lo, two MFMAs) and B = the
+// tile's K rows, which lanes load from HBM straight into the operand layout
+// (lane (n, g): 16 bytes of row n at 16 g + 64 ks).  Softmax per wave with a
+// running maximum (online), P·V on the VALU with V read as one dword (two dims)
+// per lane and position (a 256-byte row per load instruction), P broadcast
+// through LDS.  The four waves' (m, l, acc) merge through LDS in fixed order.
+// head_dim 64 keeps the LDS-staged VALU kernel (attn_partial_kernel).
 #include "wh_common.hpp"
+
+typedef _Float16 at_half8 __attribute__((ext_vector_type(8)));
+typedef float at_f4 __attribute__((ext_vector_type(4)));
+typedef int at_i4 __attribute__((ext_vector_type(4)));
+
+// raw buffer loads of 16 and 4 bytes (llvm.amdgcn.raw.buffer.load.*)
+__device__ at_i4 at_buffer_load_x4(at_i4 rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+__device__ int at_buffer_load_x1(at_i4 rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.i32");
 
 namespace {
 
 constexpr int kAttnThreads = 256;
+
+// Buffer resource of a raw byte range: loads at offsets >= nbytes return 0
+// without a memory access.
+__device__ __forceinline__ at_i4 at_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  at_i4 r;
+  r[0] = static_cast<int>(static_cast<uint32_t>(a));
+  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xFFFFu);
+  r[2] = static_cast<int>(nbytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float at_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Maximum / sum over each row of 16 lanes, in every lane of the row (fixed
+// order: quad swaps, then half-row and row mirrors).
+__device__ __forceinline__ float at_row_max(float v) {
+  v = fmaxf(v, at_dpp<0xB1>(v));
+  v = fmaxf(v, at_dpp<0x4E>(v));
+  v = fmaxf(v, at_dpp<0x141>(v));
+  return fmaxf(v, at_dpp<0x140>(v));
+}
+__device__ __forceinline__ float at_row_sum(float v) {
+  v += at_dpp<0xB1>(v);
+  v += at_dpp<0x4E>(v);
+  v += at_dpp<0x141>(v);
+  return v + at_dpp<0x140>(v);
+}
+
+// GMAX: 4 (G <= 4 query heads per KV head) or 8 (G <= 8).
+template <int GMAX>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_mfma_kernel(
+    const float* __restrict__ qkv, _Float16* __restrict__ k_cache, _Float16* __restrict__ v_cache,
+    const float* __restrict__ inv_freq, float* __restrict__ part, int pos, int n_heads, int n_kv_heads,
+    int chunk, int n_chunks, float scale) {
+  constexpr int D = 128;
+  extern __shared__ __align__(16) float sm[];
+  const int G = n_heads / n_kv_heads;
+  const int kvh = blockIdx.x;
+  const int c = blockIdx.y;
+  const int p0 = c * chunk;
+  const int np = min(chunk, pos + 1 - p0);  // positions of this chunk (>= 1)
+  const int t = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63, n = lane & 15, g = lane >> 4;
+  const bool own = pos < p0 + chunk;  // pos lies in this (the last) chunk
+  float* qs = sm;                                          // [GMAX][D] rotated queries
+  _Float16* kvnew = reinterpret_cast<_Float16*>(qs + GMAX * D);  // [2][D] new k (rotated), v
+  float* pbuf = qs + GMAX * D + D;                         // [4 waves][16][GMAX] softmax weights
+  float* mw = pbuf + 4 * 16 * GMAX;                        // [4][GMAX] wave maxima, then sums
+  float* lw = mw + 4 * GMAX;
+  float* aw = lw + 4 * GMAX;                               // [4][GMAX][D] wave accumulators
+
+  // K / V rows of this head: row r (0-based in the chunk) starts r * RS bytes
+  // after row p0; rows from pos on read as zeros (the buffer range ends there),
+  // the row of pos is filled in from the fresh k / v below
+  const uint32_t RS = static_cast<uint32_t>(n_kv_heads) * D * 2;
+  const int nload = own ? pos - p0 : np;
+  const uint32_t range = nload > 0 ? static_cast<uint32_t>(nload - 1) * RS + D * 2 : 0u;
+  const size_t head0 = (static_cast<size_t>(p0) * n_kv_heads + kvh) * D;
+  const at_i4 krs = at_rsrc(k_cache + head0, range);
+  const at_i4 vrs = at_rsrc(v_cache + head0, range);
+  auto load_k = [&](int tile, at_i4 (&kk)[4]) {
+    const int off = static_cast<int>(static_cast<uint32_t>(16 * tile + n) * RS) + 16 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) kk[ks] = at_buffer_load_x4(krs, off + 64 * ks, 0, 0);
+  };
+  auto load_v = [&](int tile, int (&vv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      vv[i] = at_buffer_load_x1(vrs, static_cast<int>(static_cast<uint32_t>(16 * tile + i) * RS) + 4 * lane, 0, 0);
+  };
+  // this thread's query pairs (thread -> (head, pair i)) and its share of
+  // the new k / v, requested before K and V (loads complete in order and
+  // these are needed first).  Every load is unconditional (indices clamped
+  // into the buffers): a load under a branch makes the compiler wait for all
+  // loads in flight where the branches join.
+  constexpr int QI = GMAX * (D / 2) / kAttnThreads;
+  const float fpos = static_cast<float>(pos);
+  float qx1[QI], qx2[QI], qf[QI];
+#pragma unroll
+  for (int u = 0; u < QI; u++) {
+    const int e = min(t + u * kAttnThreads, G * (D / 2) - 1);
+    const int h = e / (D / 2), i = e % (D / 2);
+    const float* q = qkv + (kvh * G + h) * D;
+    qx1[u] = q[i];
+    qx2[u] = q[i + D / 2];
+    qf[u] = inv_freq[i];
+  }
+  const float* kn = qkv + n_heads * D + kvh * D;
+  const float* vn = qkv + n_heads * D + n_kv_heads * D + kvh * D;
+  const float kx1 = kn[t % (D / 2)], kx2 = kn[t % (D / 2) + D / 2], kf = inv_freq[t % (D / 2)];
+  const float vx = vn[t % D];
+  __builtin_amdgcn_sched_barrier(0);
+  at_i4 kc[4];
+  int vc[16];
+  int tile = wave;
+  load_k(tile, kc);  // rows past the chunk's valid range read as zeros
+  load_v(tile, vc);
+  __builtin_amdgcn_sched_barrier(0);  // the rotations below wait for the query loads
+
+  // rotated queries into LDS.  No branch: threads past the last pair write
+  // the last pair's values again (a branch would let the compiler move the
+  // loads above into it, after the K / V loads)
+#pragma unroll
+  for (int u = 0; u < QI; u++) {
+    const int e = min(t + u * kAttnThreads, G * (D / 2) - 1);
+    const int h = e / (D / 2), i = e % (D / 2);
+    float sn, cs;
+    sincosf(fpos * qf[u], &sn, &cs);
+    qs[h * D + i] = qx1[u] * cs - qx2[u] * sn;
+    qs[h * D + i + D / 2] = qx1[u] * sn + qx2[u] * cs;
+  }
+  {
+    // the new token: rotate k, round k and v to f16; the chunk of pos stores
+    // them in the cache
+    float sn, cs;
+    sincosf(fpos * kf, &sn, &cs);
+    const _Float16 a = static_cast<_Float16>(kx1 * cs - kx2 * sn);
+    const _Float16 b = static_cast<_Float16>(kx1 * sn + kx2 * cs);
+    const _Float16 v = static_cast<_Float16>(vx);
+    const size_t off = (static_cast<size_t>(pos) * n_kv_heads + kvh) * D;
+    if (own && t < D / 2) {
+      kvnew[t] = a;
+      kvnew[t + D / 2] = b;
+      k_cache[off + t] = a;
+      k_cache[off + t + D / 2] = b;
+    } else if (own && t >= D && t < 2 * D) {
+      const int d = t - D;  // t % D == d: vx is vn[d]
+      kvnew[D + d] = v;
+      v_cache[off + d] = v;
+    }
+  }
+  // LDS-only barrier: a __syncthreads() would also wait for the K / V loads in flight
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // A operands: row m < G is query head m, split into f16 hi + lo
+  at_half8 qh[4], ql[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float x = n < G ? qs[n * D + 32 * ks + 8 * g + j] : 0.f;
+      const _Float16 hi = static_cast<_Float16>(x);
+      qh[ks][j] = hi;
+      ql[ks][j] = static_cast<_Float16>(x - static_cast<float>(hi));
+    }
+  }
+
+  float m_run[GMAX], l_run[GMAX], acc[GMAX][2];
+#pragma unroll
+  for (int h = 0; h < GMAX; h++) {
+    m_run[h] = -INFINITY;
+    l_run[h] = 0.f;
+    acc[h][0] = acc[h][1] = 0.f;
+  }
+  float* pw = pbuf + wave * 16 * GMAX;
+  for (; 16 * tile < np; tile += 4) {
+    at_i4 kn_[4];
+    int vn_[16];
+    const bool more = 16 * (tile + 4) < np;
+    if (more) {
+      load_k(tile + 4, kn_);
+      load_v(tile + 4, vn_);
+    }
+    if (own && tile == (pos - p0) / 16) {
+      // the row of pos from the fresh k / v
+      const int r = (pos - p0) % 16;
+      if (n == r) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) kc[ks] = *reinterpret_cast<const at_i4*>(kvnew + 32 * ks + 8 * g);
+      }
+      vc[r] = *reinterpret_cast<const int*>(kvnew + D + 2 * lane);
+    }
+    at_f4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+      const at_half8 kb = __builtin_bit_cast(at_half8, kc[ks]);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kb, S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kb, S, 0, 0, 0);
+    }
+    // lane (n, g): scores of heads 4 g .. 4 g + 3 at tile position n
+    const bool valid = 16 * tile + n < np;
+    float s[4], mt[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      s[j] = valid ? S[j] * scale : -INFINITY;
+      mt[j] = at_row_max(s[j]);
+    }
+    float m_new[GMAX], alpha[GMAX];
+#pragma unroll
+    for (int h = 0; h < GMAX; h++) {
+      const float th = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mt[h & 3]), 16 * (h >> 2)));
+      m_new[h] = fmaxf(m_run[h], th);  // finite: the tile holds a valid position
+      alpha[h] = expf(m_run[h] - m_new[h]);  // 0 while m_run is -inf
+    }
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float mn = m_new[j];
+      if constexpr (GMAX == 8) mn = g == 1 ? m_new[4 + j] : mn;
+      p[j] = valid ? expf(s[j] - mn) : 0.f;
+    }
+    float lt[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) lt[j] = at_row_sum(p[j]);
+    if (g < GMAX / 4) *reinterpret_cast<float4*>(pw + n * GMAX + 4 * g) = make_float4(p[0], p[1], p[2], p[3]);
+#pragma unroll
+    for (int h = 0; h < GMAX; h++) {
+      const float th = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lt[h & 3]), 16 * (h >> 2)));
+      l_run[h] = __builtin_fmaf(l_run[h], alpha[h], th);
+      m_run[h] = m_new[h];
+      acc[h][0] *= alpha[h];
+      acc[h][1] *= alpha[h];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    // P V: lane -> dims 2 lane, 2 lane + 1
+    const int npos = min(16, np - 16 * tile);
+    for (int i = 0; i < npos; i++) {
+      const float4 pa = *reinterpret_cast<const float4*>(pw + i * GMAX);
+      float pb[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (GMAX == 8) {
+        const float4 q2 = *reinterpret_cast<const float4*>(pw + i * GMAX + 4);
+        pb[0] = q2.x, pb[1] = q2.y, pb[2] = q2.z, pb[3] = q2.w;
+      }
+      const uint32_t w = static_cast<uint32_t>(vc[i]);
+      const float v0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu)));
+      const float v1 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb[0], pb[1], pb[2], pb[3]};
+#pragma unroll
+      for (int h = 0; h < GMAX; h++) {
+        acc[h][0] = __builtin_fmaf(pv[h], v0, acc[h][0]);
+        acc[h][1] = __builtin_fmaf(pv[h], v1, acc[h][1]);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    if (more) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) kc[ks] = kn_[ks];
+#pragma unroll
+      for (int i = 0; i < 16; i++) vc[i] = vn_[i];
+    }
+  }
+
+  // merge the four waves (fixed order); a wave without positions holds m = -inf
+  if (lane < GMAX) {
+    float mv = m_run[0], lv = l_run[0];
+#pragma unroll
+    for (int h = 1; h < GMAX; h++)
+      if (lane == h) mv = m_run[h], lv = l_run[h];
+    mw[wave * GMAX + lane] = mv;
+    lw[wave * GMAX + lane] = lv;
+  }
+#pragma unroll
+  for (int h = 0; h < GMAX; h++)
+    *reinterpret_cast<float2*>(aw + (wave * GMAX + h) * D + 2 * lane) = make_float2(acc[h][0], acc[h][1]);
+  __syncthreads();
+  for (int e = t; e < G * (D / 2); e += kAttnThreads) {
+    const int h = e / (D / 2), dp = e % (D / 2);
+    float M = mw[h];
+#pragma unroll
+    for (int w = 1; w < 4; w++) M = fmaxf(M, mw[w * GMAX + h]);
+    float L = 0.f, A0 = 0.f, A1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float ew = expf(mw[w * GMAX + h] - M);  // 0 for a wave without positions
+      const float2 a = *reinterpret_cast<const float2*>(aw + (w * GMAX + h) * D + 2 * dp);
+      L = __builtin_fmaf(lw[w * GMAX + h], ew, L);
+      A0 = __builtin_fmaf(a.x, ew, A0);
+      A1 = __builtin_fmaf(a.y, ew, A1);
+    }
+    float* o = part + (static_cast<size_t>(kvh * G + h) * n_chunks + c) * (D + 2);
+    o[2 + 2 * dp] = A0;
+    o[3 + 2 * dp] = A1;
+    if (dp == 0) {
+      o[0] = M;
+      o[1] = L;
+    }
+  }
+}
+
+template <int GMAX>
+size_t partial_mfma_lds() {
+  return 4u * (GMAX * 128 + 128 + 4 * 16 * GMAX + 2 * 4 * GMAX + 4 * GMAX * 128);
+}
 
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
@@ -319,12 +630,15 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
   const dim3 cgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(head_dim / kCombDims));
   dim3 grid(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(n_chunks));
   if (head_dim == 128) {
-    const size_t lds = partial_lds<128>(G, chunk);
-    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<128>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    attn_partial_kernel<128><<<grid, kAttnThreads, lds, s>>>(
-        qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
-        static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
+    if (G <= 4) {
+      attn_partial_mfma_kernel<4><<<grid, kAttnThreads, partial_mfma_lds<4>(), s>>>(
+          qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
+          static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
+    } else {
+      attn_partial_mfma_kernel<8><<<grid, kAttnThreads, partial_mfma_lds<8>(), s>>>(
+          qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
+          static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
+    }
     WH_LAUNCH_CHECK("attention kernel launch");
     attn_combine_kernel<128><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
   } else {
