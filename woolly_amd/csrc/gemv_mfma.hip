@@ -338,6 +338,30 @@ __device__ __forceinline__ int mg_sum8_packed(int v) {
   return v + mg_dpp<kDppHalfMirror>(v);
 }
 
+// Sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) in every
+// lane, as (v[l] + v[l ^ 16]) + (v[l ^ 32] + v[l ^ 48]), with gfx950's
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Inline asm
+// with explicit wait states around each swap: the builtins' code returned one
+// register for both swapped halves.
+__device__ __forceinline__ float mg_sum_lane_groups(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  a = b = __builtin_bit_cast(uint32_t, v);
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+// The four limb sums of one block as one f32, 2^24 C0 + 2^16 C1 + 2^8 C2 + C3:
+// the halves 2^8 C0 + C1 and 2^8 C2 + C3 in int32 (exact and without overflow:
+// |C| < 2^20 in the single-token kernel), converted (exactly for the 4-bit
+// formats, whose halves stay below 2^24) and combined with one fma.
+__device__ __forceinline__ float mg_limbs(const mg_v4i& C) {
+  const int hi = C[0] * 256 + C[1];
+  const int lo = C[2] * 256 + C[3];
+  return __builtin_fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
+}
+
 // Bits 2t .. 2t + 1 of v (t = 0..3) moved to bits 4..5 of byte t.
 __device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
   return ((v << 4) | (v << 10) | (v << 16) | (v << 22)) & 0x30303030u;
@@ -602,12 +626,14 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   };
 
   // Sum of group q over the 16 waves (fixed order), then the output row.
+  // All 64 lanes: lane (n, g) adds waves 4g .. 4g + 3 of row n, the lane
+  // groups are then summed across (a short chain on the finishing wave, which
+  // computes its own chunk after this).
   auto finish = [&](int q) {
+    const float* pp = part + (q & 1) * kMgWaves * 16 + 64 * g + n;
+    const float v0 = pp[0], v1 = pp[16], v2 = pp[32], v3 = pp[48];
+    const float v = mg_sum_lane_groups((v0 + v1) + (v2 + v3));
     if (lane >= 16) return;
-    const float* pp = part + (q & 1) * kMgWaves * 16 + n;
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < kMgWaves; w++) v += pp[16 * w];
     const int gi = FFN ? (q >> 1) : q;
     const int row = r0 + 16 * gi + n;
     if constexpr (FFN) {
@@ -688,10 +714,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             float sacc = 0.f;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
-                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
-                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
-                                                                           static_cast<float>(C[t][3]))));
+              const float f = mg_limbs(C[t]);
               sacc = __builtin_fmaf(d64 * static_cast<float>(rowp[192 + 4 * t + g]), f, sacc);
             }
             acc += ldexpf(sacc, -ex[seg]);
@@ -719,10 +742,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             float sacc = 0.f;
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
-                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
-                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
-                                                                           static_cast<float>(C[t][3]))));
+              const float f = mg_limbs(C[t]);
               const float ds = d * static_cast<float>(mg_q4k_scale(rowp, 4 * t + g));
               sacc = __builtin_fmaf(ds, f, sacc);
               sacc = __builtin_fmaf(dmin, bsum[t], sacc);
@@ -756,10 +776,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
             float sacc = 0.f;
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-              const float f = __builtin_fmaf(static_cast<float>(C[t][0]), 16777216.f,
-                                             __builtin_fmaf(static_cast<float>(C[t][1]), 65536.f,
-                                                            __builtin_fmaf(static_cast<float>(C[t][2]), 256.f,
-                                                                           static_cast<float>(C[t][3]))));
+              const float f = mg_limbs(C[t]);
               const float d = whd::f16_bits_to_f32(dm[t] & 0xFFFFu);
               sacc = __builtin_fmaf(d, f, sacc);
               if constexpr (Q41) sacc = __builtin_fmaf(whd::f16_bits_to_f32(dm[t] >> 16), bsum[t], sacc);
@@ -772,8 +789,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
         }
       }
       if (seg == NSEG - 1 && live) {
-        float v = acc + __shfl_xor(acc, 16, 64);
-        v += __shfl_xor(v, 32, 64);
+        const float v = mg_sum_lane_groups(acc);
         if (g == 0) part[(q & 1) * kMgWaves * 16 + wave * 16 + n] = v;
         acc = 0.f;
       }
