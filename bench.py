@@ -20,7 +20,10 @@ Prints ONE JSON line with:
                  graph's per-replay cost stays hidden), median of 5 measurements
                  after ~0.1 s of clock settling; traffic = HBM bytes per launch
                  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary,
-                 null when that summary was taken from other kernel sources
+                 null when that summary was taken from other kernel sources;
+                 read_floor: the same bytes read by wh_read_probe in the GEMV's
+                 workgroup geometry with no compute, timed the same way (what one
+                 launch of this access pattern reaches on this part)
   ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
                  M=512, same run (the metric's second part; M=1 rotates 3 layers'
                  weights, 297 MB, past the Infinity Cache)
@@ -325,6 +328,53 @@ def bench_decode(steps: int, c: dict = L8B, types: dict | None = None, head_type
             "ctx": c["ctx"], "layers": c["n_layers"], "logits_finite": bool(np.all(np.isfinite(logits)))}
 
 
+def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N_ROWS, k: int = K,
+                       replicas: int = REPLICAS) -> float:
+    """The read floor of the headline GEMV's access pattern (wh_read_probe): the
+    same N rows of K/32 Q4_0 blocks, rotated through the same number of copies
+    and timed the same way (graph replay between events, after clock settling),
+    read in the GEMV's workgroup geometry without storing or computing anything.
+    mode 0: one step in flight per wave, as the GEMV; mode 1: up to four.
+    Returns ms per launch."""
+    from woolly_amd import _lib, synth
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+
+    w = synth.quantized_weight(Q4_0, n, k, seed=3)
+    row_bytes = k // 32 * TYPE_SIZE[Q4_0]
+    stream = Stream()
+    wbufs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
+    out = DeviceBuffer(4 * (n // 16 + 1))  # one checksum per workgroup
+    lib = _lib.load()
+
+    def launch(i: int) -> None:
+        _lib.check(lib.wh_read_probe(wbufs[i % replicas].ptr, row_bytes, n, mode, out.ptr, stream.handle))
+
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    with Graph.capture(stream) as graph:
+        for i in range(steps):
+            launch(i)
+    graph.launch(stream)
+    stream.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARM_S:
+        graph.launch(stream)
+        stream.synchronize()
+    n_rep = max(1, -(-TIMED_LAUNCHES // steps))
+    e0, e1 = Event(), Event()
+    reps = []
+    for _ in range(TIMED_REPLAYS):
+        e0.record(stream)
+        for _ in range(n_rep):
+            graph.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        reps.append(e0.elapsed_ms(e1) / n_rep)
+    graph.destroy()
+    return float(np.median(reps)) / steps
+
+
 def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
     """Device-to-device copies of a known size (HIP's copy kernel): the reference
     the HBM byte counters of the GEMV are scaled by.  Returns GB/s."""
@@ -518,6 +568,15 @@ def main() -> int:
     achieved = value
     log(f"[bench] gemv: {ms_step * 1e3:.2f} us/step back-to-back, per-launch mean "
         f"{mean_ms * 1e3:.2f} us (median {med_ms * 1e3:.2f})")
+    # the same bytes read in the GEMV's geometry with nothing else done: what
+    # this access pattern and one launch per call can reach on this part
+    floor = {}
+    for mode, name in ((0, "gemv_geometry_1_step_in_flight"), (1, "gemv_geometry_4_steps_in_flight")):
+        ms = bench_stream_floor(mode, args.steps, args.warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        floor[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"[bench] read floor ({name}): {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    floor["gemv_us_over_floor_us"] = round(ms_step * 1e3 / floor["gemv_geometry_1_step_in_flight"]["us"], 3)
 
     ffn = {}
     if not args.no_ffn:
@@ -628,6 +687,7 @@ def main() -> int:
             "launch_us_mean": round(ms_step * 1e3, 3),
             "launches_timed": bench_gemv.launches_timed,
             "launch_us_eager_event_pairs": round(mean_ms * 1e3, 3),
+            "read_floor": floor,
         },
         "ffn_layer_us": ffn or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,

@@ -212,6 +212,9 @@ extern "C" {
     pub fn wh_memcpy_d2h(dst: *mut c_void, src: *const c_void, nbytes: usize, stream: wh_stream_t) -> c_int;
     pub fn wh_memcpy_d2d(dst: *mut c_void, src: *const c_void, nbytes: usize, stream: wh_stream_t) -> c_int;
     pub fn wh_fill_bytes(dst: *mut c_void, value: c_int, nbytes: usize, stream: wh_stream_t) -> c_int;
+    // measurement aid (no counterpart in the reference)
+    pub fn wh_read_probe(src: *const c_void, row_bytes: usize, n_rows: usize, mode: c_int, out: *mut u32,
+                         stream: wh_stream_t) -> c_int;
     pub fn wh_stream_create(out: *mut wh_stream_t) -> c_int;
     pub fn wh_stream_destroy(stream: wh_stream_t) -> c_int;
     pub fn wh_stream_synchronize(stream: wh_stream_t) -> c_int;

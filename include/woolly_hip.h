@@ -113,6 +113,16 @@ WH_API int wh_graph_end_capture(wh_stream_t stream, wh_graph_t* out);
 WH_API int wh_graph_launch(wh_graph_t graph, wh_stream_t stream);
 WH_API int wh_graph_destroy(wh_graph_t graph);
 
+/* Measurement aid, no counterpart in the reference (for benchmarks of the
+ * GEMV): reads an n_rows x row_bytes device matrix (row_bytes <= 4096) in the
+ * geometry of the single-token matrix-core GEMV (workgroups of 16 waves, one
+ * row per wave per step, 16-byte loads) without storing or computing
+ * anything but a checksum per workgroup: out is a device array of at least
+ * ceil(n_rows / 16) dwords.  mode 0: one step in flight per wave, as the
+ * GEMV; mode 1: up to four. */
+WH_API int wh_read_probe(const void* src, size_t row_bytes, size_t n_rows, int mode, uint32_t* out,
+                         wh_stream_t stream);
+
 /* ------------------------------------------------------------------ format */
 /* get_block_size / get_type_size, crates/woolly-gguf/src/dequantize.rs:208-242.
  * Return 0 for types this backend does not handle. */

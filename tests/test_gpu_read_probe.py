@@ -1,0 +1,42 @@
+"""wh_read_probe (the benchmark's read floor): every byte of every row is read,
+in the GEMV's workgroup geometry: workgroup b's checksum is the xor of all
+32-bit words of its rows."""
+import re
+
+import numpy as np
+import pytest
+
+from tests._gpu import down, up
+from woolly_amd import _lib, device
+from woolly_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("n_rows,row_bytes", [(300, 2304), (14336, 2304), (1000, 4096), (17, 1024), (4096, 576)])
+def test_read_probe_checksums(gpu, mode, n_rows, row_bytes):
+    print(f"[case] read_probe mode={mode} {n_rows}x{row_bytes}", flush=True)
+    rng = np.random.default_rng(n_rows + row_bytes)
+    m = rng.integers(0, 2**32, (n_rows, row_bytes // 4), dtype=np.uint64).astype(np.uint32)
+    mb = up(m)[0]
+    groups = (n_rows + 15) // 16
+    cus = int(re.search(r"(\d+) CUs", device.device_name()).group(1))
+    grid0 = min(groups, cus)
+    rows_per_wg = -(-groups // grid0) * 16
+    grid = -(-n_rows // rows_per_wg)
+    out = DeviceBuffer(4 * (n_rows // 16 + 1))
+    lib = _lib.load()
+    _lib.check(lib.wh_read_probe(mb.ptr, row_bytes, n_rows, mode, out.ptr, None))
+    got = down(out, np.uint32, grid)
+    want = np.array([np.bitwise_xor.reduce(m[b * rows_per_wg:(b + 1) * rows_per_wg].reshape(-1))
+                     for b in range(grid)], np.uint32)
+    assert np.array_equal(got, want)
+
+
+def test_read_probe_rejects_bad_arguments(gpu):
+    lib = _lib.load()
+    buf = DeviceBuffer(4096)
+    assert lib.wh_read_probe(buf.ptr, 4097, 1, 0, buf.ptr, None) == _lib.WH_ERR_INVALID_ARGUMENT
+    assert lib.wh_read_probe(buf.ptr, 64, 1, 2, buf.ptr, None) == _lib.WH_ERR_INVALID_ARGUMENT
+    assert lib.wh_read_probe(None, 64, 1, 0, buf.ptr, None) == _lib.WH_ERR_INVALID_ARGUMENT

@@ -141,6 +141,7 @@ SIGNATURES = {
     "wh_memcpy_d2h": (_int, [_vp, _vp, _sz, _vp]),
     "wh_memcpy_d2d": (_int, [_vp, _vp, _sz, _vp]),
     "wh_fill_bytes": (_int, [_vp, _int, _sz, _vp]),
+    "wh_read_probe": (_int, [_vp, _sz, _sz, _int, _vp, _vp]),
     "wh_stream_create": (_int, [C.POINTER(_vp)]),
     "wh_stream_destroy": (_int, [_vp]),
     "wh_stream_synchronize": (_int, [_vp]),
