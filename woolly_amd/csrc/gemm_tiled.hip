@@ -456,11 +456,16 @@ __device__ __forceinline__ void wait_stages(int n) {
 
 // Y (or split-K partial plane blockIdx.y) for one BM x 256 tile over blocks
 // [kb0, kb1).  Grid: x = tiles (XCD-grouped order), y = K splits.
-template <int TYPE, int BM>
+// FFNP (the FFN's gate and up in one pass, no split-K): a tile's 256 weight
+// rows are 128 rows of W (gate) and the same 128 rows of W2 (up); every wave
+// holds gate and up tiles of the same rows side by side (row groups 2m and
+// 2m + 1), and the epilogue writes y = silu(gate x) * (up x) for n_rows
+// output columns (tensor_utils.rs:512-532), so neither product reaches HBM.
+template <int TYPE, int BM, bool FFNP = false>
 __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
-    const uint8_t* __restrict__ W, const _Float16* __restrict__ frag, const float* __restrict__ rscale,
-    const float* __restrict__ bsum, const float* __restrict__ dmin, float* __restrict__ y, int n_tokens,
-    int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles) {
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const _Float16* __restrict__ frag,
+    const float* __restrict__ rscale, const float* __restrict__ bsum, const float* __restrict__ dmin,
+    float* __restrict__ y, int n_tokens, int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles) {
   using C = TCfg<BM>;
   constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = nstage<TYPE, BM>();
   constexpr int A_STAGE = C::A_STAGE;
@@ -489,7 +494,8 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   const int xcd = bid % 8, local = bid / 8;
   const int L = xcd * q + min(xcd, rem) + local;
   const int T = L / tiles_n, R = L % tiles_n;
-  const int t0 = T * BM, r0 = R * TBN;
+  constexpr int HALF = TBN / 2;  // FFNP: rows of each matrix per tile
+  const int t0 = T * BM, r0 = R * (FFNP ? HALF : TBN);
 
   const int kb0 = blockIdx.y * blocks_per_split;
   const int kb1 = min(nb, kb0 + blocks_per_split);
@@ -501,11 +507,15 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   // last row, and copies past the chunk (gi >= TBN * DWB, the rounding of the
   // last instruction) land in the slot's tail, which is never read.  Offsets
   // fit 32 bits (checked by the launcher).
+  // FFNP: chunk rows [0, 128) are gate rows r0.., [128, 256) the same up rows;
+  // the boundary (128 DWB dwords) is a multiple of 64, so each wave's copy
+  // instruction reads from one matrix.
+  static_assert(!FFNP || (HALF * DWB) % 64 == 0, "gate / up halves of the stage chunk in whole copy instructions");
   uint32_t b_off[B_DMA];
 #pragma unroll
   for (int c = 0; c < B_DMA; c++) {
     const int gi = min(static_cast<int>(threadIdx.x) + TWAVES * 64 * c, TBN * DWB - 1);
-    const int row = min(r0 + gi / DWB, n_rows - 1);
+    const int row = min(r0 + (FFNP ? (gi / DWB) % HALF : gi / DWB), n_rows - 1);
     b_off[c] = static_cast<uint32_t>(static_cast<size_t>(row) * row_bytes) + 4u * static_cast<uint32_t>(gi % DWB);
   }
   const uint32_t smem_base = lds_addr(smem);
@@ -529,7 +539,12 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint32_t bslot = slot + A_STAGE;
     const uint32_t kboff = static_cast<uint32_t>(kb) * TS;
 #pragma unroll
-    for (int c = 0; c < B_DMA; c++) copy4_to_lds(W, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
+    for (int c = 0; c < B_DMA; c++) {
+      const uint8_t* wb = W;
+      if constexpr (FFNP)  // this wave's copy c lies in the up half (a wave-uniform choice: the base is an SGPR pair)
+        if (TWAVES * 64 * c + 64 * __builtin_amdgcn_readfirstlane(wave) >= HALF * DWB) wb = W2;
+      copy4_to_lds(wb, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
+    }
     if constexpr (has_min<TYPE>()) {
       // block sums [SB][BM] of this token tile: S_CH chunks of 16 B, S_PW per
       // wave, copied by lanes 0 .. S_PW - 1 (one instruction per wave)
@@ -607,7 +622,8 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       load_a(j);
 #pragma unroll
       for (int n = 0; n < NT; n++) {
-        const int row = wn + 16 * n + ln;
+        // FFNP: group 2m is gate rows wn / 2 + 16 m.., group 2m + 1 the same up rows
+        const int row = FFNP ? ((n & 1) ? HALF : 0) + wn / 2 + 16 * (n >> 1) + ln : wn + 16 * n + ln;
         const uint8_t* rb = bslot + row * (DWB * 4) + j * TS;     // this block's bytes
         const uint16_t* r16 = reinterpret_cast<const uint16_t*>(rb);
         if constexpr (TYPE == wh::kGemmQ8H) {
@@ -725,6 +741,26 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     }
   }
 
+  if constexpr (FFNP) {
+    // h = silu(g) * u for the gate / up pairs, as (g * (1 / (1 + e^-g))) * u
+#pragma unroll
+    for (int i = 0; i < IT; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int t = t0 + wm + 16 * i + 4 * g + r;
+        if (t >= n_tokens) continue;
+        const float sc = rscale[t];
+#pragma unroll
+        for (int m = 0; m < NT / 2; m++) {
+          const int col = r0 + wn / 2 + 16 * m + ln;
+          if (col >= n_rows) continue;
+          const float gv = acc[i][2 * m][r] * sc, uv = acc[i][2 * m + 1][r] * sc;
+          y[static_cast<size_t>(t) * n_rows + col] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
+        }
+      }
+    }
+    return;
+  }
   // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
   float* out = y + static_cast<size_t>(blockIdx.y) * n_tokens * n_rows;
 #pragma unroll
@@ -770,11 +806,39 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
-  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, frag, rs, bs, dmin, part, static_cast<int>(n_tokens),
-                                                           static_cast<int>(n_rows), nb, bps, tiles_n,
-                                                           tiles_m * tiles_n);
+  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
+                                                           static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
+                                                           bps, tiles_n, tiles_m * tiles_n);
   WH_LAUNCH_CHECK("tiled gemm kernel launch");
   return WH_OK;
+}
+
+// The FFN's gate and up (n_ff rows each) in one pass: h = silu(gate x) * (up x).
+template <int TYPE, int BM>
+int launch_ffn_bm(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k, size_t n_tokens,
+                  const _Float16* frag, const float* rs, const float* bs, float* h, hipStream_t s) {
+  const int nb = static_cast<int>(k / 32);
+  const int tiles_n = static_cast<int>((n_ff + TBN / 2 - 1) / (TBN / 2));
+  const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
+  const size_t lds = tiled_lds_bytes<TYPE, BM>();
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM, true>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  gemm_tiled_kernel<TYPE, BM, true><<<static_cast<unsigned>(tiles_m * tiles_n), TWAVES * 64, lds, s>>>(
+      gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
+      tiles_m * tiles_n);
+  WH_LAUNCH_CHECK("tiled ffn gate/up kernel launch");
+  return WH_OK;
+}
+
+template <int TYPE>
+int launch_ffn_typed(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k, size_t n_tokens,
+                     const _Float16* frag, const float* rs, const float* bs, float* h, hipStream_t s) {
+  switch (tile_bm(n_tokens)) {
+    case 16: return launch_ffn_bm<TYPE, 16>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
+    case 32: return launch_ffn_bm<TYPE, 32>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
+    case 64: return launch_ffn_bm<TYPE, 64>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
+    default: return launch_ffn_bm<TYPE, 128>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
+  }
 }
 
 template <int TYPE>
@@ -1032,11 +1096,24 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
     return WH_ERR_INVALID_SHAPE;
   const TiledWs t1 = tiled_ws(type, n_ff, hidden, n_tokens, workspace);
   int st = tiled_pack<kPackNorm>(type, t1, x, nullptr, gamma, eps, n_tokens, hidden, hidden, s);
-  if (!st) st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s);
-  if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s);
   if (st) return st;
   const TiledWs t2 = tiled_ws(type, hidden, n_ff, n_tokens, workspace);
-  st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
+  if (gemm_tiled_splits(2 * n_ff, n_tokens, hidden) == 1) {
+    // enough tiles without split-K: gate and up in one pass, h = silu(g) * u
+    // written by its epilogue (g holds h), then packed for the down projection
+    const uint8_t* gp = static_cast<const uint8_t*>(gate);
+    const uint8_t* upp = static_cast<const uint8_t*>(up);
+    switch (type) {
+      case WH_TYPE_Q4_0: st = launch_ffn_typed<WH_TYPE_Q4_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
+      case WH_TYPE_Q4_1: st = launch_ffn_typed<WH_TYPE_Q4_1>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
+      default: st = launch_ffn_typed<WH_TYPE_Q8_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
+    }
+    if (!st) st = tiled_pack<kPackPlain>(type, t2, g, nullptr, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
+  } else {
+    st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s);
+    if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s);
+    if (!st) st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
+  }
   if (st) return st;
   return tiled_run(type, down, hidden, n_ff, n_tokens, t2, out, s);
 }
