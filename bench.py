@@ -328,6 +328,55 @@ def bench_decode(steps: int, c: dict = L8B, types: dict | None = None, head_type
             "ctx": c["ctx"], "layers": c["n_layers"], "logits_finite": bool(np.all(np.isfinite(logits)))}
 
 
+def bench_attention(iters: int, c: dict = L8B) -> dict:
+    """Decode attention alone (wh_attention_decode: the partial and combine
+    kernels) at the config-4 shape, position ctx - 1, over copies of the f16
+    KV cache rotated so that more than 256 MB (the Infinity Cache) is in
+    rotation; calls captured into a HIP graph and replayed.  Returns µs per
+    call and the cache bytes read per call (2 ctx n_kv_heads head_dim 2)."""
+    from woolly_amd import ops
+    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+
+    nh, nkv, d, ctx = c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ctx"]
+    rng = np.random.default_rng(8)
+    kc = rng.standard_normal((ctx, nkv, d)).astype(np.float16)
+    vc = rng.standard_normal((ctx, nkv, d)).astype(np.float16)
+    nbytes = kc.nbytes + vc.nbytes
+    reps = max(1, -(-300_000_000 // nbytes))
+    kbs = [DeviceBuffer.from_array(kc) for _ in range(reps)]
+    vbs = [DeviceBuffer.from_array(vc) for _ in range(reps)]
+    qkv = DeviceBuffer.from_array(rng.standard_normal((nh + 2 * nkv) * d).astype(np.float32))
+    inv = DeviceBuffer.from_array(ops.rope_inv_freq(c["rope_base"], d))
+    out = DeviceBuffer(4 * nh * d)
+    wsz = ops.attention_workspace_bytes(nh, nkv, d, ctx)
+    ws = DeviceBuffer(wsz)
+    stream = Stream()
+    pos = ctx - 1
+
+    def run(i):
+        ops.attention_decode(qkv, kbs[i % reps], vbs[i % reps], pos, nh, nkv, d, inv, out, ws, wsz, stream)
+
+    for i in range(reps):
+        run(i)
+    stream.synchronize()
+    with Graph.capture(stream) as graph:
+        for i in range(iters):
+            run(i)
+    graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    res = []
+    for _ in range(5):
+        e0.record(stream)
+        graph.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        res.append(e0.elapsed_ms(e1) / iters)
+    graph.destroy()
+    ms = float(np.median(res))
+    return {"us": round(ms * 1e3, 3), "kv_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "ctx": ctx}
+
+
 def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N_ROWS, k: int = K,
                        replicas: int = REPLICAS) -> float:
     """The read floor of the headline GEMV's access pattern (wh_read_probe): the
@@ -509,7 +558,8 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other decode GEMV configurations (4096x4096 Q4_0, Q8_0, Q4_1)")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-4 decode step")
-    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "ffn", "gemm", "decode", "decode_q4_k_m"],
+    ap.add_argument("--only", choices=["gemv", "ffn1", "ffn512", "ffn", "gemm", "decode", "decode_q4_k_m",
+                                       "attention"],
                     default=None,
                     help="run one leg only (for profiling); prints that leg's timing")
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm / --only ffn")
@@ -550,6 +600,9 @@ def main() -> int:
         return 0
     if args.only == "decode":
         print(json.dumps({"decode_step": bench_decode(10)}))
+        return 0
+    if args.only == "attention":
+        print(json.dumps({"attention_decode": bench_attention(64)}))
         return 0
     if args.only == "decode_q4_k_m":
         print(json.dumps({"decode_step_q4_k_m": bench_decode(10, types=Q4_K_M, head_type=14)}))
@@ -640,8 +693,11 @@ def main() -> int:
                               "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t)}
             log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
 
-    decode = decode_km = None
+    decode = decode_km = attn = None
     if not args.no_decode:
+        attn = bench_attention(64)
+        log(f"[bench] decode attention (config 4 shape, ctx {attn['ctx']}): {attn['us']} us, {attn['GBps']} GB/s "
+            f"over the {attn['kv_bytes']} cache bytes")
         decode = bench_decode(20)
         log(f"[bench] decode step (config 4, ctx {decode['ctx']}): {decode['ms_per_token']} ms/token, "
             f"{decode['tokens_per_s']} tokens/s, {decode['GBps']} GB/s")
@@ -695,6 +751,7 @@ def main() -> int:
         "gemv_other_configs": gemv_cfg or None,
         "decode_step_llama3_8b_q4_0": decode,
         "decode_step_llama3_8b_q4_k_m": decode_km,
+        "decode_attention_llama3_8b_ctx4096": attn,
         "cpu_baseline": cpu,
         "cpu_baseline_scalar": cpu_scalar,
     }
