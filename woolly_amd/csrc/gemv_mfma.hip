@@ -314,20 +314,28 @@ __device__ __forceinline__ int mg_dpp(int v) {
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141, kDppMirror = 0x140;  // lane i <-> 7 - i (of 8), 15 - i (of 16)
 
-// Maximum of v over the 64 lanes (exact: max does not depend on the order).
-__device__ __forceinline__ float mg_wave_max(float v) {
-  auto step = [](float x, int y) { return fmaxf(x, __builtin_bit_cast(float, y)); };
-  const int b = __builtin_bit_cast(int, v);
-  v = step(v, mg_dpp<kDppXor1>(b));
-  v = step(v, mg_dpp<kDppXor2>(__builtin_bit_cast(int, v)));
-  v = step(v, mg_dpp<kDppHalfMirror>(__builtin_bit_cast(int, v)));
-  v = step(v, mg_dpp<kDppMirror>(__builtin_bit_cast(int, v)));  // every lane: the max of its 16-lane row
-  const int vi = __builtin_bit_cast(int, v);
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+// Maximum of an unsigned integer over the 64 lanes, uniform: one DPP max per
+// step within rows of 16 lanes, then the four rows' maxima on the scalar unit.
+__device__ __forceinline__ uint32_t mg_wave_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(mg_dpp<kDppXor1>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(mg_dpp<kDppXor2>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(mg_dpp<kDppHalfMirror>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(mg_dpp<kDppMirror>(static_cast<int>(v))));
+  const int vi = static_cast<int>(v);
+  const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 0));
+  const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 16));
+  const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 32));
+  const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 48));
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// f32 -> i32 as v_cvt_i32_f32 converts (NaN -> 0, out of range -> clamped),
+// with no C++ undefined behaviour for such inputs: the limbs of a chunk that
+// takes the exact path are converted too (without a branch) and never read.
+__device__ __forceinline__ int mg_cvt_i32(float v) {
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
 }
 
 // Sum over each group of 8 lanes (lanes 8k .. 8k + 7) of two small integers
@@ -501,19 +509,18 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   bool exact[NSEG];
 #pragma unroll
   for (int seg = 0; seg < NSEG; seg++) {
-    float mx = 0.f;
-    bool fin = true;
+    // the chunk's largest |x| as the maximum of the bit patterns of |x| (they
+    // order like the values, and a NaN or an infinity lies above every finite
+    // value, which sends the chunk down the exact path)
+    uint32_t um = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      mx = fmaxf(mx, fabsf(xv[seg][i]));
-      fin = fin && __builtin_isfinite(xv[seg][i]);  // fmaxf drops NaN
-    }
-    exact[seg] = __any(!fin);
-    mx = mg_wave_max(mx);
+    for (int i = 0; i < 4; i++) um = max(um, __builtin_bit_cast(uint32_t, xv[seg][i]) & 0x7FFFFFFFu);
+    um = mg_wave_max_u32(um);
+    exact[seg] = um >= 0x7F800000u;
     int e = 0;
-    if (mx > 0.f && !exact[seg]) {
+    if (um != 0u && !exact[seg]) {
       int ee;
-      frexpf(mx, &ee);
+      frexpf(__builtin_bit_cast(float, um), &ee);
       e = 30 - ee;
     }
     ex[seg] = e;
@@ -527,8 +534,8 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       // |x * 2^e| < 2^30: the conversion is exact for the chunk's larger elements
-      const int xi = exact[seg] ? 0 : static_cast<int>(rintf(ldexpf(xv[seg][i], e)));
-      z[i] = static_cast<uint32_t>(xi + 0x808080) ^ 0x808080u;
+      const int xi = mg_cvt_i32(rintf(ldexpf(xv[seg][i], e)));
+      z[i] = (static_cast<uint32_t>(xi) + 0x808080u) ^ 0x808080u;
     }
     // the lane's four elements feed four consecutive k-slots (all but Q4_K):
     // transpose the 4 x 4 bytes so that row[r] holds limb r of elements 0..3
@@ -947,19 +954,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
     for (int t = 0; t < MT; t++) {
       const float4 v = xnorm(t, seg);
       const float xv[4] = {v.x, v.y, v.z, v.w};
-      float mx = 0.f;
-      bool fin = true;
+      // the largest |x| as the maximum of the bit patterns of |x| (inf / NaN above every finite value)
+      uint32_t um = 0u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        mx = fmaxf(mx, fabsf(xv[i]));
-        fin = fin && __builtin_isfinite(xv[i]);
-      }
-      const bool exact = __any(!fin);
-      mx = mg_wave_max(mx);
+      for (int i = 0; i < 4; i++) um = max(um, __builtin_bit_cast(uint32_t, xv[i]) & 0x7FFFFFFFu);
+      um = mg_wave_max_u32(um);
+      const bool exact = um >= 0x7F800000u;
       int e = 0;
-      if (mx > 0.f && !exact) {
+      if (um != 0u && !exact) {
         int ee;
-        frexpf(mx, &ee);
+        frexpf(__builtin_bit_cast(float, um), &ee);
         e = 30 - ee;
       }
       ex_u[seg][t] = __builtin_amdgcn_readfirstlane(e);
