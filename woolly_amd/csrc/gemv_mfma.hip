@@ -338,14 +338,6 @@ __device__ __forceinline__ int mg_cvt_i32(float v) {
   return r;
 }
 
-// Sum over each group of 8 lanes (lanes 8k .. 8k + 7) of two small integers
-// packed as 16-bit fields, each in [0, 8192) after the sum (no carries).
-__device__ __forceinline__ int mg_sum8_packed(int v) {
-  v += mg_dpp<kDppXor1>(v);
-  v += mg_dpp<kDppXor2>(v);
-  return v + mg_dpp<kDppHalfMirror>(v);
-}
-
 // Sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) in every
 // lane, as (v[l] + v[l ^ 16]) + (v[l ^ 32] + v[l ^ 48]), with gfx950's
 // v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Inline asm
@@ -525,7 +517,6 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
     }
     ex[seg] = e;
     int8_t* xop = reinterpret_cast<int8_t*>(stage + seg * STG);
-    int* bs_lds = reinterpret_cast<int*>(stage + seg * STG + 8 * kMgLimbBytes);
     // Signed base-256 digits of xi = 2^24 l0 + 2^16 l1 + 2^8 l2 + l3 (l1..l3
     // in [-128, 127]): adding 128 to each of the three low digits makes them
     // bytes without carries, so the bytes of (xi + 0x808080) ^ 0x808080 are
@@ -562,20 +553,6 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
 #pragma unroll
       for (int r = 0; r < 4; r++) *reinterpret_cast<uint32_t*>(pb + 32 * r) = row[r];
     }
-    int bs[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) bs[r] = __builtin_amdgcn_sdot4(static_cast<int>(row[r]), 0x01010101, 0, false);
-    // a block is 8 consecutive lanes (Q6_K needs no sums: its bias is in the quants)
-    if constexpr (!Q6K) {
-      // per lane each sum lies in [-512, 512): biased by 512, two per dword
-      const int p01 = mg_sum8_packed((bs[0] + 512) | ((bs[1] + 512) << 16));
-      const int p23 = mg_sum8_packed((bs[2] + 512) | ((bs[3] + 512) << 16));
-      bs[0] = (p01 & 0xFFFF) - 8 * 512;
-      bs[1] = (p01 >> 16) - 8 * 512;
-      bs[2] = (p23 & 0xFFFF) - 8 * 512;
-      bs[3] = (p23 >> 16) - 8 * 512;
-      if ((lane & 7) == 0) *reinterpret_cast<int4*>(bs_lds + 4 * (lane >> 3)) = make_int4(bs[0], bs[1], bs[2], bs[3]);
-    }
   }
   if (res_reg && static_cast<int>(threadIdx.x) < r1 - r0) rows_lds[threadIdx.x] = resv;
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -585,12 +562,11 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   long xo[8];
   mg_v4i cin[2];  // Q4_0: -8 * limb sums of block 4t + g (accumulator input)
   mg_v4i cq[Q6K ? 4 : 1];  // Q6_K: -32 * limb sums of 16-element group 4t + g
-  float bsum[2];  // Q4_1: sum of the block's activations, in units of 2^-e
+  float bsum[2];  // Q4_1 / Q4_K: sum of the block's activations, in units of 2^-e
 #pragma unroll
   for (int lb = 0; lb < 8; lb++) xo[lb] = 0;
   auto get_x = [&](int seg) {
     const int8_t* xop = reinterpret_cast<const int8_t*>(stage + seg * STG);
-    const int* bs_lds = reinterpret_cast<const int*>(stage + seg * STG + 8 * kMgLimbBytes);
 #pragma unroll
     for (int lb = 0; lb < 8; lb++) {
       // Q6_K: rows 8 (lb & 1) + 4 h + limb carry half h of block lb (k groups 2h, 2h + 1)
@@ -607,14 +583,28 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
         cq[lb >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[lb], static_cast<long>(0xE0E0E0E0E0E0E0E0ull), cq[lb >> 1], 0, 0, 0);
       return;
     }
+    // Limb sums of each block, the same for every weight row: MFMAs of the
+    // blocks' A operands against a B operand of equal bytes, so lane (n, g)'s
+    // accumulator t holds (times the byte) the sums of limbs 0..3 of block
+    // 4t + g.  Q4_0: -8 times them start its accumulators; Q4_1 / Q4_K: their
+    // base-256 combination is the block's activation sum.
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-      const int4 v = *reinterpret_cast<const int4*>(bs_lds + 4 * (4 * t + g));
-      if constexpr (TYPE == WH_TYPE_Q4_0) cin[t] = (mg_v4i){-8 * v.x, -8 * v.y, -8 * v.z, -8 * v.w};
-      else cin[t] = (mg_v4i){0, 0, 0, 0};
-      bsum[t] = __builtin_fmaf(static_cast<float>(v.x), 16777216.f,
-                               __builtin_fmaf(static_cast<float>(v.y), 65536.f,
-                                              __builtin_fmaf(static_cast<float>(v.z), 256.f, static_cast<float>(v.w))));
+      cin[t] = (mg_v4i){0, 0, 0, 0};
+      bsum[t] = 0.f;
+      if constexpr (TYPE == WH_TYPE_Q4_0) {
+#pragma unroll
+        for (int lb = 4 * t; lb < 4 * t + 4; lb++)
+          cin[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[lb], static_cast<long>(0xF8F8F8F8F8F8F8F8ull), cin[t], 0, 0, 0);
+      } else if constexpr (Q41 || Q4K) {
+        mg_v4i v = {0, 0, 0, 0};
+#pragma unroll
+        for (int lb = 4 * t; lb < 4 * t + 4; lb++)
+          v = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo[lb], static_cast<long>(0x0101010101010101ull), v, 0, 0, 0);
+        bsum[t] = __builtin_fmaf(static_cast<float>(v[0]), 16777216.f,
+                                 __builtin_fmaf(static_cast<float>(v[1]), 65536.f,
+                                                __builtin_fmaf(static_cast<float>(v[2]), 256.f, static_cast<float>(v[3]))));
+      }
     }
   };
   if constexpr (NSEG == 1) get_x(0);
