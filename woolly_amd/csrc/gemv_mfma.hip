@@ -471,6 +471,16 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   // Nothing that waits for x may be scheduled above the weight loads: the
   // first step's weights must be requested before x's latency is waited out.
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NSEG == 1) {
+    // No wave starts the VALU-heavy prologue below before every wave has
+    // requested its first weights (a barrier without a memory wait): the
+    // oldest-first issue order otherwise lets the prologues of a SIMD's older
+    // waves hold back the youngest wave's loads, whose data then lands last.
+    // (Rows of several segments request four times the activations first and
+    // lose more waiting here than they gain.)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   float rms = 1.f;
   if constexpr (NORM) {
