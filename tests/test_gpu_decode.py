@@ -69,6 +69,39 @@ def test_attention_qkv_fused(gpu, orc, t, hidden, q_rows, kv_rows):
     check(got, ref, f"qkv t={t} {hidden}")
 
 
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_attention_qkv_nonfinite(gpu, orc, bad):
+    """One inf or NaN in x: rms_norm's rms is then inf or NaN, x_hat is NaN at
+    that element (inf / inf, NaN) and 0 or NaN elsewhere, so every projection
+    is NaN in the reference (tensor_utils.rs:446-480 followed by the matvec);
+    the fused kernel (W (x * gamma)) / rms gives NaN everywhere as well.  A
+    finite x whose squares overflow (rms = inf) gives x_hat = 0 and zeros."""
+    hidden, q_rows, kv_rows = 4096, 4096, 1024
+    print(f"[case] qkv nonfinite {bad}", flush=True)
+    ws = [synth.quantized_weight(Q4_0, n, hidden, seed=30 + i) for i, n in enumerate((q_rows, kv_rows, kv_rows))]
+    g = (1 + 0.1 * np.random.default_rng(5).standard_normal(hidden)).astype(np.float32)
+    wb = [up(w)[0] for w in ws]
+    gb = up(g)[0]
+    out = DeviceBuffer(4 * (q_rows + 2 * kv_rows))
+    wsb = DeviceBuffer(ops.attention_qkv_workspace_bytes(hidden))
+    x = synth.activations(hidden, seed=6)
+    x[1234] = bad
+    ops.attention_qkv(Q4_0, *wb, q_rows, kv_rows, hidden, gb, 1e-5, up(x)[0], out, wsb,
+                      ops.attention_qkv_workspace_bytes(hidden))
+    got = down(out, np.float32, q_rows + 2 * kv_rows)
+    xn = np.zeros((1, hidden))
+    orc.lib.orc_rms_norm_f64(x.ctypes.data, g.ctypes.data, 1e-5, 1, hidden, xn.ctypes.data)
+    ref = np.concatenate([orc.matvec_f64(Q4_0, w, xn.astype(np.float32).ravel(), n, hidden)[1]
+                          for w, n in zip(ws, (q_rows, kv_rows, kv_rows))])
+    assert np.all(np.isnan(ref)) and np.all(np.isnan(got))
+    # squares that overflow f32 (|x| ~ 1e30): rms = inf in f32, x_hat = 0
+    big = (synth.activations(hidden, seed=7) * np.float32(1e30)).astype(np.float32)
+    ops.attention_qkv(Q4_0, *wb, q_rows, kv_rows, hidden, gb, 1e-5, up(big)[0], out, wsb,
+                      ops.attention_qkv_workspace_bytes(hidden))
+    got = down(out, np.float32, q_rows + 2 * kv_rows)
+    assert np.all(got == 0.0)
+
+
 @pytest.mark.parametrize("t", [Q4_0, Q8_0])
 @pytest.mark.parametrize("m,k", [(4096, 4096), (4096, 14336), (300, 96)])
 def test_matvec_residual_in_place(gpu, orc, t, m, k):

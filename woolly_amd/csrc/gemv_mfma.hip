@@ -482,9 +482,14 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  float rms = 1.f;
   if constexpr (NORM) {
-    // rms = sqrt(sum x^2 / K + eps), x_hat = (x / rms) * gamma (tensor_utils.rs:446-480)
+    // RMSNorm (tensor_utils.rs:446-480): W ((x / rms) * gamma) is formed as
+    // (W (x * gamma)) / rms, rms = sqrt(sum x^2 / K + eps).  The limbs are
+    // those of x * gamma; each wave's share of sum x^2 goes to LDS, and a
+    // row's product is divided by rms where the row is finished, after step
+    // barriers that have made every share visible, so the prologue needs no
+    // barrier of its own.  (Per element this differs from the reference's
+    // (x / rms) * gamma by its roundings only.)
     float ss = 0.f;
 #pragma unroll
     for (int seg = 0; seg < NSEG; seg++)
@@ -492,18 +497,12 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
       for (int i = 0; i < 4; i++) ss = __builtin_fmaf(xv[seg][i], xv[seg][i], ss);
     ss = whd::wave_sum(ss);
     if (lane == 0) misc[wave] = ss;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < kMgWaves; w++) tot += misc[w];
-    rms = sqrtf(tot / static_cast<float>(K) + a.eps);
 #pragma unroll
     for (int seg = 0; seg < NSEG; seg++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) xv[seg][i] = (xv[seg][i] / rms) * gv[seg][i];
+      for (int i = 0; i < 4; i++) xv[seg][i] *= gv[seg][i];
   }
+
 
   // ---- limbs of each chunk -> this wave's staging area (the MFMA A operands are
   // read from it: the lanes of rows 4j..4j+3 of block j's operand, zeros elsewhere)
@@ -620,14 +619,14 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   if constexpr (NSEG == 1) get_x(0);
 
   // Elements 64 g + 4 jj .. + 3 of this wave's chunk of segment seg (the
-  // activations of the exact path, normalised like the limbs), read again from
+  // activations of the exact path, times gamma like the limbs), read again from
   // x (and gamma) so that no register holds the activations past the limbs.
   auto xquad = [&](int seg, int jj) -> float4 {
     const int el = (seg * S + 4 * wave) * 64 + 64 * g + 4 * jj;
     float4 v = *reinterpret_cast<const float4*>(a.x + el);
     if constexpr (NORM) {
       const float4 gm = *reinterpret_cast<const float4*>(a.gamma + el);
-      v = make_float4((v.x / rms) * gm.x, (v.y / rms) * gm.y, (v.z / rms) * gm.z, (v.w / rms) * gm.w);
+      v = make_float4(v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w);
     }
     return v;
   };
@@ -639,8 +638,15 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   auto finish = [&](int q) {
     const float* pp = part + (q & 1) * kMgWaves * 16 + 64 * g + n;
     const float v0 = pp[0], v1 = pp[16], v2 = pp[32], v3 = pp[48];
-    const float v = mg_sum_lane_groups((v0 + v1) + (v2 + v3));
+    float v = mg_sum_lane_groups((v0 + v1) + (v2 + v3));
     if (lane >= 16) return;
+    if constexpr (NORM) {
+      // the waves' shares of sum x^2, in fixed order
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMgWaves; w++) tot += misc[w];
+      v = v / sqrtf(tot / static_cast<float>(K) + a.eps);
+    }
     const int gi = FFN ? (q >> 1) : q;
     const int row = r0 + 16 * gi + n;
     if constexpr (FFN) {
