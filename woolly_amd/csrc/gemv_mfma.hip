@@ -890,23 +890,55 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
     if (t >= M || !owns) return make_float4(0.f, 0.f, 0.f, 0.f);
     return *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + (seg * S + 4 * wave) * 64 + 4 * lane);
   };
+  // The same as a buffer load whose range is empty for a token slot past M or
+  // a wave without a chunk (zeros, no memory access): no branch around the
+  // load, which would make the compiler wait for every load in flight where
+  // the branches join.
+  auto xload_nb = [&](int t, int seg) -> float4 {
+    const bool ok = t < M && owns;
+    const mg_v4i rs = mg_rsrc(a.x + (ok ? static_cast<size_t>(t) * K + (seg * S + 4 * wave) * 64 : static_cast<size_t>(0)),
+                              ok ? 1024u : 0u);
+    return __builtin_bit_cast(float4, mg_buffer_load_x4(rs, 16 * lane, 0, 0));
+  };
 
-  // ---- each token's RMSNorm scale (a workgroup reduction of sum x^2)
-  float rms[MT];
+  // XPRE (up to 8 chunks per wave, 4 with the longest rows, whose four loads
+  // per step leave fewer registers): every chunk's activations are requested
+  // first and kept in registers, then the first weights, so that neither the
+  // RMSNorm reduction nor the limbs wait for the weights (loads complete in
+  // order); with more chunks the activations are read where they are used and
+  // the weights are requested after the RMSNorm's barrier.
+  constexpr bool XPRE = MT * NSEG * (NL >= 4 ? 2 : 1) <= 8;
+  float4 xr[XPRE ? NSEG : 1][XPRE ? MT : 1];
+  auto xget = [&](int t, int seg) -> float4 {
+    if constexpr (XPRE) return xr[seg][t];
+    else return xload(t, seg);
+  };
   float4 gv[NSEG];
-#pragma unroll
-  for (int t = 0; t < MT; t++) rms[t] = 1.f;
   if constexpr (NORM) {
 #pragma unroll
     for (int seg = 0; seg < NSEG; seg++)
       gv[seg] = owns ? *reinterpret_cast<const float4*>(a.gamma + (seg * S + 4 * wave) * 64 + 4 * lane)
                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if constexpr (XPRE) {
+#pragma unroll
+    for (int seg = 0; seg < (XPRE ? NSEG : 0); seg++)
+#pragma unroll
+      for (int t = 0; t < (XPRE ? MT : 0); t++) xr[seg][t] = xload_nb(t, seg);
+    load(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // ---- each token's RMSNorm scale (a workgroup reduction of sum x^2)
+  float rms[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) rms[t] = 1.f;
+  if constexpr (NORM) {
 #pragma unroll
     for (int t = 0; t < MT; t++) {
       float ss = 0.f;
 #pragma unroll
       for (int seg = 0; seg < NSEG; seg++) {
-        const float4 v = xload(t, seg);
+        const float4 v = xget(t, seg);
         ss = __builtin_fmaf(v.x, v.x, ss);
         ss = __builtin_fmaf(v.y, v.y, ss);
         ss = __builtin_fmaf(v.z, v.z, ss);
@@ -928,7 +960,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
     if (threadIdx.x < MT) rms_lds[threadIdx.x] = rms[threadIdx.x];
   }
   for (int i = threadIdx.x; i < MT * R; i += kMgWaves * 64) rows_lds[i] = 0.f;
-  load(0, 0);
+  if constexpr (!XPRE) load(0, 0);
 
   // ---- limbs of every (segment, token) chunk -> A operands in registers
   // two-token layout: a lane's rows belong to the even blocks (n < 8) or the
@@ -944,7 +976,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
 #pragma unroll
       for (int b = 0; b < NA; b++) xa[seg][tg][b] = 0;
   auto xnorm = [&](int t, int seg) -> float4 {
-    float4 v = xload(t, seg);
+    float4 v = xget(t, seg);
     if constexpr (NORM) {
       v.x = (v.x / rms[t]) * gv[seg].x;
       v.y = (v.y / rms[t]) * gv[seg].y;
