@@ -928,10 +928,10 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
     load(0, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // ---- each token's RMSNorm scale (a workgroup reduction of sum x^2)
-  float rms[MT];
-#pragma unroll
-  for (int t = 0; t < MT; t++) rms[t] = 1.f;
+  // ---- RMSNorm (tensor_utils.rs:446-480) as (W (x * gamma)) / rms per token:
+  // each wave's share of every token's sum x^2 goes to LDS here; wave 0 forms
+  // the tokens' rms after the first step's barrier, and a token's rows are
+  // divided by its rms where they are finished (no barrier in the prologue).
   if constexpr (NORM) {
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -947,17 +947,6 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
       ss = whd::wave_sum(ss);
       if (lane == 0) misc[wave * MT + t] = ss;
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      float tot = 0.f;
-#pragma unroll
-      for (int w = 0; w < kMgWaves; w++) tot += misc[w * MT + t];
-      rms[t] = sqrtf(tot / static_cast<float>(K) + a.eps);
-    }
-    if (threadIdx.x < MT) rms_lds[threadIdx.x] = rms[threadIdx.x];
   }
   for (int i = threadIdx.x; i < MT * R; i += kMgWaves * 64) rows_lds[i] = 0.f;
   if constexpr (!XPRE) load(0, 0);
@@ -978,10 +967,10 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
   auto xnorm = [&](int t, int seg) -> float4 {
     float4 v = xget(t, seg);
     if constexpr (NORM) {
-      v.x = (v.x / rms[t]) * gv[seg].x;
-      v.y = (v.y / rms[t]) * gv[seg].y;
-      v.z = (v.z / rms[t]) * gv[seg].z;
-      v.w = (v.w / rms[t]) * gv[seg].w;
+      v.x *= gv[seg].x;
+      v.y *= gv[seg].y;
+      v.z *= gv[seg].z;
+      v.w *= gv[seg].w;
     }
     return v;
   };
@@ -1086,6 +1075,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kMgWaves; w++) v += pp[w * MT * 16];
+      if constexpr (NORM) v = v / rms_lds[t];
       if constexpr (FFN) {
         if ((q & 1) == 0) {
           misc[t * 16 + n] = v;  // gate, combined with up one group later
@@ -1121,6 +1111,17 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      if constexpr (NORM) {
+        // every wave's shares of sum x^2 are visible (the step barrier); the
+        // first finish, and the first gate value written over them, come after
+        // the next barrier
+        if (q == 0 && seg == 0 && wave == 0 && lane < MT) {
+          float tot = 0.f;
+#pragma unroll
+          for (int w = 0; w < kMgWaves; w++) tot += misc[w * MT + lane];
+          rms_lds[lane] = sqrtf(tot / static_cast<float>(K) + a.eps);
+        }
+      }
       if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
       if (owns) {
         const uint8_t* rowp = slot + n * rstr + wave * CB;
@@ -1156,7 +1157,6 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
         for (uint32_t em = exact_u[seg]; em != 0u; em &= em - 1u) {
           const int t = __builtin_ctz(em);
           if (g != (MS == 4 ? (t & 3) : t)) continue;
-          const float rt = NORM ? rms_lds[t] : 1.f;
           float sx = 0.f;
 #pragma unroll 1
           for (int p = 0; p < 4; p++)
@@ -1165,7 +1165,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
               float4 v = *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + el);
               if constexpr (NORM) {
                 const float4 gm = *reinterpret_cast<const float4*>(a.gamma + el);
-                v = make_float4((v.x / rt) * gm.x, (v.y / rt) * gm.y, (v.z / rt) * gm.z, (v.w / rt) * gm.w);
+                v = make_float4(v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w);
               }
               return v;
             });
