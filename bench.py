@@ -577,7 +577,7 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the path is single-GPU; it would shard by output rows, one GPU per row block)", file=sys.stderr)
         return 2
 
     from woolly_amd import device

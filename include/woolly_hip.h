@@ -199,8 +199,8 @@ WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbyt
 
 /* The same product with the activations given as x_dtype: WH_TYPE_F32 (as
  * wh_quantized_matmul) or WH_TYPE_BF16 (X row-major [n_tokens][k] bfloat16,
- * 8-byte aligned), the activation type config 2 of the benchmark names
- * ("f32/bf16"; SURVEY's wh_qgemm(.., X, x_dtype, ..)).  bf16 values are
+ * 8-byte aligned), the activation types of the prefill benchmark configuration
+ * ("f32/bf16", a wh_qgemm(.., X, x_dtype, ..) signature).  bf16 values are
  * widened exactly to f32, so the result equals wh_quantized_matmul on the
  * widened X.  The workspace (wh_quantized_matmul_x_workspace_bytes) is needed
  * for bf16 at any token count; WH_ERR_UNSUPPORTED_TYPE for another x_dtype. */
