@@ -98,3 +98,30 @@ def test_mt_ffn_parity(gpu, orc, t, hidden, n_ff, m):
     r, a = rel_l2(got, ref), max_abs(got, ref)
     report(f"mt ffn t={t} {hidden}/{n_ff} m={m}", r, a, ref)
     assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
+@pytest.mark.parametrize("bad", [np.inf, np.nan])
+def test_mt_ffn_nonfinite_token(gpu, orc, bad):
+    """One token's x holds an inf or a NaN: its RMSNorm scale is inf / NaN, so
+    the reference's x_hat is NaN there and every output of that token is NaN;
+    the fused kernels divide each token's rows by its own rms at the finish, so
+    the other tokens of the same group stay within the bars."""
+    t, hidden, n_ff, m = Q4_0, 4096, 1024, 4
+    print(f"[case] mt ffn nonfinite {bad}", flush=True)
+    L = synth.ffn_layer(t, hidden, n_ff, m, seed=77)
+    L["x"] = L["x"].copy()
+    L["x"].reshape(m, hidden)[1, 1234] = bad
+    bufs = {key: up(v) for key, v in L.items()}
+    ob = DeviceBuffer(4 * m * hidden)
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, m)
+    ws = DeviceBuffer(wsz)
+    ops.ffn_swiglu(t, bufs["gate"][1], bufs["up"][1], bufs["down"][1], hidden, n_ff,
+                   bufs["gamma"][1], 1e-5, bufs["x"][1], m, ob.ptr, ws.ptr, wsz)
+    got = down(ob, np.float32, m * hidden).reshape(m, hidden)
+    ref = orc.ffn_rows_f64(t, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5,
+                           L["x"], np.arange(m))
+    assert np.all(np.isnan(ref[1])) and np.all(np.isnan(got[1]))
+    ok = [0, 2, 3]
+    r, a = rel_l2(got[ok], ref[ok]), max_abs(got[ok], ref[ok])
+    report(f"mt ffn nonfinite {bad}", r, a, ref[ok])
+    assert r <= REL_L2 and a <= max_abs_bar(ref[ok])
