@@ -527,62 +527,67 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 }
 
 // out[h][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c.
-// One pass: a workgroup covers 64 dims of one head with four chunk groups (one
-// wave each, chunks grp, grp + 4, ...); every lane loads kBatch chunks' (m, l,
-// acc[d]) at once and merges them into its running (M, L, A) in chunk order
-// (M' = max(M, m_c), L' = L e^{M - M'} + l_c e^{m_c - M'}, likewise A), then
-// the four groups merge the same way in fixed order through LDS.
-constexpr int kCombDims = 64, kCombGroups = kAttnThreads / kCombDims;
-__device__ __forceinline__ void softmax_merge(float& M, float& L, float& A, float m, float l, float a) {
-  const float mn = fmaxf(M, m);
-  const float so = expf(M - mn), sn = expf(m - mn);
-  L = __builtin_fmaf(L, so, l * sn);
-  A = __builtin_fmaf(A, so, a * sn);
-  M = mn;
+// A workgroup covers 64 dims of one head.  Every wave loads (m, l) of chunks
+// lane, lane + 64, ... and this wave's 16 accumulators of the first 64 chunks
+// (chunks 4 i + wave, i < 16: one 256-byte row per load) in one burst, forms
+// M with a wave maximum, one weight e^{m_c - M} per lane and L with a wave sum
+// (fixed order), then sums w_c acc_c[d] over its chunks with the weights read
+// across lanes; contexts of more than 64 chunks repeat the accumulation per 64.
+// The four waves' sums add in fixed order through LDS.  A chunk whose m is
+// -inf gets weight 0; NaN anywhere makes the head NaN, as a softmax over the
+// positions does.
+constexpr int kCombDims = 64, kCombPer = 16;
+__device__ __forceinline__ float at_rl(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                     float* __restrict__ out, int n_chunks) {
-  __shared__ float sm[kCombGroups][kCombDims], sl[kCombGroups][kCombDims], sa[kCombGroups][kCombDims];
-  const int h = blockIdx.x, lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  __shared__ float sacc[kAttnThreads / 64][kCombDims];
+  const int h = blockIdx.x, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int d = blockIdx.y * kCombDims + lane;
-  const float* ph = part + static_cast<size_t>(h) * n_chunks * (D + 2);
-  constexpr int kBatch = 16;
-  float M = -INFINITY, L = 0.f, A = 0.f;
-  bool any = false;
-  for (int c0 = grp; c0 < n_chunks; c0 += kBatch * kCombGroups) {
-    float mv[kBatch], lv[kBatch], av[kBatch];
+  constexpr int kStride = (D + 2) * 4;  // bytes per chunk record (m, l, acc[D])
+  const at_i4 rs = at_rsrc(part + static_cast<size_t>(h) * n_chunks * (D + 2),
+                           static_cast<uint32_t>(n_chunks) * kStride);
+  // first 64 chunks: (m, l) of chunk `lane`, then acc[d] of this wave's chunks
+  // (offsets past the head's records read 0)
+  const float m0 = __builtin_bit_cast(float, at_buffer_load_x1(rs, lane * kStride, 0, 0));
+  const float l0 = __builtin_bit_cast(float, at_buffer_load_x1(rs, lane * kStride + 4, 0, 0));
+  float av[kCombPer];
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      const int c = c0 + b * kCombGroups;
-      const float* pc = ph + static_cast<size_t>(c < n_chunks ? c : 0) * (D + 2);
-      mv[b] = pc[0];
-      lv[b] = pc[1];
-      av[b] = pc[2 + d];
-    }
+  for (int i = 0; i < kCombPer; i++)
+    av[i] = __builtin_bit_cast(float, at_buffer_load_x1(rs, (4 * i + wave) * kStride + 8 + 4 * d, 0, 0));
+  float mx = lane < n_chunks ? m0 : -INFINITY;
+  for (int c = lane + 64; c < n_chunks; c += 64)
+    mx = fmaxf(mx, __builtin_bit_cast(float, at_buffer_load_x1(rs, c * kStride, 0, 0)));
+  mx = at_row_max(mx);
+  const float M = fmaxf(fmaxf(at_rl(mx, 0), at_rl(mx, 16)),
+                        fmaxf(at_rl(mx, 32), at_rl(mx, 48)));
+  float w = lane < n_chunks ? expf(m0 - M) : 0.f;
+  float lp = w * l0;
+  float a = 0.f;
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      if (c0 + b * kCombGroups >= n_chunks) break;
-      if (!any) {
-        M = mv[b], L = lv[b], A = av[b];
-        any = true;
-      } else {
-        softmax_merge(M, L, A, mv[b], lv[b], av[b]);
-      }
-    }
+  for (int i = 0; i < kCombPer; i++) a = __builtin_fmaf(at_rl(w, 4 * i + wave), av[i], a);
+  for (int c0 = 64; c0 < n_chunks; c0 += 64) {
+    const int c = c0 + lane;
+    const float mc = __builtin_bit_cast(float, at_buffer_load_x1(rs, c * kStride, 0, 0));
+    const float lc = __builtin_bit_cast(float, at_buffer_load_x1(rs, c * kStride + 4, 0, 0));
+#pragma unroll
+    for (int i = 0; i < kCombPer; i++)
+      av[i] = __builtin_bit_cast(float, at_buffer_load_x1(rs, (c0 + 4 * i + wave) * kStride + 8 + 4 * d, 0, 0));
+    w = c < n_chunks ? expf(mc - M) : 0.f;
+    lp = __builtin_fmaf(w, lc, lp);
+#pragma unroll
+    for (int i = 0; i < kCombPer; i++) a = __builtin_fmaf(at_rl(w, 4 * i + wave), av[i], a);
   }
-  sm[grp][lane] = M;
-  sl[grp][lane] = L;
-  sa[grp][lane] = A;
+  lp = at_row_sum(lp);
+  const float L = (at_rl(lp, 0) + at_rl(lp, 16)) +
+                  (at_rl(lp, 32) + at_rl(lp, 48));
+  sacc[wave][lane] = a;
   __syncthreads();
-  if (grp == 0) {
-    // groups with no chunk (n_chunks < 4) hold M = -inf and are skipped
-#pragma unroll
-    for (int g = 1; g < kCombGroups; g++)
-      if (g < n_chunks) softmax_merge(M, L, A, sm[g][lane], sl[g][lane], sa[g][lane]);
-    out[h * D + d] = A / L;
-  }
+  if (wave == 0) out[h * D + d] = ((sacc[0][lane] + sacc[1][lane]) + (sacc[2][lane] + sacc[3][lane])) / L;
 }
 
 // Positions per workgroup: enough chunks for about two workgroups per CU,
