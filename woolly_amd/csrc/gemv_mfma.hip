@@ -94,6 +94,9 @@ constexpr int kMgLimbBytes = 4 * 32;            // four limbs of one block
 // limb staging bytes per chunk: the limbs, then the limb sums of each
 // 32-element block
 constexpr int mg_stage_bytes(int type) { return 8 * kMgLimbBytes + (type == WH_TYPE_Q6_K ? 0 : 8 * 16); }
+// several-token kernel: the limbs of one chunk, or of both tokens' chunks in
+// the two-token layout
+constexpr int mt_stage_bytes(int type, int mt) { return mt == 2 ? 16 * kMgLimbBytes : mg_stage_bytes(type); }
 constexpr int kMgNt = 2;                       // streaming (non-temporal) loads
 constexpr int kMgNorm = 1, kMgFfn = 2;         // kernel variants
 constexpr int kMgDepth1 = 1;                   // steps in flight for one-segment rows
@@ -843,8 +846,8 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
   constexpr bool FFN = (MODE & kMgFfn) != 0;
   constexpr bool NORM = (MODE & kMgNorm) != 0;
   constexpr int CB = mg_chunk_bytes(TYPE);  // a multiple of 16: segments start 16-byte aligned
-  constexpr int STG = mg_stage_bytes(TYPE);
   constexpr int MT = MS * TG;  // token slots
+  constexpr int STG = mt_stage_bytes(TYPE, MT);
   constexpr float kScale = TYPE == WH_TYPE_Q4_0 ? 0.0625f : 1.0f;
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1005,24 +1008,35 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
       const uint32_t pb2 = __builtin_amdgcn_perm(z[1], z[0], 0x04000501u);
       const uint32_t pc = __builtin_amdgcn_perm(z[3], z[2], 0x06020703u);
       const uint32_t pd = __builtin_amdgcn_perm(z[3], z[2], 0x04000501u);
-      int8_t* pw = reinterpret_cast<int8_t*>(stage) + (lane >> 3) * kMgLimbBytes + mg_slot_offset<TYPE>(4 * (lane & 7));
+      // two-token layout: token t's limbs in the t-th half of the stage
+      int8_t* pw = reinterpret_cast<int8_t*>(stage) + (MS == 2 ? t * 8 * kMgLimbBytes : 0) +
+                   (lane >> 3) * kMgLimbBytes + mg_slot_offset<TYPE>(4 * (lane & 7));
       *reinterpret_cast<uint32_t*>(pw) = __builtin_amdgcn_perm(pc, pa, 0x05040100u);
       *reinterpret_cast<uint32_t*>(pw + 32) = __builtin_amdgcn_perm(pc, pa, 0x07060302u);
       *reinterpret_cast<uint32_t*>(pw + 64) = __builtin_amdgcn_perm(pd, pb2, 0x05040100u);
       *reinterpret_cast<uint32_t*>(pw + 96) = __builtin_amdgcn_perm(pd, pb2, 0x07060302u);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_wave_barrier();
-      // this token's rows of the A operands (four-token layout: rows 4 (t & 3)
-      // .. + 3 of token group t / 4; two-token layout: rows 8 (b & 1) + 4 t ..)
-      {
+      if constexpr (MS == 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        // this token's rows of the A operands: rows 4 (t & 3) .. + 3 of token group t / 4
         const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + 32 * (n & 3) + 8 * g;
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-          const int slot = MS == 4 ? (t & 3) : 2 * (b & 1) + t;
-          if ((n >> 2) == slot)
-            xa[seg][MS == 4 ? t >> 2 : 0][MS == 4 ? b : b >> 1] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
-        }
+        for (int b = 0; b < 8; b++)
+          if ((n >> 2) == (t & 3)) xa[seg][t >> 2][b] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
       }
+    }
+    if constexpr (MS == 2) {
+      // two-token layout: rows 8 (b & 1) + 4 t .. + 3 hold token t's limbs of
+      // block b, so a lane's rows belong to token (n >> 2) & 1 and to the
+      // blocks of parity n >> 3: four reads from that token's half, no branch
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + ((n >> 2) & 1) * 8 * kMgLimbBytes +
+                         (n >> 3) * kMgLimbBytes + 32 * (n & 3) + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 4; j++) xa[seg][0][j] = *reinterpret_cast<const long*>(xs + 2 * j * kMgLimbBytes);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
     }
@@ -1037,7 +1051,10 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
         const int* e4 = &ex_u[seg][4 * tg];
         ex_l[seg][tg] = g == 0 ? e4[0] : g == 1 ? e4[1] : g == 2 ? e4[2] : e4[3];
       } else {
-        ex_l[seg][tg] = (g & 1) ? ex_u[seg][1] : ex_u[seg][0];
+        // values, not the elements: a conditional over two lvalues selects an
+        // address, and the array would live in scratch memory
+        const int e0 = ex_u[seg][0], e1 = ex_u[seg][MT > 1 ? 1 : 0];
+        ex_l[seg][tg] = (g & 1) ? e1 : e0;
       }
     }
 
@@ -1205,7 +1222,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
 size_t mt_lds_bytes(int type, int seg_pairs, int mt, int rows_per_wg) {
   const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * mg_chunk_bytes(type));
   const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), 16u);
-  return 2u * 16u * rstr + static_cast<size_t>(kMgWaves) * mg_stage_bytes(type) +
+  return 2u * 16u * rstr + static_cast<size_t>(kMgWaves) * mt_stage_bytes(type, mt) +
          4u * (2u * kMgWaves * mt * 16 + static_cast<size_t>(kMgWaves) * mt + mt + static_cast<size_t>(mt) * rows_per_wg);
 }
 
