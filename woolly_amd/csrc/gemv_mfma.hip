@@ -357,7 +357,7 @@ __device__ __forceinline__ float mg_sum_lane_groups(float v) {
 
 // The four limb sums of one block as one f32, 2^24 C0 + 2^16 C1 + 2^8 C2 + C3:
 // the halves 2^8 C0 + C1 and 2^8 C2 + C3 in int32 (exact and without overflow:
-// |C| < 2^20 in the single-token kernel), converted (exactly for the 4-bit
+// |C| < 2^20: each sum covers one 32-element block), converted (exactly for the 4-bit
 // formats, whose halves stay below 2^24) and combined with one fma.
 __device__ __forceinline__ float mg_limbs(const mg_v4i& C) {
   const int hi = C[0] * 256 + C[1];
@@ -1020,9 +1020,13 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
         __builtin_amdgcn_wave_barrier();
         // this token's rows of the A operands: rows 4 (t & 3) .. + 3 of token group t / 4
         const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + 32 * (n & 3) + 8 * g;
+        if ((n >> 2) == (t & 3)) {
+          long v[8];
 #pragma unroll
-        for (int b = 0; b < 8; b++)
-          if ((n >> 2) == (t & 3)) xa[seg][t >> 2][b] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
+          for (int b = 0; b < 8; b++) v[b] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
+#pragma unroll
+          for (int b = 0; b < 8; b++) xa[seg][t >> 2][b] = v[b];
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
       }
@@ -1073,11 +1077,6 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
            (static_cast<long>(__builtin_amdgcn_alignbit(w2, w1, 16)) << 32);
       qb = static_cast<long>(pw[9 + 2 * g]) | (static_cast<long>(pw[10 + 2 * g]) << 32);
     }
-  };
-  auto combine = [](const mg_v4i& C) -> float {
-    return __builtin_fmaf(static_cast<float>(C[0]), 16777216.f,
-                          __builtin_fmaf(static_cast<float>(C[1]), 65536.f,
-                                         __builtin_fmaf(static_cast<float>(C[2]), 256.f, static_cast<float>(C[3]))));
   };
 
   // Sum of group q over the 16 waves (fixed order) for every token, then the output rows.
@@ -1157,13 +1156,13 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
             if constexpr (MS == 4) {
               const mg_v4i ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p], qa, zero, 0, 0, 0);
               const mg_v4i cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p + 1], qb, zero, 0, 0, 0);
-              sacc[tg] = __builtin_fmaf(da, combine(ca), sacc[tg]);
-              sacc[tg] = __builtin_fmaf(db, combine(cb), sacc[tg]);
+              sacc[tg] = __builtin_fmaf(da, mg_limbs(ca), sacc[tg]);
+              sacc[tg] = __builtin_fmaf(db, mg_limbs(cb), sacc[tg]);
             } else {
               const long ae = n < 8 ? xa[seg][tg][p] : 0, ao = n < 8 ? 0 : xa[seg][tg][p];
               mg_v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, qa, zero, 0, 0, 0);
               c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ao, qb, c, 0, 0, 0);
-              sacc[tg] = __builtin_fmaf((g >> 1) ? db : da, combine(c), sacc[tg]);
+              sacc[tg] = __builtin_fmaf((g >> 1) ? db : da, mg_limbs(c), sacc[tg]);
             }
           }
         }
