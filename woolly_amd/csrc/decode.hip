@@ -196,8 +196,21 @@ int layer_step(const wh_llama_model* m, const wh_llama_layer& L, size_t pos, flo
     const void* mats[3] = {L.wq, L.wk, L.wv};
     const size_t rows[3] = {qd, kvd, kvd};
     const int ty[3] = {t.q, t.k, t.v};
+    // exactly two groups of different types (Q4_K_M): one launch when a kernel takes the pair
+    int n0 = 1;
+    while (n0 < 3 && ty[n0] == ty[0]) n0++;
+    bool done = false;
+    if (n0 < 3 && (n0 == 2 || ty[1] == ty[2])) {
+      size_t off_b = 0;
+      for (int j = 0; j < n0; j++) off_b += rows[j];
+      st = wh::launch_gemv_mfma2(ty[0], mats, rows, n0, ty[n0], mats + n0, rows + n0, 3 - n0, x, L.attn_norm,
+                                 m->eps, w.qkv, w.qkv + off_b, m->hidden, s);
+      if (st == WH_OK) done = true;
+      else if (st != WH_ERR_INVALID_SHAPE) return st;
+      st = WH_OK;
+    }
     size_t off = 0;
-    for (int i = 0; i < 3 && !st;) {
+    for (int i = 0; i < 3 && !st && !done;) {
       int n = 1;
       while (i + n < 3 && ty[i + n] == ty[i]) n++;
       st = gemv_fused_or_split(ty[i], mats + i, rows + i, n, x, L.attn_norm, m->eps, nullptr, w.qkv + off, m->hidden,

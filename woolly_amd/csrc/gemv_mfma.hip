@@ -373,7 +373,7 @@ __device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
 // NL: 16-byte loads per lane per step (row segments of up to 1024 NL bytes).
 // DEPTH: steps whose loads are in flight in registers (one-segment rows only).
 template <int TYPE, int NSEG, int NL, int MODE, int DEPTH>
-__global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a) {
+__device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
   static_assert(DEPTH >= 1 && (DEPTH == 1 || NSEG == 1), "register prefetch of several steps needs one segment");
   constexpr int PB = MgFmt<TYPE>::PB;
   constexpr bool FFN = (MODE & kMgFfn) != 0;
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   float* misc = part + 2 * kMgWaves * 16;                                                    // [16] + [16]
   float* rows_lds = misc + 32;  // the workgroup's output rows (the residual, then += W x)
 
-  const int r0 = blockIdx.x * a.rows_per_wg;
+  const int r0 = bid * a.rows_per_wg;
   const int r1 = min(a.n_out, r0 + a.rows_per_wg);
   const int G = (r1 - r0 + 15) >> 4;
   const int GT = FFN ? 2 * G : G;          // row groups streamed
@@ -819,6 +819,25 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) a.y[r0 + i] = rows_lds[i];
+}
+
+template <int TYPE, int NSEG, int NL, int MODE, int DEPTH>
+__global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma_kernel(const MgArgs a) {
+  gemv_mfma_body<TYPE, NSEG, NL, MODE, DEPTH>(a, static_cast<int>(blockIdx.x));
+}
+
+// Two groups of row-stacked matrices of different block types over the same x
+// and RMSNorm in one launch (the decode step's q + k in Q4_K and v in Q6_K of
+// Q4_K_M files): workgroups [0, grid_a) run group a, the rest group b, each
+// with its own rows, LDS layout and output.  A launch's fixed costs are most
+// of a small GEMV's time, so one launch replaces two.
+template <int TA, int NLA, int TB, int NLB, int MODE>
+__global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma2_kernel(const MgArgs a, const MgArgs b, int grid_a) {
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < grid_a)
+    gemv_mfma_body<TA, 1, NLA, MODE, kMgDepth1>(a, bid);
+  else
+    gemv_mfma_body<TB, 1, NLB, MODE, kMgDepth1>(b, bid - grid_a);
 }
 
 // ---------------------------------------------------------------- several tokens
@@ -1344,10 +1363,12 @@ bool gemv_mfma_ok(int type, size_t n_out, size_t k) {
 // mats / rows: up to three row-stacked matrices with the same K (ffn: gate, up
 // with n_out rows each).  Returns WH_ERR_INVALID_SHAPE without launching when
 // the layout does not fit this kernel.
-int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
-                     const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
-                     hipStream_t s) {
-  if (n_out == 0) return WH_OK;
+namespace {
+// The arguments, segments, grid and LDS bytes of one single-token launch;
+// WH_ERR_INVALID_SHAPE when the layout does not fit the kernel.
+int mg_prepare(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
+               const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k, MgArgs* out,
+               int* nseg_out, size_t* grid_out, size_t* lds_out) {
   if (!gemv_mfma_ok(type, n_out, k) || n_mats < 1 || n_mats > 3 || (ffn && (n_mats != 2 || !gamma)))
     return WH_ERR_INVALID_SHAPE;
   for (int i = 0; i < n_mats; i++)
@@ -1382,6 +1403,29 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   const size_t grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
   const size_t lds = mg_lds_bytes(type, a.seg_pairs, nseg, a.rows_per_wg);
   if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
+  *out = a;
+  *nseg_out = nseg;
+  *grid_out = grid;
+  *lds_out = lds;
+  return WH_OK;
+}
+
+// loads per lane per step that mg_dispatch gives a one-segment row
+int mg_nl_one_segment(int type, const MgArgs& a) {
+  const int seg_bytes = a.seg_pairs / 4 * mg_chunk_bytes(type) + ((mg_chunk_bytes(type) & 15) ? 15 : 0);
+  return seg_bytes <= 3072 ? 3 : 4;
+}
+}  // namespace
+
+int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
+                     const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
+                     hipStream_t s) {
+  if (n_out == 0) return WH_OK;
+  MgArgs a{};
+  int nseg = 0;
+  size_t grid = 0, lds = 0;
+  const int st = mg_prepare(type, mats, rows, n_mats, ffn, x, gamma, eps, residual, y, n_out, k, &a, &nseg, &grid, &lds);
+  if (st) return st;
   const int mode = ffn ? (kMgNorm | kMgFfn) : (gamma ? kMgNorm : 0);
   switch (type) {
     case WH_TYPE_Q4_0: return mg_typed<WH_TYPE_Q4_0>(a, nseg, mode, static_cast<int>(grid), lds, s);
@@ -1392,6 +1436,36 @@ int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int 
   }
 }
 
+
+int launch_gemv_mfma2(int type_a, const void* const* mats_a, const size_t* rows_a, int n_a, int type_b,
+                      const void* const* mats_b, const size_t* rows_b, int n_b, const float* x, const float* gamma,
+                      float eps, float* y_a, float* y_b, size_t k, hipStream_t s) {
+  if (!gamma || type_a != WH_TYPE_Q4_K || type_b != WH_TYPE_Q6_K || n_a < 1 || n_b < 1 || n_a + n_b > 3)
+    return WH_ERR_INVALID_SHAPE;
+  size_t out_a = 0, out_b = 0;
+  for (int i = 0; i < n_a; i++) out_a += rows_a[i];
+  for (int i = 0; i < n_b; i++) out_b += rows_b[i];
+  if (out_a == 0 || out_b == 0) return WH_ERR_INVALID_SHAPE;
+  MgArgs a{}, b{};
+  int nseg_a = 0, nseg_b = 0;
+  size_t grid_a = 0, grid_b = 0, lds_a = 0, lds_b = 0;
+  if (mg_prepare(type_a, mats_a, rows_a, n_a, false, x, gamma, eps, nullptr, y_a, out_a, k, &a, &nseg_a, &grid_a,
+                 &lds_a) ||
+      mg_prepare(type_b, mats_b, rows_b, n_b, false, x, gamma, eps, nullptr, y_b, out_b, k, &b, &nseg_b, &grid_b,
+                 &lds_b))
+    return WH_ERR_INVALID_SHAPE;
+  // the one instantiation: one segment each, three loads per step for Q4_K,
+  // four for Q6_K (K = 4096, Llama-3-8B)
+  if (nseg_a != 1 || nseg_b != 1 || mg_nl_one_segment(type_a, a) != 3 || mg_nl_one_segment(type_b, b) != 4)
+    return WH_ERR_INVALID_SHAPE;
+  const size_t lds = lds_a > lds_b ? lds_a : lds_b;
+  auto* fn = &gemv_mfma2_kernel<WH_TYPE_Q4_K, 3, WH_TYPE_Q6_K, 4, kMgNorm>;
+  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(lds)));
+  fn<<<static_cast<unsigned>(grid_a + grid_b), kMgWaves * 64, lds, s>>>(a, b, static_cast<int>(grid_a));
+  WH_LAUNCH_CHECK("gemv (mfma, two types) kernel launch");
+  return WH_OK;
+}
 
 // Several tokens (2..16) on the matrix cores: plain Y[t] = W X[t] (mats =
 // {W}) or, with ffn, H[t] = silu(gate x_hat[t]) * (up x_hat[t]) (mats = {gate,

@@ -122,6 +122,13 @@ bool gemv_mfma_ok(int type, size_t n_out, size_t k);
 int launch_gemv_mfma(int type, const void* const* mats, const size_t* rows, int n_mats, bool ffn, const float* x,
                      const float* gamma, float eps, const float* residual, float* y, size_t n_out, size_t k,
                      hipStream_t stream);
+// Two groups of row-stacked matrices of different types over one x with the
+// RMSNorm prologue, in one launch (group a -> y_a, group b -> y_b); taken for
+// Q4_K + Q6_K with one-segment rows, WH_ERR_INVALID_SHAPE (nothing launched)
+// otherwise.
+int launch_gemv_mfma2(int type_a, const void* const* mats_a, const size_t* rows_a, int n_a, int type_b,
+                      const void* const* mats_b, const size_t* rows_b, int n_b, const float* x, const float* gamma,
+                      float eps, float* y_a, float* y_b, size_t k, hipStream_t stream);
 // 2..16 tokens on the matrix cores (gemv_mfma.hip, Q4_0 and Q8_0): plain
 // Y[t] = W X[t] (mats = {W}) or, with ffn, H[t] = silu(gate x_hat[t]) *
 // (up x_hat[t]) with each token's RMSNorm (mats = {gate, up}); x is [m][k], row
