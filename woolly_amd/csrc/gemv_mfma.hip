@@ -856,7 +856,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma2_kernel(const MgArgs 
 // share one accumulator and lane group g holds token g & 1 of block
 // 2p + (g >> 1), half the accumulator conversions of the four-token layout.
 template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS>
-__global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) {
+__device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
   static_assert(TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q8_0, "several-token GEMV: Q4_0 and Q8_0");
   static_assert(TG * NSEG <= 4, "A operands of every segment in registers");
   static_assert(MS == 4 || (MS == 2 && TG == 1), "two-token layout: one group");
@@ -887,7 +887,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
   float* rms_lds = misc + kMgWaves * MT;        // [MT] RMSNorm scale of each token
   float* rows_lds = rms_lds + MT;               // [MT][R] the workgroup's output rows
 
-  const int r0 = blockIdx.x * R;
+  const int r0 = bid * R;
   const int r1 = min(a.n_out, r0 + R);
   const int G = (r1 - r0 + 15) >> 4;
   const int GT = FFN ? 2 * G : G;
@@ -1235,6 +1235,11 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) 
     const int t = i / (r1 - r0), r = i - t * (r1 - r0);
     a.y[static_cast<size_t>(t) * a.ldy + r0 + r] = rows_lds[t * R + r];
   }
+}
+
+template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS>
+__global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) {
+  gemv_mt_body<TYPE, NSEG, NL, MODE, TG, MS>(a, static_cast<int>(blockIdx.x));
 }
 
 size_t mt_lds_bytes(int type, int seg_pairs, int mt, int rows_per_wg) {
