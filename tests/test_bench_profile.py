@@ -30,3 +30,15 @@ def test_missing_summary(tmp_path, monkeypatch):
 def test_digest_covers_every_gemv_source():
     assert len(bench.kernel_sources_digest()) == 16
     assert all((bench.ROOT / rel).is_file() for rel in bench.GEMV_KERNEL_SOURCES)
+
+
+def test_committed_headline_summaries_are_current():
+    """The committed kernel-trace and counter summaries of the headline GEMV
+    were taken from this tree's GEMV sources: a change to them without a new
+    profile fails here, before the bench line reports traffic as stale."""
+    want = bench.kernel_sources_digest()
+    for name in ("gemv_q4_0_14336x4096_pmc.txt", "gemv_q4_0_14336x4096_kernel_trace.txt"):
+        text = (bench.ROOT / "profiles" / name).read_text()
+        recorded = [ln.split()[1] for ln in text.splitlines() if ln.startswith("kernel_sources_sha256:")]
+        assert recorded == [want], (name, recorded, want)
+    assert bench.traffic_from_profile()[1] == "current"
