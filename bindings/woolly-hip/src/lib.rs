@@ -122,6 +122,18 @@ pub struct wh_ffn_weights {
     pub n_ff: usize,
 }
 
+/// Counters of the device copies kept behind the `*_host` variants.
+#[repr(C)]
+#[derive(Debug, Default, Clone, Copy)]
+pub struct wh_host_cache_stats {
+    pub hits: u64,
+    pub misses: u64,
+    pub evictions: u64,
+    pub entries: usize,
+    pub bytes: usize,
+    pub max_bytes: usize,
+}
+
 /// One decoder layer (device pointers); a `*_type` of 0 means the model's type.
 #[repr(C)]
 #[derive(Clone, Copy, Debug)]
@@ -283,6 +295,11 @@ extern "C" {
                               out: *mut c_float) -> c_int;
     pub fn wh_quantized_matvec_host(r#type: c_int, weights: *const c_void, weight_nbytes: usize,
                                     input: *const c_float, output: *mut c_float, m: usize, k: usize) -> c_int;
+    // device copies of host weights behind the host variants (dequantization_cache.rs:121-165)
+    pub fn wh_host_cache_configure(max_bytes: usize) -> c_int;
+    pub fn wh_host_cache_evict(host_ptr: *const c_void, nbytes: usize, evicted: *mut usize) -> c_int;
+    pub fn wh_host_cache_clear() -> c_int;
+    pub fn wh_host_cache_get_stats(out: *mut wh_host_cache_stats) -> c_int;
 
     // decode step (lazy_transformer.rs:98-456, 1155-1335)
     pub fn wh_rope_inv_freq(base: c_float, head_dim: usize, out_host: *mut c_float) -> c_int;

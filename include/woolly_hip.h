@@ -274,6 +274,38 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
 WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight_nbytes,
                                     const float* input, float* output, size_t m, size_t k);
 
+/* Device copies of host weights behind the two host variants above.  Off by
+ * default: every call then uploads its whole block input (a 33 MB matrix
+ * crosses PCIe for an 8 us GEMV).  With a budget above 0, a call's block input
+ * is uploaded once per (device, host address, byte count) and later calls with
+ * the same key reuse the device copy, so a call moves only its activations and
+ * outputs; its small device buffers come from a pool, so a cached call
+ * allocates nothing.  This is the device-side counterpart of the reference's
+ * per-tensor cache (DequantizationCache::get_or_dequantize,
+ * crates/woolly-core/src/model/dequantization_cache.rs:121-165) and assumes, as
+ * that cache does, that cached bytes do not change (GGUF mmap slices): a caller
+ * that rewrites host memory evicts its range first.  Least recently used
+ * entries are dropped beyond the budget; an input larger than the budget is
+ * not cached.  Thread-safe: an entry dropped while another call uses it is
+ * freed when that call returns.  Device-resident handles (wh_weight_upload)
+ * remain the fast path: no PCIe copy and no host synchronisation per call. */
+typedef struct wh_host_cache_stats {
+  uint64_t hits;      /* calls that found their block input on the device */
+  uint64_t misses;    /* calls that uploaded it (cached or not) */
+  uint64_t evictions; /* entries dropped by the budget, evict or clear */
+  size_t entries;     /* entries held */
+  size_t bytes;       /* device bytes held by the entries */
+  size_t max_bytes;   /* the budget (0: off) */
+} wh_host_cache_stats;
+/* Sets the budget; 0 turns the cache off and frees every entry and pooled buffer. */
+WH_API int wh_host_cache_configure(size_t max_bytes);
+/* Drops every entry whose host range overlaps [host_ptr, host_ptr + nbytes)
+ * (nbytes 0: the entries that start at host_ptr), on every device. */
+WH_API int wh_host_cache_evict(const void* host_ptr, size_t nbytes, size_t* evicted);
+/* Drops every entry and frees the pooled buffers (the budget is kept). */
+WH_API int wh_host_cache_clear(void);
+WH_API int wh_host_cache_get_stats(wh_host_cache_stats* out);
+
 /* ---------------------------------------------------- decode step (M = 1) */
 /* The pieces of one transformer layer for a single new token
  * (LazyTransformer::process_layer, crates/woolly-core/src/model/lazy_transformer.rs:98-258)

@@ -96,6 +96,17 @@ class wh_gguf_tensor(C.Structure):
     ]
 
 
+class wh_host_cache_stats(C.Structure):
+    _fields_ = [
+        ("hits", C.c_uint64),
+        ("misses", C.c_uint64),
+        ("evictions", C.c_uint64),
+        ("entries", C.c_size_t),
+        ("bytes", C.c_size_t),
+        ("max_bytes", C.c_size_t),
+    ]
+
+
 class wh_llama_layer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate",
                                           "w_up", "w_down", "k_cache", "v_cache")] + \
@@ -177,6 +188,10 @@ SIGNATURES = {
                               C.POINTER(_sz)]),
     "wh_dequantize_host": (_int, [_int, _vp, _sz, _sz, _f32p]),
     "wh_quantized_matvec_host": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz]),
+    "wh_host_cache_configure": (_int, [_sz]),
+    "wh_host_cache_evict": (_int, [_vp, _sz, C.POINTER(_sz)]),
+    "wh_host_cache_clear": (_int, []),
+    "wh_host_cache_get_stats": (_int, [C.POINTER(wh_host_cache_stats)]),
     "wh_rope_inv_freq": (_int, [C.c_float, _sz, _vp]),
     "wh_attention_qkv_workspace_bytes": (_sz, [_sz]),
     "wh_attention_qkv": (_int, [_int, _vp, _vp, _vp, _sz, _sz, _sz, _f32p, C.c_float, _f32p, _f32p,

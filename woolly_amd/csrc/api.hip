@@ -7,7 +7,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
+#include <map>
+#include <memory>
 #include <mutex>
+#include <vector>
 
 #include "wh_common.hpp"
 
@@ -26,9 +30,20 @@ thread_local char g_last_error[512] = "";
 
 hipStream_t hs(wh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-constexpr int kMaxDevices = 64;
-int g_cu_count[kMaxDevices] = {0};
-std::mutex g_cu_mutex;
+// per-device caches of device attributes (0: not yet queried)
+std::atomic<int> g_cu_count[wh::kMaxDevices];
+std::atomic<int> g_max_lds[wh::kMaxDevices];
+
+// A device attribute of the current device, queried once and cached in c.
+int cached_attribute(std::atomic<int>* c, hipDeviceAttribute_t attr, int fallback) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= wh::kMaxDevices) return fallback;
+  int v = c[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, attr, dev) != hipSuccess || v <= 0) v = fallback;
+  c[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
 
 int check_block_args(const char* fn, int type, size_t k) {
   if (!wh::is_block_type(type))
@@ -90,28 +105,24 @@ int hip_error(hipError_t err, const char* what) {
   return set_error(st, "%s failed: %s (%d)", what, hipGetErrorString(err), static_cast<int>(err));
 }
 
-int cu_count() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
-  {
-    std::lock_guard<std::mutex> lk(g_cu_mutex);
-    if (g_cu_count[dev] > 0) return g_cu_count[dev];
-  }
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-    n = 256;
-  std::lock_guard<std::mutex> lk(g_cu_mutex);
-  g_cu_count[dev] = n;
-  return n;
-}
+int cu_count() { return cached_attribute(g_cu_count, hipDeviceAttributeMultiprocessorCount, 256); }
 
 size_t max_lds_per_block() {
+  return static_cast<size_t>(cached_attribute(g_max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 65536));
+}
+
+int ensure_dynamic_lds(LdsLimit& lim, const void* fn, size_t bytes) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 65536;
-  int v = 0;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-    return 65536;
-  return static_cast<size_t>(v);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
+  const int want = static_cast<int>(bytes);
+  if (dev >= 0 && lim.set[dev].load(std::memory_order_relaxed) >= want) return WH_OK;
+  WH_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, want));
+  if (dev >= 0) {
+    int cur = lim.set[dev].load(std::memory_order_relaxed);
+    while (cur < want && !lim.set[dev].compare_exchange_weak(cur, want, std::memory_order_relaxed)) {
+    }
+  }
+  return WH_OK;
 }
 
 }  // namespace wh
@@ -650,15 +661,237 @@ WH_API int wh_weight_info(const wh_weight* weight, int* type, size_t* n_rows, si
   return WH_OK;
 }
 
+}  // extern "C"
+
 // -------------------------------------------------- synchronous host variants
 namespace {
-struct DevBuf {
-  void* p = nullptr;
-  ~DevBuf() {
-    if (p) (void)hipFree(p);
+// One device copy of host block bytes; freed with the last reference.
+struct DevBlocks {
+  void* dev = nullptr;
+  size_t nbytes = 0;
+  DevBlocks() = default;
+  DevBlocks(const DevBlocks&) = delete;
+  DevBlocks& operator=(const DevBlocks&) = delete;
+  ~DevBlocks() {
+    if (dev) (void)hipFree(dev);
   }
 };
+
+// A pooled device buffer of at least `cap` bytes for a call's activations and outputs.
+struct PoolBuf {
+  int dev = -1;
+  size_t cap = 0;
+  void* p = nullptr;
+};
+
+// The host-weight cache (wh_host_cache_*): entries keyed by (device, host
+// address, byte count) with a last-use tick for LRU eviction, and a per-device
+// pool of small buffers.  Allocated once and never destroyed, so no hipFree
+// runs while the HIP runtime shuts down at process exit.
+struct HostCache {
+  struct Key {
+    int dev;
+    uintptr_t host;
+    size_t nbytes;
+    bool operator<(const Key& o) const {
+      if (dev != o.dev) return dev < o.dev;
+      if (host != o.host) return host < o.host;
+      return nbytes < o.nbytes;
+    }
+  };
+  struct Slot {
+    std::shared_ptr<DevBlocks> blocks;
+    uint64_t last_use;
+  };
+  std::mutex mu;
+  std::map<Key, Slot> entries;
+  std::vector<PoolBuf> pool;
+  size_t max_bytes = 0, bytes = 0;
+  uint64_t hits = 0, misses = 0, evictions = 0, tick = 0;
+
+  // drops entries, least recently used first, until the budget holds (mu held)
+  void trim() {
+    while (bytes > max_bytes && !entries.empty()) {
+      auto lru = entries.begin();
+      for (auto it = entries.begin(); it != entries.end(); ++it)
+        if (it->second.last_use < lru->second.last_use) lru = it;
+      bytes -= lru->second.blocks->nbytes;
+      entries.erase(lru);
+      evictions++;
+    }
+  }
+};
+
+HostCache& host_cache() {
+  static HostCache* c = new HostCache();
+  return *c;
+}
+
+// Uploads `nbytes` of host blocks into a fresh device buffer.
+int upload_blocks(const void* host, size_t nbytes, std::shared_ptr<DevBlocks>* out) {
+  auto b = std::make_shared<DevBlocks>();
+  WH_HIP_TRY(hipMalloc(&b->dev, nbytes));
+  b->nbytes = nbytes;
+  WH_HIP_TRY(hipMemcpy(b->dev, host, nbytes, hipMemcpyHostToDevice));
+  *out = std::move(b);
+  return WH_OK;
+}
+
+// The device copy of a call's block input: from the cache when it is on,
+// otherwise (or when the input exceeds the budget) a copy owned by the call.
+int blocks_on_device(const void* host, size_t nbytes, std::shared_ptr<DevBlocks>* out) {
+  int dev = 0;
+  WH_HIP_TRY(hipGetDevice(&dev));
+  HostCache& c = host_cache();
+  const HostCache::Key key{dev, reinterpret_cast<uintptr_t>(host), nbytes};
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    if (c.max_bytes > 0) {
+      auto it = c.entries.find(key);
+      if (it != c.entries.end()) {
+        it->second.last_use = ++c.tick;
+        c.hits++;
+        *out = it->second.blocks;
+        return WH_OK;
+      }
+    }
+    c.misses++;
+    if (c.max_bytes == 0 || nbytes > c.max_bytes) {
+      // uncached: the call owns the copy
+      return upload_blocks(host, nbytes, out);
+    }
+  }
+  // upload outside the lock; a concurrent call for the same key may have
+  // inserted meanwhile, and then its copy is used
+  std::shared_ptr<DevBlocks> b;
+  int st = upload_blocks(host, nbytes, &b);
+  if (st) return st;
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (c.max_bytes == 0 || nbytes > c.max_bytes) {  // reconfigured during the upload
+    *out = std::move(b);
+    return WH_OK;
+  }
+  auto ins = c.entries.emplace(key, HostCache::Slot{b, ++c.tick});
+  if (ins.second) {
+    c.bytes += nbytes;
+    c.trim();
+  } else {
+    ins.first->second.last_use = c.tick;
+  }
+  *out = ins.first->second.blocks;
+  return WH_OK;
+}
+
+// A pooled buffer of at least `bytes` on the current device (returned with pool_put).
+int pool_get(size_t bytes, PoolBuf* out) {
+  int dev = 0;
+  WH_HIP_TRY(hipGetDevice(&dev));
+  HostCache& c = host_cache();
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    for (size_t i = 0; i < c.pool.size(); i++) {
+      if (c.pool[i].dev == dev && c.pool[i].cap >= bytes) {
+        *out = c.pool[i];
+        c.pool.erase(c.pool.begin() + static_cast<std::ptrdiff_t>(i));
+        return WH_OK;
+      }
+    }
+  }
+  PoolBuf b;
+  b.dev = dev;
+  b.cap = align_up(bytes < 4096 ? 4096 : bytes, 4096);
+  WH_HIP_TRY(hipMalloc(&b.p, b.cap));
+  *out = b;
+  return WH_OK;
+}
+
+// Returns a buffer to the pool while the cache is on, frees it otherwise.
+void pool_put(PoolBuf& b) {
+  if (!b.p) return;
+  HostCache& c = host_cache();
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    if (c.max_bytes > 0 && c.pool.size() < 64) {
+      c.pool.push_back(b);
+      b.p = nullptr;
+      return;
+    }
+  }
+  (void)hipFree(b.p);
+  b.p = nullptr;
+}
+
+// A pooled buffer that goes back to the pool (or is freed) when the call returns.
+struct ScopedPoolBuf {
+  PoolBuf b;
+  ~ScopedPoolBuf() { pool_put(b); }
+};
 }  // namespace
+
+extern "C" {
+
+WH_API int wh_host_cache_configure(size_t max_bytes) {
+  HostCache& c = host_cache();
+  std::vector<PoolBuf> freed;
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    c.max_bytes = max_bytes;
+    c.trim();
+    if (max_bytes == 0) freed.swap(c.pool);
+  }
+  for (PoolBuf& b : freed) (void)hipFree(b.p);
+  return WH_OK;
+}
+
+WH_API int wh_host_cache_evict(const void* host_ptr, size_t nbytes, size_t* evicted) {
+  HostCache& c = host_cache();
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(host_ptr);
+  size_t n = 0;
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    for (auto it = c.entries.begin(); it != c.entries.end();) {
+      const uintptr_t elo = it->first.host, ehi = elo + it->first.nbytes;
+      const bool hit = nbytes == 0 ? elo == lo : (elo < lo + nbytes && lo < ehi);
+      if (hit) {
+        c.bytes -= it->second.blocks->nbytes;
+        it = c.entries.erase(it);
+        n++;
+      } else {
+        ++it;
+      }
+    }
+    c.evictions += n;
+  }
+  if (evicted) *evicted = n;
+  return WH_OK;
+}
+
+WH_API int wh_host_cache_clear(void) {
+  HostCache& c = host_cache();
+  std::vector<PoolBuf> freed;
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    c.evictions += c.entries.size();
+    c.entries.clear();
+    c.bytes = 0;
+    freed.swap(c.pool);
+  }
+  for (PoolBuf& b : freed) (void)hipFree(b.p);
+  return WH_OK;
+}
+
+WH_API int wh_host_cache_get_stats(wh_host_cache_stats* out) {
+  if (!out) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "wh_host_cache_get_stats: null output");
+  HostCache& c = host_cache();
+  std::lock_guard<std::mutex> lk(c.mu);
+  out->hits = c.hits;
+  out->misses = c.misses;
+  out->evictions = c.evictions;
+  out->entries = c.entries.size();
+  out->bytes = c.bytes;
+  out->max_bytes = c.max_bytes;
+  return WH_OK;
+}
 
 WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t nelements, float* out) {
   const size_t ts = wh::type_size(type);
@@ -673,13 +906,14 @@ WH_API int wh_dequantize_host(int type, const void* data, size_t nbytes, size_t 
           : (nelements / wh::block_elems(type) + (nelements % wh::block_elems(type) != 0)) * ts;
   if (nbytes < in_bytes || ((type == WH_TYPE_F32 || type == WH_TYPE_F16) && nbytes != in_bytes))
     return wh_dequantize(type, data, nbytes, nelements, out, nullptr);
-  DevBuf din, dout;
-  WH_HIP_TRY(hipMalloc(&din.p, in_bytes));
-  WH_HIP_TRY(hipMalloc(&dout.p, nelements * sizeof(float)));
-  WH_HIP_TRY(hipMemcpy(din.p, data, in_bytes, hipMemcpyHostToDevice));
-  int st = wh_dequantize(type, din.p, in_bytes, nelements, static_cast<float*>(dout.p), nullptr);
+  std::shared_ptr<DevBlocks> din;
+  int st = blocks_on_device(data, in_bytes, &din);
   if (st) return st;
-  WH_HIP_TRY(hipMemcpy(out, dout.p, nelements * sizeof(float), hipMemcpyDeviceToHost));
+  ScopedPoolBuf dout;
+  if ((st = pool_get(nelements * sizeof(float), &dout.b))) return st;
+  st = wh_dequantize(type, din->dev, in_bytes, nelements, static_cast<float*>(dout.b.p), nullptr);
+  if (st) return st;
+  WH_HIP_TRY(hipMemcpy(out, dout.b.p, nelements * sizeof(float), hipMemcpyDeviceToHost));
   return WH_OK;
 }
 
@@ -693,16 +927,18 @@ WH_API int wh_quantized_matvec_host(int type, const void* weights, size_t weight
   if (!output || (k > 0 && (!weights || !input)))
     return wh::set_error(WH_ERR_INVALID_ARGUMENT, "quantized_matvec_host: null pointer");
   const size_t wbytes = m * (k / wh::block_elems(type)) * wh::type_size(type);
-  DevBuf dw, dx, dy;
-  if (wbytes) WH_HIP_TRY(hipMalloc(&dw.p, wbytes));
-  if (k) WH_HIP_TRY(hipMalloc(&dx.p, k * sizeof(float)));
-  WH_HIP_TRY(hipMalloc(&dy.p, m * sizeof(float)));
-  if (wbytes) WH_HIP_TRY(hipMemcpy(dw.p, weights, wbytes, hipMemcpyHostToDevice));
-  if (k) WH_HIP_TRY(hipMemcpy(dx.p, input, k * sizeof(float), hipMemcpyHostToDevice));
-  st = wh_quantized_matvec(type, dw.p, wbytes, static_cast<const float*>(dx.p),
-                           static_cast<float*>(dy.p), m, k, nullptr);
+  std::shared_ptr<DevBlocks> dw;
+  if (wbytes && (st = blocks_on_device(weights, wbytes, &dw))) return st;
+  // x and y in one pooled buffer: x at 0, y at the next 256-byte boundary
+  const size_t xoff = align_up(k * sizeof(float), 256);
+  ScopedPoolBuf io;
+  if ((st = pool_get(xoff + m * sizeof(float), &io.b))) return st;
+  float* dx = static_cast<float*>(io.b.p);
+  float* dy = reinterpret_cast<float*>(static_cast<char*>(io.b.p) + xoff);
+  if (k) WH_HIP_TRY(hipMemcpy(dx, input, k * sizeof(float), hipMemcpyHostToDevice));
+  st = wh_quantized_matvec(type, dw ? dw->dev : nullptr, wbytes, dx, dy, m, k, nullptr);
   if (st) return st;
-  WH_HIP_TRY(hipMemcpy(output, dy.p, m * sizeof(float), hipMemcpyDeviceToHost));
+  WH_HIP_TRY(hipMemcpy(output, dy, m * sizeof(float), hipMemcpyDeviceToHost));
   return WH_OK;
 }
 

@@ -648,8 +648,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
     attn_combine_kernel<128><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
   } else {
     const size_t lds = partial_lds<64>(G, chunk);
-    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_partial_kernel<64>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    WH_ENSURE_LDS(lds, &attn_partial_kernel<64>);
     attn_partial_kernel<64><<<grid, kAttnThreads, lds, s>>>(
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);

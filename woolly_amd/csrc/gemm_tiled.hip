@@ -803,8 +803,7 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   constexpr int ALIGN = TYPE == wh::kGemmQ4F ? 8 : SB;   // kGemmQ4F: whole super-blocks per split
   bps = (bps + ALIGN - 1) / ALIGN * ALIGN;
   const size_t lds = tiled_lds_bytes<TYPE, BM>();
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM>);
   dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
   gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
                                                            static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
@@ -821,8 +820,7 @@ int launch_ffn_bm(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k,
   const int tiles_n = static_cast<int>((n_ff + TBN / 2 - 1) / (TBN / 2));
   const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
   const size_t lds = tiled_lds_bytes<TYPE, BM>();
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_tiled_kernel<TYPE, BM, true>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, true>);
   gemm_tiled_kernel<TYPE, BM, true><<<static_cast<unsigned>(tiles_m * tiles_n), TWAVES * 64, lds, s>>>(
       gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
       tiles_m * tiles_n);

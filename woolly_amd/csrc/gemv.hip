@@ -719,8 +719,7 @@ bool stream_ok(const GemvArgs& a, size_t k) {
 
 template <int TYPE, bool FFN, int RD, int MODE>
 int launch_ring(const GemvArgs& a, int grid, size_t lds, hipStream_t s) {
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_ring_kernel<TYPE, FFN, RD, MODE>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, &gemv_ring_kernel<TYPE, FFN, RD, MODE>);
   gemv_ring_kernel<TYPE, FFN, RD, MODE><<<grid, kWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
   return WH_OK;
@@ -767,10 +766,7 @@ int launch_stream(GemvArgs a, size_t k, hipStream_t s) {
     if (ring_lds_bytes(TYPE, K, nm, 2) <= maxl)
       return launch_ring<TYPE, FFN, 2, MODE>(a, grid, ring_lds_bytes(TYPE, K, nm, 2), s);
   }
-  if (lds > 65536) {
-    WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream_kernel<TYPE, FFN, MODE>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-  }
+  if (lds > 65536) WH_ENSURE_LDS(lds, &gemv_stream_kernel<TYPE, FFN, MODE>);
   gemv_stream_kernel<TYPE, FFN, MODE><<<grid, kWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK(FFN ? "ffn gate/up kernel launch" : "gemv kernel launch");
   return WH_OK;

@@ -1279,8 +1279,7 @@ int mg_segments(int type, size_t ppr) {
 template <int TYPE, int NSEG, int NL, int MODE, int DEPTH = 1>
 int mg_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
   auto* fn = &gemv_mfma_kernel<TYPE, NSEG, NL, MODE, DEPTH>;
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, fn);
   fn<<<grid, kMgWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK("gemv (mfma) kernel launch");
   return WH_OK;
@@ -1318,8 +1317,7 @@ int mg_typed(const MgArgs& a, int nseg, int mode, int grid, size_t lds, hipStrea
 template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS = 4>
 int mt_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
   auto* fn = &gemv_mt_kernel<TYPE, NSEG, NL, MODE, TG, MS>;
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, fn);
   fn<<<grid, kMgWaves * 64, lds, s>>>(a);
   WH_LAUNCH_CHECK("gemv (several tokens) kernel launch");
   return WH_OK;
@@ -1465,8 +1463,7 @@ int launch_gemv_mfma2(int type_a, const void* const* mats_a, const size_t* rows_
     return WH_ERR_INVALID_SHAPE;
   const size_t lds = lds_a > lds_b ? lds_a : lds_b;
   auto* fn = &gemv_mfma2_kernel<WH_TYPE_Q4_K, 3, WH_TYPE_Q6_K, 4, kMgNorm>;
-  WH_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 static_cast<int>(lds)));
+  WH_ENSURE_LDS(lds, fn);
   fn<<<static_cast<unsigned>(grid_a + grid_b), kMgWaves * 64, lds, s>>>(a, b, static_cast<int>(grid_a));
   WH_LAUNCH_CHECK("gemv (mfma, two types) kernel launch");
   return WH_OK;

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/woolly_hip.h"
 
 namespace wh {
@@ -83,13 +85,35 @@ inline size_t kquant_repacked_bytes(int type, size_t n_rows, size_t k) {
 // Rewrites a Q4_K / Q6_K matrix (n_rows x k, 16-byte aligned) into the format above (kquant.hip).
 int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void* out, hipStream_t stream);
 
-// Number of compute units of the current device (cached per device).
+// Number of compute units of the current device (cached per device, no lock).
 int cu_count();
 // Looks up the current device's copy of the no-allocation decode step's
 // static scratch (decode.hip); called by wh_init.
 int init_step_scratch();
-// Largest LDS allocation one workgroup may use on the current device.
+// Largest LDS allocation one workgroup may use on the current device (cached
+// per device, no lock).
 size_t max_lds_per_block();
+
+// Devices the per-device caches of the library track.
+constexpr int kMaxDevices = 64;
+// The dynamic LDS limit set so far for one kernel, per device.
+struct LdsLimit {
+  std::atomic<int> set[kMaxDevices];
+};
+// Raises fn's dynamic LDS limit on the current device to at least `bytes`.
+// hipFuncSetAttribute is called only when a launch needs more than the limit
+// already set on this device (it costs microseconds of host time, which every
+// eager launch would otherwise pay).  Concurrent first calls may both set it.
+int ensure_dynamic_lds(LdsLimit& lim, const void* fn, size_t bytes);
+// The same with the kernel's own record, a static of the enclosing launcher
+// (one per template instantiation, so one per kernel).  The kernel comes last
+// so that template arguments with commas need no parentheses.
+#define WH_ENSURE_LDS(bytes, ...)                                                                          \
+  do {                                                                                                     \
+    static ::wh::LdsLimit _wh_lim;                                                                         \
+    const int _wh_st = ::wh::ensure_dynamic_lds(_wh_lim, reinterpret_cast<const void*>(__VA_ARGS__), (bytes)); \
+    if (_wh_st != 0) return _wh_st;                                                                        \
+  } while (0)
 
 // Launchers implemented in the .hip translation units.  Arguments have been
 // validated by the C ABI layer; these only choose kernels and launch them.

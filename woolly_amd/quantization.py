@@ -177,3 +177,34 @@ class optimized:  # noqa: N801 -- mirrors `quantization::optimized`
         if storage.scheme not in _DTYPE:
             raise QuantizationError.UnsupportedScheme("Unsupported storage type")
         return _dequantize(storage.scheme, storage.blocks)
+
+
+class device_cache:  # noqa: N801 -- the device copies behind the host-memory entry points
+    """Device copies of host weights behind simd.quantized_matvec and the
+    dequantize functions (wh_host_cache_*): the device-side counterpart of
+    DequantizationCache::get_or_dequantize
+    (crates/woolly-core/src/model/dequantization_cache.rs:121-165).  Off by
+    default; with a budget, a weight array is uploaded once per host address
+    and size and reused until evicted.  Cached arrays must not change."""
+
+    @staticmethod
+    def configure(max_bytes: int) -> None:
+        """Sets the byte budget; 0 turns the cache off and frees everything."""
+        _lib.check(_lib.load().wh_host_cache_configure(int(max_bytes)))
+
+    @staticmethod
+    def evict(array: np.ndarray) -> int:
+        """Drops every entry overlapping the array's bytes; returns how many."""
+        n = _lib.C.c_size_t(0)
+        _lib.check(_lib.load().wh_host_cache_evict(array.ctypes.data, array.nbytes, _lib.C.byref(n)))
+        return int(n.value)
+
+    @staticmethod
+    def clear() -> None:
+        _lib.check(_lib.load().wh_host_cache_clear())
+
+    @staticmethod
+    def stats() -> dict:
+        st = _lib.wh_host_cache_stats()
+        _lib.check(_lib.load().wh_host_cache_get_stats(_lib.C.byref(st)))
+        return {name: int(getattr(st, name)) for name, _ in st._fields_}
