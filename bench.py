@@ -23,10 +23,19 @@ Prints ONE JSON line with:
                  null when that summary was taken from other kernel sources;
                  read_floor: the same bytes read by wh_read_probe in the GEMV's
                  workgroup geometry with no compute, timed the same way (what one
-                 launch of this access pattern reaches on this part)
-  ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1 and
-                 M=512, same run (the metric's second part; M=1 rotates 3 layers'
-                 weights, 297 MB, past the Infinity Cache)
+                 launch of this access pattern reaches on this part), and as one
+                 flat range with every load in flight at once (what one launch
+                 reading these bytes reaches); launch_us_eager_*: the same GEMV
+                 launched one call at a time without a graph
+  ffn_layer_us   the fused SwiGLU FFN layer (Llama-3-8B shape, Q4_0) at M=1, 2, 4
+                 and 512, same run (the metric's second part; M <= 16 rotates
+                 3 layers' weights, 297 MB, past the Infinity Cache)
+  every leg      graph replays between events on the launch stream after ~0.1 s
+                 of clock settling, median of 5 measurements of >= 10 ms each;
+                 "spread" = (max - min) / median of the 5
+  prefill_*      config 2's M sweep (f32 and bf16 activations); the K-quant
+                 formats and Q4_1 at a few tokens, and at M=512 with blocks
+                 converted once per weight handle (and, for comparison, per call)
   gemv_other_configs  the other decode GEMV configurations: Q4_0 4096x4096,
                  Q8_0 and Q4_1 14336x4096, and the other decode-step shapes (k/v
                  projections, FFN down, the Q8_0 128256x4096 output head):
@@ -58,9 +67,10 @@ METRIC = "Q4_0 GEMV achieved HBM GB/s (% of peak); FFN-layer µs at M=1 and M=51
 Q4_0 = 2
 N_ROWS, K = 14336, 4096
 REPLICAS = 10
-WARM_S = 0.1          # untimed replays before each timed GEMV measurement (clock settling)
-TIMED_REPLAYS = 5     # timed measurements; the median is reported
-TIMED_LAUNCHES = 1000  # launches per measurement (back-to-back replays of the K-launch graph)
+WARM_S = 0.1          # untimed replays before each leg's timed measurements (clock settling)
+TIMED_REPLAYS = 5     # timed measurements per leg; the median is reported, with the spread
+TIMED_LAUNCHES = 1000  # GEMV: launches per measurement (back-to-back replays of the K-launch graph)
+MIN_MEASURE_MS = 10.0  # every leg: a measurement lasts at least this long
 
 
 TYPE_SIZE = {2: 18, 3: 20, 8: 34, 12: 144, 14: 210}
@@ -73,6 +83,47 @@ def gemv_bytes(n: int, k: int, t: int = Q4_0) -> int:
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def time_graph(run, n_calls: int, stream, min_launches: int = 1) -> tuple[float, float]:
+    """The timing every leg shares: run(i) for i < n_calls is captured once
+    into a HIP graph; one replay does the first-launch setup, untimed replays
+    run the GPU for WARM_S seconds (its clocks settle), then TIMED_REPLAYS
+    measurements each time back-to-back replays of the graph between two
+    events on the launch stream (at least min_launches calls and
+    MIN_MEASURE_MS per measurement, so the per-replay cost of a short graph
+    stays hidden behind the previous replay's kernels).  Returns (median ms
+    per call, spread = (max - min) / median of the measurements)."""
+    from woolly_amd.device import Event, Graph
+
+    with Graph.capture(stream) as graph:
+        for i in range(n_calls):
+            run(i)
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    graph.launch(stream)  # first-launch setup
+    e1.record(stream)
+    e1.synchronize()
+    first_ms = max(e0.elapsed_ms(e1), 1e-3)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARM_S:
+        graph.launch(stream)
+        stream.synchronize()
+    n_rep = max(1, -(-min_launches // n_calls), int(np.ceil(MIN_MEASURE_MS / first_ms)))
+    reps = []
+    for _ in range(TIMED_REPLAYS):
+        e0.record(stream)
+        for _ in range(n_rep):
+            graph.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        reps.append(e0.elapsed_ms(e1) / (n_rep * n_calls))
+    graph.destroy()
+    e0.destroy()
+    e1.destroy()
+    med = float(np.median(reps))
+    time_graph.calls_timed = n_rep * n_calls
+    return med, (max(reps) - min(reps)) / med
 
 
 def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int = K, seed: int = 3,
@@ -97,38 +148,28 @@ def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int =
         launch(i)
     stream.synchronize()
 
-    # The K timed launches are captured once into a HIP graph and replayed
-    # with one launch, so the host's per-call overhead does not throttle the
-    # GPU; events on the launch stream bracket each replay.  Untimed replays
-    # first run the GPU for ~100 ms so that its clocks have settled; the
-    # reported time is the median of TIMED_REPLAYS replays.
-    with Graph.capture(stream) as graph:
-        for i in range(steps):
-            launch(i)
-    graph.launch(stream)  # first-launch setup
-    stream.synchronize()
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < WARM_S:
-        graph.launch(stream)
-        stream.synchronize()
-    # each measurement: back-to-back replays of the graph between two events,
-    # at least TIMED_LAUNCHES launches, so that the per-replay cost of a short
-    # graph is hidden behind the previous replay's kernels
-    n_rep = max(1, -(-TIMED_LAUNCHES // steps))
-    e0, e1 = Event(), Event()
-    reps = []
-    for _ in range(TIMED_REPLAYS):
-        e0.record(stream)
-        for _ in range(n_rep):
-            graph.launch(stream)
-        e1.record(stream)
-        e1.synchronize()
-        reps.append(e0.elapsed_ms(e1) / n_rep)
-    ms_total = float(np.median(reps))
-    graph.destroy()
-    bench_gemv.launches_timed = n_rep * steps
+    # The K timed launches are captured once into a HIP graph and replayed, so
+    # the host's per-call overhead does not throttle the GPU (at least
+    # TIMED_LAUNCHES launches per measurement, median of TIMED_REPLAYS)
+    ms_per, spread = time_graph(launch, steps, stream, TIMED_LAUNCHES)
+    bench_gemv.launches_timed = time_graph.calls_timed
+    bench_gemv.spread = spread
 
-    # per-launch kernel duration: an event pair around every launch
+    # eager launches (no graph), as a caller launching one call at a time sees
+    # them: 200 back-to-back calls between two events, and an event pair
+    # around each of 200 calls
+    n_eager = 200
+    e0, e1 = Event(), Event()
+    for i in range(20):
+        launch(i)
+    e0.record(stream)
+    for i in range(n_eager):
+        launch(i)
+    e1.record(stream)
+    e1.synchronize()
+    bench_gemv.eager_back_to_back_ms = e0.elapsed_ms(e1) / n_eager
+    e0.destroy()
+    e1.destroy()
     n_pairs = min(steps, 200)
     evs = [(Event(), Event()) for _ in range(n_pairs)]
     for i, (a, b) in enumerate(evs):
@@ -140,60 +181,62 @@ def bench_gemv(steps: int, warmup: int, t: int = Q4_0, n: int = N_ROWS, k: int =
     for a, b in evs:
         a.destroy()
         b.destroy()
-    return ms_total / steps, float(np.median(durs)), float(np.mean(durs))
+    return ms_per, float(np.median(durs)), float(np.mean(durs))
 
 
-def bench_ffn(m: int, iters: int, t: int = Q4_0, replicas: int | None = None) -> float:
-    """The SwiGLU FFN layer (config 3, Llama-3-8B shape), µs per call.  The
-    weights of `replicas` layers (default: enough copies for > 256 MB, the
-    Infinity Cache, when the call streams its weights once, M <= 2) are
-    rotated, and the calls are captured into a HIP graph and replayed."""
+def bench_ffn(m: int, iters: int, t: int = Q4_0, replicas: int | None = None,
+              prepared: bool = False) -> tuple[float, float]:
+    """The SwiGLU FFN layer (config 3, Llama-3-8B shape), (µs per call,
+    spread).  The weights of `replicas` layers (default: enough copies for
+    > 256 MB, the Infinity Cache, when the call streams its weights once,
+    M <= 16) are rotated; the calls are captured into a HIP graph and replayed
+    (time_graph).  prepared: the weights are wh_weight handles whose K-quant
+    blocks were converted once for prefill (wh_weight_prepare_prefill)."""
     from woolly_amd import ops, synth
-    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+    from woolly_amd.device import DeviceBuffer, Stream
 
     hidden, n_ff = 4096, 14336
     L = synth.ffn_layer(t, hidden, n_ff, m, seed=5)
     wbytes = L["gate"].nbytes + L["up"].nbytes + L["down"].nbytes
     if replicas is None:
-        replicas = max(1, -(-300_000_000 // wbytes)) if m <= 2 else 1
+        replicas = max(1, -(-300_000_000 // wbytes)) if m <= 16 else 1
     stream = Stream()
-    copies = [{k: DeviceBuffer.from_array(L[k]) for k in ("gate", "up", "down")} for _ in range(replicas)]
+    if prepared:
+        shapes = {"gate": (n_ff, hidden), "up": (n_ff, hidden), "down": (hidden, n_ff)}
+        copies = [{k: ops.Weight(t, *shapes[k], L[k]) for k in shapes} for _ in range(replicas)]
+        for c in copies:
+            for w in c.values():
+                w.prepare_prefill(stream)
+        ptrs = [{k: w.ptr for k, w in c.items()} for c in copies]
+    else:
+        copies = [{k: DeviceBuffer.from_array(L[k]) for k in ("gate", "up", "down")} for _ in range(replicas)]
+        ptrs = copies
     b = {k: DeviceBuffer.from_array(L[k]) for k in ("gamma", "x")}
     out = DeviceBuffer(4 * m * hidden)
     wsz = ops.ffn_workspace_bytes(hidden, n_ff, m, ggml_type=t)
     ws = DeviceBuffer(wsz)
 
     def run(i):
-        c = copies[i % replicas]
+        c = ptrs[i % replicas]
         ops.ffn_swiglu(t, c["gate"], c["up"], c["down"], hidden, n_ff, b["gamma"], 1e-5, b["x"],
                        m, out, ws, wsz, stream)
 
     for i in range(3):
         run(i)
     stream.synchronize()
-    n = max(iters, replicas)
-    with Graph.capture(stream) as graph:
-        for i in range(n):
-            run(i)
-    graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = Event(), Event()
-    e0.record(stream)
-    for _ in range(3):
-        graph.launch(stream)
-    e1.record(stream)
-    e1.synchronize()
-    graph.destroy()
-    return e0.elapsed_ms(e1) / (3 * n) * 1000.0
+    ms, spread = time_graph(run, max(iters, replicas), stream)
+    return ms * 1000.0, spread
 
 
-def bench_gemm(m: int, iters: int, t: int = Q4_0, bf16: bool = False) -> float:
+def bench_gemm(m: int, iters: int, t: int = Q4_0, bf16: bool = False, prepared: bool = False) -> tuple[float, float]:
     """Prefill GEMM Y[m, 14336] = X[m, 4096] W^T (config 2; Q4_0 unless t; X in
-    bfloat16 with bf16), µs per call.  For m <= 64, where the call streams its
-    33 MB of weights about once, 10 weight copies (> 256 MB, the Infinity
-    Cache) are rotated; the calls are captured into a HIP graph and replayed."""
+    bfloat16 with bf16), (µs per call, spread).  For m <= 64, where the call
+    streams its 33 MB of weights about once, 10 weight copies (> 256 MB, the
+    Infinity Cache) are rotated; the calls are captured into a HIP graph and
+    replayed (time_graph).  prepared: the weights are wh_weight handles whose
+    K-quant blocks were converted once for prefill."""
     from woolly_amd import ops, synth
-    from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
+    from woolly_amd.device import DeviceBuffer, Stream
 
     w = synth.quantized_weight(t, N_ROWS, K, seed=4)
     x = np.concatenate([synth.activations(K, seed=400 + i) for i in range(min(m, 64))])
@@ -202,7 +245,13 @@ def bench_gemm(m: int, iters: int, t: int = Q4_0, bf16: bool = False) -> float:
         x = (x.view(np.uint32) >> 16).astype(np.uint16)
     replicas = 10 if m <= 64 else 1
     stream = Stream()
-    wbs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
+    if prepared:
+        handles = [ops.Weight(t, N_ROWS, K, w) for _ in range(replicas)]
+        for h in handles:
+            h.prepare_prefill(stream)
+        wbs = [h.ptr for h in handles]
+    else:
+        wbs = [DeviceBuffer.from_array(w) for _ in range(replicas)]
     xb = DeviceBuffer.from_array(x)
     yb = DeviceBuffer(4 * m * N_ROWS)
     wsz = (ops.matmul_x_workspace_bytes(t, N_ROWS, K, m, ops.TYPE_BF16) if bf16
@@ -219,20 +268,8 @@ def bench_gemm(m: int, iters: int, t: int = Q4_0, bf16: bool = False) -> float:
     for i in range(3):
         run(i)
     stream.synchronize()
-    n = max(iters, replicas)
-    with Graph.capture(stream) as graph:
-        for i in range(n):
-            run(i)
-    graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = Event(), Event()
-    e0.record(stream)
-    for _ in range(3):
-        graph.launch(stream)
-    e1.record(stream)
-    e1.synchronize()
-    graph.destroy()
-    return e0.elapsed_ms(e1) / (3 * n) * 1000.0
+    ms, spread = time_graph(run, max(iters, replicas), stream)
+    return ms * 1000.0, spread
 
 
 # config 4: Llama-3-8B-shaped decode step
@@ -309,23 +346,13 @@ def bench_decode(steps: int, c: dict = L8B, types: dict | None = None, head_type
     for _ in range(3):
         model.decode_step(pos, xb, lb, ws, wsz, stream)
     stream.synchronize()
-    with Graph.capture(stream) as graph:
-        model.decode_step(pos, xb, lb, ws, wsz, stream)
-    graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = Event(), Event()
-    e0.record(stream)
-    for _ in range(steps):
-        graph.launch(stream)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
-    graph.destroy()
+    ms, spread = time_graph(lambda i: model.decode_step(pos, xb, lb, ws, wsz, stream), 1, stream, steps)
     logits = lb.download(np.float32, c["vocab"])
     nb = decode_bytes(c, types, head_type)
     return {"tokens_per_s": round(1000.0 / ms, 1), "ms_per_token": round(ms, 4), "bytes_per_token": nb,
             "GBps": round(nb / (ms * 1e-3) / 1e9, 1), "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "ctx": c["ctx"], "layers": c["n_layers"], "logits_finite": bool(np.all(np.isfinite(logits)))}
+            "ctx": c["ctx"], "layers": c["n_layers"], "spread": round(spread, 4),
+            "logits_finite": bool(np.all(np.isfinite(logits)))}
 
 
 def bench_attention(iters: int, c: dict = L8B) -> dict:
@@ -359,22 +386,9 @@ def bench_attention(iters: int, c: dict = L8B) -> dict:
     for i in range(reps):
         run(i)
     stream.synchronize()
-    with Graph.capture(stream) as graph:
-        for i in range(iters):
-            run(i)
-    graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = Event(), Event()
-    res = []
-    for _ in range(5):
-        e0.record(stream)
-        graph.launch(stream)
-        e1.record(stream)
-        e1.synchronize()
-        res.append(e0.elapsed_ms(e1) / iters)
-    graph.destroy()
-    ms = float(np.median(res))
-    return {"us": round(ms * 1e3, 3), "kv_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "ctx": ctx}
+    ms, spread = time_graph(run, max(iters, reps), stream)
+    return {"us": round(ms * 1e3, 3), "kv_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "ctx": ctx,
+            "spread": round(spread, 4)}
 
 
 def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N_ROWS, k: int = K,
@@ -383,7 +397,9 @@ def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N
     same N rows of K/32 Q4_0 blocks, rotated through the same number of copies
     and timed the same way (graph replay between events, after clock settling),
     read in the GEMV's workgroup geometry without storing or computing anything.
-    mode 0: one step in flight per wave, as the GEMV; mode 1: up to four.
+    mode 0: one step in flight per wave, as the GEMV; mode 1: up to four;
+    mode 2: not the GEMV's geometry: the same bytes as one flat range, one
+    contiguous piece per workgroup, every load of a lane in flight at once.
     Returns ms per launch."""
     from woolly_amd import _lib, synth
     from woolly_amd.device import DeviceBuffer, Event, Graph, Stream
@@ -401,27 +417,8 @@ def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N
     for i in range(warmup):
         launch(i)
     stream.synchronize()
-    with Graph.capture(stream) as graph:
-        for i in range(steps):
-            launch(i)
-    graph.launch(stream)
-    stream.synchronize()
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < WARM_S:
-        graph.launch(stream)
-        stream.synchronize()
-    n_rep = max(1, -(-TIMED_LAUNCHES // steps))
-    e0, e1 = Event(), Event()
-    reps = []
-    for _ in range(TIMED_REPLAYS):
-        e0.record(stream)
-        for _ in range(n_rep):
-            graph.launch(stream)
-        e1.record(stream)
-        e1.synchronize()
-        reps.append(e0.elapsed_ms(e1) / n_rep)
-    graph.destroy()
-    return float(np.median(reps)) / steps
+    ms, _ = time_graph(launch, steps, stream, TIMED_LAUNCHES)
+    return ms
 
 
 def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
@@ -565,6 +562,8 @@ def main() -> int:
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of --only gemm / --only ffn")
     ap.add_argument("--type", type=int, default=Q4_0,
                     help="ggml type id of --only gemm / ffn1 / ffn512 (default Q4_0)")
+    ap.add_argument("--prepared", action="store_true",
+                    help="--only gemm / ffn: K-quant weights as handles converted once (wh_weight_prepare_prefill)")
     ap.add_argument("--gemv-shape", type=int, nargs=3, default=None, metavar=("TYPE", "N", "K"),
                     help="ggml type id and shape of --only gemv (default Q4_0 14336 4096)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -595,8 +594,9 @@ def main() -> int:
                           "GBps": round(gemv_bytes(n, k, t) / (ms_step * 1e-3) / 1e9, 1)}))
         return 0
     if args.only == "gemm":
-        print(json.dumps({f"gemm_m{args.gemm_m}_us": round(bench_gemm(args.gemm_m, 5, args.type), 2),
-                          "type": args.type}))
+        us, spread = bench_gemm(args.gemm_m, 5, args.type, prepared=args.prepared)
+        print(json.dumps({f"gemm_m{args.gemm_m}_us": round(us, 2), "spread": round(spread, 4), "type": args.type,
+                          "prepared": args.prepared}))
         return 0
     if args.only == "decode":
         print(json.dumps({"decode_step": bench_decode(10)}))
@@ -609,38 +609,40 @@ def main() -> int:
         return 0
     if args.only in ("ffn1", "ffn512", "ffn"):
         m = 1 if args.only == "ffn1" else 512 if args.only == "ffn512" else args.gemm_m
-        print(json.dumps({f"ffn_m{m}_us": round(bench_ffn(m, 20 if m == 1 else 3, args.type), 2),
-                          "type": args.type}))
+        us, spread = bench_ffn(m, 20 if m == 1 else 3, args.type, prepared=args.prepared)
+        print(json.dumps({f"ffn_m{m}_us": round(us, 2), "spread": round(spread, 4), "type": args.type,
+                          "prepared": args.prepared}))
         return 0
     ms_step, med_ms, mean_ms = bench_gemv(args.steps, args.warmup)
+    eager_b2b_ms, gemv_spread = bench_gemv.eager_back_to_back_ms, bench_gemv.spread
     traffic, traffic_status = traffic_from_profile()
     nbytes = gemv_bytes(N_ROWS, K)
     value = nbytes / (ms_step * 1e-3) / 1e9
     # the GEMV is the only kernel of a step: its average launch duration is the
     # timed region (graph replay, events on the launch stream) divided by K
     achieved = value
-    log(f"[bench] gemv: {ms_step * 1e3:.2f} us/step back-to-back, per-launch mean "
-        f"{mean_ms * 1e3:.2f} us (median {med_ms * 1e3:.2f})")
+    log(f"[bench] gemv: {ms_step * 1e3:.2f} us/step in a graph (spread {gemv_spread:.3f}), eager back-to-back "
+        f"{eager_b2b_ms * 1e3:.2f} us, eager between event pairs mean {mean_ms * 1e3:.2f} us (median {med_ms * 1e3:.2f})")
     # the same bytes read in the GEMV's geometry with nothing else done: what
-    # this access pattern and one launch per call can reach on this part
+    # this access pattern and one launch per call can reach on this part; and
+    # the same bytes with every load in flight at once (the floor of one launch)
     floor = {}
-    for mode, name in ((0, "gemv_geometry_1_step_in_flight"), (1, "gemv_geometry_4_steps_in_flight")):
+    for mode, name in ((0, "gemv_geometry_1_step_in_flight"), (1, "gemv_geometry_4_steps_in_flight"),
+                       (2, "flat_every_load_in_flight")):
         ms = bench_stream_floor(mode, args.steps, args.warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         floor[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"[bench] read floor ({name}): {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
     floor["gemv_us_over_floor_us"] = round(ms_step * 1e3 / floor["gemv_geometry_1_step_in_flight"]["us"], 3)
+    floor["gemv_us_over_flat_floor_us"] = round(ms_step * 1e3 / floor["flat_every_load_in_flight"]["us"], 3)
 
-    ffn = {}
+    ffn, ffn_spread = {}, {}
     if not args.no_ffn:
-        ffn["m1"] = round(bench_ffn(1, 50), 2)
-        log(f"[bench] ffn m=1: {ffn['m1']} us")
-        # a few tokens (speculative / batched decode): one pass of the weights
-        for m in (2, 4):
-            ffn[f"m{m}"] = round(bench_ffn(m, 50), 2)
-            log(f"[bench] ffn m={m}: {ffn[f'm{m}']} us ({ffn[f'm{m}'] / ffn['m1']:.2f}x m=1)")
-        ffn["m512"] = round(bench_ffn(512, 3), 2)
-        log(f"[bench] ffn m=512: {ffn['m512']} us")
+        for m in (1, 2, 4, 512):
+            us, sp = bench_ffn(m, 50 if m <= 16 else 3)
+            ffn[f"m{m}"], ffn_spread[f"m{m}"] = round(us, 2), round(sp, 4)
+            log(f"[bench] ffn m={m}: {ffn[f'm{m}']} us (spread {sp:.3f})"
+                + (f", {us / ffn['m1']:.2f}x m=1" if m > 1 and m <= 16 else ""))
 
     gemm, gemm_kq = {}, {}
     if not args.no_gemm:
@@ -648,27 +650,40 @@ def main() -> int:
         # the MFMA path issues two fp16 products per multiply-add (activation
         # hi and lo halves), so its MFMA work is twice that.
         for m in (1, 2, 4, 8, 16, 64, 512, 2048):
-            us = bench_gemm(m, 20 if m <= 64 else 5)
+            us, sp = bench_gemm(m, 20 if m <= 64 else 5)
             tf = 2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12
-            gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2)}
-            log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s")
+            gemm[f"m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2), "spread": round(sp, 4)}
+            log(f"[bench] gemm m={m}: {us:.2f} us, {tf:.1f} TFLOP/s (spread {sp:.3f})")
         for m in (8, 512):
-            us = bench_gemm(m, 20 if m <= 64 else 5, bf16=True)
-            gemm[f"m{m}_bf16"] = {"us": round(us, 2), "tflops": round(2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12, 2)}
+            us, sp = bench_gemm(m, 20 if m <= 64 else 5, bf16=True)
+            gemm[f"m{m}_bf16"] = {"us": round(us, 2), "tflops": round(2.0 * m * N_ROWS * K / (us * 1e-6) / 1e12, 2),
+                                  "spread": round(sp, 4)}
             log(f"[bench] gemm bf16 activations m={m}: {us:.2f} us")
-        # K-quant weights at M=512: the call includes rewriting the matrix into
-        # 32-element f32-scale blocks (Q6_K: zero-padded 16-element halves)
-        for name, t in (("q4_k", 12), ("q6_k", 14)):
-            us = bench_gemm(512, 5, t)
-            tf = 2.0 * 512 * N_ROWS * K / (us * 1e-6) / 1e12
-            gemm_kq[f"gemm_{name}_m512"] = {"us": round(us, 2), "tflops": round(tf, 2)}
-            log(f"[bench] gemm {name} m=512: {us:.2f} us, {tf:.1f} TFLOP/s")
+        # K-quant weights (and Q4_1): a few tokens stream the blocks once
+        # (several-token GEMV); at M=512 the tiled GEMM, on a copy converted
+        # once per handle (wh_weight_prepare_prefill) and, for comparison, with
+        # the conversion inside every call
+        for name, t in (("q4_k", 12), ("q6_k", 14), ("q4_1", 3)):
+            for m in ((1, 2, 8, 16) if t == 12 else (1, 8)):
+                us, sp = bench_gemm(m, 20, t)
+                gemm_kq[f"gemm_{name}_m{m}"] = {"us": round(us, 2), "spread": round(sp, 4)}
+                log(f"[bench] gemm {name} m={m}: {us:.2f} us")
+            if t == 3:
+                continue
+            for prep in (True, False):
+                us, sp = bench_gemm(512, 5, t, prepared=prep)
+                tf = 2.0 * 512 * N_ROWS * K / (us * 1e-6) / 1e12
+                key = f"gemm_{name}_m512" + ("" if prep else "_converting")
+                gemm_kq[key] = {"us": round(us, 2), "tflops": round(tf, 2), "spread": round(sp, 4)}
+                log(f"[bench] gemm {name} m=512{'' if prep else ' (conversion per call)'}: {us:.2f} us, "
+                    f"{tf:.1f} TFLOP/s")
         if not args.no_ffn:
             for name, t in (("q4_k", 12), ("q6_k", 14)):
-                gemm_kq[f"ffn_{name}_m1_us"] = round(bench_ffn(1, 50, t), 2)
-                gemm_kq[f"ffn_{name}_m512_us"] = round(bench_ffn(512, 3, t), 2)
-                log(f"[bench] ffn {name}: m=1 {gemm_kq[f'ffn_{name}_m1_us']} us, "
-                    f"m=512 {gemm_kq[f'ffn_{name}_m512_us']} us")
+                us1, _ = bench_ffn(1, 50, t)
+                us512, sp = bench_ffn(512, 3, t, prepared=True)
+                gemm_kq[f"ffn_{name}_m1_us"] = round(us1, 2)
+                gemm_kq[f"ffn_{name}_m512_us"] = round(us512, 2)
+                log(f"[bench] ffn {name}: m=1 {us1:.2f} us, m=512 {us512:.2f} us (prepared handles)")
 
     # the other decode GEMV configurations (config 0, 1a, 1b); replicas keep
     # each timed set of weights above the 256 MB Infinity Cache
@@ -690,7 +705,8 @@ def main() -> int:
             ms, _, _ = bench_gemv(100, 10, t, n, k, seed, reps)
             gbs = gemv_bytes(n, k, t) / (ms * 1e-3) / 1e9
             gemv_cfg[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
-                              "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t)}
+                              "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": gemv_bytes(n, k, t),
+                              "spread": round(bench_gemv.spread, 4)}
             log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
 
     decode = decode_km = attn = None
@@ -743,9 +759,12 @@ def main() -> int:
             "launch_us_mean": round(ms_step * 1e3, 3),
             "launches_timed": bench_gemv.launches_timed,
             "launch_us_eager_event_pairs": round(mean_ms * 1e3, 3),
+            "launch_us_eager_back_to_back": round(eager_b2b_ms * 1e3, 3),
+            "spread": round(gemv_spread, 4),
             "read_floor": floor,
         },
         "ffn_layer_us": ffn or None,
+        "ffn_layer_spread": ffn_spread or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,
         "prefill_kquant_14336x4096": gemm_kq or None,
         "gemv_other_configs": gemv_cfg or None,

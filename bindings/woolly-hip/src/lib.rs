@@ -289,6 +289,9 @@ extern "C" {
     pub fn wh_weight_data(weight: *const wh_weight) -> *const c_void;
     pub fn wh_weight_info(weight: *const wh_weight, r#type: *mut c_int, n_rows: *mut usize, k: *mut usize,
                           nbytes: *mut usize) -> c_int;
+    // convert-once copy for prefill (dequantization_cache.rs:121-165)
+    pub fn wh_weight_prepare_prefill(weight: *mut wh_weight, stream: wh_stream_t, prepared_bytes: *mut usize)
+                                     -> c_int;
 
     // synchronous host-memory variants
     pub fn wh_dequantize_host(r#type: c_int, data: *const c_void, nbytes: usize, nelements: usize,

@@ -119,7 +119,9 @@ WH_API int wh_graph_destroy(wh_graph_t graph);
  * row per wave per step, 16-byte loads) without storing or computing
  * anything but a checksum per workgroup: out is a device array of at least
  * ceil(n_rows / 16) dwords.  mode 0: one step in flight per wave, as the
- * GEMV; mode 1: up to four. */
+ * GEMV; mode 1: up to four; mode 2: the matrix read as one flat byte range,
+ * one contiguous piece per workgroup (one workgroup per CU, more for
+ * matrices past 64 MiB), every load of a lane in flight at once. */
 WH_API int wh_read_probe(const void* src, size_t row_bytes, size_t n_rows, int mode, uint32_t* out,
                          wh_stream_t stream);
 
@@ -263,6 +265,21 @@ WH_API int wh_weight_free(wh_weight* weight);
 WH_API const void* wh_weight_data(const wh_weight* weight);
 WH_API int wh_weight_info(const wh_weight* weight, int* type, size_t* n_rows, size_t* k,
                           size_t* nbytes);
+/* Converts a Q4_K / Q6_K handle's blocks once, on the stream, into the block
+ * layout of the tiled prefill GEMM (the same values: 32-element blocks with
+ * f32 scales d * s_j, Q6_K's 16-element halves padded) and keeps that copy
+ * with the handle until wh_weight_free; calls of wh_quantized_matmul and
+ * wh_ffn_swiglu with more than two tokens whose weight pointer is the
+ * handle's data (wh_weight_data) then skip the per-call conversion.  This is
+ * the device-side counterpart of the reference's convert-once cache
+ * (DequantizationCache::get_or_dequantize,
+ * crates/woolly-core/src/model/dequantization_cache.rs:121-165,
+ * LazyModelWeights::get_tensor_cached, model/lazy_loader.rs:599-659).  The
+ * copy takes 656 bytes per 1024 elements for Q4_K (576 in the file) and 1280
+ * for Q6_K (840) of device memory.  A no-op for the other block types, whose blocks the
+ * GEMM reads directly.  Idempotent; *prepared_bytes (may be null) receives
+ * the copy's size. */
+WH_API int wh_weight_prepare_prefill(wh_weight* weight, wh_stream_t stream, size_t* prepared_bytes);
 
 /* ------------------------------------- synchronous host-pointer variants */
 /* Same semantics as the device entry points, on host memory, blocking.  They

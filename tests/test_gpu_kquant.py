@@ -244,3 +244,53 @@ def test_kquant_matmul_unaligned_weights(gpu, orc, t):
     ref = orc.matmul_rows_f64(t, w, n, k, x, m, np.arange(m))
     assert rel_l2(got, ref) <= 1e-4 and max_abs(got, ref) <= 1e-3
     assert rel_l2(got, kq_matmul(t, w, x, m, n, k)) <= 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_kquant_prepared_prefill(gpu, orc, t):
+    """wh_weight_prepare_prefill converts a handle's blocks once (the reference's
+    convert-once cache, dequantization_cache.rs:121-165); matmul and FFN calls
+    on the handle's data then skip the per-call conversion and give the same
+    bits as the converting call, at the north-star bar against the f64 oracle.
+    Preparing again is a no-op; a Q4_0 handle needs no copy."""
+    m, n, k = 64, 512, 4096
+    w = synth.quantized_weight(t, n, k, seed=500 + t)
+    x = synth.activations(m * k, seed=501).reshape(m, k)
+    plain = kq_matmul(t, w, x, m, n, k)
+    wh = ops.Weight(t, n, k, w)
+    size = wh.prepare_prefill()
+    assert size == (n * (k // 32 * 20 + k // 256 * 4) if t == Q4_K else n * k // 16 * 20)
+    assert wh.prepare_prefill() == size
+    xb, xp = up(x)
+    yb = DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_workspace_bytes(t, n, k, m)
+    ws = DeviceBuffer(wsz)
+    ops.quantized_matmul(t, wh.ptr, wh.nbytes, n, k, xp, m, yb.ptr, ws, wsz)
+    got = down(yb, np.float32, m * n).reshape(m, n)
+    assert same(got, plain)
+    ref = orc.matmul_rows_f64(t, w, n, k, x, m, np.arange(m))
+    assert rel_l2(got, ref) <= 1e-4 and max_abs(got, ref) <= 1e-3
+    # the FFN layer with prepared gate / up / down handles against the converting call
+    hidden, n_ff, mf = 4096, 1024, 64
+    L = synth.ffn_layer(t, hidden, n_ff, mf, seed=510 + t)
+    bufs = {name: up(v) for name, v in L.items()}
+    wsz = ops.ffn_workspace_bytes(hidden, n_ff, mf, ggml_type=t)
+    ws = DeviceBuffer(wsz)
+    ob = DeviceBuffer(4 * mf * hidden)
+    ops.ffn_swiglu(t, bufs["gate"][1], bufs["up"][1], bufs["down"][1], hidden, n_ff,
+                   bufs["gamma"][1], 1e-5, bufs["x"][1], mf, ob.ptr, ws.ptr, wsz)
+    base = down(ob, np.float32, mf * hidden)
+    hw = {name: ops.Weight(t, *((n_ff, hidden) if name != "down" else (hidden, n_ff)), L[name])
+          for name in ("gate", "up", "down")}
+    for h in hw.values():
+        assert h.prepare_prefill() > 0
+    ob2 = DeviceBuffer(4 * mf * hidden)
+    ops.ffn_swiglu(t, hw["gate"].ptr, hw["up"].ptr, hw["down"].ptr, hidden, n_ff,
+                   bufs["gamma"][1], 1e-5, bufs["x"][1], mf, ob2.ptr, ws.ptr, wsz)
+    assert same(down(ob2, np.float32, mf * hidden), base)
+    for h in hw.values():
+        h.free()
+    wh.free()
+    q = ops.Weight(2, 64, 256, synth.quantized_weight(2, 64, 256, seed=1))
+    assert q.prepare_prefill() == 0
+    q.free()

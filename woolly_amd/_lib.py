@@ -186,6 +186,7 @@ SIGNATURES = {
     "wh_weight_data": (_vp, [_vp]),
     "wh_weight_info": (_int, [_vp, C.POINTER(_int), C.POINTER(_sz), C.POINTER(_sz),
                               C.POINTER(_sz)]),
+    "wh_weight_prepare_prefill": (_int, [_vp, _vp, C.POINTER(_sz)]),
     "wh_dequantize_host": (_int, [_int, _vp, _sz, _sz, _f32p]),
     "wh_quantized_matvec_host": (_int, [_int, _vp, _sz, _f32p, _f32p, _sz, _sz]),
     "wh_host_cache_configure": (_int, [_sz]),

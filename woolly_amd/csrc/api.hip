@@ -22,6 +22,8 @@ struct wh_weight {
   size_t nbytes;
   void* data;
   int device;
+  void* prefill = nullptr;    // wh_weight_prepare_prefill's copy (K-quants)
+  size_t prefill_bytes = 0;
 };
 
 namespace {
@@ -88,6 +90,17 @@ int check_ptr(const char* fn, const char* what, const void* p, size_t align) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Handles with a prepared prefill copy, by their data pointer.  Allocated once
+// and never destroyed (no destructor runs after the HIP runtime at exit).
+struct PreparedRegistry {
+  std::mutex mu;
+  std::map<const void*, const wh_weight*> by_data;
+};
+PreparedRegistry& prepared_registry() {
+  static PreparedRegistry* r = new PreparedRegistry();
+  return *r;
+}
+
 }  // namespace
 
 namespace wh {
@@ -109,6 +122,15 @@ int cu_count() { return cached_attribute(g_cu_count, hipDeviceAttributeMultiproc
 
 size_t max_lds_per_block() {
   return static_cast<size_t>(cached_attribute(g_max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 65536));
+}
+
+const void* prepared_kquant(const void* w, int type, size_t n_rows, size_t k) {
+  PreparedRegistry& r = prepared_registry();
+  std::lock_guard<std::mutex> lk(r.mu);
+  auto it = r.by_data.find(w);
+  if (it == r.by_data.end()) return nullptr;
+  const wh_weight* h = it->second;
+  return (h->type == type && h->n_rows == n_rows && h->k == k) ? h->prefill : nullptr;
 }
 
 int ensure_dynamic_lds(LdsLimit& lim, const void* fn, size_t bytes) {
@@ -637,8 +659,42 @@ WH_API int wh_weight_upload(int type, size_t n_rows, size_t k, const void* host_
   return WH_OK;
 }
 
+WH_API int wh_weight_prepare_prefill(wh_weight* weight, wh_stream_t stream, size_t* prepared_bytes) {
+  if (!weight) return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_prepare_prefill: null handle");
+  if (prepared_bytes) *prepared_bytes = weight->prefill_bytes;
+  if (!wh::is_kquant(weight->type) || weight->prefill || weight->n_rows == 0 || weight->k == 0) return WH_OK;
+  if (!wh::aligned(weight->data, 16))
+    return wh::set_error(WH_ERR_INVALID_ARGUMENT, "weight_prepare_prefill: data is not 16-byte aligned");
+  const size_t bytes = wh::kquant_repacked_bytes(weight->type, weight->n_rows, weight->k);
+  void* copy = nullptr;
+  WH_HIP_TRY(hipMalloc(&copy, bytes));
+  const int st = wh::launch_repack_kquant(weight->type, weight->data, weight->n_rows, weight->k, copy, hs(stream));
+  if (st) {
+    (void)hipFree(copy);
+    return st;
+  }
+  weight->prefill = copy;
+  weight->prefill_bytes = bytes;
+  {
+    PreparedRegistry& r = prepared_registry();
+    std::lock_guard<std::mutex> lk(r.mu);
+    r.by_data[weight->data] = weight;
+  }
+  if (prepared_bytes) *prepared_bytes = bytes;
+  return WH_OK;
+}
+
 WH_API int wh_weight_free(wh_weight* weight) {
   if (!weight) return WH_OK;
+  if (weight->prefill) {
+    {
+      PreparedRegistry& r = prepared_registry();
+      std::lock_guard<std::mutex> lk(r.mu);
+      r.by_data.erase(weight->data);
+    }
+    (void)hipFree(weight->prefill);
+    weight->prefill = nullptr;
+  }
   if (weight->data) {
     const hipError_t e = hipFree(weight->data);
     delete weight;

@@ -1040,10 +1040,13 @@ int launch_gemm_kquant(int type, const void* w, size_t n_rows, size_t k, const f
   const size_t kk = kquant_gemm_k(type, k);
   char* rp = static_cast<char*>(workspace);
   const TiledWs t = tiled_ws(it, n_rows, kk, n_tokens, rp + al256(kquant_repacked_bytes(type, n_rows, k)));
-  int st = launch_repack_kquant(type, w, n_rows, k, rp, s);
+  // a handle's copy prepared once (wh_weight_prepare_prefill), else a conversion per call
+  const char* src = static_cast<const char*>(prepared_kquant(w, type, n_rows, k));
+  int st = src ? WH_OK : launch_repack_kquant(type, w, n_rows, k, rp, s);
+  if (!src) src = rp;
   if (!st) st = tiled_pack<kPackPlain>(it, t, x, nullptr, nullptr, 0.f, n_tokens, kk, k, s);
   if (st) return st;
-  return kquant_run(type, rp, n_rows, k, n_tokens, t, y, s);
+  return kquant_run(type, src, n_rows, k, n_tokens, t, y, s);
 }
 
 size_t ffn_kquant_workspace_bytes(int type, size_t hidden, size_t n_ff, size_t n_tokens) {
@@ -1073,18 +1076,25 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
         !gemm_kquant_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16) ||
         !aligned(workspace, 256) || workspace_bytes < ffn_kquant_workspace_bytes(type, hidden, n_ff, n_tokens))
       return WH_ERR_INVALID_SHAPE;
+    // each matrix: its handle's prepared copy, or converted into rp for this call
+    auto repacked = [&](const void* w, size_t rows, size_t k, const char** out_rp) -> int {
+      const char* pre = static_cast<const char*>(prepared_kquant(w, type, rows, k));
+      *out_rp = pre ? pre : rp;
+      return pre ? WH_OK : launch_repack_kquant(type, w, rows, k, rp, s);
+    };
+    const char* src = nullptr;
     const TiledWs t1 = tiled_ws(it, n_ff, H2, n_tokens, ws);
     int st = tiled_pack<kPackNorm>(it, t1, x, nullptr, gamma, eps, n_tokens, H2, hidden, s);
-    if (!st) st = launch_repack_kquant(type, gate, n_ff, hidden, rp, s);
-    if (!st) st = kquant_run(type, rp, n_ff, hidden, n_tokens, t1, g, s);
-    if (!st) st = launch_repack_kquant(type, up, n_ff, hidden, rp, s);
-    if (!st) st = kquant_run(type, rp, n_ff, hidden, n_tokens, t1, u, s);
+    if (!st) st = repacked(gate, n_ff, hidden, &src);
+    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, g, s);
+    if (!st) st = repacked(up, n_ff, hidden, &src);
+    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, u, s);
     if (st) return st;
     const TiledWs t2 = tiled_ws(it, hidden, F2, n_tokens, ws);
     st = tiled_pack<kPackSwiglu>(it, t2, g, u, nullptr, 0.f, n_tokens, F2, n_ff, s);
-    if (!st) st = launch_repack_kquant(type, down, hidden, n_ff, rp, s);
+    if (!st) st = repacked(down, hidden, n_ff, &src);
     if (st) return st;
-    return kquant_run(type, rp, hidden, n_ff, n_tokens, t2, out, s);
+    return kquant_run(type, src, hidden, n_ff, n_tokens, t2, out, s);
   }
   if (!gemm_tiled_ok(type, gate, x, n_ff, hidden, n_tokens) || !gemm_tiled_ok(type, up, x, n_ff, hidden, n_tokens) ||
       !gemm_tiled_ok(type, down, g, hidden, n_ff, n_tokens) || !aligned(gamma, 16) || !aligned(u, 16))

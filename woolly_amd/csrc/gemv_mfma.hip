@@ -58,317 +58,9 @@
 // different A rows (rows 8 (j & 1) + 4 h + limb), so lane group G of
 // accumulator t holds the sums of 16-element group 4 t + G, scaled by
 // d * s / 64 (exact).
-#include "wh_blocks.hpp"
-
-typedef int mg_v4i __attribute__((ext_vector_type(4)));
-
-// raw buffer load of 16 bytes (llvm.amdgcn.raw.buffer.load.v4i32)
-__device__ mg_v4i mg_buffer_load_x4(mg_v4i rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+#include "gemv_mfma_dev.hpp"
 
 namespace {
-
-// Buffer resource of a raw byte range: loads at offsets >= nbytes return 0
-// without a memory access.
-__device__ __forceinline__ mg_v4i mg_rsrc(const void* base, uint32_t nbytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  mg_v4i r;
-  r[0] = static_cast<int>(static_cast<uint32_t>(a));
-  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xFFFFu);  // stride 0
-  r[2] = static_cast<int>(nbytes);
-  r[3] = 0x00020000;  // 32-bit data format, raw access
-  return r;
-}
-
-constexpr int kMgWaves = 16;                   // waves per workgroup
-constexpr int kMgSegMax = 16 * 64 * 4;        // bytes of one row segment (at most 4 loads)
-// LDS row stride of a ring slot: the segment (and its lead room) rounded up
-// to an odd number of 16-byte units, so that the 16 rows of a step start in
-// 16 different bank quads.  Callers include 16 bytes of overflow room in
-// lead_room: lanes whose 16-byte piece lies past the segment store it there
-// (it is zeros: the buffer range ends at the segment), so that the copy into
-// LDS needs no branch.
-__host__ __device__ constexpr uint32_t mg_row_stride(uint32_t seg_bytes, uint32_t lead_room) {
-  return ((seg_bytes + 15u) & ~15u) + lead_room + (((((seg_bytes + 15u) & ~15u) + lead_room) >> 4) & 1u ? 0u : 16u);
-}
-constexpr int kMgLimbBytes = 4 * 32;            // four limbs of one block
-// limb staging bytes per chunk: the limbs, then the limb sums of each
-// 32-element block
-constexpr int mg_stage_bytes(int type) { return 8 * kMgLimbBytes + (type == WH_TYPE_Q6_K ? 0 : 8 * 16); }
-// several-token kernel: the limbs of one chunk, or of both tokens' chunks in
-// the two-token layout
-constexpr int mt_stage_bytes(int type, int mt) { return mt == 2 ? 16 * kMgLimbBytes : mg_stage_bytes(type); }
-constexpr int kMgNt = 2;                       // streaming (non-temporal) loads
-constexpr int kMgNorm = 1, kMgFfn = 2;         // kernel variants
-constexpr int kMgDepth1 = 1;                   // steps in flight for one-segment rows
-
-template <int TYPE>
-struct MgFmt;
-template <>
-struct MgFmt<WH_TYPE_Q4_0> {
-  static constexpr int PB = 36;  // bytes of two blocks
-};
-template <>
-struct MgFmt<WH_TYPE_Q4_1> {
-  static constexpr int PB = 40;
-};
-template <>
-struct MgFmt<WH_TYPE_Q8_0> {
-  static constexpr int PB = 68;
-};
-template <>
-struct MgFmt<WH_TYPE_Q4_K> {
-  static constexpr int PB = 0;  // not used: one 144-byte block per chunk
-};
-template <>
-struct MgFmt<WH_TYPE_Q6_K> {
-  static constexpr int PB = 0;  // not used: one 210-byte block per chunk
-};
-
-// bytes of one 256-weight chunk of a format the kernel takes; 0 otherwise
-constexpr int mg_chunk_bytes(int type) {
-  return type == WH_TYPE_Q4_0 ? 144
-         : type == WH_TYPE_Q4_1 ? 160
-         : type == WH_TYPE_Q8_0 ? 272
-         : type == WH_TYPE_Q4_K ? 144
-         : type == WH_TYPE_Q6_K ? 210
-                                : 0;
-}
-
-// Output rows [0, n_out).  Plain mode: row r is row r of the matrices W0, W1,
-// W2 stacked (n0 rows of W0, n1 of W1, the rest of W2).  FFN mode: W0 = gate,
-// W1 = up, y[r] = silu(gate_r . x_hat) * (up_r . x_hat).  gamma set: x is
-// RMS-normalised first; residual set: y[r] = residual[r] + (W x)[r].
-struct MgArgs {
-  const uint8_t* W0;
-  const uint8_t* W1;
-  const uint8_t* W2;
-  int n0, n1;
-  const float* x;
-  const float* gamma;
-  float eps;
-  const float* residual;
-  float* y;
-  int n_out, ppr, seg_pairs, rows_per_wg;
-  int m, ldy;  // several-token kernel: tokens (rows of x, K apart) and the row stride of y
-};
-
-// k-slot (0..7) of lane group g that element el (0..31) of a block feeds:
-// Q4: slots 0..3 = low nibbles of quant bytes 4g..4g+3 (elements 4g..4g+3),
-// slots 4..7 = their high nibbles (elements 16+4g..); Q8_0 and Q6_K: element
-// 8g + slot.
-// Q4_K: quant byte 4g + b of a group holds elements 8g + 2b (low nibble, slot
-// b) and 8g + 2b + 1 (high nibble, slot 4 + b).
-template <int TYPE>
-__device__ __forceinline__ int mg_slot_offset(int el) {
-  if constexpr (TYPE == WH_TYPE_Q8_0 || TYPE == WH_TYPE_Q6_K) return el;
-  if constexpr (TYPE == WH_TYPE_Q4_K) return 8 * (el >> 3) + ((el & 1) ? 4 : 0) + ((el & 7) >> 1);
-  return 8 * ((el & 15) >> 2) + (el & 3) + (el >= 16 ? 4 : 0);
-}
-
-// B operand of lane group g for the two blocks of the pair at pw (LDS).
-template <int TYPE>
-__device__ __forceinline__ void mg_quants(const uint32_t* pw, int g, long& qa, long& qb) {
-  auto split = [](uint32_t u) -> long {
-    return static_cast<long>(u & 0x0F0F0F0Fu) | (static_cast<long>((u >> 4) & 0x0F0F0F0Fu) << 32);
-  };
-  if constexpr (TYPE == WH_TYPE_Q4_0) {
-    // [dA|q0 q1] [q2..5] .. [q14 q15|dB] [B q0..3] ..: quant bytes 4g..4g+3 of block A
-    // start at byte 2 + 4g
-    qa = split(__builtin_amdgcn_alignbit(pw[g + 1], pw[g], 16));
-    qb = split(pw[5 + g]);
-  } else if constexpr (TYPE == WH_TYPE_Q4_1) {
-    // [dA|mA] [A q0..3] .. [A q12..15] [dB|mB] [B q0..3] ..
-    qa = split(pw[1 + g]);
-    qb = split(pw[6 + g]);
-  } else {
-    // [dA|q0 q1] [q2..5] .. [q30 q31|dB] [B q0..3] ..: quant bytes 8g..8g+7 of block A
-    // start at byte 2 + 8g
-    const uint32_t w0 = pw[2 * g], w1 = pw[2 * g + 1], w2 = pw[2 * g + 2];
-    const uint32_t lo = __builtin_amdgcn_alignbit(w1, w0, 16);
-    const uint32_t hi = __builtin_amdgcn_alignbit(w2, w1, 16);
-    qa = static_cast<long>(lo) | (static_cast<long>(hi) << 32);
-    qb = static_cast<long>(pw[9 + 2 * g]) | (static_cast<long>(pw[10 + 2 * g]) << 32);
-  }
-}
-
-// Per-element dot product of one pair (64 weights at byte pointer p, in LDS)
-// with 64 activations (already RMS-normalised in the norm modes), xs(jj)
-// giving elements 4 jj .. 4 jj + 3: w = (q - 8) * d, q * d + m or q * d as in
-// dequantize_q4_0 / _q4_1 / _q8_0, then w * x accumulated in element order.
-// Used for chunks with non-finite activations.
-template <int TYPE, typename XS>
-__device__ float mg_pair_exact(const uint8_t* p, XS xs) {
-  constexpr int BB = whd::BlockFmt<TYPE>::BYTES;
-  float s = 0.f;
-#pragma unroll 1
-  for (int blk = 0; blk < 2; blk++) {
-    const uint8_t* b = p + blk * BB;
-    const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8));
-    float m = 0.f;
-    if constexpr (TYPE == WH_TYPE_Q4_1)
-      m = whd::f16_bits_to_f32(static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8));
-#pragma unroll 1
-    for (int jj = 0; jj < 8; jj++) {
-      const float4 xq = xs(8 * blk + jj);
-      const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-      const int el = 4 * jj + c;
-      float w;
-      if constexpr (TYPE == WH_TYPE_Q4_0) {
-        const uint32_t q = b[2 + (el & 15)];
-        w = static_cast<float>(static_cast<int>(el < 16 ? (q & 15u) : (q >> 4)) - 8) * d;
-      } else if constexpr (TYPE == WH_TYPE_Q4_1) {
-        const uint32_t q = b[4 + (el & 15)];
-        w = __fadd_rn(__fmul_rn(static_cast<float>(el < 16 ? (q & 15u) : (q >> 4)), d), m);
-      } else {
-        w = static_cast<float>(static_cast<int8_t>(b[2 + el])) * d;
-      }
-      s = __builtin_fmaf(w, xa[c], s);
-      }
-    }
-  }
-  return s;
-}
-
-// 6-bit scale j (0..7) of a Q4_K block (dequantize.rs:423-431): src = 3j/2,
-// even j: b[src] & 63, odd j: ((b[src] >> 6) | ((b[src + 1] & 15) << 2)) & 63.
-__device__ __forceinline__ uint32_t mg_q4k_scale(const uint8_t* b, int j) {
-  const int src = (3 * j) >> 1;
-  return (j & 1) ? (((static_cast<uint32_t>(b[src]) >> 6) | ((static_cast<uint32_t>(b[src + 1]) & 15u) << 2)) & 63u)
-                 : (static_cast<uint32_t>(b[src]) & 63u);
-}
-
-// Q4_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block at
-// blk, w = ((d * s) * q) + dmin as dequantize_q4_k_scalar evaluates it.
-template <typename XS>
-__device__ float mg_q4k_exact(const uint8_t* blk, int g, XS xs) {
-  const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[12]) | (static_cast<uint32_t>(blk[13]) << 8));
-  const float dmin = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[14]) | (static_cast<uint32_t>(blk[15]) << 8));
-  float s = 0.f;
-#pragma unroll 1
-  for (int jj = 0; jj < 16; jj++) {
-    const float4 xq = xs(jj);
-    const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-    const int el = 4 * jj + c;
-    const int i = 64 * g + el;
-    const float ds = __fmul_rn(d, static_cast<float>(mg_q4k_scale(blk, i >> 5)));
-    const uint32_t qb = blk[16 + (i >> 1)];
-    const float w = __fadd_rn(__fmul_rn(ds, static_cast<float>((i & 1) ? (qb >> 4) : (qb & 15u))), dmin);
-    s = __builtin_fmaf(w, xa[c], s);
-    }
-  }
-  return s;
-}
-
-// Q6_K counterpart of mg_pair_exact: elements 64 g .. 64 g + 63 of the block
-// at blk, w = ((d * s) * (q - 32)) / 64 as dequantize_q6_k evaluates it.
-template <typename XS>
-__device__ float mg_q6k_exact(const uint8_t* blk, int g, XS xs) {
-  const float d = whd::f16_bits_to_f32(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
-  float s = 0.f;
-#pragma unroll 1
-  for (int jj = 0; jj < 16; jj++) {
-    const float4 xq = xs(jj);
-    const float xa[4] = {xq.x, xq.y, xq.z, xq.w};
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-    const int el = 4 * jj + c;
-    const int i = 64 * g + el;
-    const int ql_idx = 64 * (i >> 7) + 32 * ((i & 127) >> 6) + 16 * ((i & 63) >> 5) + (i & 15);
-    const int qh_idx = 32 * (i >> 7) + 16 * ((i & 127) >> 6) + 8 * ((i & 63) >> 5) + ((i & 31) >> 2);
-    const int sh = 2 * (i & 3);
-    const uint32_t qhv = blk[128 + qh_idx];
-    uint32_t q;
-    if (i < 128) {
-      q = (blk[ql_idx] & 15u) | (((qhv >> sh) & 3u) << 4);
-    } else {
-      const uint32_t e2 = sh < 6 ? ((qhv >> (sh + 2)) & 3u) : (qh_idx + 1 < 64 ? (blk[129 + qh_idx] & 3u) : 0u);
-      q = (static_cast<uint32_t>(blk[ql_idx]) >> 4) | (e2 << 4);
-    }
-    const float w = __fmul_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(blk[192 + (i >> 4)])),
-                                        static_cast<float>(static_cast<int>(q) - 32)),
-                              0.015625f);
-    s = __builtin_fmaf(w, xa[c], s);
-    }
-  }
-  return s;
-}
-
-// Two dwords of LDS bytes at p, which lies mis (0 or 2) bytes past a dword
-// boundary.  Pointer arithmetic only: an integer round trip would turn the
-// LDS reads into flat loads, which wait behind the global loads in flight.
-__device__ __forceinline__ void mg_lds_u64(const uint8_t* p, int mis, uint32_t& lo, uint32_t& hi) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(p - mis);
-  const uint32_t sh = static_cast<uint32_t>(mis) * 8u;
-  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-  lo = __builtin_amdgcn_alignbit(w1, w0, sh);
-  hi = __builtin_amdgcn_alignbit(w2, w1, sh);
-}
-
-// Cross-lane moves on the VALU (DPP) instead of ds_bpermute shuffles, which
-// go through the LDS pipe.
-template <int CTRL>
-__device__ __forceinline__ int mg_dpp(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141, kDppMirror = 0x140;  // lane i <-> 7 - i (of 8), 15 - i (of 16)
-
-// Maximum of an unsigned integer over the 64 lanes, uniform: one DPP max per
-// step within rows of 16 lanes, then the four rows' maxima on the scalar unit.
-__device__ __forceinline__ uint32_t mg_wave_max_u32(uint32_t v) {
-  v = max(v, static_cast<uint32_t>(mg_dpp<kDppXor1>(static_cast<int>(v))));
-  v = max(v, static_cast<uint32_t>(mg_dpp<kDppXor2>(static_cast<int>(v))));
-  v = max(v, static_cast<uint32_t>(mg_dpp<kDppHalfMirror>(static_cast<int>(v))));
-  v = max(v, static_cast<uint32_t>(mg_dpp<kDppMirror>(static_cast<int>(v))));
-  const int vi = static_cast<int>(v);
-  const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 0));
-  const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 16));
-  const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 32));
-  const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(vi, 48));
-  return max(max(r0, r1), max(r2, r3));
-}
-
-// f32 -> i32 as v_cvt_i32_f32 converts (NaN -> 0, out of range -> clamped),
-// with no C++ undefined behaviour for such inputs: the limbs of a chunk that
-// takes the exact path are converted too (without a branch) and never read.
-__device__ __forceinline__ int mg_cvt_i32(float v) {
-  int r;
-  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
-  return r;
-}
-
-// Sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) in every
-// lane, as (v[l] + v[l ^ 16]) + (v[l ^ 32] + v[l ^ 48]), with gfx950's
-// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Inline asm
-// with explicit wait states around each swap: the builtins' code returned one
-// register for both swapped halves.
-__device__ __forceinline__ float mg_sum_lane_groups(float v) {
-  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-  v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-  a = b = __builtin_bit_cast(uint32_t, v);
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-}
-
-// The four limb sums of one block as one f32, 2^24 C0 + 2^16 C1 + 2^8 C2 + C3:
-// the halves 2^8 C0 + C1 and 2^8 C2 + C3 in int32 (exact and without overflow:
-// |C| < 2^20: each sum covers one 32-element block), converted (exactly for the 4-bit
-// formats, whose halves stay below 2^24) and combined with one fma.
-__device__ __forceinline__ float mg_limbs(const mg_v4i& C) {
-  const int hi = C[0] * 256 + C[1];
-  const int lo = C[2] * 256 + C[3];
-  return __builtin_fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
-}
-
-// Bits 2t .. 2t + 1 of v (t = 0..3) moved to bits 4..5 of byte t.
-__device__ __forceinline__ uint32_t mg_spread2(uint32_t v) {
-  return ((v << 4) | (v << 10) | (v << 16) | (v << 22)) & 0x30303030u;
-}
 
 // NL: 16-byte loads per lane per step (row segments of up to 1024 NL bytes).
 // DEPTH: steps whose loads are in flight in registers (one-segment rows only).
@@ -840,412 +532,11 @@ __global__ __launch_bounds__(kMgWaves * 64) void gemv_mfma2_kernel(const MgArgs 
     gemv_mfma_body<TB, 1, NLB, MODE, kMgDepth1>(b, bid - grid_a);
 }
 
-// ---------------------------------------------------------------- several tokens
-// The matrix-core GEMV for 2..16 tokens (Q4_0, Q8_0): Y[t] = W X[t] (plain
-// mode) or the FFN gate/up pair with each token's RMSNorm prologue and the
-// SwiGLU epilogue (FFN mode), in the data flow of gemv_mfma_kernel.  The A
-// operand of one MFMA carries the limbs of four tokens for ONE block (rows
-// 4 t + limb, t = token within its group of four), so each block's weights,
-// unpacked once, meet one MFMA per group of four tokens and stream from HBM
-// once for all tokens; lane group g of the result holds token 4 tg + g's four
-// limb sums of the block.  Q4_0's -8 goes into the B operand: nibble ^ 8 read
-// as a signed 4-bit number is q - 8, kept in the high half of each byte
-// (16 (q - 8), an exact int8), and the block scale enters as d / 16.  The A
-// operands of every segment stay in registers (TG * NSEG <= 4).
-// MS = 2 (two tokens): rows 8 (b & 1) + 4 t + limb, so blocks 2p and 2p + 1
-// share one accumulator and lane group g holds token g & 1 of block
-// 2p + (g >> 1), half the accumulator conversions of the four-token layout.
-template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS>
-__device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
-  static_assert(TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q8_0, "several-token GEMV: Q4_0 and Q8_0");
-  static_assert(TG * NSEG <= 4, "A operands of every segment in registers");
-  static_assert(MS == 4 || (MS == 2 && TG == 1), "two-token layout: one group");
-  constexpr int PB = MgFmt<TYPE>::PB;
-  constexpr int BB = PB / 2;  // bytes of one block
-  constexpr bool FFN = (MODE & kMgFfn) != 0;
-  constexpr bool NORM = (MODE & kMgNorm) != 0;
-  constexpr int CB = mg_chunk_bytes(TYPE);  // a multiple of 16: segments start 16-byte aligned
-  constexpr int MT = MS * TG;  // token slots
-  constexpr int STG = mt_stage_bytes(TYPE, MT);
-  constexpr float kScale = TYPE == WH_TYPE_Q4_0 ? 0.0625f : 1.0f;
-  extern __shared__ __align__(16) uint8_t lds[];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int n = lane & 15, g = lane >> 4;
-  const int S = a.seg_pairs;
-  const int M = a.m;
-  const uint32_t seg_bytes = static_cast<uint32_t>(S >> 2) * CB;
-  const uint32_t rstr = mg_row_stride(seg_bytes, 16u);
-  const uint32_t slot_bytes = 16 * rstr;
-  const size_t row_bytes = static_cast<size_t>(a.ppr >> 2) * CB;
-  const int K = a.ppr * 64;
-  const int R = a.rows_per_wg;
-  uint8_t* ring = lds;
-  uint8_t* stage = lds + 2 * slot_bytes + wave * STG;
-  float* part = reinterpret_cast<float*>(lds + 2 * slot_bytes + kMgWaves * STG);  // [2][16 waves][MT][16]
-  float* misc = part + 2 * kMgWaves * MT * 16;  // [16 waves][MT] norm sums, later [MT][16] gate values
-  float* rms_lds = misc + kMgWaves * MT;        // [MT] RMSNorm scale of each token
-  float* rows_lds = rms_lds + MT;               // [MT][R] the workgroup's output rows
-
-  const int r0 = bid * R;
-  const int r1 = min(a.n_out, r0 + R);
-  const int G = (r1 - r0 + 15) >> 4;
-  const int GT = FFN ? 2 * G : G;
-  const bool owns = wave < (S >> 2);
-
-  auto row_src = [&](int q, const uint8_t** base) -> bool {
-    const int gi = FFN ? (q >> 1) : q;
-    const int row = r0 + 16 * gi + wave;
-    if (q >= GT || row >= r1) return false;
-    *base = (FFN && (q & 1) ? a.W1 : a.W0) + static_cast<size_t>(row) * row_bytes;
-    return true;
-  };
-  mg_v4i buf[NL];
-  auto load = [&](int q, int seg) {
-    const uint8_t* base = a.W0;
-    const bool ok = row_src(q, &base);
-    const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes, ok ? seg_bytes : 0u);
-#pragma unroll
-    for (int i = 0; i < NL; i++) buf[i] = mg_buffer_load_x4(rs, 16 * (64 * i + lane), 0, kMgNt);
-  };
-  auto xload = [&](int t, int seg) -> float4 {
-    if (t >= M || !owns) return make_float4(0.f, 0.f, 0.f, 0.f);
-    return *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + (seg * S + 4 * wave) * 64 + 4 * lane);
-  };
-  // The same as a buffer load whose range is empty for a token slot past M or
-  // a wave without a chunk (zeros, no memory access): no branch around the
-  // load, which would make the compiler wait for every load in flight where
-  // the branches join.
-  auto xload_nb = [&](int t, int seg) -> float4 {
-    const bool ok = t < M && owns;
-    const mg_v4i rs = mg_rsrc(a.x + (ok ? static_cast<size_t>(t) * K + (seg * S + 4 * wave) * 64 : static_cast<size_t>(0)),
-                              ok ? 1024u : 0u);
-    return __builtin_bit_cast(float4, mg_buffer_load_x4(rs, 16 * lane, 0, 0));
-  };
-
-  // XPRE (up to 8 chunks per wave, 4 with the longest rows, whose four loads
-  // per step leave fewer registers): every chunk's activations are requested
-  // first and kept in registers, then the first weights, so that neither the
-  // RMSNorm reduction nor the limbs wait for the weights (loads complete in
-  // order); with more chunks the activations are read where they are used and
-  // the weights are requested after the RMSNorm's barrier.
-  constexpr bool XPRE = MT * NSEG * (NL >= 4 ? 2 : 1) <= 8;
-  float4 xr[XPRE ? NSEG : 1][XPRE ? MT : 1];
-  auto xget = [&](int t, int seg) -> float4 {
-    if constexpr (XPRE) return xr[seg][t];
-    else return xload(t, seg);
-  };
-  float4 gv[NSEG];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int seg = 0; seg < NSEG; seg++)
-      gv[seg] = owns ? *reinterpret_cast<const float4*>(a.gamma + (seg * S + 4 * wave) * 64 + 4 * lane)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  if constexpr (XPRE) {
-#pragma unroll
-    for (int seg = 0; seg < (XPRE ? NSEG : 0); seg++)
-#pragma unroll
-      for (int t = 0; t < (XPRE ? MT : 0); t++) xr[seg][t] = xload_nb(t, seg);
-    load(0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // ---- RMSNorm (tensor_utils.rs:446-480) as (W (x * gamma)) / rms per token:
-  // each wave's share of every token's sum x^2 goes to LDS here; wave 0 forms
-  // the tokens' rms after the first step's barrier, and a token's rows are
-  // divided by its rms where they are finished (no barrier in the prologue).
-  if constexpr (NORM) {
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      float ss = 0.f;
-#pragma unroll
-      for (int seg = 0; seg < NSEG; seg++) {
-        const float4 v = xget(t, seg);
-        ss = __builtin_fmaf(v.x, v.x, ss);
-        ss = __builtin_fmaf(v.y, v.y, ss);
-        ss = __builtin_fmaf(v.z, v.z, ss);
-        ss = __builtin_fmaf(v.w, v.w, ss);
-      }
-      ss = whd::wave_sum(ss);
-      if (lane == 0) misc[wave * MT + t] = ss;
-    }
-  }
-  for (int i = threadIdx.x; i < MT * R; i += kMgWaves * 64) rows_lds[i] = 0.f;
-  if constexpr (!XPRE) load(0, 0);
-
-  // ---- limbs of every (segment, token) chunk -> A operands in registers
-  // two-token layout: a lane's rows belong to the even blocks (n < 8) or the
-  // odd ones, so one register per block pair holds its nonzero operand
-  constexpr int NA = MS == 4 ? 8 : 4;
-  long xa[NSEG][TG][NA];
-  int ex_u[NSEG][MT];       // chunk exponent (wave-uniform)
-  uint32_t exact_u[NSEG];   // bit t: token t's chunk holds inf / NaN (computed per element)
-#pragma unroll
-  for (int seg = 0; seg < NSEG; seg++)
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++)
-#pragma unroll
-      for (int b = 0; b < NA; b++) xa[seg][tg][b] = 0;
-  auto xnorm = [&](int t, int seg) -> float4 {
-    float4 v = xget(t, seg);
-    if constexpr (NORM) {
-      v.x *= gv[seg].x;
-      v.y *= gv[seg].y;
-      v.z *= gv[seg].z;
-      v.w *= gv[seg].w;
-    }
-    return v;
-  };
-#pragma unroll
-  for (int seg = 0; seg < NSEG; seg++) {
-    exact_u[seg] = 0u;
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      const float4 v = xnorm(t, seg);
-      const float xv[4] = {v.x, v.y, v.z, v.w};
-      // the largest |x| as the maximum of the bit patterns of |x| (inf / NaN above every finite value)
-      uint32_t um = 0u;
-#pragma unroll
-      for (int i = 0; i < 4; i++) um = max(um, __builtin_bit_cast(uint32_t, xv[i]) & 0x7FFFFFFFu);
-      um = mg_wave_max_u32(um);
-      const bool exact = um >= 0x7F800000u;
-      int e = 0;
-      if (um != 0u && !exact) {
-        int ee;
-        frexpf(__builtin_bit_cast(float, um), &ee);
-        e = 30 - ee;
-      }
-      ex_u[seg][t] = __builtin_amdgcn_readfirstlane(e);
-      if (exact) exact_u[seg] |= 1u << t;
-      uint32_t z[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int xi = exact ? 0 : static_cast<int>(rintf(ldexpf(xv[i], e)));
-        z[i] = static_cast<uint32_t>(xi + 0x808080) ^ 0x808080u;
-      }
-      const uint32_t pa = __builtin_amdgcn_perm(z[1], z[0], 0x06020703u);
-      const uint32_t pb2 = __builtin_amdgcn_perm(z[1], z[0], 0x04000501u);
-      const uint32_t pc = __builtin_amdgcn_perm(z[3], z[2], 0x06020703u);
-      const uint32_t pd = __builtin_amdgcn_perm(z[3], z[2], 0x04000501u);
-      // two-token layout: token t's limbs in the t-th half of the stage
-      int8_t* pw = reinterpret_cast<int8_t*>(stage) + (MS == 2 ? t * 8 * kMgLimbBytes : 0) +
-                   (lane >> 3) * kMgLimbBytes + mg_slot_offset<TYPE>(4 * (lane & 7));
-      *reinterpret_cast<uint32_t*>(pw) = __builtin_amdgcn_perm(pc, pa, 0x05040100u);
-      *reinterpret_cast<uint32_t*>(pw + 32) = __builtin_amdgcn_perm(pc, pa, 0x07060302u);
-      *reinterpret_cast<uint32_t*>(pw + 64) = __builtin_amdgcn_perm(pd, pb2, 0x05040100u);
-      *reinterpret_cast<uint32_t*>(pw + 96) = __builtin_amdgcn_perm(pd, pb2, 0x07060302u);
-      if constexpr (MS == 4) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_wave_barrier();
-        // this token's rows of the A operands: rows 4 (t & 3) .. + 3 of token group t / 4
-        const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + 32 * (n & 3) + 8 * g;
-        if ((n >> 2) == (t & 3)) {
-          long v[8];
-#pragma unroll
-          for (int b = 0; b < 8; b++) v[b] = *reinterpret_cast<const long*>(xs + b * kMgLimbBytes);
-#pragma unroll
-          for (int b = 0; b < 8; b++) xa[seg][t >> 2][b] = v[b];
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    if constexpr (MS == 2) {
-      // two-token layout: rows 8 (b & 1) + 4 t .. + 3 hold token t's limbs of
-      // block b, so a lane's rows belong to token (n >> 2) & 1 and to the
-      // blocks of parity n >> 3: four reads from that token's half, no branch
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_wave_barrier();
-      const int8_t* xs = reinterpret_cast<const int8_t*>(stage) + ((n >> 2) & 1) * 8 * kMgLimbBytes +
-                         (n >> 3) * kMgLimbBytes + 32 * (n & 3) + 8 * g;
-#pragma unroll
-      for (int j = 0; j < 4; j++) xa[seg][0][j] = *reinterpret_cast<const long*>(xs + 2 * j * kMgLimbBytes);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-  // exponent of the token this lane's results belong to (4 tg + g; two-token layout: g & 1)
-  int ex_l[NSEG][TG];
-#pragma unroll
-  for (int seg = 0; seg < NSEG; seg++)
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-      if constexpr (MS == 4) {
-        const int* e4 = &ex_u[seg][4 * tg];
-        ex_l[seg][tg] = g == 0 ? e4[0] : g == 1 ? e4[1] : g == 2 ? e4[2] : e4[3];
-      } else {
-        // values, not the elements: a conditional over two lvalues selects an
-        // address, and the array would live in scratch memory
-        const int e0 = ex_u[seg][0], e1 = ex_u[seg][MT > 1 ? 1 : 0];
-        ex_l[seg][tg] = (g & 1) ? e1 : e0;
-      }
-    }
-
-  // B operand of lane group g for the two blocks of the pair at pw (LDS)
-  auto quants = [&](const uint32_t* pw, long& qa, long& qb) {
-    if constexpr (TYPE == WH_TYPE_Q4_0) {
-      auto split = [](uint32_t u) -> long {
-        const uint32_t v = u ^ 0x88888888u;  // nibble ^ 8: q - 8 as a signed 4-bit number
-        return static_cast<long>((v << 4) & 0xF0F0F0F0u) | (static_cast<long>(v & 0xF0F0F0F0u) << 32);
-      };
-      qa = split(__builtin_amdgcn_alignbit(pw[g + 1], pw[g], 16));
-      qb = split(pw[5 + g]);
-    } else {
-      const uint32_t w0 = pw[2 * g], w1 = pw[2 * g + 1], w2 = pw[2 * g + 2];
-      qa = static_cast<long>(__builtin_amdgcn_alignbit(w1, w0, 16)) |
-           (static_cast<long>(__builtin_amdgcn_alignbit(w2, w1, 16)) << 32);
-      qb = static_cast<long>(pw[9 + 2 * g]) | (static_cast<long>(pw[10 + 2 * g]) << 32);
-    }
-  };
-
-  // Sum of group q over the 16 waves (fixed order) for every token, then the output rows.
-  auto finish = [&](int q) {
-    const int gi = FFN ? (q >> 1) : q;
-    const int row = r0 + 16 * gi + n;
-    if (MS == 2 && g >= 2) return;
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-      const int t = MS * tg + g;
-      const float* pp = part + ((q & 1) * kMgWaves * MT + t) * 16 + n;
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < kMgWaves; w++) v += pp[w * MT * 16];
-      if constexpr (NORM) v = v / rms_lds[t];
-      if constexpr (FFN) {
-        if ((q & 1) == 0) {
-          misc[t * 16 + n] = v;  // gate, combined with up one group later
-        } else if (row < r1) {
-          const float gt = misc[t * 16 + n];
-          rows_lds[t * R + row - r0] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
-        }
-      } else if (row < r1) {
-        rows_lds[t * R + row - r0] = v;
-      }
-    }
-  };
-
-  float acc[TG];
-#pragma unroll
-  for (int tg = 0; tg < TG; tg++) acc[tg] = 0.f;
-  for (int q = 0; q < GT; q++) {
-#pragma unroll
-    for (int seg = 0; seg < NSEG; seg++) {
-      const int s = q * NSEG + seg;
-      uint8_t* slot = ring + (s & 1) * slot_bytes;
-      {
-        uint8_t* dst = slot + wave * rstr;
-        const uint32_t end16 = (seg_bytes + 15u) & ~15u;
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-          const uint32_t o = 16u * (64 * i + lane);
-          *reinterpret_cast<mg_v4i*>(dst + (o < end16 ? o : end16)) = buf[i];
-        }
-      }
-      if (seg + 1 < NSEG) load(q, seg + 1);
-      else load(q + 1, 0);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if constexpr (NORM) {
-        // every wave's shares of sum x^2 are visible (the step barrier); the
-        // first finish, and the first gate value written over them, come after
-        // the next barrier
-        if (q == 0 && seg == 0 && wave == 0 && lane < MT) {
-          float tot = 0.f;
-#pragma unroll
-          for (int w = 0; w < kMgWaves; w++) tot += misc[w * MT + lane];
-          rms_lds[lane] = sqrtf(tot / static_cast<float>(K) + a.eps);
-        }
-      }
-      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
-      if (owns) {
-        const uint8_t* rowp = slot + n * rstr + wave * CB;
-        float sacc[TG];
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++) sacc[tg] = 0.f;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-          long qa, qb;
-          quants(reinterpret_cast<const uint32_t*>(rowp + p * PB), qa, qb);
-          const float da = whd::f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + p * PB)) * kScale;
-          const float db = whd::f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + p * PB + BB)) * kScale;
-#pragma unroll
-          for (int tg = 0; tg < TG; tg++) {
-            const mg_v4i zero = {0, 0, 0, 0};
-            if constexpr (MS == 4) {
-              const mg_v4i ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p], qa, zero, 0, 0, 0);
-              const mg_v4i cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[seg][tg][2 * p + 1], qb, zero, 0, 0, 0);
-              sacc[tg] = __builtin_fmaf(da, mg_limbs(ca), sacc[tg]);
-              sacc[tg] = __builtin_fmaf(db, mg_limbs(cb), sacc[tg]);
-            } else {
-              const long ae = n < 8 ? xa[seg][tg][p] : 0, ao = n < 8 ? 0 : xa[seg][tg][p];
-              mg_v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, qa, zero, 0, 0, 0);
-              c = __builtin_amdgcn_mfma_i32_16x16x32_i8(ao, qb, c, 0, 0, 0);
-              sacc[tg] = __builtin_fmaf((g >> 1) ? db : da, mg_limbs(c), sacc[tg]);
-            }
-          }
-        }
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++) acc[tg] += ldexpf(sacc[tg], -ex_l[seg][tg]);
-        // tokens whose chunk is not finite: their limbs are zero, the lanes of
-        // the token add the chunk per element (the reference's order)
-        for (uint32_t em = exact_u[seg]; em != 0u; em &= em - 1u) {
-          const int t = __builtin_ctz(em);
-          if (g != (MS == 4 ? (t & 3) : t)) continue;
-          float sx = 0.f;
-#pragma unroll 1
-          for (int p = 0; p < 4; p++)
-            sx += mg_pair_exact<TYPE>(rowp + p * PB, [&](int jj) {
-              const int el = (seg * S + 4 * wave) * 64 + 64 * p + 4 * jj;
-              float4 v = *reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * K + el);
-              if constexpr (NORM) {
-                const float4 gm = *reinterpret_cast<const float4*>(a.gamma + el);
-                v = make_float4(v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w);
-              }
-              return v;
-            });
-#pragma unroll
-          for (int tg = 0; tg < TG; tg++)
-            if (t / MS == tg) acc[tg] += sx;
-        }
-      }
-      if (seg == NSEG - 1) {
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++) {
-          if constexpr (MS == 4) {
-            part[(((q & 1) * kMgWaves + wave) * MT + 4 * tg + g) * 16 + n] = acc[tg];
-          } else {
-            // token g & 1: the even blocks' sum (lane group g) + the odd blocks' (g + 2)
-            const float v = acc[tg] + __shfl_xor(acc[tg], 32, 64);
-            if (g < 2) part[(((q & 1) * kMgWaves + wave) * MT + g) * 16 + n] = v;
-          }
-          acc[tg] = 0.f;
-        }
-      }
-    }
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  for (int i = threadIdx.x; i < M * (r1 - r0); i += kMgWaves * 64) {
-    const int t = i / (r1 - r0), r = i - t * (r1 - r0);
-    a.y[static_cast<size_t>(t) * a.ldy + r0 + r] = rows_lds[t * R + r];
-  }
-}
-
-template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS>
-__global__ __launch_bounds__(kMgWaves * 64) void gemv_mt_kernel(const MgArgs a) {
-  gemv_mt_body<TYPE, NSEG, NL, MODE, TG, MS>(a, static_cast<int>(blockIdx.x));
-}
-
-size_t mt_lds_bytes(int type, int seg_pairs, int mt, int rows_per_wg) {
-  const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * mg_chunk_bytes(type));
-  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), 16u);
-  return 2u * 16u * rstr + static_cast<size_t>(kMgWaves) * mt_stage_bytes(type, mt) +
+size_t mt_lds_bytes(int type, int seg_pairs, int nseg, int mt, int rows_per_wg) {
+  const int cb = mg_chunk_bytes(type);
+  const size_t seg_bytes = static_cast<size_t>(seg_pairs / 4 * cb);
+  const size_t rstr = mg_row_stride(static_cast<uint32_t>(seg_bytes), ((cb & 15) ? 16u : 0u) + 16u);
+  return 2u * 16u * rstr + static_cast<size_t>(kMgWaves) * (mt_stage_bytes(type, mt) + mt_xsum_bytes(type, nseg, mt)) +
          4u * (2u * kMgWaves * mt * 16 + static_cast<size_t>(kMgWaves) * mt + mt + static_cast<size_t>(mt) * rows_per_wg);
 }
 
@@ -1312,45 +603,6 @@ int mg_typed(const MgArgs& a, int nseg, int mode, int grid, size_t lds, hipStrea
     case kMgNorm: return mg_dispatch<TYPE, kMgNorm>(a, nseg, grid, lds, s);
     default: return mg_dispatch<TYPE, kMgNorm | kMgFfn>(a, nseg, grid, lds, s);
   }
-}
-
-template <int TYPE, int NSEG, int NL, int MODE, int TG, int MS = 4>
-int mt_launch(const MgArgs& a, int grid, size_t lds, hipStream_t s) {
-  auto* fn = &gemv_mt_kernel<TYPE, NSEG, NL, MODE, TG, MS>;
-  WH_ENSURE_LDS(lds, fn);
-  fn<<<grid, kMgWaves * 64, lds, s>>>(a);
-  WH_LAUNCH_CHECK("gemv (several tokens) kernel launch");
-  return WH_OK;
-}
-
-template <int TYPE, int NL, int MODE>
-int mt_dispatch_nl(const MgArgs& a, int nseg, int tg, int grid, size_t lds, hipStream_t s) {
-  if (a.m == 2) {
-    switch (nseg) {
-      case 1: return mt_launch<TYPE, 1, NL, MODE, 1, 2>(a, grid, lds, s);
-      case 2: return mt_launch<TYPE, 2, NL, MODE, 1, 2>(a, grid, lds, s);
-      default: return mt_launch<TYPE, 4, NL, MODE, 1, 2>(a, grid, lds, s);
-    }
-  }
-  if (nseg == 1) {
-    switch (tg) {
-      case 1: return mt_launch<TYPE, 1, NL, MODE, 1>(a, grid, lds, s);
-      case 2: return mt_launch<TYPE, 1, NL, MODE, 2>(a, grid, lds, s);
-      case 3: return mt_launch<TYPE, 1, NL, MODE, 3>(a, grid, lds, s);
-      default: return mt_launch<TYPE, 1, NL, MODE, 4>(a, grid, lds, s);
-    }
-  }
-  if (nseg == 2) return tg == 1 ? mt_launch<TYPE, 2, NL, MODE, 1>(a, grid, lds, s) : mt_launch<TYPE, 2, NL, MODE, 2>(a, grid, lds, s);
-  return mt_launch<TYPE, 4, NL, MODE, 1>(a, grid, lds, s);
-}
-
-template <int TYPE, int MODE>
-int mt_dispatch(const MgArgs& a, int nseg, int tg, int grid, size_t lds, hipStream_t s) {
-  const int seg_bytes = a.seg_pairs / 4 * mg_chunk_bytes(TYPE);
-  if (nseg == 4 && seg_bytes <= 2048)
-    return a.m == 2 ? mt_launch<TYPE, 4, 2, MODE, 1, 2>(a, grid, lds, s) : mt_launch<TYPE, 4, 2, MODE, 1>(a, grid, lds, s);
-  return seg_bytes <= 3072 ? mt_dispatch_nl<TYPE, 3, MODE>(a, nseg, tg, grid, lds, s)
-                           : mt_dispatch_nl<TYPE, 4, MODE>(a, nseg, tg, grid, lds, s);
 }
 
 }  // namespace
@@ -1476,8 +728,7 @@ int launch_gemv_mfma2(int type_a, const void* const* mats_a, const size_t* rows_
 int launch_gemv_mt(int type, const void* const* mats, bool ffn, const float* x, size_t m, const float* gamma,
                    float eps, float* y, size_t ldy, size_t n_out, size_t k, hipStream_t s) {
   if (n_out == 0 || m == 0) return WH_OK;
-  if ((type != WH_TYPE_Q4_0 && type != WH_TYPE_Q8_0) || m < 2 || m > 16 || !gemv_mfma_ok(type, n_out, k) ||
-      (ffn && !gamma))
+  if (m < 2 || m > 16 || !gemv_mfma_ok(type, n_out, k) || (ffn && !gamma))
     return WH_ERR_INVALID_SHAPE;
   const size_t ppr = k / 64;
   const int nseg = mg_segments(type, ppr);
@@ -1505,14 +756,19 @@ int launch_gemv_mt(int type, const void* const* mats, bool ffn, const float* x, 
   const size_t grid0 = groups < cus ? groups : cus;
   a.rows_per_wg = static_cast<int>((groups + grid0 - 1) / grid0 * 16);
   const size_t grid = (n_out + a.rows_per_wg - 1) / a.rows_per_wg;
-  const size_t lds = mt_lds_bytes(type, a.seg_pairs, m == 2 ? 2 : 4 * tg, a.rows_per_wg);
+  // token slots: two in the two-token layout (not for Q6_K), else four per group
+  const int mt = (m == 2 && type != WH_TYPE_Q6_K) ? 2 : 4 * tg;
+  const size_t lds = mt_lds_bytes(type, a.seg_pairs, nseg, mt, a.rows_per_wg);
   if (lds > max_lds_per_block()) return WH_ERR_INVALID_SHAPE;
   const int g = static_cast<int>(grid);
-  if (type == WH_TYPE_Q4_0)
-    return ffn ? mt_dispatch<WH_TYPE_Q4_0, kMgNorm | kMgFfn>(a, nseg, tg, g, lds, s)
-               : mt_dispatch<WH_TYPE_Q4_0, 0>(a, nseg, tg, g, lds, s);
-  return ffn ? mt_dispatch<WH_TYPE_Q8_0, kMgNorm | kMgFfn>(a, nseg, tg, g, lds, s)
-             : mt_dispatch<WH_TYPE_Q8_0, 0>(a, nseg, tg, g, lds, s);
+  switch (type) {
+    case WH_TYPE_Q4_0: return launch_gemv_mt_q4_0(a, ffn, nseg, tg, g, lds, s);
+    case WH_TYPE_Q4_1: return launch_gemv_mt_q4_1(a, ffn, nseg, tg, g, lds, s);
+    case WH_TYPE_Q8_0: return launch_gemv_mt_q8_0(a, ffn, nseg, tg, g, lds, s);
+    case WH_TYPE_Q4_K: return launch_gemv_mt_q4_k(a, ffn, nseg, tg, g, lds, s);
+    case WH_TYPE_Q6_K: return launch_gemv_mt_q6_k(a, ffn, nseg, tg, g, lds, s);
+    default: return WH_ERR_INVALID_SHAPE;
+  }
 }
 
 }  // namespace wh

@@ -84,6 +84,9 @@ inline size_t kquant_repacked_bytes(int type, size_t n_rows, size_t k) {
 }
 // Rewrites a Q4_K / Q6_K matrix (n_rows x k, 16-byte aligned) into the format above (kquant.hip).
 int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void* out, hipStream_t stream);
+// The copy of a K-quant matrix in the format above that wh_weight_prepare_prefill
+// made for the handle whose data is w (with this type and shape), or null.
+const void* prepared_kquant(const void* w, int type, size_t n_rows, size_t k);
 
 // Number of compute units of the current device (cached per device, no lock).
 int cu_count();

@@ -152,6 +152,13 @@ class Weight:
         _lib.check(_lib.load().wh_weight_info(self.handle, None, None, None, C.byref(nb)))
         return int(nb.value)
 
+    def prepare_prefill(self, stream: Stream | None = None) -> int:
+        """wh_weight_prepare_prefill: Q4_K / Q6_K blocks converted once into the
+        tiled GEMM's layout and kept with the handle; returns the copy's bytes."""
+        nb = C.c_size_t()
+        _lib.check(_lib.load().wh_weight_prepare_prefill(self.handle, _s(stream), C.byref(nb)))
+        return int(nb.value)
+
     def free(self) -> None:
         if self.handle:
             _lib.check(_lib.load().wh_weight_free(self.handle))
