@@ -442,21 +442,43 @@ def copy_probe(nbytes: int = 256 << 20, reps: int = 5) -> float:
     return 2 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
 
 
-# The sources the headline GEMV kernel is built from: a committed profile
-# summary is current only if it records the same digest of them.
-GEMV_KERNEL_SOURCES = ("woolly_amd/csrc/gemv_mfma.hip", "woolly_amd/csrc/gemv.hip",
-                       "woolly_amd/csrc/wh_common.hpp", "woolly_amd/csrc/wh_blocks.hpp")
+# The sources each family of kernels is built from (the kernel file, the
+# headers it includes).  Every summary under profiles/ names its group and
+# records the digest of the group's sources: it is current only while the
+# tree's sources have the same digest (checked by tests/test_bench_profile.py).
+_C = "woolly_amd/csrc/"
+_COMMON = (_C + "wh_common.hpp", _C + "wh_blocks.hpp")
+KERNEL_SOURCE_GROUPS = {
+    # single-token matrix-core GEMV and the streaming kernels it falls back to
+    "gemv": (_C + "gemv_mfma.hip", _C + "gemv_mfma_dev.hpp", _C + "gemv.hip") + _COMMON,
+    # several-token GEMV (2..16 tokens), one translation unit per block type
+    "gemv_mt": (_C + "gemv_mt.hpp", _C + "gemv_mfma_dev.hpp", _C + "gemv_mt_q4_0.hip", _C + "gemv_mt_q4_1.hip",
+                _C + "gemv_mt_q8_0.hip", _C + "gemv_mt_q4_k.hip", _C + "gemv_mt_q6_k.hip") + _COMMON,
+    # tiled prefill GEMM, its packing, the K-quant conversion, the fallbacks
+    "gemm": (_C + "gemm_tiled.hip", _C + "gemm.hip", _C + "kquant.hip", _C + "elementwise.hip") + _COMMON,
+    "attention": (_C + "attention.hip",) + _COMMON,
+}
+# the decode step launches kernels of every group above and of decode.hip / embed.hip
+KERNEL_SOURCE_GROUPS["decode"] = tuple(sorted(set(sum(KERNEL_SOURCE_GROUPS.values(), ())) |
+                                              {_C + "decode.hip", _C + "embed.hip"}))
+GEMV_KERNEL_SOURCES = KERNEL_SOURCE_GROUPS["gemv"]
 PMC_PROFILE = ROOT / "profiles" / "gemv_q4_0_14336x4096_pmc.txt"
 
 
-def kernel_sources_digest() -> str:
-    """sha256 over the headline kernel's source files, in a fixed order."""
+def sources_digest(paths) -> str:
+    """sha256 over the given source files (paths relative to the repo root), in
+    the order given, each prefixed with its path."""
     import hashlib
 
     h = hashlib.sha256()
-    for rel in GEMV_KERNEL_SOURCES:
+    for rel in paths:
         h.update(rel.encode() + b"\0" + (ROOT / rel).read_bytes())
     return h.hexdigest()[:16]
+
+
+def kernel_sources_digest(group: str = "gemv") -> str:
+    """The digest of one kernel group's sources (default: the headline GEMV's)."""
+    return sources_digest(KERNEL_SOURCE_GROUPS[group])
 
 
 def traffic_from_profile() -> tuple[int | None, str]:
@@ -568,11 +590,11 @@ def main() -> int:
                     help="ggml type id and shape of --only gemv (default Q4_0 14336 4096)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only device-to-device copies of 256 MiB (counter calibration)")
-    ap.add_argument("--sources-digest", action="store_true",
-                    help="print the digest of the headline GEMV kernel's sources and exit (no GPU)")
+    ap.add_argument("--sources-digest", nargs="?", const="gemv", default=None, choices=sorted(KERNEL_SOURCE_GROUPS),
+                    help="print the digest of a kernel group's sources (default: the headline GEMV's) and exit")
     args = ap.parse_args()
     if args.sources_digest:
-        print(kernel_sources_digest())
+        print(kernel_sources_digest(args.sources_digest))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "

@@ -32,6 +32,10 @@ def test_digest_covers_every_gemv_source():
     assert all((bench.ROOT / rel).is_file() for rel in bench.GEMV_KERNEL_SOURCES)
 
 
+def _stamp(text: str, key: str) -> list[str]:
+    return [ln.split()[1] for ln in text.splitlines() if ln.startswith(key + ":") and len(ln.split()) > 1]
+
+
 def test_committed_headline_summaries_are_current():
     """The committed kernel-trace and counter summaries of the headline GEMV
     were taken from this tree's GEMV sources: a change to them without a new
@@ -39,6 +43,30 @@ def test_committed_headline_summaries_are_current():
     want = bench.kernel_sources_digest()
     for name in ("gemv_q4_0_14336x4096_pmc.txt", "gemv_q4_0_14336x4096_kernel_trace.txt"):
         text = (bench.ROOT / "profiles" / name).read_text()
-        recorded = [ln.split()[1] for ln in text.splitlines() if ln.startswith("kernel_sources_sha256:")]
-        assert recorded == [want], (name, recorded, want)
+        assert _stamp(text, "kernel_sources_sha256") == [want], (name, _stamp(text, "kernel_sources_sha256"), want)
     assert bench.traffic_from_profile()[1] == "current"
+
+
+def test_every_committed_summary_is_current():
+    """Every summary under profiles/ names the kernel group it profiles and the
+    digest of that group's sources (python bench.py --sources-digest GROUP); it
+    must equal the digest of this tree's sources, so that no committed figure
+    describes kernels that have since changed."""
+    files = sorted((bench.ROOT / "profiles").glob("*.txt"))
+    assert len(files) >= 10
+    for f in files:
+        text = f.read_text()
+        groups = _stamp(text, "kernel_group")
+        assert len(groups) == 1 and groups[0] in bench.KERNEL_SOURCE_GROUPS, (f.name, groups)
+        want = bench.kernel_sources_digest(groups[0])
+        assert _stamp(text, "kernel_sources_sha256") == [want], (f.name, groups[0], want)
+
+
+def test_source_groups_name_existing_files():
+    for group, paths in bench.KERNEL_SOURCE_GROUPS.items():
+        assert paths and all((bench.ROOT / rel).is_file() for rel in paths), group
+    # every kernel translation unit belongs to some group
+    hip = {p.relative_to(bench.ROOT).as_posix() for p in (bench.ROOT / "woolly_amd" / "csrc").glob("*.hip")}
+    covered = set(sum(bench.KERNEL_SOURCE_GROUPS.values(), ()))
+    assert hip - covered <= {"woolly_amd/csrc/api.hip", "woolly_amd/csrc/gguf.hip", "woolly_amd/csrc/dequant.hip",
+                             "woolly_amd/csrc/probe.hip"}, hip - covered

@@ -461,8 +461,9 @@ def test_llama_config_from_gguf_metadata():
 
 
 def _llama_gguf(hidden=256, n_heads=4, n_kv=2, n_ff=512, vocab=64, kv_meta=True, ff_meta=None, output=True,
-                embd=True):
-    """A one-layer Q8_0 llama GGUF file's builder (no GPU needed to build it)."""
+                embd=True, embd_type=8):
+    """A one-layer Q8_0 llama GGUF file's builder (no GPU needed to build it);
+    token_embd.weight in Q8_0, or F16 with embd_type = 1."""
     from woolly_amd.gguf import GGMLType
 
     d = hidden // n_heads
@@ -482,11 +483,26 @@ def _llama_gguf(hidden=256, n_heads=4, n_kv=2, n_ff=512, vocab=64, kv_meta=True,
                        "ffn_down": (hidden, n_ff)}.items():
         b.add_tensor(f"blk.0.{nm}.weight", [k, n], GGMLType.Q8_0, q8(n, k, len(nm)))
     b.add_tensor("output_norm.weight", [hidden], GGMLType.F32, norm)
-    if embd:
+    if embd and embd_type == 1:
+        table = synth.activations(vocab * hidden, seed=99).astype(np.float16).tobytes()
+        b.add_tensor("token_embd.weight", [hidden, vocab], GGMLType.F16, table)
+    elif embd:
         b.add_tensor("token_embd.weight", [hidden, vocab], GGMLType.Q8_0, q8(vocab, hidden, 99))
     if output:
         b.add_tensor("output.weight", [hidden, vocab], GGMLType.Q8_0, q8(vocab, hidden, 98))
     return b
+
+
+def test_llama_from_gguf_rejects_tied_head_of_other_types(tmp_path):
+    """Without output.weight the head is token_embd.weight (lazy_transformer.rs:1301-1316);
+    an F16 table loads as an embedding but the head GEMV takes only the quantized
+    block types, so from_gguf refuses it before uploading anything (no GPU is
+    touched)."""
+    from woolly_amd import ops
+
+    ld = load(_llama_gguf(output=False, embd_type=1).build(), tmp_path)
+    with pytest.raises(ValueError, match="output head"):
+        ops.LlamaModel.from_gguf(ld, max_ctx=8)
 
 
 def test_llama_from_gguf_rejects_mismatched_dims():

@@ -15,9 +15,11 @@ WH_PARITY_LOG to collect them as JSON lines).
 
 Bars (north_star): rel-L2 <= 1e-4 and max-abs <= 1e-3 of the f64 oracle for
 matmul / FFN outputs and for the step's logits.  The step's hidden state is a
-residual sum with RMS ~1e3 after 32 layers, where one f32 ulp of its largest
-elements already exceeds 1e-3; it is held to rel-L2 <= 1e-4 and to max-abs
-<= 1e-3 per 300 of its RMS, the rule the FFN tests apply to large outputs.
+residual sum that the random-init layers grow to RMS ~3.3e4 after 32 layers
+(the seeded model's value; asserted below 5e4 so that the bar cannot loosen
+unseen), where one f32 ulp of its largest elements already exceeds 1e-3; it is
+held to rel-L2 <= 1e-4 and to max-abs <= 1e-3 per 300 of its RMS, the rule the
+FFN tests apply to large outputs.
 Token rows of a GEMM or FFN are independent, so for M >= 64 the oracle checks
 the first, a middle and the last token tile's rows."""
 import numpy as np
@@ -197,5 +199,6 @@ def test_decode_step_config4_full(gpu, orc):
     report("config4_decode_step_hidden", rx, ax, x)
     report("config4_decode_step_logits", rl, al, logits)
     rms_x = float(np.sqrt(np.mean(x ** 2)))
+    assert rms_x <= 5e4, rms_x  # the scaled max-abs bar stays <= 0.17
     assert rx <= REL_L2 and ax <= MAX_ABS * max(1.0, rms_x / 300.0)
     assert rl <= REL_L2 and al <= MAX_ABS

@@ -398,7 +398,7 @@ def test_llama_model_from_gguf_q4_k_m(gpu, orc, tmp_path):
         check(got_l, logits, f"gguf q4_k_m pos={pos} logits", abs_bar=1e-3)
 
 
-EMB_TYPES = [0, 1, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K]
+EMB_TYPES = [0, 1, Q4_0, Q4_1, 6, 7, Q8_0, Q4_K, Q6_K]  # F32, F16, the 32- and 256-element blocks
 
 
 def emb_table(t, vocab, hidden, seed):

@@ -199,6 +199,42 @@ def test_matmul_bf16_activations(gpu, orc, t, m, n, k):
     assert r <= REL_L2 and a <= max_abs_bar(ref)
 
 
+@pytest.mark.parametrize("m", [8, 512])
+def test_matmul_bf16_config2_full_size(gpu, orc, m):
+    """Config 2 with bf16 activations at its full shape (Q4_0, N = 14336,
+    K = 4096, the sizes bench.py times): M = 8 runs the several-token GEMV on
+    the widened X, M = 512 the tiled kernel packing bf16 directly; both equal
+    the f32 product on the exactly widened X bit for bit and meet the bars
+    against f64 (every row at M = 8; the first, a middle and the last 16-token
+    tiles' rows at M = 512)."""
+    n, k = 14336, 4096
+    print(f"[case] matmul bf16 config 2 full size m={m}", flush=True)
+    w = synth.quantized_weight(Q4_0, n, k, seed=4)
+    xf = synth.activations(m * k, seed=40 + m).reshape(m, k)
+    xb16 = (xf.view(np.uint32) >> 16).astype(np.uint16)
+    xw = (xb16.astype(np.uint32) << 16).view(np.float32)
+    wb, wp = up(w)
+    xbb, xbp = up(xb16)
+    xwb, xwp = up(xw)
+    y_bf, y_f = DeviceBuffer(4 * m * n), DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_x_workspace_bytes(Q4_0, n, k, m, ops.TYPE_BF16)
+    ws = DeviceBuffer(max(wsz, 256))
+    ops.quantized_matmul_x(Q4_0, wp, w.nbytes, n, k, xbp, ops.TYPE_BF16, m, y_bf.ptr, ws, wsz)
+    wsz2 = ops.matmul_workspace_bytes(Q4_0, n, k, m)
+    ws2 = DeviceBuffer(max(wsz2, 256))
+    ops.quantized_matmul(Q4_0, wp, w.nbytes, n, k, xwp, m, y_f.ptr, ws2, wsz2)
+    got = down(y_bf, np.float32, m * n).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), down(y_f, np.float32, m * n).reshape(m, n).view(np.uint32))
+    if m <= 64:
+        rows = np.arange(m)
+    else:
+        rows = np.concatenate([np.arange(16), np.arange(m // 2, m // 2 + 16), np.arange(m - 16, m)])
+    ref = orc.matmul_rows_f64(Q4_0, w, n, k, xw, m, rows)
+    r, a = rel_l2(got[rows], ref), max_abs(got[rows], ref)
+    report(f"matmul bf16 config2 full m={m} {n}x{k}", r, a, ref)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
 def test_matmul_x_rejects_other_activation_types(gpu):
     w = synth.quantized_weight(Q4_0, 64, 256, seed=1)
     wb, wp = up(w)

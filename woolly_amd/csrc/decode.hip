@@ -344,9 +344,12 @@ WH_API int wh_llama_layer_decode(const wh_llama_model* model, size_t layer, size
 
 namespace {
 
-// Checks and launches of one step (x already holds the token's embedding);
-// every check runs before the first launch, so a rejected call changes
-// neither x nor the caches.
+// Checks and launches of one step (x already holds the token's embedding).
+// Every argument check runs before the first launch, so a call those checks
+// reject changes neither x nor the caches.  A failure reported by a launch
+// inside the layers (a HIP error, or a kernel layout rejected as
+// INVALID_SHAPE) stops the step there: x and the earlier layers' cache rows
+// at pos may then already be written.
 int decode_step(const char* fn, const wh_llama_model* model, const uint32_t* token, size_t pos, float* x,
                 float* logits, void* workspace, size_t workspace_bytes, hipStream_t s) {
   int st = check_model(fn, model);

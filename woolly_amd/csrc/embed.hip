@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_kernel(const uint8_t* 
     const uint8_t* row = table + static_cast<size_t>(id) * (hidden / 256) * TS;
     whd::kq_quad<TYPE>(row + (q >> 6) * TS, static_cast<int>(q & 63), v);
   } else {
-    constexpr uint32_t TS = TYPE == WH_TYPE_Q4_0 ? 18 : (TYPE == WH_TYPE_Q4_1 ? 20 : 34);
+    constexpr uint32_t TS = whd::BlockFmt<TYPE>::BYTES;  // Q4_0, Q4_1, Q5_0, Q5_1, Q8_0
     const uint8_t* row = table + static_cast<size_t>(id) * (hidden / 32) * TS;
     whd::decode_quad<TYPE, 2>(row + (q >> 3) * TS, static_cast<int>(q & 7), v);
   }
@@ -72,6 +72,8 @@ int launch_embedding_lookup(int type, const void* table, size_t vocab, size_t hi
     case WH_TYPE_F16: return launch_typed<WH_TYPE_F16>(table, vocab, hidden, ids, n_tokens, out, s);
     case WH_TYPE_Q4_0: return launch_typed<WH_TYPE_Q4_0>(table, vocab, hidden, ids, n_tokens, out, s);
     case WH_TYPE_Q4_1: return launch_typed<WH_TYPE_Q4_1>(table, vocab, hidden, ids, n_tokens, out, s);
+    case WH_TYPE_Q5_0: return launch_typed<WH_TYPE_Q5_0>(table, vocab, hidden, ids, n_tokens, out, s);
+    case WH_TYPE_Q5_1: return launch_typed<WH_TYPE_Q5_1>(table, vocab, hidden, ids, n_tokens, out, s);
     case WH_TYPE_Q8_0: return launch_typed<WH_TYPE_Q8_0>(table, vocab, hidden, ids, n_tokens, out, s);
     case WH_TYPE_Q4_K: return launch_typed<WH_TYPE_Q4_K>(table, vocab, hidden, ids, n_tokens, out, s);
     case WH_TYPE_Q6_K: return launch_typed<WH_TYPE_Q6_K>(table, vocab, hidden, ids, n_tokens, out, s);

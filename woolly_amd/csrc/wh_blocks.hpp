@@ -17,6 +17,14 @@ struct BlockFmt<WH_TYPE_Q4_1> {
   static constexpr int BYTES = 20;
 };
 template <>
+struct BlockFmt<WH_TYPE_Q5_0> {
+  static constexpr int BYTES = 22;
+};
+template <>
+struct BlockFmt<WH_TYPE_Q5_1> {
+  static constexpr int BYTES = 24;
+};
+template <>
 struct BlockFmt<WH_TYPE_Q8_0> {
   static constexpr int BYTES = 34;
 };

@@ -354,6 +354,12 @@ class LlamaModel:
         if tied and embd is None:
             raise ValueError("GGUF file has neither output.weight nor token_embd.weight")
         head_info = embd if tied else info("output.weight")
+        # the head is a quantized GEMV of one of these block types (a tied
+        # F32 / F16 / Q5 embedding table would fail at the first logits step)
+        head_types = (GGML_Q4_0, GGML_Q4_1, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K)
+        if int(head_info.ggml_type) not in head_types:
+            raise ValueError(f"output head {'token_embd.weight (tied)' if tied else 'output.weight'} has ggml type "
+                             f"{int(head_info.ggml_type)}; the head GEMV takes Q4_0, Q4_1, Q8_0, Q4_K or Q6_K")
         if len(head_info.shape()) != 2 or int(head_info.shape()[0]) != hidden:
             raise ValueError(f"output head has dims {list(head_info.shape())}, the config needs [{hidden}, vocab]")
         vocab = int(head_info.shape()[1])
