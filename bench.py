@@ -33,6 +33,9 @@ Prints ONE JSON line with:
   every leg      graph replays between events on the launch stream after ~0.1 s
                  of clock settling, median of 5 measurements of >= 10 ms each;
                  "spread" = (max - min) / median of the 5
+  host_slice_*   the synchronous host-slice drop-in on the headline matrix: wall
+                 µs per call uploading the weights each call, and with the device
+                 copies of host weights on
   prefill_*      config 2's M sweep (f32 and bf16 activations); the K-quant
                  formats and Q4_1 at a few tokens, and at M=512 with blocks
                  converted once per weight handle (and, for comparison, per call)
@@ -391,6 +394,32 @@ def bench_attention(iters: int, c: dict = L8B) -> dict:
             "spread": round(spread, 4)}
 
 
+def bench_host_matvec(calls: int = 20) -> dict:
+    """The synchronous host-slice drop-in (quantization.simd.quantized_matvec ->
+    wh_quantized_matvec_host) on the headline matrix, wall-clock µs per call
+    (host arrays in, host array out, the call returns when y is on the host):
+    uploading the weights on every call, and with the device copies of host
+    weights on (wh_host_cache_configure), where a call after the first moves
+    only x and y."""
+    from woolly_amd import synth
+    from woolly_amd.quantization import QuantizationScheme, QuantizedStorage, device_cache, simd
+
+    w = synth.quantized_weight(Q4_0, N_ROWS, K, seed=3)
+    x = synth.activations(K, seed=3)
+    y = np.zeros(N_ROWS, np.float32)
+    st = QuantizedStorage(QuantizationScheme.Q4_0, w)
+    out = {}
+    for name, budget in (("uploading_each_call", 0), ("cached", 1 << 30)):
+        device_cache.configure(budget)
+        simd.quantized_matvec(st, x, y, N_ROWS, K)  # first call (uploads when cached)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            simd.quantized_matvec(st, x, y, N_ROWS, K)
+        out[name] = round((time.perf_counter() - t0) / calls * 1e6, 1)
+    device_cache.configure(0)
+    return out
+
+
 def bench_stream_floor(mode: int, steps: int = 200, warmup: int = 20, n: int = N_ROWS, k: int = K,
                        replicas: int = REPLICAS) -> float:
     """The read floor of the headline GEMV's access pattern (wh_read_probe): the
@@ -731,6 +760,11 @@ def main() -> int:
                               "spread": round(bench_gemv.spread, 4)}
             log(f"[bench] gemv {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
 
+    host_mv = None
+    if not args.no_configs:
+        host_mv = bench_host_matvec()
+        log(f"[bench] host-slice GEMV (wh_quantized_matvec_host), us per call: {host_mv}")
+
     decode = decode_km = attn = None
     if not args.no_decode:
         attn = bench_attention(64)
@@ -790,6 +824,7 @@ def main() -> int:
         "prefill_gemm_q4_0_14336x4096": gemm or None,
         "prefill_kquant_14336x4096": gemm_kq or None,
         "gemv_other_configs": gemv_cfg or None,
+        "host_slice_gemv_q4_0_14336x4096_us": host_mv,
         "decode_step_llama3_8b_q4_0": decode,
         "decode_step_llama3_8b_q4_k_m": decode_km,
         "decode_attention_llama3_8b_ctx4096": attn,

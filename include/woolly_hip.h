@@ -509,7 +509,8 @@ WH_API int wh_gguf_tensor_data(const wh_gguf* g, uint64_t i, const void** data, 
 /* Uploads tensor i to a device weight handle straight from the mapping
  * (wh_weight_upload with K = dims[0], rows = dims[1] * dims[2] * ...):
  * replaces load_tensor_data_direct's to_vec (loader.rs:291) and the f32
- * dequantization cache.  Q4_0, Q4_1, Q8_0, F32 and F16 tensors. */
+ * dequantization cache.  Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, F32 and F16 tensors
+ * (the types wh_weight_upload takes). */
 WH_API int wh_gguf_upload(const wh_gguf* g, uint64_t i, wh_weight** out);
 
 /* Metadata value types (metadata.rs:13-42). */
