@@ -204,7 +204,9 @@ def test_decode_step_checks_the_head_before_any_layer():
 
 def test_embedding_lookup_argument_errors_need_no_gpu():
     lib = _lib.load()
-    assert lib.wh_embedding_lookup(6, 0x10000, 10, 256, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_UNSUPPORTED_TYPE
+    # Q2_K (10) has no embedding decoder; Q5_0 (6) has one, so its shape is checked next
+    assert lib.wh_embedding_lookup(10, 0x10000, 10, 256, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_UNSUPPORTED_TYPE
+    assert lib.wh_embedding_lookup(6, 0x10000, 10, 48, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_embedding_lookup(12, 0x10000, 10, 128, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_INVALID_SHAPE
     assert lib.wh_embedding_lookup(2, None, 10, 256, 0x10000, 1, 0x10000, None) == _lib.WH_ERR_INVALID_ARGUMENT
     assert lib.wh_embedding_lookup(2, 0x10000, 10, 256, 0x10000, 0, 0x10000, None) == _lib.WH_OK
