@@ -220,7 +220,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_mfma_kernel(
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) kc[ks] = *reinterpret_cast<const at_i4*>(kvnew + 32 * ks + 8 * g);
       }
-      vc[r] = *reinterpret_cast<const int*>(kvnew + D + 2 * lane);
+      const int vnew = *reinterpret_cast<const int*>(kvnew + D + 2 * lane);
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        if (i == r) vc[i] = vnew;
     }
     at_f4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -265,9 +268,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_mfma_kernel(
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    // P V: lane -> dims 2 lane, 2 lane + 1
-    const int npos = min(16, np - 16 * tile);
-    for (int i = 0; i < npos; i++) {
+    // P V: lane -> dims 2 lane, 2 lane + 1, over all 16 positions of the
+    // tile (a position past the chunk's last has p = 0 and a V row of zeros
+    // from the buffer range, so it adds nothing)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
       const float4 pa = *reinterpret_cast<const float4*>(pw + i * GMAX);
       float pb[4] = {0.f, 0.f, 0.f, 0.f};
       if constexpr (GMAX == 8) {
@@ -541,13 +546,34 @@ __device__ __forceinline__ float at_rl(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
+// Workgroup j -> (head h, 64-dim slice hf).  Workgroups go to the 8 XCDs in
+// turn (linear index mod 8), so with a multiple of 8 KV heads every partial
+// workgroup of KV head kvh ran on XCD kvh mod 8; the heads of kvh are then
+// combined on that XCD, whose L2 holds their partials.  Placement affects
+// speed only.
+template <int D>
+__device__ __forceinline__ void at_combine_slot(int j, int n_kv_heads, int G, int& h, int& hf) {
+  constexpr int H = D / kCombDims;
+  if (n_kv_heads % 8 == 0) {
+    const int x = j & 7, r = j >> 3, per = G * H;
+    h = (x + 8 * (r / per)) * G + (r % per) / H;
+    hf = r % H;
+  } else {
+    h = j / H;
+    hf = j % H;
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
-                                                                    float* __restrict__ out, int n_chunks) {
+                                                                    float* __restrict__ out, int n_chunks,
+                                                                    int n_kv_heads, int G) {
   __shared__ float sacc[kAttnThreads / 64][kCombDims];
-  const int h = blockIdx.x, lane = threadIdx.x & 63;
+  int h, hf;
+  at_combine_slot<D>(static_cast<int>(blockIdx.x), n_kv_heads, G, h, hf);
+  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int d = blockIdx.y * kCombDims + lane;
+  const int d = hf * kCombDims + lane;
   constexpr int kStride = (D + 2) * 4;  // bytes per chunk record (m, l, acc[D])
   const at_i4 rs = at_rsrc(part + static_cast<size_t>(h) * n_chunks * (D + 2),
                            static_cast<uint32_t>(n_chunks) * kStride);
@@ -632,7 +658,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
   const int G = static_cast<int>(n_heads / n_kv_heads);
   float* part = static_cast<float*>(ws);
   const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
-  const dim3 cgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(head_dim / kCombDims));
+  const dim3 cgrid(static_cast<unsigned>(n_heads * (head_dim / kCombDims)));
   dim3 grid(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(n_chunks));
   if (head_dim == 128) {
     if (G <= 4) {
@@ -645,7 +671,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
           static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     }
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<128><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
+    attn_combine_kernel<128><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks, static_cast<int>(n_kv_heads), G);
   } else {
     const size_t lds = partial_lds<64>(G, chunk);
     WH_ENSURE_LDS(lds, &attn_partial_kernel<64>);
@@ -653,7 +679,7 @@ int launch_attention_decode(const float* qkv, void* k_cache, void* v_cache, size
         qkv, static_cast<_Float16*>(k_cache), static_cast<_Float16*>(v_cache), inv_freq, part,
         static_cast<int>(pos), static_cast<int>(n_heads), static_cast<int>(n_kv_heads), chunk, n_chunks, scale);
     WH_LAUNCH_CHECK("attention kernel launch");
-    attn_combine_kernel<64><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks);
+    attn_combine_kernel<64><<<cgrid, kAttnThreads, 0, s>>>(part, out, n_chunks, static_cast<int>(n_kv_heads), G);
   }
   WH_LAUNCH_CHECK("attention combine launch");
   return WH_OK;

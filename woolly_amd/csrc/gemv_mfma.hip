@@ -66,6 +66,24 @@ namespace {
 // DEPTH: steps whose loads are in flight in registers (one-segment rows only).
 template <int TYPE, int NSEG, int NL, int MODE, int DEPTH>
 __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
+  // The fused modes (RMSNorm, gate + up) read more arguments before their
+  // first weight load: they request them in one burst.  The plain mode keeps
+  // the compiler's order, which measured faster for it (7.87 against 7.97 us
+  // at 14336 x 4096).
+  constexpr bool BURST = MODE != 0;
+  struct WPtrs {
+    const uint8_t *W0, *W1, *W2;
+  };
+  WPtrs pinned{};
+  if constexpr (BURST) {
+    mg_args_now(a);
+    pinned = WPtrs{mg_ptr_now(a.W0), mg_ptr_now(a.W1), mg_ptr_now(a.W2)};
+  }
+  // the weight pointers: the pinned copies, or the arguments themselves
+  const auto& wsrc = [&]() -> const auto& {
+    if constexpr (BURST) return pinned;
+    else return a;
+  }();
   static_assert(DEPTH >= 1 && (DEPTH == 1 || NSEG == 1), "register prefetch of several steps needs one segment");
   constexpr int PB = MgFmt<TYPE>::PB;
   constexpr bool FFN = (MODE & kMgFfn) != 0;
@@ -107,16 +125,18 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
     const int row = r0 + 16 * gi + wave;
     if (q >= GT || row >= r1) return false;
     int local = row;
-    const uint8_t* w = a.W0;
+    const uint8_t* w = wsrc.W0;
     if constexpr (FFN) {
-      w = (q & 1) ? a.W1 : a.W0;
+      const uint8_t* const w0 = wsrc.W0;  // values, not a choice of addresses
+      const uint8_t* const w1 = wsrc.W1;
+      w = (q & 1) ? w1 : w0;
     } else {
       if (local >= a.n0) {
         local -= a.n0;
-        w = a.W1;
+        w = wsrc.W1;
         if (local >= a.n1) {
           local -= a.n1;
-          w = a.W2;
+          w = wsrc.W2;
         }
       }
     }
@@ -125,7 +145,7 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
   };
   mg_v4i buf[DEPTH][NL];
   auto load = [&](int q, int seg, int d) {
-    const uint8_t* base = a.W0;
+    const uint8_t* base = wsrc.W0;
     const bool ok = row_src(q, &base);
     const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
     const mg_v4i rs = mg_rsrc(base + static_cast<size_t>(seg) * seg_bytes - lead, ok ? seg_bytes + lead : 0u);

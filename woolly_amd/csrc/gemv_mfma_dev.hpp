@@ -33,6 +33,32 @@ __device__ mg_v4i mg_buffer_load_x4(mg_v4i rsrc, int voffset, int soffset, int a
 
 namespace {
 
+// Every argument is requested at once, in one burst of scalar loads.  Left to
+// itself the compiler reads each field where a branch first needs it, which
+// makes the kernel-argument reads a chain of dependent round trips (each a
+// load and a wait) ahead of the first weight load.  The empty asm statement
+// takes every field as an input, so all of them are loaded before it; it
+// modifies none, so the compiler may still keep or re-read each as it likes.
+__device__ __forceinline__ void mg_args_now(const wh::MgArgs& a) {
+  asm volatile("" ::"s"(a.W0), "s"(a.W1), "s"(a.W2), "s"(a.x), "s"(a.gamma), "s"(a.residual), "s"(a.y));
+  asm volatile("" ::"s"(a.n0), "s"(a.n1), "s"(a.eps), "s"(a.n_out), "s"(a.ppr), "s"(a.seg_pairs),
+               "s"(a.rows_per_wg), "s"(a.m), "s"(a.ldy));
+}
+
+// A weight pointer held in scalar registers for the whole kernel: a choice
+// between the argument's pointers (W0 / W1 / W2 by row) is otherwise compiled
+// as a kernel-argument load at a computed offset, one more round trip before
+// the first weight load.  Returned as a generic pointer made from a global one,
+// so the loads through it stay global loads.
+__device__ __forceinline__ const uint8_t* mg_ptr_now(const uint8_t* p) {
+  const uint64_t w = reinterpret_cast<uint64_t>(p);
+  uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w));
+  uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w >> 32));
+  asm volatile("" : "+s"(lo), "+s"(hi));
+  using G = __attribute__((address_space(1))) const uint8_t;
+  return (const uint8_t*)(G*)((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Buffer resource of a raw byte range: loads at offsets >= nbytes return 0
 // without a memory access.
 __device__ __forceinline__ mg_v4i mg_rsrc(const void* base, uint32_t nbytes) {
