@@ -191,7 +191,10 @@ WH_API int wh_gemv_select(int mode, int* previous);
  * The MFMA path (more than 2 tokens) needs a device workspace of
  * wh_quantized_matmul_workspace_bytes(type, n_rows, k, n_tokens) bytes (256-byte
  * aligned); the call itself never allocates.  WH_ERR_BUFFER_TOO_SMALL if it
- * is missing or short. */
+ * is missing or short.  Where the output tiles would leave CUs idle in their
+ * last round (e.g. 14336 rows at 512 tokens), the size includes one f32 tile
+ * of 128 tokens x 256 rows per CU and a flag per CU (32 MiB + 1 KiB at 256
+ * CUs) for the stream-K split; calls that overlap on one workspace race. */
 WH_API size_t wh_quantized_matmul_workspace_bytes(int type, size_t n_rows, size_t k,
                                                   size_t n_tokens);
 WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbytes,

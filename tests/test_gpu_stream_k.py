@@ -1,0 +1,85 @@
+"""The tiled prefill GEMM's stream-K mode against the f64 oracle.
+
+When the tiles of a GEMM would leave CUs idle in their last round (224 tiles
+of 128 tokens x 256 rows on 256 CUs at M = 512, N = 14336), one workgroup per
+CU takes an equal share of the (tile, stage) units, and tiles shared by
+consecutive workgroups are completed by the workgroup holding their first
+stage, which adds the other owners' partial accumulators in owner order.
+These cases check the shapes where that happens: two owners per tile, three
+owners per tile (a workgroup's share lying strictly inside one tile), a
+partial last token tile, every 32-element block type, and repeated calls
+giving bit-identical results (the sum order does not depend on timing)."""
+import numpy as np
+import pytest
+
+from tests._gpu import down, report, up
+from tests._oracle import max_abs, rel_l2
+from woolly_amd import ops, synth
+from woolly_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
+REL_L2 = 1e-4
+
+
+def max_abs_bar(ref) -> float:
+    """max-abs <= 1e-3 against the f64 reference, relative to the output RMS
+    above an RMS of 300 (one f32 ulp at RMS 1e4 is already 1e-3)."""
+    rms = float(np.sqrt(np.mean(np.asarray(ref, np.float64) ** 2)))
+    return 1e-3 * max(1.0, rms / 300.0)
+
+
+def sk_units(n, k, m, cus):
+    """(tiles, stages per tile, units per workgroup) of the stream-K split, as
+    the launcher forms it (128-token tiles, 256 rows, 2 blocks per stage)."""
+    tiles = -(-m // 128) * -(-n // 256)
+    tile_st = k // 64
+    return tiles, tile_st, -(-tiles * tile_st // cus)
+
+
+def owners_per_tile(n, k, m, cus=256):
+    tiles, tile_st, upw = sk_units(n, k, m, cus)
+    return max(len({u // upw for u in range(t * tile_st, (t + 1) * tile_st)}) for t in range(tiles))
+
+
+def run_matmul(t, w, n, k, x, m):
+    wb, wp = up(w)
+    xb, xp = up(x)
+    yb = DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_workspace_bytes(t, n, k, m)
+    ws = DeviceBuffer(max(wsz, 1))
+    outs = []
+    for _ in range(3):
+        ops.quantized_matmul(t, wp, w.nbytes, n, k, xp, m, yb.ptr, ws, wsz)
+        outs.append(down(yb, np.float32, m * n).reshape(m, n))
+    return outs
+
+
+# token rows checked against the oracle: both ends of every 128-token tile
+ROWS = [0, 1, 126, 127, 128, 200, 255, 256, 383, 384, 450, 511]
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
+@pytest.mark.parametrize("n,k,m", [(14336, 4096, 512),   # 224 tiles: two owners per shared tile
+                                   (10240, 1024, 512),   # 160 tiles of 16 stages: three owners
+                                   (14336, 1024, 300)])  # 168 tiles, the last token tile partial
+def test_stream_k_matmul(gpu, orc, t, n, k, m):
+    print(f"[case] stream-K matmul type={t} m={m} n={n} k={k} owners<={owners_per_tile(n, k, m)}", flush=True)
+    w = synth.quantized_weight(t, n, k, seed=n + k + t)
+    x = synth.activations(m * k, seed=m + t).reshape(m, k)
+    outs = run_matmul(t, w, n, k, x, m)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "repeated calls differ"
+    rows = np.array([r for r in ROWS if r < m], dtype=np.int64)
+    ref = orc.matmul_rows_f64(t, w, n, k, x, m, rows)
+    got = outs[0][rows]
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    report(f"stream-K matmul t={t} m={m} n={n} k={k}", r, a, ref)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
+def test_stream_k_shapes_cover_three_owners():
+    """The cases above include a tile with three owners (a workgroup's units
+    strictly inside one tile) at 256 CUs, and the two-owner headline shape."""
+    assert owners_per_tile(10240, 1024, 512) == 3
+    assert owners_per_tile(14336, 4096, 512) == 2

@@ -34,11 +34,19 @@
 //     tile, whose activation fragments then stay in that XCD's L2.
 #include "wh_blocks.hpp"
 
+// raw buffer load / store of 16 bytes (llvm.amdgcn.raw.buffer.{load,store}.v4f32)
+__device__ float __attribute__((ext_vector_type(4))) gt_buffer_load_x4(int __attribute__((ext_vector_type(4))) rsrc,
+                                                                       int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ void gt_buffer_store_x4(float __attribute__((ext_vector_type(4))) v, int __attribute__((ext_vector_type(4))) rsrc,
+                                   int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.store.v4f32");
+
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int TBN = 256;              // weight rows per tile
 constexpr int TWAVES = 8;             // 2 per SIMD
@@ -156,7 +164,11 @@ template <int MODE, bool XB = false>
 __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __restrict__ x, const float* __restrict__ x2,
                                                      const float* __restrict__ gamma, float eps, int n_tokens,
                                                      int k, int kx, int type, int bm, _Float16* __restrict__ frag,
-                                                     float* __restrict__ rscale, float* __restrict__ bsum) {
+                                                     float* __restrict__ rscale, float* __restrict__ bsum,
+                                                     uint32_t* __restrict__ sk_flags, int sk_n) {
+  // the stream-K flags of the GEMMs that read this packing start cleared
+  if (blockIdx.x == 0)
+    for (int i = static_cast<int>(threadIdx.x); i < sk_n; i += static_cast<int>(blockDim.x)) sk_flags[i] = 0u;
   __shared__ float red[kPackMaxThreads / 64];
   __shared__ float red2[kPackMaxThreads / 64];
   const int NTH = static_cast<int>(blockDim.x), nw = NTH >> 6;
@@ -442,6 +454,22 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Stream-K partial tiles: a buffer resource over one slot (128 KB or less)
+// and the cache policy of the slot's loads and stores, sc1 (bit 4 of the
+// buffer instructions' cache-policy operand on gfx950): the policy the memory
+// model gives agent-scope atomic loads and stores, coherent across the XCDs'
+// L2s without a cache-wide writeback or invalidate.
+constexpr int kSkCoherent = 16;
+__device__ __forceinline__ int __attribute__((ext_vector_type(4))) sk_rsrc(const float* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  int __attribute__((ext_vector_type(4))) r;
+  r[0] = static_cast<int>(static_cast<uint32_t>(a));
+  r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xFFFFu);
+  r[2] = 1 << 20;  // 1 MB of records: every slot offset is in range
+  r[3] = 0x00020000;
+  return r;
+}
+
 // ---------------------------------------------------------------- GEMM
 // Waits until at most min(n, J) stages of N copies each are in flight.
 template <int N, int J>
@@ -456,16 +484,27 @@ __device__ __forceinline__ void wait_stages(int n) {
 
 // Y (or split-K partial plane blockIdx.y) for one BM x 256 tile over blocks
 // [kb0, kb1).  Grid: x = tiles (XCD-grouped order), y = K splits.
+// SK (stream-K; one workgroup per CU, used when the tiles do not fill the CUs
+// evenly): the work is the sequence of (tile, stage) units in tile order, and
+// workgroup v (XCD-grouped numbering) takes units [v upw, (v + 1) upw), so a
+// tile can be shared by consecutive workgroups.  A workgroup whose range
+// starts inside a tile computes that part first, stores its raw accumulators
+// in its slot of sk_part and raises its flag (sk_sub + 1; the packing kernel
+// cleared the flags); the workgroup holding the tile's first stage adds the
+// other owners' slots in owner order, then scales and stores, so the result
+// does not depend on timing.  Its wait is bounded: if a flag has not come,
+// it computes the rest of the tile itself.
 // FFNP (the FFN's gate and up in one pass, no split-K): a tile's 256 weight
 // rows are 128 rows of W (gate) and the same 128 rows of W2 (up); every wave
 // holds gate and up tiles of the same rows side by side (row groups 2m and
 // 2m + 1), and the epilogue writes y = silu(gate x) * (up x) for n_rows
 // output columns (tensor_utils.rs:512-532), so neither product reaches HBM.
-template <int TYPE, int BM, bool FFNP = false>
+template <int TYPE, int BM, bool FFNP = false, bool SK = false>
 __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const _Float16* __restrict__ frag,
     const float* __restrict__ rscale, const float* __restrict__ bsum, const float* __restrict__ dmin,
-    float* __restrict__ y, int n_tokens, int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles) {
+    float* __restrict__ y, int n_tokens, int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles,
+    uint32_t* __restrict__ sk_flags, float* __restrict__ sk_part, int sk_upw, int sk_sub) {
   using C = TCfg<BM>;
   constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = nstage<TYPE, BM>();
   constexpr int A_STAGE = C::A_STAGE;
@@ -488,19 +527,41 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   const int wm = (wave / C::WGN) * C::WTM;   // token offset of the wave tile
   const int wn = (wave % C::WGN) * C::WTN;   // row offset of the wave tile
 
-  // tile index: tiles resident on one XCD (workgroup id mod 8) are consecutive
   const int bid = blockIdx.x;
-  const int q = n_tiles / 8, rem = n_tiles % 8;
-  const int xcd = bid % 8, local = bid / 8;
-  const int L = xcd * q + min(xcd, rem) + local;
-  const int T = L / tiles_n, R = L % tiles_n;
   constexpr int HALF = TBN / 2;  // FFNP: rows of each matrix per tile
-  const int t0 = T * BM, r0 = R * (FFNP ? HALF : TBN);
-
-  const int kb0 = blockIdx.y * blocks_per_split;
-  const int kb1 = min(nb, kb0 + blocks_per_split);
-  const int n_stages = kb1 > kb0 ? (kb1 - kb0) / SB : 0;
   const size_t row_bytes = static_cast<size_t>(nb) * TS;
+  const int tile_st = nb / SB;   // stages of a whole tile
+  // units [u, u_end) of this workgroup; without SK one segment: a tile (tiles
+  // resident on one XCD, workgroup id mod 8, are consecutive) and the stages
+  // of split blockIdx.y
+  int u = 0, u_end = 1, v = 0;
+  if constexpr (SK) {
+    v = (bid % 8) * static_cast<int>(gridDim.x / 8) + bid / 8;
+    u = v * sk_upw;
+    u_end = min(n_tiles * tile_st, u + sk_upw);
+  }
+  __shared__ int sk_ok;
+  for (bool first = true; u < u_end; first = false) {
+  int L, st_a, st_b;
+  if constexpr (SK) {
+    L = u / tile_st;
+    st_a = u % tile_st;
+    st_b = min(tile_st, st_a + (u_end - u));
+    u += st_b - st_a;
+  } else {
+    const int q = n_tiles / 8, rem = n_tiles % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    L = xcd * q + min(xcd, rem) + local;
+    const int kbs = blockIdx.y * blocks_per_split;
+    st_a = kbs / SB;
+    st_b = min(nb, kbs + blocks_per_split) / SB;
+    if (st_b < st_a) st_b = st_a;
+    u = u_end;
+  }
+  const int T = L / tiles_n, R = L % tiles_n;
+  const int t0 = T * BM, r0 = R * (FFNP ? HALF : TBN);
+  // every wave is done with the ring of the previous segment before it is refilled
+  if (!first) __syncthreads();
 
   // Byte offset (from W) of each raw weight dword this lane copies per stage:
   // dword gi of the stage's [row][DWB] chunk; rows past the end re-read the
@@ -522,6 +583,8 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   // MFMA lane l (k-group l / 16, token l % 16) of a fragment, stored token-major
   const uint32_t frag_lane_off = 16u * (4u * (lane & 15) + (lane >> 4));
 
+  // the stages of the current pass: [kb0, kb0 + SB n_stages) in blocks
+  int kb0 = st_a * SB, n_stages = st_b - st_a;
   auto issue = [&](int st) {
     if (st >= n_stages) return;
     const uint32_t slot = smem_base + (st % NSTAGE) * STAGE;
@@ -596,6 +659,21 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     }
   };
 
+  // A head part (SK) that does not get every other owner's slot in time runs
+  // a second pass over the rest of the tile, into the same accumulators.
+  for (int pass = 0; pass < 2; pass++) {
+  if (pass > 0) {
+    __syncthreads();  // the ring of the first pass is no longer read
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < IT; i++) cc[b][h][i] = float4v{0.f, 0.f, 0.f, 0.f};
+    pd[0] = pd[1] = pm[0] = pm[1] = 0.f;
+#pragma unroll
+    for (int i = 0; i < IT; i++) psx[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
 #pragma unroll
   for (int st = 0; st < NSTAGE - 1; st++) issue(st);
   for (int st = 0; st < n_stages; st++) {
@@ -720,13 +798,70 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
 #pragma unroll
     for (int i = 0; i < IT; i++) scale_one(NT - 2 + h, (SB * (NT / 2) - 1) & 1, h, i);
   wait_vmcnt<0>();  // (no copies remain: every issued stage was consumed)
+  if constexpr (!SK) break;
+  if (pass > 0 || st_a > 0 || st_b == tile_st) break;  // a tail part, the whole tile, or done here
+  // head part: wait for the owners of the rest of the tile (workgroups
+  // v + 1 .. w_last), then add their slots in order
+  const int w_last = min(static_cast<int>(gridDim.x) - 1, ((L + 1) * tile_st - 1) / sk_upw);
+  if (threadIdx.x == 0) {
+    int ok = 1;
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+    for (int w = v + 1; w <= w_last && ok; w++) {
+      while (__hip_atomic_load(sk_flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+             static_cast<uint32_t>(sk_sub + 1)) {
+        if (__builtin_amdgcn_s_memrealtime() - t_start > 100000u) {  // 1 ms at 100 MHz
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    sk_ok = ok;
+  }
+  __syncthreads();
+  if (sk_ok) {
+    for (int w = v + 1; w <= w_last; w++) {
+      // the slot through device-coherent loads (sc1: the policy of an
+      // agent-scope atomic load), all issued before the first is used
+      const i32x4 rs = sk_rsrc(sk_part + static_cast<size_t>(w) * BM * TBN);
+#pragma unroll
+      for (int i = 0; i < IT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+          acc[i][n] += gt_buffer_load_x4(rs, 16 * ((i * NT + n) * (TWAVES * 64) + static_cast<int>(threadIdx.x)), 0,
+                                         kSkCoherent);
+    }
+    break;
+  }
+  kb0 = st_b * SB;  // the rest of the tile, here
+  n_stages = tile_st - st_b;
+  }  // pass
+  if constexpr (SK) {
+    if (st_a > 0) {
+      // a tail part: the raw accumulators to this workgroup's slot through
+      // device-coherent stores (sc1, write-through), then its flag
+      const i32x4 rs = sk_rsrc(sk_part + static_cast<size_t>(v) * BM * TBN);
+#pragma unroll
+      for (int i = 0; i < IT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+          gt_buffer_store_x4(acc[i][n], rs, 16 * ((i * NT + n) * (TWAVES * 64) + static_cast<int>(threadIdx.x)), 0,
+                             kSkCoherent);
+      // every store of the slot complete before the flag is raised
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_store(sk_flags + v, static_cast<uint32_t>(sk_sub + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+  }
 
   if constexpr (TYPE == wh::kGemmQ4F) {
     // Q4_K's dmin: acc += dmin[sb][row] * S[sb][token] over this split's
     // super-blocks (split bounds are multiples of 8 blocks), S the packing's
     // super-block sums in the same scaled domain as acc
     const int nsb = nb / 8;
-    for (int sb = kb0 / 8; sb < kb1 / 8; sb++) {
+    for (int sb = st_a * SB / 8; sb < st_b * SB / 8; sb++) {
       float dm[NT];
 #pragma unroll
       for (int n = 0; n < NT; n++) dm[n] = dmin[static_cast<size_t>(sb) * n_rows + min(r0 + wn + 16 * n + ln, n_rows - 1)];
@@ -759,7 +894,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         }
       }
     }
-    return;
+    continue;
   }
   // epilogue: undo the row scale; split-K partials go to plane blockIdx.y
   float* out = y + static_cast<size_t>(blockIdx.y) * n_tokens * n_rows;
@@ -777,6 +912,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       }
     }
   }
+  }  // segment
 }
 
 __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* __restrict__ part, int splits,
@@ -793,21 +929,55 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(const float* _
 // holds it (one tile) or 128 beyond.
 int tile_bm(size_t n_tokens) { return n_tokens <= 16 ? 16 : (n_tokens <= 32 ? 32 : (n_tokens <= 64 ? 64 : 128)); }
 
+// Stream-K grid for n_tiles tiles of tile_st stages each: one workgroup per
+// CU when the tiles would leave CUs idle in their last round and every
+// workgroup's share is at least half a tile; 0 (one workgroup per tile)
+// otherwise.  The 4- and 8-bit GGUF formats only (the K-quant formats add
+// their dmin term per tile and split).
+int sk_grid(int type, size_t n_tiles, size_t tile_st) {
+  if (type != WH_TYPE_Q4_0 && type != WH_TYPE_Q4_1 && type != WH_TYPE_Q8_0) return 0;
+  const size_t g = static_cast<size_t>(wh::cu_count());
+  if (g == 0 || g % 8 != 0 || n_tiles % g == 0 || n_tiles * 2 <= g) return 0;
+  const size_t upw = (n_tiles * tile_st + g - 1) / g;
+  return 2 * upw >= tile_st ? static_cast<int>(g) : 0;
+}
+
+// The stream-K state of a launch: flags and partial slots (SkWs::g workgroups).
+struct SkWs {
+  uint32_t* flags;
+  float* part;
+  int g;    // stream-K grid, 0 for one workgroup per tile
+  int sub;  // which of the GEMMs after one packing this is (its flag value - 1)
+};
+
 template <int TYPE, int BM>
 int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
-              const float* rs, const float* bs, const float* dmin, float* part, int splits, hipStream_t s) {
+              const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
+              hipStream_t s) {
   const int nb = static_cast<int>(k / 32);
   const int tiles_n = static_cast<int>((n_rows + TBN - 1) / TBN);
   const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
+  const int n_tiles = tiles_m * tiles_n;
+  const size_t lds = tiled_lds_bytes<TYPE, BM>();
+  if constexpr (TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q4_1 || TYPE == WH_TYPE_Q8_0) {
+    if (splits == 1 && sk.g > 0 && sk_grid(TYPE, n_tiles, nb / SB) == sk.g) {
+      const int upw = (n_tiles * (nb / SB) + sk.g - 1) / sk.g;
+      WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, true>);
+      gemm_tiled_kernel<TYPE, BM, false, true><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
+          w, nullptr, frag, rs, bs, dmin, part, static_cast<int>(n_tokens), static_cast<int>(n_rows), nb, nb, tiles_n,
+          n_tiles, sk.flags, sk.part, upw, sk.sub);
+      WH_LAUNCH_CHECK("tiled gemm kernel launch");
+      return WH_OK;
+    }
+  }
   int bps = (nb + splits - 1) / splits;
   constexpr int ALIGN = TYPE == wh::kGemmQ4F ? 8 : SB;   // kGemmQ4F: whole super-blocks per split
   bps = (bps + ALIGN - 1) / ALIGN * ALIGN;
-  const size_t lds = tiled_lds_bytes<TYPE, BM>();
   WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM>);
-  dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), static_cast<unsigned>(splits));
+  dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(splits));
   gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
                                                            static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
-                                                           bps, tiles_n, tiles_m * tiles_n);
+                                                           bps, tiles_n, n_tiles, nullptr, nullptr, 0, 0);
   WH_LAUNCH_CHECK("tiled gemm kernel launch");
   return WH_OK;
 }
@@ -815,38 +985,49 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
 // The FFN's gate and up (n_ff rows each) in one pass: h = silu(gate x) * (up x).
 template <int TYPE, int BM>
 int launch_ffn_bm(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k, size_t n_tokens,
-                  const _Float16* frag, const float* rs, const float* bs, float* h, hipStream_t s) {
+                  const _Float16* frag, const float* rs, const float* bs, float* h, const SkWs& sk, hipStream_t s) {
   const int nb = static_cast<int>(k / 32);
   const int tiles_n = static_cast<int>((n_ff + TBN / 2 - 1) / (TBN / 2));
   const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
+  const int n_tiles = tiles_m * tiles_n;
   const size_t lds = tiled_lds_bytes<TYPE, BM>();
+  if (sk.g > 0 && sk_grid(TYPE, n_tiles, nb / SB) == sk.g) {
+    const int upw = (n_tiles * (nb / SB) + sk.g - 1) / sk.g;
+    WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, true, true>);
+    gemm_tiled_kernel<TYPE, BM, true, true><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
+        gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
+        n_tiles, sk.flags, sk.part, upw, sk.sub);
+    WH_LAUNCH_CHECK("tiled ffn gate/up kernel launch");
+    return WH_OK;
+  }
   WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, true>);
-  gemm_tiled_kernel<TYPE, BM, true><<<static_cast<unsigned>(tiles_m * tiles_n), TWAVES * 64, lds, s>>>(
+  gemm_tiled_kernel<TYPE, BM, true><<<static_cast<unsigned>(n_tiles), TWAVES * 64, lds, s>>>(
       gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
-      tiles_m * tiles_n);
+      n_tiles, nullptr, nullptr, 0, 0);
   WH_LAUNCH_CHECK("tiled ffn gate/up kernel launch");
   return WH_OK;
 }
 
 template <int TYPE>
 int launch_ffn_typed(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k, size_t n_tokens,
-                     const _Float16* frag, const float* rs, const float* bs, float* h, hipStream_t s) {
+                     const _Float16* frag, const float* rs, const float* bs, float* h, const SkWs& sk, hipStream_t s) {
   switch (tile_bm(n_tokens)) {
-    case 16: return launch_ffn_bm<TYPE, 16>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
-    case 32: return launch_ffn_bm<TYPE, 32>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
-    case 64: return launch_ffn_bm<TYPE, 64>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
-    default: return launch_ffn_bm<TYPE, 128>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, s);
+    case 16: return launch_ffn_bm<TYPE, 16>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, sk, s);
+    case 32: return launch_ffn_bm<TYPE, 32>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, sk, s);
+    case 64: return launch_ffn_bm<TYPE, 64>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, sk, s);
+    default: return launch_ffn_bm<TYPE, 128>(gate, up, n_ff, k, n_tokens, frag, rs, bs, h, sk, s);
   }
 }
 
 template <int TYPE>
 int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
-                 const float* rs, const float* bs, const float* dmin, float* part, int splits, hipStream_t s) {
+                 const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
+                 hipStream_t s) {
   switch (tile_bm(n_tokens)) {
-    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
-    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
-    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
-    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, s);
+    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
+    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
+    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
+    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
   }
 }
 
@@ -913,6 +1094,27 @@ int gemm_tiled_splits(size_t n_rows, size_t n_tokens, size_t k) {
   return s;
 }
 
+// Stream-K workgroups of a workspace laid out for a GEMM over n_rows rows:
+// the grid of that GEMM, or of the FFN's gate and up over n_rows rows each in
+// one pass (the same packing), whichever uses stream-K; 0 when neither does.
+static int sk_slots(int type, size_t n_rows, size_t n_tokens, size_t k) {
+  const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
+  const size_t tiles_m = (n_tokens + bm - 1) / bm, tile_st = k / 32 / SB;
+  if (gemm_tiled_splits(n_rows, n_tokens, k) == 1) {
+    const int g = sk_grid(type, tiles_m * ((n_rows + TBN - 1) / TBN), tile_st);
+    if (g) return g;
+  }
+  if (gemm_tiled_splits(2 * n_rows, n_tokens, k) == 1)
+    return sk_grid(type, tiles_m * ((n_rows + TBN / 2 - 1) / (TBN / 2)), tile_st);
+  return 0;
+}
+
+static size_t sk_bytes(int slots, size_t n_tokens) {
+  return slots ? al256(static_cast<size_t>(slots) * 4) +
+                     static_cast<size_t>(slots) * static_cast<size_t>(tile_bm(n_tokens)) * TBN * 4
+               : 0;
+}
+
 size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   const size_t tm = (n_tokens + bm - 1) / bm * bm;   // padded tokens
@@ -920,16 +1122,19 @@ size_t gemm_tiled_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size
   if (needs_bsum(type)) b += al256(tm * bsum_groups(type, k) * 4);
   const int splits = gemm_tiled_splits(n_rows, n_tokens, k);
   if (splits > 1) b += al256(static_cast<size_t>(splits) * n_rows * n_tokens * 4);
-  return b;
+  return b + sk_bytes(sk_slots(type, n_rows, n_tokens, k), n_tokens);
 }
 
 // Workspace of one tiled GEMM: packed activations, row scales, Q4_1 block
-// sums, split-K partial planes.
+// sums, split-K partial planes, stream-K flags and partial tiles.
 struct TiledWs {
   _Float16* frag;
   float* rs;
   float* bs;
   float* part;  // null without split-K
+  uint32_t* sk_flags;
+  float* sk_part;
+  int sk_n;     // stream-K slots (0: none)
   int bm, splits;
   size_t tm;
 };
@@ -949,6 +1154,12 @@ static TiledWs tiled_ws(int type, size_t n_rows, size_t k, size_t n_tokens, void
   }
   t.splits = gemm_tiled_splits(n_rows, n_tokens, k);
   t.part = t.splits > 1 ? reinterpret_cast<float*>(ws) : nullptr;
+  if (t.splits > 1) ws += al256(static_cast<size_t>(t.splits) * n_rows * n_tokens * 4);
+  t.sk_n = sk_slots(type, n_rows, n_tokens, k);
+  if (t.sk_n) {
+    t.sk_flags = reinterpret_cast<uint32_t*>(ws);
+    t.sk_part = reinterpret_cast<float*>(ws + al256(static_cast<size_t>(t.sk_n) * 4));
+  }
   return t;
 }
 
@@ -961,23 +1172,26 @@ static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x
   threads = threads < 256 ? 256 : (threads > kPackMaxThreads ? kPackMaxThreads : (threads + 63) / 64 * 64);
   pack_a_kernel<MODE, XB><<<static_cast<unsigned>(t.tm), static_cast<unsigned>(threads), 0, s>>>(x, x2, gamma, eps, static_cast<int>(n_tokens),
                                                                   static_cast<int>(k), static_cast<int>(kx), type, t.bm,
-                                                                  t.frag, t.rs, t.bs);
+                                                                  t.frag, t.rs, t.bs, t.sk_flags, t.sk_n);
   WH_LAUNCH_CHECK("pack kernel launch");
   return WH_OK;
 }
 
 // The GEMM over packed activations (and the split-K reduce) into y.
+// sub: which of the GEMMs that read one packing this is (0, 1), so that their
+// stream-K flags differ.
 static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t, float* y,
-                     hipStream_t s, const float* dmin = nullptr) {
+                     hipStream_t s, const float* dmin = nullptr, int sub = 0) {
   const uint8_t* wp = static_cast<const uint8_t*>(w);
   float* part = t.splits > 1 ? t.part : y;
+  const SkWs sk{t.sk_flags, t.sk_part, t.sk_n, sub};
   int st;
   switch (type) {
-    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
-    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
-    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
-    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
-    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, s); break;
+    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
+    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
+    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
+    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
+    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
     default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
   }
   if (st != WH_OK) return st;
@@ -1023,10 +1237,10 @@ bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size
 // GEMM on a repacked K-quant matrix rp (its GEMM format, rows of k elements)
 // over packed activations t; Q4_K's dmin table follows the blocks.
 static int kquant_run(int type, const char* rp, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t,
-                      float* y, hipStream_t s) {
+                      float* y, hipStream_t s, int sub = 0) {
   const float* dmin_t =
       type == WH_TYPE_Q4_K ? reinterpret_cast<const float*>(rp + n_rows * (k / 32) * 20) : nullptr;
-  return tiled_run(kquant_gemm_type(type), rp, n_rows, kquant_gemm_k(type, k), n_tokens, t, y, s, dmin_t);
+  return tiled_run(kquant_gemm_type(type), rp, n_rows, kquant_gemm_k(type, k), n_tokens, t, y, s, dmin_t, sub);
 }
 
 size_t gemm_kquant_workspace_bytes(int type, size_t n_rows, size_t n_tokens, size_t k) {
@@ -1086,9 +1300,9 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
     const TiledWs t1 = tiled_ws(it, n_ff, H2, n_tokens, ws);
     int st = tiled_pack<kPackNorm>(it, t1, x, nullptr, gamma, eps, n_tokens, H2, hidden, s);
     if (!st) st = repacked(gate, n_ff, hidden, &src);
-    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, g, s);
+    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, g, s, 0);
     if (!st) st = repacked(up, n_ff, hidden, &src);
-    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, u, s);
+    if (!st) st = kquant_run(type, src, n_ff, hidden, n_tokens, t1, u, s, 1);
     if (st) return st;
     const TiledWs t2 = tiled_ws(it, hidden, F2, n_tokens, ws);
     st = tiled_pack<kPackSwiglu>(it, t2, g, u, nullptr, 0.f, n_tokens, F2, n_ff, s);
@@ -1111,15 +1325,16 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
     // written by its epilogue (g holds h), then packed for the down projection
     const uint8_t* gp = static_cast<const uint8_t*>(gate);
     const uint8_t* upp = static_cast<const uint8_t*>(up);
+    const SkWs sk{t1.sk_flags, t1.sk_part, t1.sk_n, 0};
     switch (type) {
-      case WH_TYPE_Q4_0: st = launch_ffn_typed<WH_TYPE_Q4_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
-      case WH_TYPE_Q4_1: st = launch_ffn_typed<WH_TYPE_Q4_1>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
-      default: st = launch_ffn_typed<WH_TYPE_Q8_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, s); break;
+      case WH_TYPE_Q4_0: st = launch_ffn_typed<WH_TYPE_Q4_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, sk, s); break;
+      case WH_TYPE_Q4_1: st = launch_ffn_typed<WH_TYPE_Q4_1>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, sk, s); break;
+      default: st = launch_ffn_typed<WH_TYPE_Q8_0>(gp, upp, n_ff, hidden, n_tokens, t1.frag, t1.rs, t1.bs, g, sk, s); break;
     }
     if (!st) st = tiled_pack<kPackPlain>(type, t2, g, nullptr, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
   } else {
-    st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s);
-    if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s);
+    st = tiled_run(type, gate, n_ff, hidden, n_tokens, t1, g, s, nullptr, 0);
+    if (!st) st = tiled_run(type, up, n_ff, hidden, n_tokens, t1, u, s, nullptr, 1);
     if (!st) st = tiled_pack<kPackSwiglu>(type, t2, g, u, nullptr, 0.f, n_tokens, n_ff, n_ff, s);
   }
   if (st) return st;

@@ -350,7 +350,8 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
   // All 64 lanes: lane (n, g) adds waves 4g .. 4g + 3 of row n, the lane
   // groups are then summed across (a short chain on the finishing wave, which
   // computes its own chunk after this).
-  auto finish = [&](int q) {
+  // to_y: the group's rows go straight to y (the last group, after the loop)
+  auto finish = [&](int q, bool to_y) {
     const float* pp = part + (q & 1) * kMgWaves * 16 + 64 * g + n;
     const float v0 = pp[0], v1 = pp[16], v2 = pp[32], v3 = pp[48];
     float v = mg_sum_lane_groups((v0 + v1) + (v2 + v3));
@@ -370,9 +371,17 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
         return;
       }
       const float gt = misc[16 + n];
-      if (row < r1) rows_lds[row - r0] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+      if (row < r1) {
+        const float out = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+        if (to_y) a.y[row] = out;
+        else rows_lds[row - r0] = out;
+      }
     } else {
-      if (row < r1) rows_lds[row - r0] = rows_lds[row - r0] + v;
+      if (row < r1) {
+        const float out = rows_lds[row - r0] + v;
+        if (to_y) a.y[row] = out;
+        else rows_lds[row - r0] = out;
+      }
     }
   };
 
@@ -408,7 +417,7 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (seg == 0 && q > 0 && q < GT && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
+      if (seg == 0 && q > 0 && q < GT && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1, false);
       if (owns && live) {
         if constexpr (NSEG > 1) get_x(seg);
         const uint32_t lead = (static_cast<uint32_t>(seg) * seg_bytes) & (kLeadRoom ? 15u : 0u);
@@ -526,11 +535,11 @@ __device__ __forceinline__ void gemv_mfma_body(const MgArgs& a, int bid) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  for (int i = threadIdx.x; i < r1 - r0; i += kMgWaves * 64) a.y[r0 + i] = rows_lds[i];
+  // The last row group goes from the wave that finishes it straight to y;
+  // every earlier group is complete in rows_lds since the barrier above.
+  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1, true);
+  const int done_rows = min(16 * (G - 1), r1 - r0);
+  for (int i = threadIdx.x; i < done_rows; i += kMgWaves * 64) a.y[r0 + i] = rows_lds[i];
 }
 
 template <int TYPE, int NSEG, int NL, int MODE, int DEPTH>

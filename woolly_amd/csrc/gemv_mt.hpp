@@ -336,8 +336,9 @@ __device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
     }
   };
 
-  // Sum of group q over the 16 waves (fixed order) for every token, then the output rows.
-  auto finish = [&](int q) {
+  // Sum of group q over the 16 waves (fixed order) for every token, then the
+  // output rows (to_y: straight to y, for the last group after the loop).
+  auto finish = [&](int q, bool to_y) {
     const int gi = FFN ? (q >> 1) : q;
     const int row = r0 + 16 * gi + n;
     if (MS == 2 && g >= 2) return;
@@ -354,10 +355,13 @@ __device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
           misc[t * 16 + n] = v;  // gate, combined with up one group later
         } else if (row < r1) {
           const float gt = misc[t * 16 + n];
-          rows_lds[t * R + row - r0] = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+          const float out = (gt * (1.0f / (1.0f + expf(-gt)))) * v;
+          if (!to_y) rows_lds[t * R + row - r0] = out;
+          else if (t < M) a.y[static_cast<size_t>(t) * a.ldy + row] = out;
         }
       } else if (row < r1) {
-        rows_lds[t * R + row - r0] = v;
+        if (!to_y) rows_lds[t * R + row - r0] = v;
+        else if (t < M) a.y[static_cast<size_t>(t) * a.ldy + row] = v;
       }
     }
   };
@@ -397,7 +401,7 @@ __device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
           rms_lds[lane] = sqrtf(tot / static_cast<float>(K) + a.eps);
         }
       }
-      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1);
+      if (seg == 0 && q > 0 && wave == ((q - 1) & (kMgWaves - 1))) finish(q - 1, false);
       if (owns) {
         const uint8_t* rowp = slot + n * rstr + lead + wave * CB;
         float sacc[TG];
@@ -548,12 +552,12 @@ __device__ __forceinline__ void gemv_mt_body(const MgArgs& a, int bid) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  for (int i = threadIdx.x; i < M * (r1 - r0); i += kMgWaves * 64) {
-    const int t = i / (r1 - r0), r = i - t * (r1 - r0);
+  // The last row group goes from the wave that finishes it straight to y;
+  // every earlier group is complete in rows_lds since the barrier above.
+  if (GT > 0 && wave == ((GT - 1) & (kMgWaves - 1))) finish(GT - 1, true);
+  const int done_rows = min(16 * (G - 1), r1 - r0);
+  for (int i = threadIdx.x; i < M * done_rows; i += kMgWaves * 64) {
+    const int t = i / done_rows, r = i - t * done_rows;
     a.y[static_cast<size_t>(t) * a.ldy + r0 + r] = rows_lds[t * R + r];
   }
 }
