@@ -5,10 +5,13 @@ of 128 tokens x 256 rows on 256 CUs at M = 512, N = 14336), one workgroup per
 CU takes an equal share of the (tile, stage) units, and tiles shared by
 consecutive workgroups are completed by the workgroup holding their first
 stage, which adds the other owners' partial accumulators in owner order.
-These cases check the shapes where that happens: two owners per tile, three
-owners per tile (a workgroup's share lying strictly inside one tile), a
-partial last token tile, every 32-element block type, and repeated calls
-giving bit-identical results (the sum order does not depend on timing)."""
+The same split replaces split-K (partial planes and a reduce launch) where
+there are fewer tiles than CUs, with 64- or 128-token tiles.  These cases
+check the shapes where that happens: two owners per tile, three owners per
+tile (a workgroup's share lying strictly inside one tile), sixteen owners
+per tile (16 tiles on 256 workgroups), a partial last token tile, every
+32-element block type, and repeated calls giving bit-identical results (the
+sum order does not depend on timing)."""
 import numpy as np
 import pytest
 
@@ -31,8 +34,10 @@ def max_abs_bar(ref) -> float:
 
 def sk_units(n, k, m, cus):
     """(tiles, stages per tile, units per workgroup) of the stream-K split, as
-    the launcher forms it (128-token tiles, 256 rows, 2 blocks per stage)."""
-    tiles = -(-m // 128) * -(-n // 256)
+    the launcher forms it (tiles of 64 or 128 tokens and 256 rows, 2 blocks
+    per stage)."""
+    bm = 64 if m <= 64 else 128
+    tiles = -(-m // bm) * -(-n // 256)
     tile_st = k // 64
     return tiles, tile_st, -(-tiles * tile_st // cus)
 
@@ -55,14 +60,16 @@ def run_matmul(t, w, n, k, x, m):
     return outs
 
 
-# token rows checked against the oracle: both ends of every 128-token tile
-ROWS = [0, 1, 126, 127, 128, 200, 255, 256, 383, 384, 450, 511]
+# token rows checked against the oracle: both ends of every 64- and 128-token tile
+ROWS = [0, 1, 62, 63, 64, 99, 126, 127, 128, 200, 255, 256, 383, 384, 450, 511]
 
 
 @pytest.mark.parametrize("t", [Q4_0, Q4_1, Q8_0])
 @pytest.mark.parametrize("n,k,m", [(14336, 4096, 512),   # 224 tiles: two owners per shared tile
                                    (10240, 1024, 512),   # 160 tiles of 16 stages: three owners
-                                   (14336, 1024, 300)])  # 168 tiles, the last token tile partial
+                                   (14336, 1024, 300),   # 168 tiles, the last token tile partial
+                                   (14336, 4096, 64),    # 56 tiles of 64 tokens: stream-K instead of split-K
+                                   (4096, 14336, 100)])  # 16 tiles of 224 stages: 16 owners per tile
 def test_stream_k_matmul(gpu, orc, t, n, k, m):
     print(f"[case] stream-K matmul type={t} m={m} n={n} k={k} owners<={owners_per_tile(n, k, m)}", flush=True)
     w = synth.quantized_weight(t, n, k, seed=n + k + t)
@@ -83,3 +90,4 @@ def test_stream_k_shapes_cover_three_owners():
     strictly inside one tile) at 256 CUs, and the two-owner headline shape."""
     assert owners_per_tile(10240, 1024, 512) == 3
     assert owners_per_tile(14336, 4096, 512) == 2
+    assert owners_per_tile(4096, 14336, 100) == 16
