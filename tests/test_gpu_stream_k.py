@@ -21,7 +21,7 @@ from woolly_amd import ops, synth
 from woolly_amd.device import DeviceBuffer
 
 pytestmark = pytest.mark.gpu
-Q4_0, Q4_1, Q8_0 = 2, 3, 8
+Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
 REL_L2 = 1e-4
 
 
@@ -82,6 +82,26 @@ def test_stream_k_matmul(gpu, orc, t, n, k, m):
     got = outs[0][rows]
     r, a = rel_l2(got, ref), max_abs(got, ref)
     report(f"stream-K matmul t={t} m={m} n={n} k={k}", r, a, ref)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n,k,m", [(14336, 4096, 512), (4096, 14336, 100)])
+def test_stream_k_kquant_matmul(gpu, orc, t, n, k, m):
+    """The K-quant formats (converted per call to 32-element blocks with f32
+    scales): the same split, Q4_K's dmin term added once per tile by the
+    workgroup that finishes it."""
+    print(f"[case] stream-K kquant matmul type={t} m={m} n={n} k={k}", flush=True)
+    w = synth.quantized_weight(t, n, k, seed=n + k + t)
+    x = synth.activations(m * k, seed=m + t).reshape(m, k)
+    outs = run_matmul(t, w, n, k, x, m)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "repeated calls differ"
+    rows = np.array([r for r in ROWS if r < m], dtype=np.int64)
+    ref = orc.matmul_rows_f64(t, w, n, k, x, m, rows)
+    got = outs[0][rows]
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    report(f"stream-K kquant matmul t={t} m={m} n={n} k={k}", r, a, ref)
     assert r <= REL_L2 and a <= max_abs_bar(ref)
 
 

@@ -859,9 +859,12 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   if constexpr (TYPE == wh::kGemmQ4F) {
     // Q4_K's dmin: acc += dmin[sb][row] * S[sb][token] over this split's
     // super-blocks (split bounds are multiples of 8 blocks), S the packing's
-    // super-block sums in the same scaled domain as acc
+    // super-block sums in the same scaled domain as acc.  Under stream-K the
+    // workgroup that finishes a tile adds the term of every super-block (the
+    // other owners' parts carry none).
     const int nsb = nb / 8;
-    for (int sb = st_a * SB / 8; sb < st_b * SB / 8; sb++) {
+    const int sb_lo = SK ? 0 : st_a * SB / 8, sb_hi = SK ? nsb : st_b * SB / 8;
+    for (int sb = sb_lo; sb < sb_hi; sb++) {
       float dm[NT];
 #pragma unroll
       for (int n = 0; n < NT; n++) dm[n] = dmin[static_cast<size_t>(sb) * n_rows + min(r0 + wn + 16 * n + ln, n_rows - 1)];
@@ -933,10 +936,11 @@ int tile_bm(size_t n_tokens) { return n_tokens <= 16 ? 16 : (n_tokens <= 32 ? 32
 // CU whenever the tiles do not fill the CUs evenly (a last round with idle
 // CUs, or fewer tiles than CUs, where split-K planes and a reduce would
 // otherwise be needed) and every workgroup's share is at least 8 stages; 0
-// (one workgroup per tile) otherwise.  The 4- and 8-bit GGUF formats only
-// (the K-quant formats add their dmin term per tile and split).
+// (one workgroup per tile) otherwise.  Every block format of the kernel.
 int sk_grid(int type, size_t n_tiles, size_t tile_st) {
-  if (type != WH_TYPE_Q4_0 && type != WH_TYPE_Q4_1 && type != WH_TYPE_Q8_0) return 0;
+  if (type != WH_TYPE_Q4_0 && type != WH_TYPE_Q4_1 && type != WH_TYPE_Q8_0 && type != wh::kGemmQ4F &&
+      type != wh::kGemmQ8H)
+    return 0;
   const size_t g = static_cast<size_t>(wh::cu_count());
   if (g == 0 || g % 8 != 0 || n_tiles % g == 0) return 0;
   const size_t upw = (n_tiles * tile_st + g - 1) / g;
@@ -960,7 +964,7 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   const int tiles_m = static_cast<int>((n_tokens + BM - 1) / BM);
   const int n_tiles = tiles_m * tiles_n;
   const size_t lds = tiled_lds_bytes<TYPE, BM>();
-  if constexpr (TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q4_1 || TYPE == WH_TYPE_Q8_0) {
+  {
     if (splits == 1 && sk.g > 0 && sk_grid(TYPE, n_tiles, nb / SB) == sk.g) {
       const int upw = (n_tiles * (nb / SB) + sk.g - 1) / sk.g;
       WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, true>);
@@ -1101,9 +1105,13 @@ int gemm_tiled_splits(size_t n_rows, size_t n_tokens, size_t k) {
 // Token tiles of 16 and 32 keep split-K: their stages are short, and the
 // hand-off of a partial tile costs more than the reduce it replaces (M=32,
 // 14336 x 4096: 31.9 against 31.3 us).
+// The K-quant formats keep split-K too (their FFN at M=512: 462 against 442
+// us with stream-K in the down projection); their tiles take stream-K only
+// where they would leave CUs idle in a last round.
 static int sk_plain(int type, size_t n_rows, size_t n_tokens, size_t k) {
   const size_t bm = static_cast<size_t>(tile_bm(n_tokens));
   if (bm < 64) return 0;
+  if ((type == kGemmQ4F || type == kGemmQ8H) && gemm_tiled_splits(n_rows, n_tokens, k) > 1) return 0;
   return sk_grid(type, ((n_tokens + bm - 1) / bm) * ((n_rows + TBN - 1) / TBN), k / 32 / SB);
 }
 // Split-K factor of the GEMM over n_rows rows: 1 where it runs stream-K.
