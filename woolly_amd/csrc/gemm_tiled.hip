@@ -379,12 +379,13 @@ __device__ __forceinline__ half8 unpack_q8(uint32_t u0, uint32_t u1) {
   return out;
 }
 
-// v_and_or_b32: (u & mask) | magic in one instruction (mask in an SGPR, magic
-// in a VGPR: gfx950's VOP3 takes no two literal constants).
+// (u & mask) | magic in one instruction: gfx950's three-input v_bitop3_b32
+// (truth table 0xEA over (u, mask, magic)).  As a builtin, not inline asm,
+// so that the compiler's hazard tracking sees the instruction and adds no
+// wait states after it (it padded every inline-asm v_and_or_b32 that fed an
+// MFMA with an s_nop); left to itself it emits a separate and and or.
 __device__ __forceinline__ uint32_t and_or(uint32_t u, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(u), "s"(mask), "v"(magic));
-  return r;
+  return __builtin_amdgcn_bitop3_b32(u, mask, magic, 0xEA);
 }
 
 // Part p (0..3) of the B operand of one weight lane, i.e. its fp16 slots
