@@ -268,6 +268,8 @@ extern "C" {
     pub fn wh_quantized_matmul_x(r#type: c_int, weights: *const c_void, weight_nbytes: usize, n_rows: usize, k: usize,
                                  x: *const c_void, x_dtype: c_int, n_tokens: usize, y: *mut c_float,
                                  workspace: *mut c_void, workspace_bytes: usize, stream: wh_stream_t) -> c_int;
+    // tuning knob (no counterpart in the reference)
+    pub fn wh_set_stream_k_wait(ticks: u32) -> c_int;
 
     // elementwise (tensor_utils.rs:446-480, 512-532)
     pub fn wh_rms_norm(x: *const c_float, weight: *const c_float, eps: c_float, tokens: usize, hidden: usize,

@@ -215,6 +215,18 @@ WH_API int wh_quantized_matmul_x(int type, const void* weights, size_t weight_nb
                                  const void* x, int x_dtype, size_t n_tokens, float* y, void* workspace,
                                  size_t workspace_bytes, wh_stream_t stream);
 
+/* Tuning knob, no counterpart in the reference: the bound of the stream-K
+ * hand-off wait of wh_quantized_matmul(_x) and wh_ffn_swiglu, in ticks of
+ * the GPU's 100 MHz real-time clock (default 100000 = 1 ms; read at every
+ * launch and captured into a graph with it).  A workgroup that finishes a
+ * shared output tile waits that long for the other workgroups' parts of the
+ * tile (they run at the same time on a GPU the call has to itself), then
+ * computes the rest of the tile itself; a GPU shared with other work may
+ * want a shorter bound.  0 makes every such workgroup compute the rest
+ * without waiting (the results differ from the default's in rounding only).
+ * Process-wide; always WH_OK. */
+WH_API int wh_set_stream_k_wait(uint32_t ticks);
+
 /* --------------------------------------------------- elementwise / norms */
 /* rms_norm (crates/woolly-core/src/tensor_utils.rs:446-480):
  *   out[t, i] = (x[t, i] / sqrt(sum_i x[t, i]^2 / hidden + eps)) * weight[i] */

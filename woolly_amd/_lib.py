@@ -175,6 +175,7 @@ SIGNATURES = {
     "wh_quantized_matmul": (_int, [_int, _vp, _sz, _sz, _sz, _f32p, _sz, _f32p, _vp, _sz, _vp]),
     "wh_quantized_matmul_x_workspace_bytes": (_sz, [_int, _sz, _sz, _sz, _int]),
     "wh_quantized_matmul_x": (_int, [_int, _vp, _sz, _sz, _sz, _vp, _int, _sz, _f32p, _vp, _sz, _vp]),
+    "wh_set_stream_k_wait": (_int, [C.c_uint32]),
     "wh_rms_norm": (_int, [_f32p, _f32p, C.c_float, _sz, _sz, _f32p, _vp]),
     "wh_swiglu": (_int, [_f32p, _f32p, _sz, _f32p, _vp]),
     "wh_ffn_workspace_bytes": (_sz, [_sz, _sz, _sz]),

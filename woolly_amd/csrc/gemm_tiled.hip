@@ -34,6 +34,8 @@
 //     tile, whose activation fragments then stay in that XCD's L2.
 #include "wh_blocks.hpp"
 
+#include <atomic>
+
 // raw buffer load / store of 16 bytes (llvm.amdgcn.raw.buffer.{load,store}.v4f32)
 __device__ float __attribute__((ext_vector_type(4))) gt_buffer_load_x4(int __attribute__((ext_vector_type(4))) rsrc,
                                                                        int voffset, int soffset, int aux)
@@ -493,8 +495,9 @@ __device__ __forceinline__ void wait_stages(int n) {
 // in its slot of sk_part and raises its flag (sk_sub + 1; the packing kernel
 // cleared the flags); the workgroup holding the tile's first stage adds the
 // other owners' slots in owner order, then scales and stores, so the result
-// does not depend on timing.  Its wait is bounded: if a flag has not come,
-// it computes the rest of the tile itself.
+// does not depend on timing.  Its wait is bounded (sk_wait ticks of the
+// 100 MHz clock, wh_set_stream_k_wait): if a flag has not come, it computes
+// the rest of the tile itself.
 // FFNP (the FFN's gate and up in one pass, no split-K): a tile's 256 weight
 // rows are 128 rows of W (gate) and the same 128 rows of W2 (up); every wave
 // holds gate and up tiles of the same rows side by side (row groups 2m and
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const _Float16* __restrict__ frag,
     const float* __restrict__ rscale, const float* __restrict__ bsum, const float* __restrict__ dmin,
     float* __restrict__ y, int n_tokens, int n_rows, int nb, int blocks_per_split, int tiles_n, int n_tiles,
-    uint32_t* __restrict__ sk_flags, float* __restrict__ sk_part, int sk_upw, int sk_sub) {
+    uint32_t* __restrict__ sk_flags, float* __restrict__ sk_part, int sk_upw, int sk_sub, uint32_t sk_wait) {
   using C = TCfg<BM>;
   constexpr int IT = C::IT, NT = C::NT, FPB = C::FPB, NSTAGE = nstage<TYPE, BM>();
   constexpr int A_STAGE = C::A_STAGE;
@@ -810,7 +813,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     for (int w = v + 1; w <= w_last && ok; w++) {
       while (__hip_atomic_load(sk_flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
              static_cast<uint32_t>(sk_sub + 1)) {
-        if (__builtin_amdgcn_s_memrealtime() - t_start > 100000u) {  // 1 ms at 100 MHz
+        if (__builtin_amdgcn_s_memrealtime() - t_start > sk_wait) {  // ticks of the 100 MHz clock
           ok = 0;
           break;
         }
@@ -956,6 +959,10 @@ struct SkWs {
   int sub;  // which of the GEMMs after one packing this is (its flag value - 1)
 };
 
+// Bound of the stream-K hand-off wait, in ticks of the 100 MHz clock read by
+// s_memrealtime (default 1 ms); read at every launch (wh_set_stream_k_wait).
+std::atomic<uint32_t> g_sk_wait{100000u};
+
 template <int TYPE, int BM>
 int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
               const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
@@ -971,7 +978,7 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
       WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, true>);
       gemm_tiled_kernel<TYPE, BM, false, true><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
           w, nullptr, frag, rs, bs, dmin, part, static_cast<int>(n_tokens), static_cast<int>(n_rows), nb, nb, tiles_n,
-          n_tiles, sk.flags, sk.part, upw, sk.sub);
+          n_tiles, sk.flags, sk.part, upw, sk.sub, g_sk_wait.load(std::memory_order_relaxed));
       WH_LAUNCH_CHECK("tiled gemm kernel launch");
       return WH_OK;
     }
@@ -983,7 +990,7 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(splits));
   gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
                                                            static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
-                                                           bps, tiles_n, n_tiles, nullptr, nullptr, 0, 0);
+                                                           bps, tiles_n, n_tiles, nullptr, nullptr, 0, 0, 0u);
   WH_LAUNCH_CHECK("tiled gemm kernel launch");
   return WH_OK;
 }
@@ -1002,14 +1009,14 @@ int launch_ffn_bm(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t k,
     WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, true, true>);
     gemm_tiled_kernel<TYPE, BM, true, true><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
         gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
-        n_tiles, sk.flags, sk.part, upw, sk.sub);
+        n_tiles, sk.flags, sk.part, upw, sk.sub, g_sk_wait.load(std::memory_order_relaxed));
     WH_LAUNCH_CHECK("tiled ffn gate/up kernel launch");
     return WH_OK;
   }
   WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, true>);
   gemm_tiled_kernel<TYPE, BM, true><<<static_cast<unsigned>(n_tiles), TWAVES * 64, lds, s>>>(
       gate, up, frag, rs, bs, nullptr, h, static_cast<int>(n_tokens), static_cast<int>(n_ff), nb, nb, tiles_n,
-      n_tiles, nullptr, nullptr, 0, 0);
+      n_tiles, nullptr, nullptr, 0, 0, 0u);
   WH_LAUNCH_CHECK("tiled ffn gate/up kernel launch");
   return WH_OK;
 }
@@ -1362,3 +1369,8 @@ int launch_ffn_tiled(int type, const void* gate, const void* up, const void* dow
 }
 
 }  // namespace wh
+
+WH_API int wh_set_stream_k_wait(uint32_t ticks) {
+  g_sk_wait.store(ticks, std::memory_order_relaxed);
+  return WH_OK;
+}

@@ -93,6 +93,16 @@ def quantized_matmul_x(ggml_type: int, weights, weight_nbytes: int, n_rows: int,
                                                  workspace_bytes, _s(stream)))
 
 
+def set_stream_k_wait(ticks: int) -> None:
+    """Bound of the prefill GEMM's stream-K hand-off wait, in ticks of the GPU's
+    100 MHz clock (default 100000 = 1 ms); 0 makes a workgroup that finishes a
+    shared tile compute the other owners' parts itself (wh_set_stream_k_wait)."""
+    _lib.check(_lib.load().wh_set_stream_k_wait(int(ticks)))
+
+
+STREAM_K_WAIT_DEFAULT = 100000
+
+
 def rms_norm(x, weight, eps: float, tokens: int, hidden: int, out,
              stream: Stream | None = None) -> None:
     _lib.check(_lib.load().wh_rms_norm(_p(x), _p(weight), eps, tokens, hidden, _p(out),
