@@ -532,6 +532,33 @@ def traffic_from_profile() -> tuple[int | None, str]:
     return int(float(fields["traffic_bytes_per_launch"])), "current"
 
 
+GEMM_PMC_PROFILE = ROOT / "profiles" / "gemm_q4_0_14336x4096_m512_mfma_pmc.txt"
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def mfma_busy_from_profile() -> tuple[float | None, str]:
+    """MFMA busy fraction of the M=512 GEMM kernel (SQ_VALU_MFMA_BUSY_CYCLES over
+    all SIMD cycles) as recorded in the committed counter summary, and its
+    status: "current" when the summary's kernel_sources_sha256 matches the gemm
+    group's sources in this tree, else "stale" (the fraction is then null) or
+    "missing"."""
+    try:
+        text = GEMM_PMC_PROFILE.read_text()
+    except OSError:
+        return None, "missing"
+    digest, frac = None, None
+    for line in text.splitlines():
+        if line.startswith("kernel_sources_sha256:"):
+            digest = line.split(":", 1)[1].split()[0]
+        if line.startswith("MFMA utilisation =") and "%" in line:
+            frac = float(line.split("=")[-1].split("%")[0]) / 100.0
+    if frac is None:
+        return None, "missing"
+    if digest != kernel_sources_digest("gemm"):
+        return None, "stale"
+    return frac, "current"
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -783,6 +810,18 @@ def main() -> int:
     if cpu_scalar:
         log(f"[bench] cpu baseline (scalar, 1 thread): {cpu_scalar['value']} GB/s")
 
+    # MFMA utilisation of the M=512 GEMM: issued fp16 MFMA work (the activation
+    # hi and lo halves, 2 x 2 M N K) over the call's time against the dense
+    # peak, and the counters' busy fraction of the kernel from the committed
+    # summary of the same sources
+    prefill_mfma = None
+    if gemm.get("m512"):
+        busy, busy_status = mfma_busy_from_profile()
+        issued = 2.0 * 2.0 * 512 * N_ROWS * K / (gemm["m512"]["us"] * 1e-6) / 1e12
+        prefill_mfma = {"issued_tflops": round(issued, 1), "peak_tflops": FP16_MFMA_PEAK_TFLOPS,
+                        "issued_frac_of_peak": round(issued / FP16_MFMA_PEAK_TFLOPS, 4),
+                        "counters_busy_frac": round(busy, 4) if busy is not None else None,
+                        "counters_profile": f"{GEMM_PMC_PROFILE.relative_to(ROOT)} ({busy_status})"}
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -822,6 +861,7 @@ def main() -> int:
         "ffn_layer_us": ffn or None,
         "ffn_layer_spread": ffn_spread or None,
         "prefill_gemm_q4_0_14336x4096": gemm or None,
+        "prefill_mfma_m512": prefill_mfma,
         "prefill_kquant_14336x4096": gemm_kq or None,
         "gemv_other_configs": gemv_cfg or None,
         "host_slice_gemv_q4_0_14336x4096_us": host_mv,

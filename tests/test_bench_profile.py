@@ -1,6 +1,7 @@
 """bench.py's link to the committed rocprofv3 summaries: the HBM traffic of the
-headline GEMV is read from profiles/gemv_q4_0_14336x4096_pmc.txt only when that
-summary's kernel_sources_sha256 names the GEMV sources of this tree."""
+headline GEMV is read from profiles/gemv_q4_0_14336x4096_pmc.txt, and the M=512
+GEMM's MFMA busy fraction from profiles/gemm_q4_0_14336x4096_m512_mfma_pmc.txt,
+only when the summary's kernel_sources_sha256 names the sources of this tree."""
 import bench
 
 
@@ -25,6 +26,33 @@ def test_stale_summary_gives_none(tmp_path, monkeypatch):
 def test_missing_summary(tmp_path, monkeypatch):
     monkeypatch.setattr(bench, "PMC_PROFILE", tmp_path / "absent.txt")
     assert bench.traffic_from_profile() == (None, "missing")
+
+
+def _write_mfma(tmp_path, digest, line="MFMA utilisation = A / B = 35.6% (all 256 CUs hold work)."):
+    p = tmp_path / "mfma.txt"
+    p.write_text("# summary\n"
+                 f"kernel_sources_sha256: {digest}   (python bench.py --sources-digest gemm)\n"
+                 f"{line}\n")
+    return p
+
+
+def test_mfma_busy_from_current_summary(tmp_path, monkeypatch):
+    monkeypatch.setattr(bench, "GEMM_PMC_PROFILE", _write_mfma(tmp_path, bench.kernel_sources_digest("gemm")))
+    frac, status = bench.mfma_busy_from_profile()
+    assert status == "current" and abs(frac - 0.356) < 1e-12
+
+
+def test_mfma_busy_stale_or_missing(tmp_path, monkeypatch):
+    monkeypatch.setattr(bench, "GEMM_PMC_PROFILE", _write_mfma(tmp_path, "0123456789abcdef"))
+    assert bench.mfma_busy_from_profile() == (None, "stale")
+    monkeypatch.setattr(bench, "GEMM_PMC_PROFILE", _write_mfma(tmp_path, bench.kernel_sources_digest("gemm"),
+                                                                line="no figure here"))
+    assert bench.mfma_busy_from_profile() == (None, "missing")
+
+
+def test_committed_gemm_counters_give_a_busy_fraction():
+    frac, status = bench.mfma_busy_from_profile()
+    assert status == "current" and 0.2 < frac < 1.0
 
 
 def test_digest_covers_every_gemv_source():
