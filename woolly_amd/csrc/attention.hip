@@ -486,7 +486,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   __syncthreads();
 
   // per head: max and sum of exp over the chunk (one wave per head at a time)
-  const int wave = t >> 6, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;  // wave scalar
   float* ml = reinterpret_cast<float*>(sc + G * chunk);  // [G][2]
   for (int g = wave; g < G; g += kAttnThreads / 64) {
     float m = -INFINITY;

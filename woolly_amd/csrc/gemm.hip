@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(const uint8_t* __rest
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int wm = (wave >> 1) * 64;
   const int wn = (wave & 1) * 64;
   const int t0 = blockIdx.y * BM;

@@ -527,7 +527,9 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (an SGPR): the copies' LDS addresses and every other
+  // per-wave offset are then scalar arithmetic, not VALU + v_readfirstlane
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = (wave / C::WGN) * C::WTM;   // token offset of the wave tile
   const int wn = (wave % C::WGN) * C::WTN;   // row offset of the wave tile
 

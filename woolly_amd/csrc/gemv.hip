@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_stream_kernel(const GemvArgs
   uint32_t* slabs = lds + K + K / 16;                       // kWaves * NM slabs of SLAB dwords
   float* red = reinterpret_cast<float*>(slabs + kWaves * NM * SLAB);  // NM * kWaves partials
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
   const int lane = threadIdx.x & 63;
   const int s = wave % ks;
   const int g = wave / ks;
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_ring_kernel(const GemvArgs a
   uint8_t* ring = reinterpret_cast<uint8_t*>(lds + K + K / 16);      // kWaves * NM * RD slots
   float* red = reinterpret_cast<float*>(ring + kWaves * NM * RD * SLOT);
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
   const int lane = threadIdx.x & 63;
   const int s = wave % ks;
   const int g = wave / ks;
