@@ -601,9 +601,9 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     for (int f = 0; f < A_DMA; f++) {
       const int fi = (wave * A_DMA + f) % A_FR;
       const int j = fi / FPB;
-      const uint32_t off =
-          static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * FPB + fi % FPB) * FRAG) + frag_lane_off;
-      copy16_to_lds(frag, off, slot + fi * FRAG);
+      // the wave-uniform part of the source in the scalar base, the lane's in the offset
+      const size_t off = ((static_cast<size_t>(T) * nb + kb + j) * FPB + fi % FPB) * FRAG;
+      copy16_to_lds(reinterpret_cast<const uint8_t*>(frag) + off, frag_lane_off, slot + fi * FRAG);
     }
     const uint32_t bslot = slot + A_STAGE;
     const uint32_t kboff = static_cast<uint32_t>(kb) * TS;
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       const uint8_t* wb = W;
       if constexpr (FFNP)  // this wave's copy c lies in the up half (a wave-uniform choice: the base is an SGPR pair)
         if (TWAVES * 64 * c + 64 * __builtin_amdgcn_readfirstlane(wave) >= HALF * DWB) wb = W2;
-      copy4_to_lds(wb, b_off[c] + kboff, bslot + 4 * (TWAVES * 64 * c + 64 * wave));
+      copy4_to_lds(wb + kboff, b_off[c], bslot + 4 * (TWAVES * 64 * c + 64 * wave));
     }
     if constexpr (has_min<TYPE>()) {
       // block sums [SB][BM] of this token tile: S_CH chunks of 16 B, S_PW per
