@@ -235,6 +235,46 @@ def test_matmul_bf16_config2_full_size(gpu, orc, m):
     assert r <= REL_L2 and a <= max_abs_bar(ref)
 
 
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_1])
+def test_matmul_bf16_wide_range(gpu, orc, t):
+    """bf16 rows spanning 2^-60 .. 2^4 (every exponent bf16 holds there, zeros
+    and a row of only tiny values included): the tiled kernel multiplies the
+    hi limbs of bf16 activations only, which is exact but for elements below
+    2^-17 of the scaled row (fp16 subnormals round them), so these rows check
+    that the left-out lo products stay within the bars against f64 and within
+    1e-6 (relative to the output RMS) of the f32 path on the widened X."""
+    m, n, k = 64, 256, 2048
+    print(f"[case] matmul bf16 wide range type={t}", flush=True)
+    rng = np.random.default_rng(77 + t)
+    w = synth.quantized_weight(t, n, k, seed=5 + t)
+    mag = np.exp2(rng.uniform(-60.0, 4.0, size=(m, k)))
+    xf = (mag * rng.choice([-1.0, 1.0], size=(m, k))).astype(np.float32)
+    xf[:, ::97] = 0.0
+    xf[1] *= np.float32(2.0 ** -30)                              # a row of only tiny values
+    xb16 = (xf.view(np.uint32) >> 16).astype(np.uint16)
+    xw = (xb16.astype(np.uint32) << 16).view(np.float32)
+    wb, wp = up(w)
+    xbb, xbp = up(xb16)
+    xwb, xwp = up(xw)
+    y_bf, y_f = DeviceBuffer(4 * m * n), DeviceBuffer(4 * m * n)
+    wsz = ops.matmul_x_workspace_bytes(t, n, k, m, ops.TYPE_BF16)
+    ws = DeviceBuffer(max(wsz, 256))
+    ops.quantized_matmul_x(t, wp, w.nbytes, n, k, xbp, ops.TYPE_BF16, m, y_bf.ptr, ws, wsz)
+    wsz2 = ops.matmul_workspace_bytes(t, n, k, m)
+    ws2 = DeviceBuffer(max(wsz2, 256))
+    ops.quantized_matmul(t, wp, w.nbytes, n, k, xwp, m, y_f.ptr, ws2, wsz2)
+    got = down(y_bf, np.float32, m * n).reshape(m, n)
+    yf = down(y_f, np.float32, m * n).reshape(m, n)
+    assert np.all(np.isfinite(got))
+    ref = orc.matmul_rows_f64(t, w, n, k, xw, m, np.arange(m))
+    for r in range(m):
+        rms = float(np.sqrt(np.mean(ref[r] ** 2)))
+        assert rms > 0.0
+        assert np.max(np.abs(got[r].astype(np.float64) - yf[r])) <= 1e-6 * rms
+        assert rel_l2(got[r], ref[r]) <= REL_L2
+    report(f"matmul bf16 wide range t={t}", rel_l2(got, ref), max_abs(got, ref), ref)
+
+
 def test_matmul_x_rejects_other_activation_types(gpu):
     w = synth.quantized_weight(Q4_0, 64, 256, seed=1)
     wb, wp = up(w)

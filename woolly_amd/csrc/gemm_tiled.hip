@@ -503,7 +503,12 @@ __device__ __forceinline__ void wait_stages(int n) {
 // holds gate and up tiles of the same rows side by side (row groups 2m and
 // 2m + 1), and the epilogue writes y = silu(gate x) * (up x) for n_rows
 // output columns (tensor_utils.rs:512-532), so neither product reaches HBM.
-template <int TYPE, int BM, bool FFNP = false, bool SK = false>
+// LO = false (activations given as bfloat16): a bf16 value carries 8
+// significant bits, so its scaled copy (the row's largest in [2^13, 2^14)) is
+// an fp16 exactly and its lo limb zero, unless it lies below 2^-17, where fp16
+// subnormals round it; the lo products, below 2^-39 of the row's largest term
+// each, are left out and the kernel issues half the MFMAs.
+template <int TYPE, int BM, bool FFNP = false, bool SK = false, bool LO = true>
 __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const _Float16* __restrict__ frag,
     const float* __restrict__ rscale, const float* __restrict__ bsum, const float* __restrict__ dmin,
@@ -698,7 +703,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       for (int i = 0; i < IT; i++) {
         const int grp = (wm >> 4) + i;
         ah[j][i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp) * FRAG + 16 * lane);
-        al[j][i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp + 1) * FRAG + 16 * lane);
+        if constexpr (LO) al[j][i] = *reinterpret_cast<const half8*>(slot + (j * FPB + 2 * grp + 1) * FRAG + 16 * lane);
       }
     };
 #pragma unroll
@@ -769,7 +774,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         for (int h = 0; h < 2; h++)
 #pragma unroll
           for (int i = 0; i < IT; i++) {
-            cc[cur][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j][i], bw[h], cc[cur][h][i], 0, 0, 0);
+            if constexpr (LO) cc[cur][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j][i], bw[h], cc[cur][h][i], 0, 0, 0);
             if (more) {
               // 8 parts (2 groups x 4) over 2 IT slots
 #pragma unroll
@@ -965,8 +970,8 @@ struct SkWs {
 // s_memrealtime (default 1 ms); read at every launch (wh_set_stream_k_wait).
 std::atomic<uint32_t> g_sk_wait{100000u};
 
-template <int TYPE, int BM>
-int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
+template <int TYPE, int BM, bool LO>
+int launch_bm_lo(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
               const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
               hipStream_t s) {
   const int nb = static_cast<int>(k / 32);
@@ -977,8 +982,8 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   {
     if (splits == 1 && sk.g > 0 && sk_grid(TYPE, n_tiles, nb / SB) == sk.g) {
       const int upw = (n_tiles * (nb / SB) + sk.g - 1) / sk.g;
-      WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, true>);
-      gemm_tiled_kernel<TYPE, BM, false, true><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
+      WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, true, LO>);
+      gemm_tiled_kernel<TYPE, BM, false, true, LO><<<static_cast<unsigned>(sk.g), TWAVES * 64, lds, s>>>(
           w, nullptr, frag, rs, bs, dmin, part, static_cast<int>(n_tokens), static_cast<int>(n_rows), nb, nb, tiles_n,
           n_tiles, sk.flags, sk.part, upw, sk.sub, g_sk_wait.load(std::memory_order_relaxed));
       WH_LAUNCH_CHECK("tiled gemm kernel launch");
@@ -988,13 +993,26 @@ int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const 
   int bps = (nb + splits - 1) / splits;
   constexpr int ALIGN = TYPE == wh::kGemmQ4F ? 8 : SB;   // kGemmQ4F: whole super-blocks per split
   bps = (bps + ALIGN - 1) / ALIGN * ALIGN;
-  WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM>);
+  WH_ENSURE_LDS(lds, &gemm_tiled_kernel<TYPE, BM, false, false, LO>);
   dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(splits));
-  gemm_tiled_kernel<TYPE, BM><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
+  gemm_tiled_kernel<TYPE, BM, false, false, LO><<<grid, TWAVES * 64, lds, s>>>(w, nullptr, frag, rs, bs, dmin, part,
                                                            static_cast<int>(n_tokens), static_cast<int>(n_rows), nb,
                                                            bps, tiles_n, n_tiles, nullptr, nullptr, 0, 0, 0u);
   WH_LAUNCH_CHECK("tiled gemm kernel launch");
   return WH_OK;
+}
+
+// lo = false: the activations were bfloat16, so the packed lo limbs are
+// (all but) zero and the products of the hi limbs alone are issued (32- to
+// 128-token tiles of the 32-element block formats, the bf16 path's shapes).
+template <int TYPE, int BM>
+int launch_bm(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
+              const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
+              hipStream_t s, bool lo) {
+  if constexpr ((TYPE == WH_TYPE_Q4_0 || TYPE == WH_TYPE_Q4_1 || TYPE == WH_TYPE_Q8_0) && BM >= 32) {
+    if (!lo) return launch_bm_lo<TYPE, BM, false>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
+  }
+  return launch_bm_lo<TYPE, BM, true>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
 }
 
 // The FFN's gate and up (n_ff rows each) in one pass: h = silu(gate x) * (up x).
@@ -1037,12 +1055,12 @@ int launch_ffn_typed(const uint8_t* gate, const uint8_t* up, size_t n_ff, size_t
 template <int TYPE>
 int launch_typed(const uint8_t* w, size_t n_rows, size_t k, size_t n_tokens, const _Float16* frag,
                  const float* rs, const float* bs, const float* dmin, float* part, int splits, const SkWs& sk,
-                 hipStream_t s) {
+                 hipStream_t s, bool lo) {
   switch (tile_bm(n_tokens)) {
-    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
-    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
-    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
-    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s);
+    case 16: return launch_bm<TYPE, 16>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s, lo);
+    case 32: return launch_bm<TYPE, 32>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s, lo);
+    case 64: return launch_bm<TYPE, 64>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s, lo);
+    default: return launch_bm<TYPE, 128>(w, n_rows, k, n_tokens, frag, rs, bs, dmin, part, splits, sk, s, lo);
   }
 }
 
@@ -1210,17 +1228,17 @@ static int tiled_pack(int type, const TiledWs& t, const float* x, const float* x
 // sub: which of the GEMMs that read one packing this is (0, 1), so that their
 // stream-K flags differ.
 static int tiled_run(int type, const void* w, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t, float* y,
-                     hipStream_t s, const float* dmin = nullptr, int sub = 0) {
+                     hipStream_t s, const float* dmin = nullptr, int sub = 0, bool lo = true) {
   const uint8_t* wp = static_cast<const uint8_t*>(w);
   float* part = t.splits > 1 ? t.part : y;
   const SkWs sk{t.sk_flags, t.sk_part, t.sk_n, sub};
   int st;
   switch (type) {
-    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
-    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
-    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
-    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
-    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s); break;
+    case WH_TYPE_Q4_0: st = launch_typed<WH_TYPE_Q4_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s, lo); break;
+    case WH_TYPE_Q4_1: st = launch_typed<WH_TYPE_Q4_1>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s, lo); break;
+    case WH_TYPE_Q8_0: st = launch_typed<WH_TYPE_Q8_0>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s, lo); break;
+    case kGemmQ4F: st = launch_typed<kGemmQ4F>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s, lo); break;
+    case kGemmQ8H: st = launch_typed<kGemmQ8H>(wp, n_rows, k, n_tokens, t.frag, t.rs, t.bs, dmin, part, t.splits, sk, s, lo); break;
     default: return set_error(WH_ERR_UNSUPPORTED_TYPE, "gemm: unsupported type %d", type);
   }
   if (st != WH_OK) return st;
@@ -1249,7 +1267,7 @@ int launch_gemm_tiled_bf16(int type, const void* w, size_t n_rows, size_t k, con
   int st = tiled_pack<kPackPlain, true>(type, t, reinterpret_cast<const float*>(x), nullptr, nullptr, 0.f, n_tokens,
                                         k, k, s);
   if (st) return st;
-  return tiled_run(type, w, n_rows, k, n_tokens, t, y, s);
+  return tiled_run(type, w, n_rows, k, n_tokens, t, y, s, nullptr, 0, /*lo=*/false);
 }
 
 // ------------------------------------------------------------- K-quants
