@@ -259,7 +259,8 @@ def test_kquant_prepared_prefill(gpu, orc, t):
     plain = kq_matmul(t, w, x, m, n, k)
     wh = ops.Weight(t, n, k, w)
     size = wh.prepare_prefill()
-    assert size == (n * (k // 32 * 20 + k // 256 * 4) if t == Q4_K else n * k // 16 * 20)
+    # Q4_K: 20-byte blocks, then the fp16 dmin table with rows of k / 256 rounded up to 8
+    assert size == (n * (k // 32 * 20 + (k // 256 + 7) // 8 * 8 * 2) if t == Q4_K else n * k // 16 * 20)
     assert wh.prepare_prefill() == size
     xb, xp = up(x)
     yb = DeviceBuffer(4 * m * n)

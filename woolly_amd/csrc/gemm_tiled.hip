@@ -100,9 +100,10 @@ constexpr bool q8_like() { return TYPE == WH_TYPE_Q8_0 || TYPE == wh::kGemmQ8H; 
 template <int TYPE>
 constexpr bool f32_scale() { return TYPE == wh::kGemmQ4F || TYPE == wh::kGemmQ8H; }
 // block sums of the activations are written by the packing ([T][b][bm]; for
-// kGemmQ4F per 256-element super-block, [T][sb][bm], for its dmin term)
+// kGemmQ4F two fp16 limbs per 256-element super-block for its dmin term)
 inline bool needs_bsum(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
-inline size_t bsum_groups(int type, size_t k) { return type == wh::kGemmQ4F ? k / 256 : k / 32; }
+// 4-byte words of block sums per token
+inline size_t bsum_groups(int type, size_t k) { return type == wh::kGemmQ4F ? wh::q4f_dmin_stride(k) : k / 32; }
 // dwords per weight row per stage (SB whole blocks)
 template <int TYPE>
 constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
@@ -144,8 +145,11 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 // ---------------------------------------------------------------- packing
 // One workgroup per token row t of the padded tile grid (token tiles of bm
 // rows).  Rows t >= n_tokens are written as zeros.  rscale[t] = 2^e with
-// max|x_t| * 2^-e in [2^13, 2^14); bsum (Q4_1 only) = per-block sums of
-// hi + lo, laid out [T][b][bm].
+// max|x_t| * 2^-e in [2^13, 2^14); bsum = per-block sums of hi + lo, laid
+// out [T][b][bm] (Q4_1), or kGemmQ4F's per-super-block sums S as the A
+// operand of its dmin products: fp16 limbs hi = fp16(S 2^-10),
+// lo = fp16(S 2^-10 - hi) (|S| < 2^22, so no overflow), laid out
+// [t][limb][q4f_dmin_stride(k)], zero past the row's super-blocks.
 // Thread p of a chunk owns the (block, k-group) pairs p, p + NTH, ... (NTH =
 // blockDim.x, 256 .. 1024 by the row length): the 8 elements of a pair are
 // two float4 loads (slot_elem order), all issued before the first use; a row
@@ -323,7 +327,16 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
           part += __shfl_xor(part, 4, 64);
           part += __shfl_xor(part, 8, 64);
           part += __shfl_xor(part, 16, 64);
-          if ((p & 31) == 0) bsum[(static_cast<size_t>(T) * (nb / 8) + (b >> 3)) * bm + (t % bm)] = part;
+          if ((p & 31) == 0) {
+            const int nsb = nb / 8, nsbp = (nsb + 7) & ~7, sb = b >> 3;
+            _Float16* sr = reinterpret_cast<_Float16*>(bsum) + static_cast<size_t>(t) * 2 * nsbp;
+            const float sv = part * 0x1p-10f;  // exact
+            const _Float16 h = static_cast<_Float16>(sv);
+            sr[sb] = h;
+            sr[nsbp + sb] = static_cast<_Float16>(sv - static_cast<float>(h));
+            if (sb == nsb - 1)  // the row's last super-block clears the padding
+              for (int z = nsb; z < nsbp; z++) sr[z] = sr[nsbp + z] = static_cast<_Float16>(0.f);
+          }
         } else if (g == 0) {
           bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
         }
@@ -868,24 +881,64 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   }
 
   if constexpr (TYPE == wh::kGemmQ4F) {
-    // Q4_K's dmin: acc += dmin[sb][row] * S[sb][token] over this split's
+    // Q4_K's dmin: acc += dmin[row][sb] * S[token][sb] over this split's
     // super-blocks (split bounds are multiples of 8 blocks), S the packing's
     // super-block sums in the same scaled domain as acc.  Under stream-K the
     // workgroup that finishes a tile adds the term of every super-block (the
-    // other owners' parts carry none).
-    const int nsb = nb / 8;
+    // other owners' parts carry none).  As matrix-core products over windows
+    // of 32 super-blocks: lane group g holds super-blocks 8g .. 8g + 7 of the
+    // window in both operands (B: the fp16 dmin table, those outside
+    // [sb_lo, sb_hi) masked to zero; A: S as hi + lo fp16 limbs of S 2^-10),
+    // and one fma per output adds 2^10 times the window's sum.
+    static_assert(!FFNP, "the gate / up pass has no dmin term");
+    const int nsb = nb / 8, nsbp = (nsb + 7) & ~7;
     const int sb_lo = SK ? 0 : st_a * SB / 8, sb_hi = SK ? nsb : st_b * SB / 8;
-    for (int sb = sb_lo; sb < sb_hi; sb++) {
-      float dm[NT];
+    const uint16_t* dm16 = reinterpret_cast<const uint16_t*>(dmin);
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(bsum);
+    // the lane index opaque here, so that the loads' offsets are formed here
+    // and not held in registers through the stage loop; 32-bit offsets (both
+    // arrays hold fewer than 2^28 halves: the launcher keeps the weight and
+    // fragment bytes below 2^32)
+    int lnv = ln;
+    asm volatile("" : "+v"(lnv));
+    for (int w0 = sb_lo & ~31; w0 < sb_hi; w0 += 32) {
+      const int s0 = w0 + 8 * g;                  // this lane's first super-block
+      const bool in = s0 < nsbp;                  // inside the table's rows
+      uint32_t mk[4];
 #pragma unroll
-      for (int n = 0; n < NT; n++) dm[n] = dmin[static_cast<size_t>(sb) * n_rows + min(r0 + wn + 16 * n + ln, n_rows - 1)];
+      for (int d = 0; d < 4; d++) {
+        const int a = s0 + 2 * d;
+        mk[d] = (a >= sb_lo && a < sb_hi ? 0x0000FFFFu : 0u) | (a + 1 >= sb_lo && a + 1 < sb_hi ? 0xFFFF0000u : 0u);
+      }
+      u32x4 bd[NT];
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        const uint32_t off = static_cast<uint32_t>(min(r0 + wn + 16 * n + lnv, n_rows - 1) * nsbp + s0);
+        bd[n] = in ? *reinterpret_cast<const u32x4*>(dm16 + off) : u32x4{0u, 0u, 0u, 0u};
+      }
+      u32x4 sh[IT], sl[IT];
 #pragma unroll
       for (int i = 0; i < IT; i++) {
-        const float4v sv = *reinterpret_cast<const float4v*>(bsum + (static_cast<size_t>(T) * nsb + sb) * BM + wm + 16 * i + 4 * g);
+        const uint32_t off = static_cast<uint32_t>((t0 + wm + 16 * i + lnv) * 2 * nsbp + s0);
+        sh[i] = in ? *reinterpret_cast<const u32x4*>(s16 + off) : u32x4{0u, 0u, 0u, 0u};
+        sl[i] = in ? *reinterpret_cast<const u32x4*>(s16 + off + nsbp) : u32x4{0u, 0u, 0u, 0u};
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
-        for (int n = 0; n < NT; n++)
+      for (int n = 0; n < NT; n++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) acc[i][n][r] = __builtin_fmaf(dm[n], sv[r], acc[i][n][r]);
+        for (int d = 0; d < 4; d++) bd[n][d] &= mk[d];
+#pragma unroll
+      for (int i = 0; i < IT; i++) {
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+          float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, sh[i]), __builtin_bit_cast(half8, bd[n]),
+                                                             float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, sl[i]), __builtin_bit_cast(half8, bd[n]), t, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][n][r] = __builtin_fmaf(1024.f, t[r], acc[i][n][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one token group's products at a time
       }
     }
   }
@@ -1285,6 +1338,7 @@ bool gemm_kquant_ok(int type, const void* w, const float* x, size_t n_rows, size
 // over packed activations t; Q4_K's dmin table follows the blocks.
 static int kquant_run(int type, const char* rp, size_t n_rows, size_t k, size_t n_tokens, const TiledWs& t,
                       float* y, hipStream_t s, int sub = 0) {
+  // (the fp16 table, passed through the kernels' dmin pointer)
   const float* dmin_t =
       type == WH_TYPE_Q4_K ? reinterpret_cast<const float*>(rp + n_rows * (k / 32) * 20) : nullptr;
   return tiled_run(kquant_gemm_type(type), rp, n_rows, kquant_gemm_k(type, k), n_tokens, t, y, s, dmin_t, sub);

@@ -81,16 +81,18 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(const uint8_t* __restrict_
 // order within a row) into:
 //   Q4_K -> {f32 d * scale_j; u8 qs[16]} per 32 elements j (quants in Q4_0's
 //     nibble order: byte i holds element i low, element i + 16 high), and the
-//     super-block's dmin as f32 in a [k / 256][n_rows] table after the blocks;
-//     the value (d * scale_j) * q + dmin is then the GEMM's d * q plus dmin
-//     times the super-block's activation sum;
+//     super-block's dmin (its fp16 bits) in an [n_rows][q4f_dmin_stride(k)]
+//     table after the blocks, zero past the row's k / 256 super-blocks; the
+//     value (d * scale_j) * q + dmin is then the GEMM's d * q plus dmin times
+//     the super-block's activation sum;
 //   Q6_K -> {f32 (d * scale_j) / 64; i8 q[16] = q - 32} per 16 elements j
 //     (the GEMM pads each to a 32-element block, upper half zero).
 // The scale products are exact in f32 (11-bit times 6- or 8-bit integers).
 // Every thread writes one output block; 16-byte aligned input.
 __global__ __launch_bounds__(256) void kq_repack_q4k_kernel(const uint8_t* __restrict__ w, size_t n_groups,
                                                             size_t groups_per_row, size_t n_rows,
-                                                            uint32_t* __restrict__ out, float* __restrict__ dmin_t) {
+                                                            uint32_t* __restrict__ out, uint16_t* __restrict__ dmin_t,
+                                                            size_t dmin_stride) {
   for (size_t gi = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; gi < n_groups;
        gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const uint8_t* b = w + (gi >> 3) * 144;
@@ -120,8 +122,11 @@ __global__ __launch_bounds__(256) void kq_repack_q4k_kernel(const uint8_t* __res
 #pragma unroll
     for (int c = 0; c < 5; c++) dst[c] = o[c];
     if (j == 0) {
-      const size_t row = gi / groups_per_row, sb = (gi % groups_per_row) >> 3;
-      dmin_t[sb * n_rows + row] = whd::f16_bits_to_f32(b16(b + 14));
+      const size_t row = gi / groups_per_row, sb = (gi % groups_per_row) >> 3, nsb = groups_per_row >> 3;
+      uint16_t* tr = dmin_t + row * dmin_stride;
+      tr[sb] = b16(b + 14);
+      if (sb + 1 == nsb)  // the row's last super-block clears the padding
+        for (size_t z = nsb; z < dmin_stride; z++) tr[z] = 0;
     }
   }
 }
@@ -200,8 +205,8 @@ int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void*
   uint32_t* o = static_cast<uint32_t*>(out);
   if (type == WH_TYPE_Q4_K) {
     const size_t n = n_rows * (k / 32);
-    float* dmin_t = reinterpret_cast<float*>(static_cast<char*>(out) + n * 20);
-    kq_repack_q4k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, k / 32, n_rows, o, dmin_t);
+    uint16_t* dmin_t = reinterpret_cast<uint16_t*>(static_cast<char*>(out) + n * 20);
+    kq_repack_q4k_kernel<<<kq_grid(n, 256), 256, 0, s>>>(p, n, k / 32, n_rows, o, dmin_t, q4f_dmin_stride(k));
   } else {
     const size_t n = n_rows * (k / 256);
     kq_repack_q6k_kernel<<<kq_grid(n, kQ6Blocks), 256, 0, s>>>(p, n, o);

@@ -71,16 +71,20 @@ inline bool is_kquant(int type) { return type == WH_TYPE_Q4_K || type == WH_TYPE
 // Block formats of the tiled prefill GEMM that K-quant matrices are repacked
 // into (internal ids, never seen at the C ABI):
 //   kGemmQ4F {f32 d; u8 qs[16]}: 32 elements d * q, Q4_0 nibble order, followed
-//            by the super-blocks' dmin as f32 [k / 256][n_rows] (the GEMM's
-//            epilogue adds dmin * sum(x) per super-block)
+//            by the super-blocks' dmin as fp16 [n_rows][q4f_dmin_stride(k)]
+//            (zeros past k / 256; the GEMM's epilogue adds dmin * sum(x) per
+//            super-block, as matrix-core products over 32 super-blocks)
 //   kGemmQ8H {f32 d; i8 q[16]}: 16 elements d * q, which the GEMM reads as a
 //            32-element block whose upper half is zero (activations packed to match)
 constexpr int kGemmQ4F = 256, kGemmQ8H = 257;
 inline int kquant_gemm_type(int type) { return type == WH_TYPE_Q4_K ? kGemmQ4F : kGemmQ8H; }
 // The GEMM's reduction length for a K-quant row of k elements.
 inline size_t kquant_gemm_k(int type, size_t k) { return type == WH_TYPE_Q4_K ? k : 2 * k; }
+// Super-blocks per row of kGemmQ4F's dmin table: k / 256 rounded up to 8
+// (16-byte rows).
+inline size_t q4f_dmin_stride(size_t k) { return (k / 256 + 7) / 8 * 8; }
 inline size_t kquant_repacked_bytes(int type, size_t n_rows, size_t k) {
-  return n_rows * (type == WH_TYPE_Q4_K ? k / 32 * 20 + k / 256 * 4 : k / 16 * 20);
+  return n_rows * (type == WH_TYPE_Q4_K ? k / 32 * 20 + q4f_dmin_stride(k) * 2 : k / 16 * 20);
 }
 // Rewrites a Q4_K / Q6_K matrix (n_rows x k, 16-byte aligned) into the format above (kquant.hip).
 int launch_repack_kquant(int type, const void* w, size_t n_rows, size_t k, void* out, hipStream_t stream);
