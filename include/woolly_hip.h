@@ -290,8 +290,9 @@ WH_API int wh_weight_info(const wh_weight* weight, int* type, size_t* n_rows, si
  * (DequantizationCache::get_or_dequantize,
  * crates/woolly-core/src/model/dequantization_cache.rs:121-165,
  * LazyModelWeights::get_tensor_cached, model/lazy_loader.rs:599-659).  The
- * copy takes 656 bytes per 1024 elements for Q4_K (576 in the file) and 1280
- * for Q6_K (840) of device memory.  A no-op for the other block types, whose blocks the
+ * copy takes 648 bytes per 1024 elements for Q4_K at rows of a multiple of
+ * 2048 elements (576 in the file; each row's dmin table is padded to 8
+ * super-blocks) and 1280 for Q6_K (840) of device memory.  A no-op for the other block types, whose blocks the
  * GEMM reads directly.  Idempotent; *prepared_bytes (may be null) receives
  * the copy's size. */
 WH_API int wh_weight_prepare_prefill(wh_weight* weight, wh_stream_t stream, size_t* prepared_bytes);
