@@ -207,7 +207,10 @@ WH_API int wh_quantized_matmul(int type, const void* weights, size_t weight_nbyt
  * 8-byte aligned), the activation types of the prefill benchmark configuration
  * ("f32/bf16", a wh_qgemm(.., X, x_dtype, ..) signature).  bf16 values are
  * widened exactly to f32, so the result equals wh_quantized_matmul on the
- * widened X.  The workspace (wh_quantized_matmul_x_workspace_bytes) is needed
+ * widened X (bit for bit unless a row holds elements below 2^-31 of its
+ * largest: for bf16 the tiled kernel issues the hi-limb products only, and
+ * such elements' lo products, each below 2^-39 of the row's largest term,
+ * are left out).  The workspace (wh_quantized_matmul_x_workspace_bytes) is needed
  * for bf16 at any token count; WH_ERR_UNSUPPORTED_TYPE for another x_dtype. */
 WH_API size_t wh_quantized_matmul_x_workspace_bytes(int type, size_t n_rows, size_t k, size_t n_tokens,
                                                     int x_dtype);
