@@ -90,7 +90,9 @@ template <>
 struct TFmt<wh::kGemmQ8H> {
   static constexpr int TS = 20, QOFF = 4;
 };
-// block value d * q + m: the kernel adds m times the activations' block sums
+// block value d q + m (Q4_1): the m of each block are collected, as the
+// stages stream past, into the B operand of products against the
+// activations' block sums, over windows of 32 blocks
 template <int TYPE>
 constexpr bool has_min() { return TYPE == WH_TYPE_Q4_1; }
 // int8 quants in natural element order (else 4-bit quants in nibble order)
@@ -99,11 +101,14 @@ constexpr bool q8_like() { return TYPE == WH_TYPE_Q8_0 || TYPE == wh::kGemmQ8H; 
 // f32 block scale (else f16)
 template <int TYPE>
 constexpr bool f32_scale() { return TYPE == wh::kGemmQ4F || TYPE == wh::kGemmQ8H; }
-// block sums of the activations are written by the packing ([T][b][bm]; for
-// kGemmQ4F two fp16 limbs per 256-element super-block for its dmin term)
+// the packing writes the activations' sums over each unit of the minimum
+// term (Q4_1: 32-element block; kGemmQ4F: 256-element super-block) as two
+// fp16 limbs, rows of units rounded up to 8
 inline bool needs_bsum(int type) { return type == WH_TYPE_Q4_1 || type == wh::kGemmQ4F; }
-// 4-byte words of block sums per token
-inline size_t bsum_groups(int type, size_t k) { return type == wh::kGemmQ4F ? wh::q4f_dmin_stride(k) : k / 32; }
+// units per token row in the sums' layout (4 bytes each: two fp16 limbs)
+inline size_t bsum_groups(int type, size_t k) {
+  return type == wh::kGemmQ4F ? wh::q4f_dmin_stride(k) : (k / 32 + 7) / 8 * 8;
+}
 // dwords per weight row per stage (SB whole blocks)
 template <int TYPE>
 constexpr int dwb() { return SB * TFmt<TYPE>::TS / 4; }
@@ -115,14 +120,12 @@ constexpr int b_dma_per_wave() { return (TBN * dwb<TYPE>() + TWAVES * 64 - 1) / 
 template <int TYPE>
 constexpr int b_stage_bytes() { return b_dma_per_wave<TYPE>() * TWAVES * 64 * 4; }
 template <int TYPE, int BM>
-constexpr int s_stage_bytes() { return has_min<TYPE>() ? SB * BM * 4 : 0; }
-template <int TYPE, int BM>
-constexpr int stage_bytes() { return TCfg<BM>::A_STAGE + b_stage_bytes<TYPE>() + s_stage_bytes<TYPE, BM>(); }
+constexpr int stage_bytes() { return TCfg<BM>::A_STAGE + b_stage_bytes<TYPE>(); }
 // Copy instructions per wave per stage (the vmcnt of one stage): activation
-// fragments, raw weight dwords, Q4_1 block sums.
+// fragments, raw weight dwords.
 template <int TYPE, int BM>
 constexpr int per_stage() {
-  return (SB * TCfg<BM>::FPB + TWAVES - 1) / TWAVES + b_dma_per_wave<TYPE>() + (has_min<TYPE>() ? 1 : 0);
+  return (SB * TCfg<BM>::FPB + TWAVES - 1) / TWAVES + b_dma_per_wave<TYPE>();
 }
 // Ring depth: as many stages as 160 KiB of LDS holds, 3 to 8 (a deeper ring
 // keeps more weight bytes in flight where a stage is small), with the copies
@@ -145,11 +148,11 @@ constexpr size_t tiled_lds_bytes() { return static_cast<size_t>(nstage<TYPE, BM>
 // ---------------------------------------------------------------- packing
 // One workgroup per token row t of the padded tile grid (token tiles of bm
 // rows).  Rows t >= n_tokens are written as zeros.  rscale[t] = 2^e with
-// max|x_t| * 2^-e in [2^13, 2^14); bsum = per-block sums of hi + lo, laid
-// out [T][b][bm] (Q4_1), or kGemmQ4F's per-super-block sums S as the A
-// operand of its dmin products: fp16 limbs hi = fp16(S 2^-10),
-// lo = fp16(S 2^-10 - hi) (|S| < 2^22, so no overflow), laid out
-// [t][limb][q4f_dmin_stride(k)], zero past the row's super-blocks.
+// max|x_t| * 2^-e in [2^13, 2^14); bsum = the sums S of hi + lo over each
+// unit of the minimum term (Q4_1: 32-element block; kGemmQ4F: 256-element
+// super-block) as the A operand of its products: fp16 limbs
+// hi = fp16(S 2^-10), lo = fp16(S 2^-10 - hi) (|S| < 2^22, so no overflow),
+// laid out [t][limb][units rounded up to 8], zero past the row's units.
 // Thread p of a chunk owns the (block, k-group) pairs p, p + NTH, ... (NTH =
 // blockDim.x, 256 .. 1024 by the row length): the 8 elements of a pair are
 // two float4 loads (slot_elem order), all issued before the first use; a row
@@ -318,27 +321,26 @@ __global__ __launch_bounds__(kPackMaxThreads) void pack_a_kernel(const float* __
       *reinterpret_cast<half8*>(frag + base) = hv;          // limb 0 (hi)
       *reinterpret_cast<half8*>(frag + base + 512) = lv;    // limb 1 (lo)
       if (bsum) {
-        // the four k-groups of a block are adjacent lanes (p = 4b + g)
+        // the unit's lanes: the four k-groups of a block are adjacent lanes
+        // (p = 4 b + g); a super-block's 8 blocks are 32 adjacent lanes
+        // (p = 32 sb + ..; rows are whole super-blocks, so all 32 are live)
         part += __shfl_xor(part, 1, 64);
         part += __shfl_xor(part, 2, 64);
-        if (type == wh::kGemmQ4F) {
-          // per 256-element super-block: its 8 blocks are 32 adjacent lanes
-          // (p = 32 sb + ..; rows are whole super-blocks, so all 32 are live)
+        const bool sup = type == wh::kGemmQ4F;
+        if (sup) {
           part += __shfl_xor(part, 4, 64);
           part += __shfl_xor(part, 8, 64);
           part += __shfl_xor(part, 16, 64);
-          if ((p & 31) == 0) {
-            const int nsb = nb / 8, nsbp = (nsb + 7) & ~7, sb = b >> 3;
-            _Float16* sr = reinterpret_cast<_Float16*>(bsum) + static_cast<size_t>(t) * 2 * nsbp;
-            const float sv = part * 0x1p-10f;  // exact
-            const _Float16 h = static_cast<_Float16>(sv);
-            sr[sb] = h;
-            sr[nsbp + sb] = static_cast<_Float16>(sv - static_cast<float>(h));
-            if (sb == nsb - 1)  // the row's last super-block clears the padding
-              for (int z = nsb; z < nsbp; z++) sr[z] = sr[nsbp + z] = static_cast<_Float16>(0.f);
-          }
-        } else if (g == 0) {
-          bsum[(static_cast<size_t>(T) * nb + b) * bm + (t % bm)] = part;
+        }
+        if ((p & (sup ? 31 : 3)) == 0) {
+          const int nu = sup ? nb / 8 : nb, nup = (nu + 7) & ~7, u = sup ? b >> 3 : b;
+          _Float16* sr = reinterpret_cast<_Float16*>(bsum) + static_cast<size_t>(t) * 2 * nup;
+          const float sv = part * 0x1p-10f;  // exact
+          const _Float16 h = static_cast<_Float16>(sv);
+          sr[u] = h;
+          sr[nup + u] = static_cast<_Float16>(sv - static_cast<float>(h));
+          if (u == nu - 1)  // the row's last unit clears the padding
+            for (int z = nu; z < nup; z++) sr[z] = sr[nup + z] = static_cast<_Float16>(0.f);
         }
       }
     }
@@ -536,10 +538,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
   constexpr int A_FR = SB * FPB;                                    // fragments per stage
   constexpr int A_DMA = (A_FR + TWAVES - 1) / TWAVES;               // copies per wave (wrapping)
   constexpr int B_DMA = b_dma_per_wave<TYPE>();
-  constexpr int S_CH = SB * BM / 4;                                 // Q4_1 block-sum chunks per stage
-  constexpr int S_PW = S_CH / TWAVES;                               // ... per wave (>= 1)
-  constexpr int S_DMA = has_min<TYPE>() ? 1 : 0;
-  constexpr int PER_STAGE = A_DMA + B_DMA + S_DMA;                  // vmcnt per stage
+  constexpr int PER_STAGE = A_DMA + B_DMA;                          // vmcnt per stage
   static_assert(PER_STAGE == per_stage<TYPE, BM>(), "copy count");
   static_assert((NSTAGE - 2) * PER_STAGE < 64, "vmcnt range");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -632,14 +631,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
         if (TWAVES * 64 * c + 64 * __builtin_amdgcn_readfirstlane(wave) >= HALF * DWB) wb = W2;
       copy4_to_lds(wb + kboff, b_off[c], bslot + 4 * (TWAVES * 64 * c + 64 * wave));
     }
-    if constexpr (has_min<TYPE>()) {
-      // block sums [SB][BM] of this token tile: S_CH chunks of 16 B, S_PW per
-      // wave, copied by lanes 0 .. S_PW - 1 (one instruction per wave)
-      const int ci = wave * S_PW + lane;
-      const int j = ci / (BM / 4), cc = ci % (BM / 4);
-      const uint32_t off = static_cast<uint32_t>(((static_cast<size_t>(T) * nb + kb + j) * BM + 4 * cc) * 4);
-      if (lane < S_PW) copy16_to_lds(bsum, off, slot + A_STAGE + BSTAGE + 16 * S_PW * wave);
-    }
   };
 
   float4v acc[IT][NT];
@@ -667,20 +658,46 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     for (int h = 0; h < 2; h++)
 #pragma unroll
       for (int i = 0; i < IT; i++) cc[b][h][i] = float4v{0.f, 0.f, 0.f, 0.f};
-  float pd[2] = {0.f, 0.f}, pm[2] = {0.f, 0.f};  // pending block scales (and Q4_1 minima)
-  float4v psx[IT];                               // pending Q4_1 block sums
+  float pd[2] = {0.f, 0.f};  // pending block scales
+  // Q4_1: the m of the current window's blocks as MFMA B operands, lane group
+  // g holding blocks 8g .. 8g + 7 of the window (blocks of other parts zero)
+  u32x4 mfr[NT];
 #pragma unroll
-  for (int i = 0; i < IT; i++) psx[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < NT; n++) mfr[n] = u32x4{0u, 0u, 0u, 0u};
   const uint32_t magic = 0x64006400u;  // fp16 1024 in both halves (held in a VGPR)
 
-  // acc[i][N] += pd[h] * cc[B][h][i] (+ pm[h] * psx[i]); constants after unrolling
+  // acc[i][N] += pd[h] * cc[B][h][i]; constants after unrolling
   auto scale_one = [&](int N, int B, int h, int i) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float v = __builtin_fmaf(pd[h], cc[B][h][i][r], acc[i][N][r]);
-      if constexpr (has_min<TYPE>()) v = __builtin_fmaf(pm[h], psx[i][r], v);
-      acc[i][N][r] = v;
+    for (int r = 0; r < 4; r++) acc[i][N][r] = __builtin_fmaf(pd[h], cc[B][h][i][r], acc[i][N][r]);
+  };
+  // Q4_1: acc += 2^10 (S 2^-10 . m) over the window starting at block w0: the
+  // A operands (the packing's fp16 limbs of the block sums S) from memory,
+  // two MFMAs per 16 x 16 outputs; then the window's m start again at zero
+  auto flush_min = [&](int w0) {
+    const int nbp = (nb + 7) & ~7;
+    const int s0 = w0 + 8 * g;
+    const bool in = s0 < nbp;
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(bsum);
+    u32x4 sh[IT], sl[IT];
+#pragma unroll
+    for (int i = 0; i < IT; i++) {
+      const uint32_t off = static_cast<uint32_t>((t0 + wm + 16 * i + ln) * 2 * nbp + s0);
+      sh[i] = in ? *reinterpret_cast<const u32x4*>(s16 + off) : u32x4{0u, 0u, 0u, 0u};
+      sl[i] = in ? *reinterpret_cast<const u32x4*>(s16 + off + nbp) : u32x4{0u, 0u, 0u, 0u};
     }
+#pragma unroll
+    for (int i = 0; i < IT; i++)
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, sh[i]), __builtin_bit_cast(half8, mfr[n]),
+                                                           float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, sl[i]), __builtin_bit_cast(half8, mfr[n]), t, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][n][r] = __builtin_fmaf(1024.f, t[r], acc[i][n][r]);
+      }
+#pragma unroll
+    for (int n = 0; n < NT; n++) mfr[n] = u32x4{0u, 0u, 0u, 0u};
   };
 
   // A head part (SK) that does not get every other owner's slot in time runs
@@ -694,9 +711,7 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
       for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int i = 0; i < IT; i++) cc[b][h][i] = float4v{0.f, 0.f, 0.f, 0.f};
-    pd[0] = pd[1] = pm[0] = pm[1] = 0.f;
-#pragma unroll
-    for (int i = 0; i < IT; i++) psx[i] = float4v{0.f, 0.f, 0.f, 0.f};
+    pd[0] = pd[1] = 0.f;
   }
 #pragma unroll
   for (int st = 0; st < NSTAGE - 1; st++) issue(st);
@@ -710,7 +725,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
     // every LDS operand of the stage, read up front
     half8 ah[SB][IT], al[SB][IT];
     uint32_t wq0[SB][NT], wq1[SB][NT], wdm[SB][NT];
-    float4v sx[SB][IT];
     auto load_a = [&](int j) {
 #pragma unroll
       for (int i = 0; i < IT; i++) {
@@ -748,11 +762,6 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
           wdm[j][n] = TYPE == WH_TYPE_Q4_1 ? (static_cast<uint32_t>(r16[0]) | (static_cast<uint32_t>(r16[1]) << 16))
                                            : static_cast<uint32_t>(r16[0]);
         }
-      }
-      if constexpr (has_min<TYPE>()) {
-        const float* ss = reinterpret_cast<const float*>(slot + A_STAGE + BSTAGE) + j * BM;
-#pragma unroll
-        for (int i = 0; i < IT; i++) sx[j][i] = *reinterpret_cast<const float4v*>(ss + wm + 16 * i + 4 * g);
       }
     }
     half8 bw[2];
@@ -803,17 +812,27 @@ __global__ __launch_bounds__(TWAVES * 64, 1) void gemm_tiled_kernel(
             pd[h] = __uint_as_float(wdm[j][2 * np + h]);
           } else {
             pd[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] & 0xFFFFu);
-            if constexpr (TYPE == WH_TYPE_Q4_1) pm[h] = whd::f16_bits_to_f32(wdm[j][2 * np + h] >> 16);
           }
           asm("" : "+v"(pd[h]));  // in a VGPR: the FMAs are then plain v_fmac_f32
-        }
-        if constexpr (has_min<TYPE>()) {
-#pragma unroll
-          for (int i = 0; i < IT; i++) psx[i] = sx[j][i];
         }
         bw[0] = bn[0];
         bw[1] = bn[1];
       }
+    }
+    if constexpr (has_min<TYPE>()) {
+      // the stage's two blocks' m (bits 16..31 of wdm) into dword (kb mod 8) / 2
+      // of lane group (kb mod 32) / 8 of the window's B operands
+      static_assert(SB == 2, "one B-operand dword per stage");
+      const int kb = kb0 + st * SB, pw = kb & 31;
+      const bool mine = g == (pw >> 3);
+      const int dq = (pw & 7) >> 1;
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        const uint32_t val = __builtin_amdgcn_perm(wdm[1][n], wdm[0][n], 0x07060302u);
+#pragma unroll
+        for (int d = 0; d < 4; d++) mfr[n][d] = (d == dq && mine) ? val : mfr[n][d];
+      }
+      if (pw == 32 - SB || st == n_stages - 1) flush_min(kb & ~31);
     }
   }
   // flush the pending scales (the last pair of the last block)
