@@ -38,7 +38,8 @@ Prints ONE JSON line with:
                  copies of host weights on
   prefill_*      config 2's M sweep (f32 and bf16 activations); the K-quant
                  formats and Q4_1 at a few tokens, and at M=512 with blocks
-                 converted once per weight handle (and, for comparison, per call)
+                 converted once per weight handle (and, for comparison, per call);
+                 Q4_1's GEMM and FFN at M=512
   gemv_other_configs  the other decode GEMV configurations: Q4_0 4096x4096,
                  Q8_0 and Q4_1 14336x4096, and the other decode-step shapes (k/v
                  projections, FFN down, the Q8_0 128256x4096 output head):
@@ -746,7 +747,11 @@ def main() -> int:
                 us, sp = bench_gemm(m, 20, t)
                 gemm_kq[f"gemm_{name}_m{m}"] = {"us": round(us, 2), "spread": round(sp, 4)}
                 log(f"[bench] gemm {name} m={m}: {us:.2f} us")
-            if t == 3:
+            if t == 3:  # no conversion: the tiled GEMM reads Q4_1 blocks as they are
+                us, sp = bench_gemm(512, 5, t)
+                tf = 2.0 * 512 * N_ROWS * K / (us * 1e-6) / 1e12
+                gemm_kq["gemm_q4_1_m512"] = {"us": round(us, 2), "tflops": round(tf, 2), "spread": round(sp, 4)}
+                log(f"[bench] gemm q4_1 m=512: {us:.2f} us, {tf:.1f} TFLOP/s")
                 continue
             for prep in (True, False):
                 us, sp = bench_gemm(512, 5, t, prepared=prep)
@@ -762,6 +767,9 @@ def main() -> int:
                 gemm_kq[f"ffn_{name}_m1_us"] = round(us1, 2)
                 gemm_kq[f"ffn_{name}_m512_us"] = round(us512, 2)
                 log(f"[bench] ffn {name}: m=1 {us1:.2f} us, m=512 {us512:.2f} us (prepared handles)")
+            us512, _ = bench_ffn(512, 3, 3)
+            gemm_kq["ffn_q4_1_m512_us"] = round(us512, 2)
+            log(f"[bench] ffn q4_1: m=512 {us512:.2f} us")
 
     # the other decode GEMV configurations (config 0, 1a, 1b); replicas keep
     # each timed set of weights above the 256 MB Infinity Cache
