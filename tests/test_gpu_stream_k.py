@@ -172,3 +172,34 @@ def test_stream_k_fallback_ffn(gpu, orc):
     # here against the bar's 3.3e-6
     assert r <= REL_L2 and a <= 2.0 * max_abs_bar(ref)
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("n,k,m", [(10240, 1024, 512),   # three owners: parts end inside the 32-block window
+                                   (4096, 14336, 100),   # sixteen owners over 14 windows per row
+                                   (2048, 1600, 200)])   # 50 blocks per row: a last window of 18
+def test_q4_1_dominant_minima(gpu, orc, n, k, m):
+    """Q4_1 blocks whose minimum m is 16 to 64 times the block scale d, of
+    either sign, against activations with a mean of 0.5, so that the m * sum(x)
+    term carries most of each output.  The tiled GEMM forms that term as
+    matrix-core products of each 32-block window's minima against the packed
+    block sums, flushed at the window's end or where a stream-K part ends, so
+    these shapes put part ends inside windows and a partial last window."""
+    print(f"[case] q4_1 dominant minima m={m} n={n} k={k} owners<={owners_per_tile(n, k, m)}", flush=True)
+    w = synth.quantized_weight(Q4_1, n, k, seed=n + k + 7)
+    blocks = w.reshape(-1, 20)
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    rng = np.random.default_rng(n + k)
+    mult = rng.uniform(16.0, 64.0, size=d.shape) * rng.choice([-1.0, 1.0], size=d.shape)
+    mins = (np.abs(d) * mult).astype(np.float16)
+    blocks[:, 2:4] = mins.view(np.uint8).reshape(-1, 2)
+    x = synth.activations(m * k, seed=m + k, mean=0.5).reshape(m, k)
+    outs = run_matmul(Q4_1, w, n, k, x, m)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "repeated calls differ"
+    rows = np.array([r for r in ROWS if r < m], dtype=np.int64)
+    ref = orc.matmul_rows_f64(Q4_1, w, n, k, x, m, rows)
+    got = outs[0][rows]
+    r, a = rel_l2(got, ref), max_abs(got, ref)
+    report(f"q4_1 dominant minima m={m} n={n} k={k}", r, a, ref)
+    assert r <= REL_L2 and a <= max_abs_bar(ref)
+    assert np.all(np.isfinite(got))
