@@ -128,20 +128,22 @@ def test_ffn_llama3_8b_m1(gpu, orc):
     assert r <= REL_L2 and a <= 1e-3
 
 
-@pytest.mark.parametrize("m", [64, 512])
-def test_ffn_llama3_8b_prefill(gpu, orc, m):
-    """Config 3 at M=64 / M=512 (MFMA path).  Token rows are independent, so the
-    f64 oracle checks a sample of rows at full size."""
+@pytest.mark.parametrize("t,m", [(Q4_0, 64), (Q4_0, 512), (Q4_1, 512)])
+def test_ffn_llama3_8b_prefill(gpu, orc, t, m):
+    """Config 3 at M=64 / M=512 (MFMA path; at 512 gate and up in one fused
+    launch, for Q4_1 with its minimum term on the matrix cores).  Token rows are
+    independent, so the f64 oracle checks a sample of rows at full size."""
     hidden, n_ff = 4096, 14336
-    L = synth.ffn_layer(Q4_0, hidden, n_ff, m, seed=5)
-    got = run_ffn(Q4_0, L, hidden, n_ff, m)
+    print(f"[case] ffn-8b type={t} m={m}", flush=True)
+    L = synth.ffn_layer(t, hidden, n_ff, m, seed=5)
+    got = run_ffn(t, L, hidden, n_ff, m)
     rows = sorted({0, 1, m // 2, m - 1})
-    ref = orc.ffn_rows_f64(Q4_0, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5,
+    ref = orc.ffn_rows_f64(t, L["gate"], L["up"], L["down"], hidden, n_ff, L["gamma"], 1e-5,
                            L["x"], rows)
     g = got[rows]
     r, a = rel_l2(g, ref), max_abs(g, ref)
     rms = float(np.sqrt(np.mean(ref ** 2)))
-    print(f"[result] ffn-8b m={m} rows={rows} rel_l2={r:.3e} max_abs={a:.3e} rms={rms:.1f}", flush=True)
+    print(f"[result] ffn-8b t={t} m={m} rows={rows} rel_l2={r:.3e} max_abs={a:.3e} rms={rms:.1f}", flush=True)
     assert r <= REL_L2 and a <= 1e-3
     assert np.all(np.isfinite(got))
 
